@@ -1,0 +1,259 @@
+"""Benchmark of the SeedVR2 DiT window-attention hot path on one MI355X.
+
+Workload (one step = one DiT block's hot path at the SeedVR2-3B 720p video
+shape, 21 frames at 1280x720 -> 6x45x80 = 21,600 video tokens + 64 text
+tokens, hidden 2560, 20 heads x 128, bf16 with fp32 accumulation):
+
+  SharedLinear QKV   2560 -> 7680        (both streams, one grouped launch)
+  AdaptiveWindowAttention, regular 3-D windows (27 windows of 780/810 tokens)
+  SharedLinear out   2560 -> 2560
+  SharedLinear MLP   2560 -> 10240, GELU
+  SharedLinear MLP   10240 -> 2560
+
+Algorithmic work per step: 4*H*d*sum_w (n_w+64)^2 attention FLOPs (206.45 G)
+plus 2*M*K*N per GEMM with M = 21,664 (3,407.45 G): 3.614 TFLOP.  Inputs and
+weights are resident in HBM before the timed region (seeded N(0,1)
+activations, N(0,0.02) weights).  The shifted-window block (64 ragged
+windows) is timed too and reported beside the headline.
+
+Prints one JSON line.  `--gpus` above 1 is refused: this build measures one GPU.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+
+VIDEO_SHAPE = (6, 45, 80)
+TEXT_TOKENS = 64
+HIDDEN, HEADS, HEAD_DIM, PAIRS = 2560, 20, 128, 21
+MLP = 10240
+TARGET = (4, 3, 3)
+
+
+def attention_flops(shifted):
+    from seedvr2_ncnn_amd import capi
+    wins, _, _ = capi.plan_windows([VIDEO_SHAPE], TARGET, shifted)
+    return sum(4 * HEADS * HEAD_DIM * (w[8] + TEXT_TOKENS) ** 2 for w in wins)
+
+
+def prologue_bytes(lv, lt):
+    # read q,k,v bf16 once + write windowed q,k,v bf16 once + int32 index and
+    # three positions per video token
+    return 2 * (lv + lt) * 3 * HIDDEN * 2 + 16 * lv
+
+
+def cpu_baseline(threads, budget_s=20.0):
+    """The oracle's optimised build (oracle/liboracle_fast.so, the reference's
+    CPU forward restated in C) timed on a bounded sample of the same block:
+    two of the 27 attention windows and 48 rows of each GEMM.  Each op's
+    rate is scaled to its full work to give a block time."""
+    import numpy as np
+    import oracle
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from common import make_awa_inputs, oracle_awa
+
+    t_start = time.time()
+    shapes, tl = [VIDEO_SHAPE], [TEXT_TOKENS]
+    case = make_awa_inputs(7, shapes, tl, HEADS, HEAD_DIM, PAIRS, bf16=True)
+    p = oracle.plan(shapes, TARGET, 0)
+    subset = [0, 13]
+    sample_attn = sum(4 * HEADS * HEAD_DIM * (int(p.windows[i, 8]) + TEXT_TOKENS) ** 2 for i in subset)
+    t0 = time.perf_counter()
+    oracle_awa(case, HEADS, HEAD_DIM, TARGET, 0, 1e-5, PAIRS, shapes, tl, window_subset=subset,
+               threads=threads, fast=True)
+    attn_rate = sample_attn / (time.perf_counter() - t0)
+    del case
+    g = np.random.default_rng(3)
+    rows = np.arange(48, dtype=np.int32)
+    gemm_time = 0.0
+    m = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2] + TEXT_TOKENS
+    sample_gemm = 0
+    for k, n, act in ((HIDDEN, 3 * HIDDEN, 0), (HIDDEN, HIDDEN, 0), (HIDDEN, MLP, 1), (MLP, HIDDEN, 0)):
+        x = g.standard_normal((48, k), dtype=np.float32)
+        w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
+        t0 = time.perf_counter()
+        oracle.linear(x, w, None, act, rows=rows, threads=threads, fast=True)
+        dt = time.perf_counter() - t0
+        sample_gemm += 2 * 48 * k * n
+        gemm_time += dt * m / 48.0
+    attn_time = attention_flops(0) / attn_rate
+    block_time = attn_time + gemm_time
+    total = attention_flops(0) + 2 * m * (HIDDEN * 3 * HIDDEN + HIDDEN * HIDDEN + 2 * HIDDEN * MLP)
+    return {
+        "value": round(total / block_time / 1e12, 6),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"oracle/liboracle_fast.so (reference CPU forward restated in C, fp32, "
+                   f"OpenMP over heads/rows) on 2 of 27 regular windows "
+                   f"({sample_attn / 1e9:.1f} GFLOP) and 48 rows of each of the 4 GEMMs "
+                   f"({sample_gemm / 1e9:.1f} GFLOP), scaled to the full block: "
+                   f"{block_time:.1f} s per block; sampled in {time.time() - t_start:.1f} s"),
+        "ms_per_block": round(block_time * 1e3, 1),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
+              "(the multi-GPU sharding is a design, not a measured path)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from seedvr2_ncnn_amd import capi
+
+    assert torch.cuda.is_available() and capi.device_count() >= 1, "needs a gfx950 GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(20240601)
+    bf = torch.bfloat16
+    lv = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2]
+    lt = TEXT_TOKENS
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(bf)
+
+    x_v, x_t = randn(lv, HIDDEN), randn(lt, HIDDEN)
+    w_qkv, w_o = randn(3 * HIDDEN, HIDDEN, std=0.02), randn(HIDDEN, HIDDEN, std=0.02)
+    w_up, w_dn = randn(MLP, HIDDEN, std=0.02), randn(HIDDEN, MLP, std=0.02)
+    b = {n: (torch.randn(n, generator=gen, device=dev) * 0.02) for n in (3 * HIDDEN, HIDDEN, MLP)}
+    norms = (1.0 + 0.02 * torch.randn(4, HEAD_DIM, generator=gen, device=dev)).contiguous()
+    freqs = (10000.0 ** (-torch.arange(PAIRS, device=dev, dtype=torch.float64) / PAIRS)).float()
+
+    qkv_v = torch.empty(lv, 3 * HIDDEN, dtype=bf, device=dev)
+    qkv_t = torch.empty(lt, 3 * HIDDEN, dtype=bf, device=dev)
+    a_v = torch.empty(lv, HIDDEN, dtype=bf, device=dev)
+    a_t = torch.empty(lt, HIDDEN, dtype=bf, device=dev)
+    o_v, o_t = torch.empty_like(a_v), torch.empty_like(a_t)
+    h_v = torch.empty(lv, MLP, dtype=bf, device=dev)
+    h_t = torch.empty(lt, MLP, dtype=bf, device=dev)
+    y_v, y_t = torch.empty_like(a_v), torch.empty_like(a_t)
+
+    plans = {s: capi.AwaPlan(capi.awa_config(HEADS, HEAD_DIM, TARGET, s, 1e-5, PAIRS),
+                             [VIDEO_SHAPE], [lt]) for s in (0, 1)}
+    ws = torch.empty(max(p.info.workspace_bytes for p in plans.values()), dtype=torch.uint8, device=dev)
+
+    ops = ["qkv", "attention", "out", "mlp_up", "mlp_down"]
+
+    def step(shifted, ev=None):
+        def mark(i):
+            if ev is not None:
+                ev[i].record()
+        mark(0)
+        capi.shared_linear(x_v, x_t, w_qkv, b[3 * HIDDEN], capi.ACT_NONE, y_video=qkv_v, y_text=qkv_t)
+        mark(1)
+        capi.awa_forward(plans[shifted], norms, freqs,
+                         qkv_v[:, :HIDDEN], qkv_v[:, HIDDEN:2 * HIDDEN], qkv_v[:, 2 * HIDDEN:],
+                         qkv_t[:, :HIDDEN], qkv_t[:, HIDDEN:2 * HIDDEN], qkv_t[:, 2 * HIDDEN:],
+                         workspace=ws, out_video=a_v, out_text=a_t)
+        mark(2)
+        capi.shared_linear(a_v, a_t, w_o, b[HIDDEN], capi.ACT_NONE, y_video=o_v, y_text=o_t)
+        mark(3)
+        capi.shared_linear(o_v, o_t, w_up, b[MLP], capi.ACT_GELU, y_video=h_v, y_text=h_t)
+        mark(4)
+        capi.shared_linear(h_v, h_t, w_dn, b[HIDDEN], capi.ACT_NONE, y_video=y_v, y_text=y_t)
+        mark(5)
+
+    def run(shifted, steps, warmup):
+        for _ in range(warmup):
+            step(shifted)
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        start.record()
+        for i in range(steps):
+            step(shifted, evs[i])
+        end.record()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        total_ms = start.elapsed_time(end)
+        per_op = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(ops)}
+        return total_ms / steps, per_op, wall
+
+    m = lv + lt
+    gemm = {"qkv": 2 * m * HIDDEN * 3 * HIDDEN, "out": 2 * m * HIDDEN * HIDDEN,
+            "mlp_up": 2 * m * HIDDEN * MLP, "mlp_down": 2 * m * MLP * HIDDEN}
+    results = {}
+    for shifted in (0, 1):
+        ms, per_op, wall = run(shifted, args.steps, args.warmup)
+        flops = dict(gemm, attention=attention_flops(shifted))
+        results[shifted] = (ms, per_op, flops, wall)
+
+    ms, per_op, flops, wall = results[0]
+    block_flops = sum(flops.values())
+    value = block_flops / (ms * 1e-3) / 1e12
+    kernels = {op: {"ms": round(per_op[op], 4), "gflop": round(flops[op] / 1e9, 3),
+                    "tflops": round(flops[op] / (per_op[op] * 1e-3) / 1e12, 1),
+                    "frac_bf16_peak": round(flops[op] / (per_op[op] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+               for op in ops}
+    up_ms = per_op["mlp_up"]
+    up_tf = flops["mlp_up"] / (up_ms * 1e-3) / 1e12
+    ms_s, per_op_s, flops_s, _ = results[1]
+    line = {
+        "metric": "window-attn+SharedLinear TFLOP/s & % bf16 MFMA peak; ms/DiT block @720p video",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) activations, N(0,0.02) weights, random init)",
+        "config": {
+            "workload": "SeedVR2-3B DiT block hot path at 720p video: 21 frames 1280x720 -> "
+                        "6x45x80 = 21600 video + 64 text tokens, hidden 2560, 20x128 heads, "
+                        "regular 3-D windows (target 4,3,3); QKV 2560->7680, window attention, "
+                        "out 2560->2560, MLP 2560->10240 GELU ->2560",
+            "video_tokens": lv, "text_tokens": lt, "hidden": HIDDEN, "heads": HEADS,
+            "head_dim": HEAD_DIM, "block_tflop": round(block_flops / 1e12, 4),
+        },
+        "pct_bf16_peak": round(100 * value / PEAK_BF16_TFLOPS, 2),
+        "ms_per_block": round(ms, 4),
+        "ms_per_block_shifted": round(ms_s, 4),
+        "tflops_shifted": round(sum(flops_s.values()) / (ms_s * 1e-3) / 1e12, 2),
+        "attention_shifted": {"ms": round(per_op_s["attention"], 4),
+                              "tflops": round(flops_s["attention"] / (per_op_s["attention"] * 1e-3) / 1e12, 1)},
+        "kernels": kernels,
+        "prologue_algorithmic_bytes": prologue_bytes(lv, lt),
+        "roofline": {
+            "kernel": "shared_linear_kernel (MLP up 2560->10240 + GELU, M=21664)",
+            "bound": "mfma",
+            "achieved": round(up_tf, 1),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(up_tf / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+        },
+        "wall_s_timed_region": round(wall, 3),
+    }
+    if not args.no_cpu_baseline:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        line["cpu_baseline"] = cpu_baseline(threads)
+    for p in plans.values():
+        p.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,171 @@
+/*
+ * seedvr2_hip.h -- C-ABI of the MI355X (gfx950) window-attention hot path.
+ *
+ * This is the boundary the C++ ncnn-surface layers (AdaptiveWindowAttention,
+ * SharedLinear) call.  Plain C: plain pointers and sizes, no HIP or torch
+ * types.  Device pointers are HIP device addresses; a stream is a hipStream_t
+ * passed as void* (NULL = the default stream).  No function throws; every
+ * function returns one of the codes below, which mirror the reference layers'
+ * int returns (src/seedvr2/adaptive_window_attention.cpp:764-978,
+ * src/seedvr2/shared_linear.cpp:83-96).
+ */
+#ifndef SEEDVR2_HIP_H
+#define SEEDVR2_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define S2_OK 0
+#define S2_ERR_INVALID (-1)    /* bad configuration, shape or arity (reference -1) */
+#define S2_ERR_PLAN (-2)       /* window plan is not a permutation (reference -2) */
+#define S2_ERR_ALLOC (-100)    /* allocation failure (reference -100) */
+#define S2_ERR_DEVICE (-200)   /* HIP runtime error or no usable gfx950 device */
+
+typedef void* s2_stream_t;
+
+typedef enum s2_dtype {
+    S2_DTYPE_F32 = 0,
+    S2_DTYPE_BF16 = 1
+} s2_dtype;
+
+typedef enum s2_activation {
+    S2_ACT_NONE = 0,
+    S2_ACT_GELU = 1    /* erf-GELU, 0.5 x (1 + erf(x / sqrt 2)) */
+} s2_activation;
+
+/* One attention window.  Same fields and meaning as the reference
+ * seedvr2::WindowSlice (adaptive_window_attention.h:16-27). */
+typedef struct s2_window_slice {
+    int sample_index;
+    int t0, t1, h0, h1, w0, w1;
+    int partition_offset;
+    int token_count;
+} s2_window_slice;
+
+/* AdaptiveWindowAttention configuration.  Field i corresponds to ParamDict
+ * id i of the reference load_param (adaptive_window_attention.cpp:700-714);
+ * id 9 (shape_values_are_int32) is a blob-decoding detail of the layer and
+ * does not reach this boundary. */
+typedef struct s2_awa_config {
+    int heads;                    /* id 0, default 20 */
+    int head_dim;                 /* id 1, default 128; 64 and 128 supported */
+    int target_windows[3];        /* ids 2,3,4, default 4,3,3 */
+    int shifted;                  /* id 5, default 0 */
+    float epsilon;                /* id 6, default 1e-5 */
+    int rope_pairs_per_axis;      /* id 7, default 21; 6*pairs <= head_dim */
+    int shared_norm;              /* id 8: informational, weights arrive as 4 rows */
+    int official_bf16_attention;  /* id 10: round q,k,v and context to bf16 */
+} s2_awa_config;
+
+typedef struct s2_awa_plan s2_awa_plan;   /* opaque, device-resident plan */
+
+typedef struct s2_awa_plan_info {
+    int batch;
+    int num_windows;
+    int video_tokens;          /* sum over samples of t*h*w */
+    int text_tokens;           /* sum of text lengths */
+    size_t workspace_bytes;    /* device workspace s2_awa_forward needs */
+} s2_awa_plan_info;
+
+/* ---- device memory (so layer host code needs no HIP headers) ---------- */
+
+/* Number of gfx950 devices visible; 0 with S2_OK when there are none. */
+int s2_device_count(int* count);
+int s2_malloc(void** ptr, size_t bytes);
+int s2_free(void* ptr);
+int s2_memcpy_h2d(void* dst, const void* src, size_t bytes, s2_stream_t stream);
+int s2_memcpy_d2h(void* dst, const void* src, size_t bytes, s2_stream_t stream);
+int s2_memcpy_d2d(void* dst, const void* src, size_t bytes, s2_stream_t stream);
+int s2_stream_synchronize(s2_stream_t stream);
+/* Last HIP error string recorded by this library on the calling thread. */
+const char* s2_last_error(void);
+
+/* ---- window plan -------------------------------------------------------- */
+
+/* Host-side window list of build_adaptive_window_plan
+ * (adaptive_window_attention.cpp:565-655): windows in the reference order
+ * (w outer, h, t inner, per sample).  video_shapes is [batch][3] (t,h,w).
+ * Pass windows == NULL to query *num_windows.  sample_window_count
+ * ([batch]) and video_tokens may be NULL.  Returns S2_OK or S2_ERR_INVALID. */
+int s2_awa_plan_windows(const int* video_shapes, int batch, const int target_windows[3],
+                        int shifted, s2_window_slice* windows, int max_windows,
+                        int* num_windows, int* sample_window_count, int* video_tokens);
+
+/* Builds the device-resident plan for one set of runtime shapes (the
+ * reference rebuilds its plan on every forward, :833-836 and :1116-1120; a
+ * caller keeps this handle while the shapes stay the same).  text_lengths is
+ * [batch], each > 0 (reference :813-814). */
+int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
+                       const int* text_lengths, int batch, s2_awa_plan** plan);
+int s2_awa_plan_get_info(const s2_awa_plan* plan, s2_awa_plan_info* info);
+/* Copies the plan's window list / per-sample window counts to host arrays. */
+int s2_awa_plan_get_windows(const s2_awa_plan* plan, s2_window_slice* windows,
+                            int max_windows, int* sample_window_count);
+int s2_awa_plan_destroy(s2_awa_plan* plan);
+
+/* Materialises the plan's per-token tables on the device with the same
+ * integer index math the forward kernels use: video_indices[L] (partition ->
+ * source token), inverse_video_indices[L], local_positions[L][3]
+ * (AdaptiveWindowPlan, adaptive_window_attention.h:29-36).  int32 device
+ * arrays; any may be NULL. */
+int s2_awa_plan_tables(const s2_awa_plan* plan, int* video_indices,
+                       int* inverse_video_indices, int* local_positions,
+                       s2_stream_t stream);
+
+/* ---- AdaptiveWindowAttention forward ------------------------------------ */
+
+/* The whole layer (reference CPU forward adaptive_window_attention.cpp:764-978,
+ * Vulkan forward :1059-1270): per window, gather video q/k/v by plan index,
+ * append the sample's text tokens, RMSNorm q and k, 3-axis RoPE, softmax
+ * (q k^T / sqrt(d)) v over window+text, scatter video rows back to source
+ * order and mean-pool text rows over the sample's windows.
+ *
+ * norm_weights: device fp32 [4][head_dim] = video_norm_q, video_norm_k,
+ *   text_norm_q, text_norm_k (the upload_model packing, :1047-1053).
+ * rope_freqs: device fp32 [rope_pairs_per_axis].
+ * video_q/k/v: device rows of width heads*head_dim with row stride
+ *   video_row_stride elements: the fused [L][3*inner] blob gives
+ *   (base, base+inner, base+2*inner, 3*inner), the split blobs give three
+ *   pointers with stride inner (reference 4- and 8-input forms, :768-797).
+ * in_dtype: F32 or BF16 for all six inputs.
+ * out_video [video_tokens][inner], out_text [text_tokens][inner] in out_dtype.
+ * workspace: device memory of at least info.workspace_bytes, 256-byte aligned.
+ * All work is enqueued on stream; nothing is synchronised. */
+int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights,
+                   const float* rope_freqs,
+                   const void* video_q, const void* video_k, const void* video_v,
+                   long video_row_stride,
+                   const void* text_q, const void* text_k, const void* text_v,
+                   long text_row_stride, s2_dtype in_dtype,
+                   void* out_video, void* out_text, s2_dtype out_dtype,
+                   void* workspace, size_t workspace_bytes, s2_stream_t stream);
+
+/* ---- SharedLinear -------------------------------------------------------- */
+
+/* fp32 -> bf16 (round to nearest even) on the device; used to keep weights
+ * resident in bf16 (SharedLinear::load_model, shared_linear.cpp:61-81). */
+int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream_t stream);
+int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream_t stream);
+
+/* SharedLinear::forward (shared_linear.cpp:83-96): one projection applied to
+ * two token streams in ONE grouped launch sharing the weight:
+ *   y_video = act(x_video W^T + b),  y_text = act(x_text W^T + b).
+ * weight: device bf16 [n][k] row-major (the reference [N][K] layout,
+ * :66-69); bias: device fp32 [n] or NULL (param 2).  x_*: device
+ * [m_*][k] in x_dtype; y_*: device [m_*][n] in y_dtype.  Either stream may
+ * have m == 0 (its pointers are then ignored).  k must be a multiple of 8. */
+int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
+                             s2_dtype x_dtype, const uint16_t* weight, const float* bias,
+                             int n, int k, int activation,
+                             void* y_video, void* y_text, s2_dtype y_dtype,
+                             s2_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SEEDVR2_HIP_H */

@@ -1,0 +1,231 @@
+"""ctypes wrapper of the CPU oracle (oracle.c) -- TEST INFRASTRUCTURE.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module, and only as the checker or the timed CPU baseline.  The product
+path (seedvr2_ncnn_amd) never imports it.
+
+The C code restates the reference CPU forward of AdaptiveWindowAttention
+(src/seedvr2/adaptive_window_attention.cpp:434-655, 764-978) and of
+SharedLinear (src/seedvr2/shared_linear.cpp:83-96); see oracle.h.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIBS: dict = {}
+
+
+class Slice(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "sample_index", "t0", "t1", "h0", "h1", "w0", "w1",
+        "partition_offset", "token_count")]
+
+
+class AwaParams(ctypes.Structure):
+    _fields_ = [
+        ("heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("target_windows", ctypes.c_int * 3),
+        ("shifted", ctypes.c_int),
+        ("epsilon", ctypes.c_float),
+        ("rope_pairs_per_axis", ctypes.c_int),
+        ("official_bf16_attention", ctypes.c_int),
+    ]
+
+
+def build() -> None:
+    """Compile liboracle.so / liboracle_fast.so with the committed Makefile."""
+    import subprocess
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib(fast: bool = False) -> ctypes.CDLL:
+    name = "liboracle_fast.so" if fast else "liboracle.so"
+    if name not in _LIBS:
+        path = os.path.join(_HERE, name)
+        if not os.path.exists(path):
+            build()
+        L = ctypes.CDLL(path)
+        P = ctypes.POINTER
+        ci, cf = ctypes.c_int, ctypes.c_float
+        L.orc_plan_count.argtypes = [P(ci), ci, P(ci), ci, P(ci), P(ci)]
+        L.orc_plan_build.argtypes = [P(ci), ci, P(ci), ci, P(Slice), ci, P(ci), P(ci),
+                                     P(ci), P(ci)]
+        L.orc_round_bf16.argtypes = [cf]
+        L.orc_round_bf16.restype = cf
+        L.orc_round_bf16_array.argtypes = [P(cf), P(cf), ctypes.c_long]
+        L.orc_rms_norm.argtypes = [P(cf), P(cf), ci, cf, P(cf)]
+        L.orc_apply_mm_rope.argtypes = [P(cf), ci, P(cf), ci, P(ci)]
+        L.orc_sdpa.argtypes = [P(cf), P(cf), P(cf), ci, ci, ci, P(cf), ci]
+        L.orc_awa_forward.argtypes = [P(AwaParams), P(cf), P(cf), P(cf), P(cf), P(cf),
+                                      P(ci), P(ci), ci,
+                                      P(cf), P(cf), P(cf), ctypes.c_long,
+                                      P(cf), P(cf), P(cf), ctypes.c_long,
+                                      P(cf), P(cf), P(ci), ci, ci]
+        L.orc_linear.argtypes = [P(cf), ci, ci, P(cf), P(cf), ci, ci, P(cf), P(ci), ci, ci]
+        _LIBS[name] = L
+    return _LIBS[name]
+
+
+def _i32(a):
+    a = np.ascontiguousarray(a, dtype=np.int32)
+    return a, a.ctypes.data_as(ctypes.POINTER(ctypes.c_int))
+
+
+def _f32(a):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a, a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+@dataclass
+class Plan:
+    """Mirror of the reference AdaptiveWindowPlan (adaptive_window_attention.h:29-36)."""
+    windows: np.ndarray                # [nwin, 9] int32, WindowSlice fields in order
+    sample_window_count: np.ndarray    # [batch]
+    video_indices: np.ndarray          # [L]
+    inverse_video_indices: np.ndarray  # [L]
+    local_positions: np.ndarray        # [L, 3]
+
+
+def plan(video_shapes, target_windows, shifted) -> Plan:
+    L = lib()
+    shapes, ps = _i32(np.asarray(video_shapes).reshape(-1, 3))
+    tgt, pt = _i32(target_windows)
+    batch = shapes.shape[0]
+    nwin, ntok = ctypes.c_int(), ctypes.c_int()
+    ret = L.orc_plan_count(ps, batch, pt, int(bool(shifted)), ctypes.byref(nwin), ctypes.byref(ntok))
+    if ret != 0:
+        raise ValueError(f"orc_plan_count returned {ret}")
+    slices = (Slice * max(nwin.value, 1))()
+    counts, pc = _i32(np.zeros(batch))
+    idx, pi = _i32(np.zeros(ntok.value))
+    inv, pv = _i32(np.zeros(ntok.value))
+    pos, pp = _i32(np.zeros((ntok.value, 3)))
+    ret = L.orc_plan_build(ps, batch, pt, int(bool(shifted)), slices, nwin.value, pc, pi, pv, pp)
+    if ret != 0:
+        raise ValueError(f"orc_plan_build returned {ret}")
+    win = np.array([[getattr(slices[i], f) for f, _ in Slice._fields_]
+                    for i in range(nwin.value)], dtype=np.int32).reshape(-1, 9)
+    return Plan(win, counts, idx, inv, pos)
+
+
+def round_bf16(x) -> np.ndarray:
+    L = lib()
+    x, px = _f32(x)
+    out = np.empty_like(x)
+    L.orc_round_bf16_array(px, out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), x.size)
+    return out
+
+
+def rms_norm(x, w, eps) -> np.ndarray:
+    L = lib()
+    x, px = _f32(x)
+    w, pw = _f32(w)
+    out = np.zeros_like(x)
+    _, po = _f32(out)
+    po = out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    L.orc_rms_norm(px, pw, x.size, eps, po)
+    return out
+
+
+def apply_mm_rope(x, freqs, pairs, position) -> np.ndarray:
+    L = lib()
+    out = np.array(x, dtype=np.float32, copy=True)
+    po = out.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    f, pf = _f32(freqs)
+    pos, pp = _i32(position)
+    L.orc_apply_mm_rope(po, out.size, pf, pairs, pp)
+    return out
+
+
+def sdpa(q, k, v, threads=1) -> np.ndarray:
+    """q,k,v: [heads, seq, d] float32."""
+    L = lib()
+    q, pq = _f32(q)
+    k, pk = _f32(k)
+    v, pv = _f32(v)
+    out = np.zeros_like(q)
+    L.orc_sdpa(pq, pk, pv, q.shape[0], q.shape[1], q.shape[2],
+               out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), threads)
+    return out
+
+
+def awa_params(heads, head_dim, target_windows, shifted, epsilon, rope_pairs, official_bf16):
+    p = AwaParams()
+    p.heads, p.head_dim = heads, head_dim
+    for i in range(3):
+        p.target_windows[i] = int(target_windows[i])
+    p.shifted = int(bool(shifted))
+    p.epsilon = float(epsilon)
+    p.rope_pairs_per_axis = rope_pairs
+    p.official_bf16_attention = int(bool(official_bf16))
+    return p
+
+
+def awa_forward(params: AwaParams, norm_vq, norm_vk, norm_tq, norm_tk, freqs,
+                video_shapes, text_lengths, video_q, video_k, video_v, text_q, text_k, text_v,
+                window_subset=None, threads=1, fast=False):
+    """Reference-equivalent CPU forward.  video_q/k/v: [Lv, inner] float32 arrays
+    (views into a fused [Lv, 3*inner] array are fine: the row stride is taken
+    from the array).  Returns (out_video [Lv, inner], out_text [Lt, inner]) or
+    raises ValueError with the reference return code."""
+    L = lib(fast)
+    inner = params.heads * params.head_dim
+    shapes, ps = _i32(np.asarray(video_shapes).reshape(-1, 3))
+    tl, ptl = _i32(text_lengths)
+
+    def rows(a):
+        a = np.asarray(a)
+        assert a.dtype == np.float32 and a.ndim == 2 and a.strides[1] == 4
+        return a, a.strides[0] // 4
+
+    vq, vs = rows(video_q)
+    vk, vs2 = rows(video_k)
+    vv, vs3 = rows(video_v)
+    tq, ts = rows(text_q)
+    tk, ts2 = rows(text_k)
+    tv, ts3 = rows(text_v)
+    assert vs == vs2 == vs3 and ts == ts2 == ts3
+    fp = lambda a: ctypes.cast(a.ctypes.data, ctypes.POINTER(ctypes.c_float))
+    lv = int(np.prod(shapes, axis=1).sum())
+    lt = int(tl.sum())
+    out_v = np.zeros((lv, inner), np.float32)
+    out_t = np.zeros((lt, inner), np.float32)
+    ws = None
+    if window_subset is not None:
+        ws, pws = _i32(window_subset)
+    norms = [_f32(a) for a in (norm_vq, norm_vk, norm_tq, norm_tk, freqs)]
+    ret = L.orc_awa_forward(ctypes.byref(params), *[n[1] for n in norms], ps, ptl, shapes.shape[0],
+                            fp(vq), fp(vk), fp(vv), vs, fp(tq), fp(tk), fp(tv), ts,
+                            fp(out_v), fp(out_t),
+                            pws if ws is not None else None, 0 if ws is None else len(ws),
+                            threads)
+    if ret != 0:
+        raise ValueError(ret)
+    return out_v, out_t
+
+
+def linear(x, w, bias=None, activation=0, rows=None, threads=1, fast=False) -> np.ndarray:
+    """Y = X W^T + b (erf-GELU when activation == 1); rows selects rows of X."""
+    L = lib(fast)
+    x, px = _f32(x)
+    w, pw = _f32(w)
+    m, k = x.shape
+    n = w.shape[0]
+    pb = None
+    if bias is not None:
+        bias, pb = _f32(bias)
+    pr, nr = None, m
+    if rows is not None:
+        rr, pr = _i32(rows)
+        nr = len(rr)
+    y = np.zeros((nr, n), np.float32)
+    L.orc_linear(px, m, k, pw, pb, n, activation,
+                 y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), pr, nr if rows is not None else 0,
+                 threads)
+    return y

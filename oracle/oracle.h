@@ -1,0 +1,120 @@
+/*
+ * CPU oracle for the SeedVR2 window-attention hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
+ * layers' CPU forward (Chisato623/seedvr2_ncnn), used as the checker by the
+ * test suite, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg.
+ * Nothing in the product path (seedvr2_ncnn_amd/) may link, load or call it.
+ *
+ * Every function names the reference file:line it restates.  Floating-point
+ * work is fp32 with the reference's operation order where the reference
+ * states one; SDPA and Gemm live in the (absent) ncnn library and are
+ * restated as textbook fp32 kernels.
+ *
+ * Pinning (how each function is checked independently of this file):
+ *   orc_plan_*        closed-form window counts/extents at the benchmark shapes,
+ *                     permutation invariants, brute force against an exact
+ *                     rational-arithmetic plan written in the tests.
+ *   orc_round_bf16    torch bfloat16 RNE conversion; tie, Inf and NaN cases.
+ *   orc_rms_norm      unit-RMS rows at weight 1; float64 numpy closed form.
+ *   orc_apply_mm_rope identity at freq 0 / position 0; complex rotation.
+ *   orc_sdpa          torch scaled_dot_product_attention in float64;
+ *                     constant-K -> mean(V); one-hot logits.
+ *   orc_linear        torch matmul in float64; GELU vs torch erf-GELU.
+ *   orc_awa_forward   an independent torch float64 implementation of the
+ *                     layer semantics; single-window pooling identity.
+ */
+#ifndef SEEDVR2_ORACLE_H
+#define SEEDVR2_ORACLE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same fields as the reference WindowSlice (adaptive_window_attention.h:16-27). */
+typedef struct orc_slice {
+    int sample_index;
+    int t0, t1, h0, h1, w0, w1;
+    int partition_offset;
+    int token_count;
+} orc_slice;
+
+/* Layer configuration: the reference ParamDict ids 0..10
+ * (adaptive_window_attention.cpp:700-714). */
+typedef struct orc_awa_params {
+    int heads;                    /* id 0 */
+    int head_dim;                 /* id 1 */
+    int target_windows[3];        /* ids 2,3,4 */
+    int shifted;                  /* id 5 */
+    float epsilon;                /* id 6 */
+    int rope_pairs_per_axis;      /* id 7 */
+    int official_bf16_attention;  /* id 10 */
+} orc_awa_params;
+
+/* Number of windows and video tokens a plan will hold (walks the same loops
+ * as orc_plan_build without storing anything).  Returns 0 or -1. */
+int orc_plan_count(const int* video_shapes, int batch, const int target_windows[3],
+                   int shifted, int* num_windows, int* total_tokens);
+
+/* build_adaptive_window_plan (adaptive_window_attention.cpp:565-655).
+ * video_shapes: [batch][3] (t,h,w).  Output arrays are sized by orc_plan_count:
+ * windows[num_windows], sample_window_count[batch], video_indices[L],
+ * inverse_video_indices[L], local_positions[L][3].  Any output may be NULL.
+ * Returns 0, -1 (bad shape) or -2 (not a permutation). */
+int orc_plan_build(const int* video_shapes, int batch, const int target_windows[3],
+                   int shifted, orc_slice* windows, int max_windows,
+                   int* sample_window_count, int* video_indices,
+                   int* inverse_video_indices, int* local_positions);
+
+/* round_bf16 (adaptive_window_attention.cpp:499-508). */
+float orc_round_bf16(float value);
+/* Elementwise round_bf16 over an array (bit patterns pass through untouched). */
+void orc_round_bf16_array(const float* in, float* out, long count);
+
+/* rms_norm (adaptive_window_attention.cpp:510-519). */
+void orc_rms_norm(const float* input, const float* weight, int size, float epsilon,
+                  float* output);
+
+/* apply_mm_rope (adaptive_window_attention.cpp:521-543). */
+void orc_apply_mm_rope(float* values, int head_dim, const float* freqs,
+                       int pairs_per_axis, const int position[3]);
+
+/* Textbook SDPA standing in for ncnn SDPA with params {5:0, 6:0.f, 7:0}
+ * (adaptive_window_attention.cpp:847-861, 943): per head,
+ * softmax(Q K^T / sqrt(d)) V, unmasked.  q,k,v,out: [heads][seq][d] fp32. */
+void orc_sdpa(const float* q, const float* k, const float* v, int heads, int seq,
+              int head_dim, float* out, int num_threads);
+
+/* AdaptiveWindowAttention::forward (adaptive_window_attention.cpp:764-978).
+ * Video rows have stride video_stride floats and hold q at +0, k at +inner
+ * (fused form) or come from separate pointers (split form): the caller passes
+ * the three base pointers either way.  Outputs are fp32 [Lv][inner] and
+ * [Lt][inner], zero-filled here.  window_subset (optional) restricts the
+ * computation to those plan windows; text output is then partial.
+ * Returns the reference's codes (0, -1, -2, -100). */
+int orc_awa_forward(const orc_awa_params* params,
+                    const float* video_norm_q, const float* video_norm_k,
+                    const float* text_norm_q, const float* text_norm_k,
+                    const float* rope_freqs,
+                    const int* video_shapes, const int* text_lengths, int batch,
+                    const float* video_q, const float* video_k, const float* video_v,
+                    long video_stride,
+                    const float* text_q, const float* text_k, const float* text_v,
+                    long text_stride,
+                    float* out_video, float* out_text,
+                    const int* window_subset, int num_subset, int num_threads);
+
+/* SharedLinear / ncnn Gemm restated (shared_linear.cpp:27-96):
+ * Y[m][n] = sum_k X[m][k] * W[n][k] + b[n], fp32; activation 1 applies
+ * erf-GELU after the bias.  rows: optional list of rows of X to compute
+ * (num_rows of them, Y then holds num_rows rows in that order). */
+void orc_linear(const float* x, int m, int k, const float* w, const float* bias, int n,
+                int activation, float* y, const int* rows, int num_rows, int num_threads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

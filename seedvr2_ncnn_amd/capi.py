@@ -1,0 +1,294 @@
+"""ctypes binding of the C-ABI in include/seedvr2_hip.h (libseedvr2_hip.so).
+
+torch supplies device memory and the current HIP stream; every computation
+happens in the gfx950 kernels behind the C-ABI.  There is no fallback: if the
+library is missing, or no gfx950 device is visible, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG, "lib", "libseedvr2_hip.so")
+LAYERS_PATH = os.path.join(_PKG, "lib", "libseedvr2_layers.so")
+
+S2_OK = 0
+S2_ERR_INVALID = -1
+S2_ERR_PLAN = -2
+S2_ERR_ALLOC = -100
+S2_ERR_DEVICE = -200
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+ACT_NONE = 0
+ACT_GELU = 1
+
+# Every symbol include/seedvr2_hip.h declares.
+EXPORTS = (
+    "s2_device_count", "s2_malloc", "s2_free", "s2_memcpy_h2d", "s2_memcpy_d2h",
+    "s2_memcpy_d2d", "s2_stream_synchronize", "s2_last_error", "s2_awa_plan_windows",
+    "s2_awa_plan_create", "s2_awa_plan_get_info", "s2_awa_plan_get_windows",
+    "s2_awa_plan_destroy", "s2_awa_plan_tables", "s2_awa_forward", "s2_cast_f32_to_bf16",
+    "s2_cast_bf16_to_f32", "s2_shared_linear_forward",
+)
+
+
+class S2Error(RuntimeError):
+    def __init__(self, code, what=""):
+        super().__init__(f"{what} returned {code}: {last_error()}")
+        self.code = code
+
+
+class WindowSlice(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "sample_index", "t0", "t1", "h0", "h1", "w0", "w1", "partition_offset", "token_count")]
+
+
+class AwaConfig(ctypes.Structure):
+    _fields_ = [
+        ("heads", ctypes.c_int),
+        ("head_dim", ctypes.c_int),
+        ("target_windows", ctypes.c_int * 3),
+        ("shifted", ctypes.c_int),
+        ("epsilon", ctypes.c_float),
+        ("rope_pairs_per_axis", ctypes.c_int),
+        ("shared_norm", ctypes.c_int),
+        ("official_bf16_attention", ctypes.c_int),
+    ]
+
+
+class PlanInfo(ctypes.Structure):
+    _fields_ = [
+        ("batch", ctypes.c_int),
+        ("num_windows", ctypes.c_int),
+        ("video_tokens", ctypes.c_int),
+        ("text_tokens", ctypes.c_int),
+        ("workspace_bytes", ctypes.c_size_t),
+    ]
+
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """Loads libseedvr2_hip.so (built by seedvr2_ncnn_amd.build); raises if absent."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run python -m seedvr2_ncnn_amd.build")
+        L = ctypes.CDLL(LIB_PATH)
+        P, vp, ci, cf = ctypes.POINTER, ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        sz, cl = ctypes.c_size_t, ctypes.c_long
+        L.s2_last_error.restype = ctypes.c_char_p
+        L.s2_device_count.argtypes = [P(ci)]
+        L.s2_malloc.argtypes = [P(vp), sz]
+        L.s2_free.argtypes = [vp]
+        for f in ("s2_memcpy_h2d", "s2_memcpy_d2h", "s2_memcpy_d2d"):
+            getattr(L, f).argtypes = [vp, vp, sz, vp]
+        L.s2_stream_synchronize.argtypes = [vp]
+        L.s2_awa_plan_windows.argtypes = [P(ci), ci, P(ci), ci, P(WindowSlice), ci, P(ci), P(ci), P(ci)]
+        L.s2_awa_plan_create.argtypes = [P(AwaConfig), P(ci), P(ci), ci, P(vp)]
+        L.s2_awa_plan_get_info.argtypes = [vp, P(PlanInfo)]
+        L.s2_awa_plan_get_windows.argtypes = [vp, P(WindowSlice), ci, P(ci)]
+        L.s2_awa_plan_destroy.argtypes = [vp]
+        L.s2_awa_plan_tables.argtypes = [vp, vp, vp, vp, vp]
+        L.s2_awa_forward.argtypes = [vp, vp, vp, vp, vp, vp, cl, vp, vp, vp, cl, ci, vp, vp, ci,
+                                     vp, sz, vp]
+        L.s2_cast_f32_to_bf16.argtypes = [vp, vp, sz, vp]
+        L.s2_cast_bf16_to_f32.argtypes = [vp, vp, sz, vp]
+        L.s2_shared_linear_forward.argtypes = [vp, ci, vp, ci, ci, vp, vp, ci, ci, ci, vp, vp, ci, vp]
+        _LIB = L
+    return _LIB
+
+
+def last_error() -> str:
+    if _LIB is None:
+        return ""
+    return (_LIB.s2_last_error() or b"").decode()
+
+
+def check(code, what=""):
+    if code != S2_OK:
+        raise S2Error(code, what)
+
+
+def device_count() -> int:
+    n = ctypes.c_int()
+    check(lib().s2_device_count(ctypes.byref(n)), "s2_device_count")
+    return n.value
+
+
+def _stream(stream=None):
+    import torch
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _ints(values):
+    values = [int(v) for v in values]
+    return (ctypes.c_int * max(1, len(values)))(*values)
+
+
+def plan_windows(video_shapes, target_windows, shifted):
+    """Window list of the host plan: (list of 9-int tuples, sample_window_count, video_tokens)."""
+    L = lib()
+    shapes = [int(x) for s in video_shapes for x in s]
+    batch = len(shapes) // 3
+    n, tokens = ctypes.c_int(), ctypes.c_int()
+    counts = (ctypes.c_int * max(1, batch))()
+    check(L.s2_awa_plan_windows(_ints(shapes), batch, _ints(target_windows), int(bool(shifted)),
+                                None, 0, ctypes.byref(n), counts, ctypes.byref(tokens)),
+          "s2_awa_plan_windows")
+    buf = (WindowSlice * max(1, n.value))()
+    check(L.s2_awa_plan_windows(_ints(shapes), batch, _ints(target_windows), int(bool(shifted)),
+                                buf, n.value, ctypes.byref(n), None, None), "s2_awa_plan_windows")
+    wins = [tuple(getattr(buf[i], f) for f, _ in WindowSlice._fields_) for i in range(n.value)]
+    return wins, [counts[i] for i in range(batch)], tokens.value
+
+
+def awa_config(heads=20, head_dim=128, target_windows=(4, 3, 3), shifted=False, epsilon=1e-5,
+               rope_pairs=21, shared_norm=False, official_bf16=False) -> AwaConfig:
+    c = AwaConfig()
+    c.heads, c.head_dim = heads, head_dim
+    for i in range(3):
+        c.target_windows[i] = int(target_windows[i])
+    c.shifted = int(bool(shifted))
+    c.epsilon = float(epsilon)
+    c.rope_pairs_per_axis = rope_pairs
+    c.shared_norm = int(bool(shared_norm))
+    c.official_bf16_attention = int(bool(official_bf16))
+    return c
+
+
+class AwaPlan:
+    """Device-resident window plan (s2_awa_plan_create / _destroy)."""
+
+    def __init__(self, config: AwaConfig, video_shapes, text_lengths):
+        self.config = config
+        self._h = ctypes.c_void_p()
+        shapes = [int(x) for s in video_shapes for x in s]
+        batch = len(text_lengths)
+        check(lib().s2_awa_plan_create(ctypes.byref(config), _ints(shapes), _ints(text_lengths),
+                                       batch, ctypes.byref(self._h)), "s2_awa_plan_create")
+        self.info = PlanInfo()
+        check(lib().s2_awa_plan_get_info(self._h, ctypes.byref(self.info)), "s2_awa_plan_get_info")
+
+    @property
+    def handle(self):
+        return self._h
+
+    def windows(self):
+        n = self.info.num_windows
+        buf = (WindowSlice * max(1, n))()
+        counts = (ctypes.c_int * max(1, self.info.batch))()
+        check(lib().s2_awa_plan_get_windows(self._h, buf, n, counts), "s2_awa_plan_get_windows")
+        wins = [tuple(getattr(buf[i], f) for f, _ in WindowSlice._fields_) for i in range(n)]
+        return wins, [counts[i] for i in range(self.info.batch)]
+
+    def tables(self, device="cuda"):
+        """(video_indices, inverse_video_indices, local_positions) computed on the device."""
+        import torch
+        L = self.info.video_tokens
+        idx = torch.full((L,), -7, dtype=torch.int32, device=device)
+        inv = torch.full((L,), -7, dtype=torch.int32, device=device)
+        pos = torch.full((L, 3), -7, dtype=torch.int32, device=device)
+        check(lib().s2_awa_plan_tables(self._h, _ptr(idx), _ptr(inv), _ptr(pos), _stream()),
+              "s2_awa_plan_tables")
+        return idx, inv, pos
+
+    def close(self):
+        if self._h:
+            lib().s2_awa_plan_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+def _dtype_code(t):
+    import torch
+    if t.dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def awa_forward(plan: AwaPlan, norm_weights, rope_freqs, video_q, video_k, video_v, text_q,
+                text_k, text_v, out_dtype=None, workspace=None, out_video=None, out_text=None,
+                stream=None):
+    """Runs s2_awa_forward on torch device tensors.  video_* / text_* are 2-D
+    row views (unit column stride, shared row stride: views into one fused
+    [L, 3*inner] tensor are fine).  Returns (out_video, out_text)."""
+    import torch
+    inner = plan.config.heads * plan.config.head_dim
+    ins = (video_q, video_k, video_v, text_q, text_k, text_v)
+    for t in ins:
+        assert t.is_cuda and t.dim() == 2 and t.stride(1) == 1 and t.shape[1] == inner
+    dt = _dtype_code(video_q)
+    assert all(_dtype_code(t) == dt for t in ins)
+    vs, ts = video_q.stride(0), text_q.stride(0)
+    assert video_k.stride(0) == vs and video_v.stride(0) == vs
+    assert text_k.stride(0) == ts and text_v.stride(0) == ts
+    odt = out_dtype or video_q.dtype
+    dev = video_q.device
+    if out_video is None:
+        out_video = torch.empty((plan.info.video_tokens, inner), dtype=odt, device=dev)
+    if out_text is None:
+        out_text = torch.empty((plan.info.text_tokens, inner), dtype=odt, device=dev)
+    if workspace is None:
+        workspace = torch.empty(plan.info.workspace_bytes, dtype=torch.uint8, device=dev)
+    check(lib().s2_awa_forward(plan.handle, _ptr(norm_weights), _ptr(rope_freqs),
+                               _ptr(video_q), _ptr(video_k), _ptr(video_v), vs,
+                               _ptr(text_q), _ptr(text_k), _ptr(text_v), ts, dt,
+                               _ptr(out_video), _ptr(out_text), _dtype_code(out_video),
+                               _ptr(workspace), workspace.numel(), _stream(stream)),
+          "s2_awa_forward")
+    return out_video, out_text
+
+
+def cast_f32_to_bf16(src, dst=None, stream=None):
+    import torch
+    if dst is None:
+        dst = torch.empty(src.shape, dtype=torch.bfloat16, device=src.device)
+    check(lib().s2_cast_f32_to_bf16(_ptr(src), _ptr(dst), src.numel(), _stream(stream)),
+          "s2_cast_f32_to_bf16")
+    return dst
+
+
+def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, out_dtype=None,
+                  y_video=None, y_text=None, stream=None):
+    """s2_shared_linear_forward: y = act(x W^T + b) for both streams."""
+    import torch
+    n, k = weight_bf16.shape
+    assert weight_bf16.dtype == torch.bfloat16 and weight_bf16.is_contiguous()
+    xd = _dtype_code(x_video)
+    assert x_text is None or _dtype_code(x_text) == xd
+    odt = out_dtype or x_video.dtype
+    m0 = x_video.shape[0]
+    m1 = 0 if x_text is None else x_text.shape[0]
+    dev = x_video.device
+    if y_video is None:
+        y_video = torch.empty((m0, n), dtype=odt, device=dev)
+    if y_text is None and m1:
+        y_text = torch.empty((m1, n), dtype=odt, device=dev)
+    check(lib().s2_shared_linear_forward(_ptr(x_video), m0, _ptr(x_text) if m1 else None, m1, xd,
+                                         _ptr(weight_bf16), _ptr(bias), n, k, activation,
+                                         _ptr(y_video), _ptr(y_text) if m1 else None,
+                                         _dtype_code(y_video), _stream(stream)),
+          "s2_shared_linear_forward")
+    return y_video, y_text

@@ -1,0 +1,551 @@
+// gfx950 kernels of the AdaptiveWindowAttention forward.
+//
+//   rope_table     cos/sin of pos*freq for every position the plan can hold
+//   awa_prologue   per (window, 64-row chunk, head): gather the window's video
+//                  rows by plan index math and the sample's text rows, RMSNorm
+//                  q and k, 3-axis RoPE, round to bf16, write window-ordered
+//                  Q and K rows and V transposed (keys contiguous per channel)
+//   awa_attention  per (window, 128-query tile, head): softmax(q k^T/sqrt d) v
+//                  over the window's video+text keys on bf16 MFMA 32x32x16
+//                  with an online softmax; video rows are scattered straight
+//                  to source order, text rows go to per-window partials
+//   awa_text_pool  deterministic mean of the text partials over the sample's
+//                  windows, in window order
+//   awa_plan_tables  video_indices / inverse / local_positions on the device
+//
+// Reference: src/seedvr2/adaptive_window_attention.cpp:764-978 (CPU forward)
+// and the Vulkan path :1059-1270 with its shaders :21-409.
+#include <math.h>
+
+#include "awa_kernels.h"
+#include "s2_device.h"
+
+namespace s2 {
+
+// ---------------------------------------------------------------------------
+// Index math shared by the kernels (append_slice order, :462-471).
+struct TokenCoord {
+    int lt, lh, lw;
+    long src;
+};
+
+__device__ __forceinline__ TokenCoord window_token(const WinMeta& w, int r) {
+    TokenCoord c;
+    const int plane = w.eh * w.ew;
+    c.lt = r / plane;
+    const int rem = r - c.lt * plane;
+    c.lh = rem / w.ew;
+    c.lw = rem - c.lh * w.ew;
+    c.src = (long)w.tok_off +
+            ((long)(w.t0 + c.lt) * w.grid_h + (w.h0 + c.lh)) * w.grid_w + (w.w0 + c.lw);
+    return c;
+}
+
+// ---------------------------------------------------------------------------
+// cos/sin table: table[pos * pairs + p] = (cos(pos*f[p]), sin(pos*f[p])), the
+// angle formed in fp32 as apply_mm_rope does (:534-536).
+__global__ void rope_table_kernel(const float* __restrict__ freqs, int pairs, int positions,
+                                  float2* __restrict__ table) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= pairs * positions) return;
+    const int pos = i / pairs;
+    const int p = i - pos * pairs;
+    const float angle = (float)pos * freqs[p];
+    table[i] = make_float2(cosf(angle), sinf(angle));
+}
+
+// ---------------------------------------------------------------------------
+// Prologue.  256 threads; each row of D channels is handled by D/8 threads
+// holding 8 consecutive channels (RoPE pairs never straddle threads).
+template <int D, typename TIn>
+__global__ __launch_bounds__(256) void awa_prologue_kernel(
+    const WinMeta* __restrict__ wins, const ChunkRef* __restrict__ chunks,
+    const TIn* __restrict__ vq, const TIn* __restrict__ vk, const TIn* __restrict__ vv,
+    long vstride, const TIn* __restrict__ tq, const TIn* __restrict__ tk,
+    const TIn* __restrict__ tv, long tstride, const float* __restrict__ norm,
+    const float2* __restrict__ rope, int pairs, float eps, int official_bf16,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_out, uint16_t* __restrict__ vt_out,
+    long seg_total) {
+#pragma clang fp contract(off)
+    constexpr int TPR = D / 8;         // threads per row
+    constexpr int RPP = 256 / TPR;     // rows per pass
+    constexpr int CHUNK = kSegAlign;   // rows per workgroup
+    constexpr int VTP = CHUNK + 8;     // padded LDS pitch of the V^T tile
+    __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VTP];
+
+    const ChunkRef ch = chunks[blockIdx.x];
+    const WinMeta w = wins[ch.window];
+    const int head = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int d0 = (tid % TPR) * 8;
+    const int rot_width = pairs * 6;
+    const long head_rows = (long)head * seg_total + w.seg_off;
+
+#pragma unroll 1
+    for (int pass = 0; pass < CHUNK / RPP; ++pass) {
+        const int rl = pass * RPP + tid / TPR;   // row within the chunk
+        const int r = ch.row0 + rl;                 // row within the window sequence
+        uint16_t qb[8], kb[8], vb[8];
+        if (r < w.seq) {
+            const TIn *sq, *sk, *sv;
+            const float *wq, *wk;
+            int pos[3];
+            if (r < w.n_video) {
+                const TokenCoord c = window_token(w, r);
+                sq = vq + c.src * vstride;
+                sk = vk + c.src * vstride;
+                sv = vv + c.src * vstride;
+                wq = norm;
+                wk = norm + D;
+                // window-local position, temporal axis offset by the text length (:901-902)
+                pos[0] = c.lt + w.text_len;
+                pos[1] = c.lh;
+                pos[2] = c.lw;
+            } else {
+                const int tt = r - w.n_video;
+                const long src = (long)w.text_off + tt;
+                sq = tq + src * tstride;
+                sk = tk + src * tstride;
+                sv = tv + src * tstride;
+                wq = norm + 2 * D;
+                wk = norm + 3 * D;
+                pos[0] = pos[1] = pos[2] = tt;     // text position (i,i,i) (:915)
+            }
+            const int col = head * D + d0;
+            float q[8], k[8], v[8];
+            load8(sq + col, q);
+            load8(sk + col, k);
+            load8(sv + col, v);
+            float sq2 = 0.f, sk2 = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                sq2 += q[i] * q[i];
+                sk2 += k[i] * k[i];
+            }
+#pragma unroll
+            for (int off = 1; off < TPR; off <<= 1) {
+                sq2 += __shfl_xor(sq2, off);
+                sk2 += __shfl_xor(sk2, off);
+            }
+            // rms_norm (:510-519): x * (1 / sqrt(sum/size + eps)) * w
+            const float inv_q = 1.f / sqrtf(sq2 / (float)D + eps);
+            const float inv_k = 1.f / sqrtf(sk2 / (float)D + eps);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                q[i] = q[i] * inv_q * wq[d0 + i];
+                k[i] = k[i] * inv_k * wk[d0 + i];
+            }
+            // apply_mm_rope (:521-543): pair (2p, 2p+1) of axis a rotated by pos[a]*f[p]
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+                const int d = d0 + 2 * pp;
+                if (d < rot_width) {
+                    const int axis = d / (2 * pairs);
+                    const int pair = (d - axis * 2 * pairs) >> 1;
+                    const float2 cs = rope[pos[axis] * pairs + pair];
+                    const float q0 = q[2 * pp], q1 = q[2 * pp + 1];
+                    const float k0 = k[2 * pp], k1 = k[2 * pp + 1];
+                    q[2 * pp] = q0 * cs.x - q1 * cs.y;
+                    q[2 * pp + 1] = q0 * cs.y + q1 * cs.x;
+                    k[2 * pp] = k0 * cs.x - k1 * cs.y;
+                    k[2 * pp + 1] = k0 * cs.y + k1 * cs.x;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                if (official_bf16) {
+                    qb[i] = round_bf16_ref_bits(q[i]);
+                    kb[i] = round_bf16_ref_bits(k[i]);
+                    vb[i] = round_bf16_ref_bits(v[i]);
+                } else {
+                    qb[i] = f32_to_bf16(q[i]);
+                    kb[i] = f32_to_bf16(k[i]);
+                    vb[i] = f32_to_bf16(v[i]);
+                }
+            }
+        } else {
+            // padding rows: zero keys are masked in attention, zero values keep
+            // p * v finite
+#pragma unroll
+            for (int i = 0; i < 8; ++i) qb[i] = kb[i] = vb[i] = 0;
+        }
+        const long orow = (head_rows + r) * D + d0;
+        *reinterpret_cast<uint4*>(q_out + orow) = pack8_bf16(qb);
+        *reinterpret_cast<uint4*>(k_out + orow) = pack8_bf16(kb);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vt_lds[(d0 + i) * VTP + rl] = vb[i];
+    }
+    __syncthreads();
+    // V^T rows: channel-major, the chunk's 64 keys contiguous (128 bytes).
+    for (int idx = tid; idx < D * (CHUNK / 8); idx += 256) {
+        const int d = idx / (CHUNK / 8);
+        const int c8 = idx - d * (CHUNK / 8);
+        const uint4 val = *reinterpret_cast<const uint4*>(&vt_lds[d * VTP + c8 * 8]);
+        *reinterpret_cast<uint4*>(vt_out + ((long)head * D + d) * seg_total + w.seg_off + ch.row0 +
+                                  c8 * 8) = val;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Flash window attention.
+//
+// Four waves; wave j owns query rows q_row0 + 32j .. +31.  Each key tile of
+// 64 keys is staged in LDS (K rows and V^T rows, double buffered).  The
+// score tile is computed transposed, S^T = K Q^T, so that each lane owns one
+// query column; the probabilities then feed O^T += V^T P^T directly from the
+// accumulator registers.  For that the A-operand row R of the S^T MFMA loads
+// key pi(R) = R with bits 2 and 3 swapped: accumulator register i = 8s+j of
+// lane group g then holds key 16s + 8g + j, which is exactly the B-operand
+// slot 8g+j of the 16-key PV step s.
+template <int D>
+__global__ __launch_bounds__(256, 2) void awa_attention_kernel(
+    const WinMeta* __restrict__ wins, const AttnItem* __restrict__ items, int slots_per_xcd,
+    const uint16_t* __restrict__ q_in, const uint16_t* __restrict__ k_in,
+    const uint16_t* __restrict__ vt_in, long seg_total, float scale_log2, int official_bf16,
+    void* __restrict__ out_video, int out_bf16, int inner, float* __restrict__ text_partial) {
+    constexpr int KT = 64;            // keys per tile
+    constexpr int KP = D + 8;         // K tile LDS pitch (elements)
+    constexpr int VP = KT + 8;        // V^T tile LDS pitch
+    constexpr int NKK = D / 16;       // MFMA k-steps over the head dim
+    constexpr int NDT = D / 32;       // 32-channel output tiles
+    constexpr int K_CHUNKS = KT * D / 8 / 256;   // 16-byte loads per thread
+    constexpr int V_CHUNKS = D * KT / 8 / 256;
+    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][KT * KP];
+    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * VP];
+
+    const int bid = blockIdx.x;
+    const AttnItem it = items[(bid % kNumXcd) * slots_per_xcd + bid / kNumXcd];
+    if (it.window < 0) return;
+    const WinMeta w = wins[it.window];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const long head_rows = (long)it.head * seg_total + w.seg_off;
+    const uint16_t* kbase = k_in + head_rows * D;
+    const uint16_t* vbase = vt_in + (long)it.head * D * seg_total + w.seg_off;
+    const int nkt = (w.seq + KT - 1) / KT;
+
+    // Q fragment (B operand of S^T = K Q^T): query row l32 of this wave,
+    // channels 16kk + 8g .. +7.
+    const int qrow = it.q_row0 + wave * 32 + l32;
+    bf16x8 qf[NKK];
+    {
+        const bool valid = qrow < w.seq;
+        const uint16_t* qp = q_in + (head_rows + qrow) * D + 8 * g;
+#pragma unroll
+        for (int kk = 0; kk < NKK; ++kk) {
+            uint4 raw = make_uint4(0, 0, 0, 0);
+            if (valid) raw = *reinterpret_cast<const uint4*>(qp + 16 * kk);
+            qf[kk] = as_bf16x8(raw);
+        }
+    }
+
+    uint4 kreg[K_CHUNKS], vreg[V_CHUNKS];
+    auto load_tile = [&](int kt) {
+        const int key0 = kt * KT;
+#pragma unroll
+        for (int c = 0; c < K_CHUNKS; ++c) {
+            const int idx = tid + 256 * c;
+            const int row = idx / (D / 8);
+            const int col = (idx % (D / 8)) * 8;
+            kreg[c] = *reinterpret_cast<const uint4*>(kbase + (long)(key0 + row) * D + col);
+        }
+#pragma unroll
+        for (int c = 0; c < V_CHUNKS; ++c) {
+            const int idx = tid + 256 * c;
+            const int d = idx / (KT / 8);
+            const int col = (idx % (KT / 8)) * 8;
+            vreg[c] = *reinterpret_cast<const uint4*>(vbase + (long)d * seg_total + key0 + col);
+        }
+    };
+    auto store_tile = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < K_CHUNKS; ++c) {
+            const int idx = tid + 256 * c;
+            const int row = idx / (D / 8);
+            const int col = (idx % (D / 8)) * 8;
+            *reinterpret_cast<uint4*>(&k_lds[buf][row * KP + col]) = kreg[c];
+        }
+#pragma unroll
+        for (int c = 0; c < V_CHUNKS; ++c) {
+            const int idx = tid + 256 * c;
+            const int d = idx / (KT / 8);
+            const int col = (idx % (KT / 8)) * 8;
+            *reinterpret_cast<uint4*>(&v_lds[buf][d * VP + col]) = vreg[c];
+        }
+    };
+
+    f32x16 o[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) o[dt][i] = 0.f;
+    float m_run = -INFINITY;   // running max (log2 domain), same in lanes l and l^32
+    float l_run = 0.f;         // this lane's share of the running sum
+
+    // row of the S^T accumulator -> key within a 32-key subtile
+    const int krow = (l32 & 0x13) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+#pragma unroll 1
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int buf = kt & 1;
+        if (kt + 1 < nkt) load_tile(kt + 1);
+
+        f32x16 s[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) s[st][i] = 0.f;
+            const uint16_t* kp = &k_lds[buf][(32 * st + krow) * KP + 8 * g];
+#pragma unroll
+            for (int kk = 0; kk < NKK; ++kk) {
+                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(kp + 16 * kk));
+                s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[st], 0, 0, 0);
+            }
+        }
+        // keys past the window's sequence (only in the last tile) are masked
+        const int key_base = kt * KT;
+        const bool tail = key_base + KT > w.seq;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                float x = s[st][i] * scale_log2;
+                if (tail) {
+                    // register i of lane group g holds key 16*(i/8) + 8g + (i%8)
+                    const int key = key_base + 32 * st + 16 * (i >> 3) + 8 * g + (i & 7);
+                    if (key >= w.seq) x = -INFINITY;
+                }
+                s[st][i] = x;
+                mx = fmaxf(mx, x);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run, mx);
+        const float alpha = exp2f(m_run - m_new);
+        m_run = m_new;
+        float psum = 0.f;
+        bf16x8 pb[4];
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+                uint16_t hb[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = exp2f(s[st][8 * half + j] - m_new);
+                    psum += p;
+                    hb[j] = f32_to_bf16(p);
+                }
+                pb[2 * st + half] = as_bf16x8(pack8_bf16(hb));
+            }
+        l_run = l_run * alpha + psum;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+            const uint16_t* vp = &v_lds[buf][(32 * dt + l32) * VP + 8 * g];
+#pragma unroll
+            for (int ps = 0; ps < 4; ++ps) {
+                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(vp + 16 * ps));
+                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ps], o[dt], 0, 0, 0);
+            }
+        }
+        if (kt + 1 < nkt) store_tile(buf ^ 1);
+        __syncthreads();
+    }
+
+    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float inv_l = 1.f / l_tot;
+    if (qrow >= w.seq) return;
+    // O^T register i of tile dt: channel 32dt + 8(i/4) + 4g + (i%4), query l32
+    if (qrow < w.n_video) {
+        const TokenCoord c = window_token(w, qrow);
+        const long obase = c.src * inner + (long)it.head * D;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const int ch = 32 * dt + 8 * a + 4 * g;
+                float vals[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float x = o[dt][4 * a + e] * inv_l;
+                    if (official_bf16) x = bf16_to_f32(round_bf16_ref_bits(x));
+                    vals[e] = x;
+                }
+                if (out_bf16) {
+                    uint2 pk;
+                    pk.x = (uint32_t)f32_to_bf16(vals[0]) | ((uint32_t)f32_to_bf16(vals[1]) << 16);
+                    pk.y = (uint32_t)f32_to_bf16(vals[2]) | ((uint32_t)f32_to_bf16(vals[3]) << 16);
+                    *reinterpret_cast<uint2*>((uint16_t*)out_video + obase + ch) = pk;
+                } else {
+                    *reinterpret_cast<float4*>((float*)out_video + obase + ch) =
+                        make_float4(vals[0], vals[1], vals[2], vals[3]);
+                }
+            }
+    } else {
+        const long obase = (long)(w.tpart_off + qrow - w.n_video) * inner + (long)it.head * D;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int a = 0; a < 4; ++a) {
+                const int ch = 32 * dt + 8 * a + 4 * g;
+                float vals[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float x = o[dt][4 * a + e] * inv_l;
+                    if (official_bf16) x = bf16_to_f32(round_bf16_ref_bits(x));
+                    vals[e] = x;
+                }
+                *reinterpret_cast<float4*>(text_partial + obase + ch) =
+                    make_float4(vals[0], vals[1], vals[2], vals[3]);
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Text mean-pool (:963-974): out = sum over the sample's windows, in plan
+// order, of partial * (1/num_windows), accumulated in fp32 from zero.
+__global__ void awa_text_pool_kernel(const SampleMeta* __restrict__ samples,
+                                     const int* __restrict__ text_sample,
+                                     const WinMeta* __restrict__ wins,
+                                     const float* __restrict__ partial, int text_tokens,
+                                     int inner, void* __restrict__ out, int out_bf16) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;   // float4 index
+    const int q4 = inner / 4;
+    if (i >= (long)text_tokens * q4) return;
+    const int row = (int)(i / q4);
+    const int c = (int)(i - (long)row * q4) * 4;
+    const SampleMeta sm = samples[text_sample[row]];
+    const int tt = row - sm.text_off;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < sm.num_windows; ++k) {
+        const int tp = wins[sm.first_window + k].tpart_off;
+        const float4 x = *reinterpret_cast<const float4*>(partial + (long)(tp + tt) * inner + c);
+        acc.x += x.x * sm.pool_scale;
+        acc.y += x.y * sm.pool_scale;
+        acc.z += x.z * sm.pool_scale;
+        acc.w += x.w * sm.pool_scale;
+    }
+    if (out_bf16) {
+        uint2 pk;
+        pk.x = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
+        pk.y = (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16);
+        *reinterpret_cast<uint2*>((uint16_t*)out + (long)row * inner + c) = pk;
+    } else {
+        *reinterpret_cast<float4*>((float*)out + (long)row * inner + c) = acc;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Plan tables (AdaptiveWindowPlan's per-token arrays) from the same index math.
+__global__ void awa_plan_tables_kernel(const WinMeta* __restrict__ wins, int* __restrict__ indices,
+                                       int* __restrict__ inverse, int* __restrict__ positions) {
+    const WinMeta w = wins[blockIdx.y];
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= w.n_video) return;
+    const TokenCoord c = window_token(w, r);
+    const int p = w.part_off + r;
+    if (indices) indices[p] = (int)c.src;
+    if (inverse) inverse[c.src] = p;
+    if (positions) {
+        positions[3 * p + 0] = c.lt;
+        positions[3 * p + 1] = c.lh;
+        positions[3 * p + 2] = c.lw;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+
+hipError_t launch_rope_table(const float* freqs, int pairs, int positions, float2* table,
+                             hipStream_t stream) {
+    const int n = pairs * positions;
+    if (n <= 0) return hipSuccess;
+    rope_table_kernel<<<(n + 255) / 256, 256, 0, stream>>>(freqs, pairs, positions, table);
+    return hipGetLastError();
+}
+
+template <int D, typename TIn>
+static hipError_t prologue_impl(const s2_awa_plan& plan, const void* vq, const void* vk,
+                                const void* vv, long vstride, const void* tq, const void* tk,
+                                const void* tv, long tstride, const float* norm,
+                                const float2* rope, uint16_t* q_out, uint16_t* k_out,
+                                uint16_t* vt_out, hipStream_t stream) {
+    dim3 grid(plan.num_chunks, plan.config.heads);
+    awa_prologue_kernel<D, TIn><<<grid, 256, 0, stream>>>(
+        plan.d_wins, plan.d_chunks, (const TIn*)vq, (const TIn*)vk, (const TIn*)vv, vstride,
+        (const TIn*)tq, (const TIn*)tk, (const TIn*)tv, tstride, norm, rope,
+        plan.config.rope_pairs_per_axis, plan.config.epsilon, plan.config.official_bf16_attention,
+        q_out, k_out, vt_out, plan.seg_total);
+    return hipGetLastError();
+}
+
+hipError_t launch_awa_prologue(const s2_awa_plan& plan, const void* vq, const void* vk,
+                               const void* vv, long vstride, const void* tq, const void* tk,
+                               const void* tv, long tstride, bool in_bf16, const float* norm,
+                               const float2* rope, uint16_t* q_out, uint16_t* k_out,
+                               uint16_t* vt_out, hipStream_t stream) {
+    const int d = plan.config.head_dim;
+    if (d == 128)
+        return in_bf16 ? prologue_impl<128, uint16_t>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
+                                                      norm, rope, q_out, k_out, vt_out, stream)
+                       : prologue_impl<128, float>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
+                                                   norm, rope, q_out, k_out, vt_out, stream);
+    if (d == 64)
+        return in_bf16 ? prologue_impl<64, uint16_t>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
+                                                     norm, rope, q_out, k_out, vt_out, stream)
+                       : prologue_impl<64, float>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
+                                                  norm, rope, q_out, k_out, vt_out, stream);
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_awa_attention(const s2_awa_plan& plan, const uint16_t* q, const uint16_t* k,
+                                const uint16_t* vt, void* out_video, bool out_bf16,
+                                float* text_partial, hipStream_t stream) {
+    const int d = plan.config.head_dim;
+    const int inner = plan.config.heads * d;
+    const float scale_log2 = 1.4426950408889634f / sqrtf((float)d);
+    const int grid = plan.slots_per_xcd * kNumXcd;
+    if (grid == 0) return hipSuccess;
+    if (d == 128)
+        awa_attention_kernel<128><<<grid, 256, 0, stream>>>(
+            plan.d_wins, plan.d_items, plan.slots_per_xcd, q, k, vt, plan.seg_total, scale_log2,
+            plan.config.official_bf16_attention, out_video, out_bf16 ? 1 : 0, inner, text_partial);
+    else if (d == 64)
+        awa_attention_kernel<64><<<grid, 256, 0, stream>>>(
+            plan.d_wins, plan.d_items, plan.slots_per_xcd, q, k, vt, plan.seg_total, scale_log2,
+            plan.config.official_bf16_attention, out_video, out_bf16 ? 1 : 0, inner, text_partial);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+hipError_t launch_awa_text_pool(const s2_awa_plan& plan, const float* partial, void* out_text,
+                                bool out_bf16, hipStream_t stream) {
+    const int inner = plan.config.heads * plan.config.head_dim;
+    const long n = (long)plan.text_tokens * (inner / 4);
+    if (n == 0) return hipSuccess;
+    awa_text_pool_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+        plan.d_samples, plan.d_text_sample, plan.d_wins, partial, plan.text_tokens, inner,
+        out_text, out_bf16 ? 1 : 0);
+    return hipGetLastError();
+}
+
+hipError_t launch_awa_plan_tables(const s2_awa_plan& plan, int* indices, int* inverse,
+                                  int* positions, hipStream_t stream) {
+    if (plan.num_windows == 0 || plan.max_window_tokens == 0) return hipSuccess;
+    dim3 grid((plan.max_window_tokens + 255) / 256, plan.num_windows);
+    awa_plan_tables_kernel<<<grid, 256, 0, stream>>>(plan.d_wins, indices, inverse, positions);
+    return hipGetLastError();
+}
+
+}  // namespace s2

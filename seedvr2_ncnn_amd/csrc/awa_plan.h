@@ -1,0 +1,102 @@
+// Window-plan data shared by the host plan builder and the gfx950 kernels.
+#pragma once
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "seedvr2_hip.h"
+
+namespace s2 {
+
+// Per-window record the kernels read (one 64-byte line per window).  The
+// per-token gather/scatter index is recomputed from these integers on the
+// device: partition-local token r of a window maps to
+//   lt = r / (eh*ew), lh = (r / ew) % eh, lw = r % ew
+//   source = tok_off + ((t0+lt)*grid_h + h0+lh)*grid_w + w0+lw
+// which is append_slice's t,h,w row-major walk
+// (adaptive_window_attention.cpp:462-471).
+struct WinMeta {
+    int sample;
+    int t0, h0, w0;
+    int et, eh, ew;       // window extents t1-t0, h1-h0, w1-w0
+    int part_off;         // WindowSlice::partition_offset
+    int n_video;          // WindowSlice::token_count
+    int seq;              // n_video + text_len (the SDPA sequence length)
+    int seg_off;          // first row of this window's padded Q/K/V segment
+    int text_off;         // first text row of the sample
+    int text_len;
+    int grid_h, grid_w;   // sample token grid h, w
+    int tok_off;          // first video row of the sample
+    int tpart_off;        // first row of this window's text partials
+    int pad_;
+};
+static_assert(sizeof(WinMeta) == 72, "WinMeta layout");
+
+// Per-sample record for the text mean-pool.
+struct SampleMeta {
+    int first_window;
+    int num_windows;
+    int text_off;
+    int text_len;
+    float pool_scale;     // 1.f / num_windows (adaptive_window_attention.cpp:963)
+};
+
+// One attention work item: (window, 128-row query tile, head).
+struct AttnItem {
+    int window;
+    int q_row0;
+    int head;
+    int pad_;
+};
+
+// Segment rows are padded to this multiple so every key tile is whole.
+constexpr int kSegAlign = 64;
+
+// MI355X has 8 XCDs; workgroups are dealt to them round-robin.
+constexpr int kNumXcd = 8;
+
+// One prologue work item: 64 rows of one window's sequence.
+struct ChunkRef {
+    int window;
+    int row0;
+};
+
+// Host window list (restates adaptive_window_attention.cpp:565-655).
+int build_window_slices(const int* video_shapes, int batch, const int target_windows[3],
+                        bool shifted, std::vector<s2_window_slice>& windows,
+                        std::vector<int>& sample_window_count, int& video_tokens);
+
+}  // namespace s2
+
+// The opaque plan handle behind s2_awa_plan*.
+struct s2_awa_plan {
+    s2_awa_config config;
+    int batch = 0;
+    int num_windows = 0;
+    int video_tokens = 0;
+    int text_tokens = 0;
+    int device = 0;
+    std::vector<int> video_shapes;          // [batch][3]
+    std::vector<int> text_lengths;          // [batch]
+    std::vector<s2_window_slice> windows;
+    std::vector<int> sample_window_count;
+    std::vector<s2::WinMeta> win_meta;
+    // device metadata, one allocation
+    void* d_meta = nullptr;
+    s2::WinMeta* d_wins = nullptr;
+    s2::SampleMeta* d_samples = nullptr;
+    int* d_text_sample = nullptr;           // [text_tokens] -> sample
+    s2::ChunkRef* d_chunks = nullptr;               // prologue chunks {window, row0}
+    s2::AttnItem* d_items = nullptr;        // [kNumXcd][slots_per_xcd]
+    int num_chunks = 0;
+    int slots_per_xcd = 0;
+    int max_window_tokens = 0;
+    int rope_positions = 0;                 // rows of the cos/sin table
+    long seg_total = 0;                     // padded rows over all windows
+    int text_partial_rows = 0;
+    // workspace layout (byte offsets)
+    size_t off_q = 0, off_k = 0, off_vt = 0, off_rope = 0, off_tpart = 0;
+    size_t workspace_bytes = 0;
+};

@@ -1,0 +1,402 @@
+// extern "C" boundary of the window-attention hot path (include/seedvr2_hip.h).
+#include <string.h>
+
+#include <algorithm>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "awa_kernels.h"
+#include "awa_plan.h"
+#include "seedvr2_hip.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail_hip(hipError_t e, const char* what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return S2_ERR_DEVICE;
+}
+
+int fail(int code, const char* what) {
+    g_last_error = what;
+    return code;
+}
+
+#define S2_HIP(call)                                  \
+    do {                                              \
+        hipError_t e_ = (call);                       \
+        if (e_ != hipSuccess) return fail_hip(e_, #call); \
+    } while (0)
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+bool valid_config(const s2_awa_config* c) {
+    return c && c->heads > 0 && (c->head_dim == 64 || c->head_dim == 128) &&
+           c->rope_pairs_per_axis >= 0 && c->rope_pairs_per_axis * 6 <= c->head_dim &&
+           c->target_windows[0] > 0 && c->target_windows[1] > 0 && c->target_windows[2] > 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* s2_last_error(void) { return g_last_error.c_str(); }
+
+int s2_device_count(int* count) {
+    if (!count) return S2_ERR_INVALID;
+    *count = 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) {
+        (void)hipGetLastError();
+        return S2_OK;
+    }
+    for (int i = 0; i < n; ++i) {
+        hipDeviceProp_t prop;
+        if (hipGetDeviceProperties(&prop, i) == hipSuccess &&
+            strncmp(prop.gcnArchName, "gfx950", 6) == 0)
+            ++*count;
+    }
+    return S2_OK;
+}
+
+int s2_malloc(void** ptr, size_t bytes) {
+    if (!ptr) return S2_ERR_INVALID;
+    *ptr = nullptr;
+    if (bytes == 0) return S2_OK;
+    hipError_t e = hipMalloc(ptr, bytes);
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) {
+        fail_hip(e, "hipMalloc");
+        return S2_ERR_ALLOC;
+    }
+    if (e != hipSuccess) return fail_hip(e, "hipMalloc");
+    return S2_OK;
+}
+
+int s2_free(void* ptr) {
+    if (ptr) S2_HIP(hipFree(ptr));
+    return S2_OK;
+}
+
+int s2_memcpy_h2d(void* dst, const void* src, size_t bytes, s2_stream_t stream) {
+    if (bytes == 0) return S2_OK;
+    S2_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_memcpy_d2h(void* dst, const void* src, size_t bytes, s2_stream_t stream) {
+    if (bytes == 0) return S2_OK;
+    S2_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_memcpy_d2d(void* dst, const void* src, size_t bytes, s2_stream_t stream) {
+    if (bytes == 0) return S2_OK;
+    S2_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_stream_synchronize(s2_stream_t stream) {
+    S2_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_awa_plan_windows(const int* video_shapes, int batch, const int target_windows[3],
+                        int shifted, s2_window_slice* windows, int max_windows,
+                        int* num_windows, int* sample_window_count, int* video_tokens) {
+    std::vector<s2_window_slice> w;
+    std::vector<int> counts;
+    int tokens = 0;
+    const int ret = s2::build_window_slices(video_shapes, batch, target_windows, shifted != 0, w,
+                                            counts, tokens);
+    if (ret != S2_OK) return fail(ret, "invalid window plan shapes");
+    if (num_windows) *num_windows = (int)w.size();
+    if (video_tokens) *video_tokens = tokens;
+    if (sample_window_count) std::copy(counts.begin(), counts.end(), sample_window_count);
+    if (windows) {
+        if ((int)w.size() > max_windows) return fail(S2_ERR_INVALID, "window buffer too small");
+        std::copy(w.begin(), w.end(), windows);
+    }
+    return S2_OK;
+}
+
+int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
+                       const int* text_lengths, int batch, s2_awa_plan** out) {
+    if (!out) return S2_ERR_INVALID;
+    *out = nullptr;
+    if (!valid_config(config) || !video_shapes || !text_lengths || batch <= 0)
+        return fail(S2_ERR_INVALID, "invalid attention configuration");
+    for (int b = 0; b < batch; ++b)
+        if (text_lengths[b] <= 0) return fail(S2_ERR_INVALID, "text length must be positive");
+
+    s2_awa_plan* plan = new (std::nothrow) s2_awa_plan();
+    if (!plan) return S2_ERR_ALLOC;
+    plan->config = *config;
+    plan->batch = batch;
+    plan->video_shapes.assign(video_shapes, video_shapes + 3 * batch);
+    plan->text_lengths.assign(text_lengths, text_lengths + batch);
+    int ret = s2::build_window_slices(video_shapes, batch, config->target_windows,
+                                      config->shifted != 0, plan->windows,
+                                      plan->sample_window_count, plan->video_tokens);
+    if (ret != S2_OK) {
+        delete plan;
+        return fail(ret, "invalid window plan shapes");
+    }
+    plan->num_windows = (int)plan->windows.size();
+    const int heads = config->heads, d = config->head_dim, inner = heads * d;
+
+    // Per-sample offsets.
+    std::vector<int> text_off(batch), tok_off(batch), first_win(batch);
+    for (int b = 0, to = 0, vo = 0, fw = 0; b < batch; ++b) {
+        text_off[b] = to;
+        tok_off[b] = vo;
+        first_win[b] = fw;
+        to += text_lengths[b];
+        vo += video_shapes[3 * b] * video_shapes[3 * b + 1] * video_shapes[3 * b + 2];
+        fw += plan->sample_window_count[b];
+    }
+    plan->text_tokens = text_off[batch - 1] + text_lengths[batch - 1];
+
+    // Window records, padded segments, text partial rows, prologue chunks.
+    std::vector<s2::ChunkRef> chunks;
+    long seg = 0;
+    int tpart = 0, rope_pos = 1;
+    plan->win_meta.resize(plan->num_windows);
+    for (int i = 0; i < plan->num_windows; ++i) {
+        const s2_window_slice& s = plan->windows[i];
+        s2::WinMeta& m = plan->win_meta[i];
+        const int b = s.sample_index;
+        m.sample = b;
+        m.t0 = s.t0; m.h0 = s.h0; m.w0 = s.w0;
+        m.et = s.t1 - s.t0; m.eh = s.h1 - s.h0; m.ew = s.w1 - s.w0;
+        m.part_off = s.partition_offset;
+        m.n_video = s.token_count;
+        m.text_len = text_lengths[b];
+        m.seq = s.token_count + m.text_len;
+        m.seg_off = (int)seg;
+        m.text_off = text_off[b];
+        m.grid_h = video_shapes[3 * b + 1];
+        m.grid_w = video_shapes[3 * b + 2];
+        m.tok_off = tok_off[b];
+        m.tpart_off = tpart;
+        m.pad_ = 0;
+        const int padded = (m.seq + s2::kSegAlign - 1) / s2::kSegAlign * s2::kSegAlign;
+        for (int r = 0; r < padded; r += s2::kSegAlign) chunks.push_back(s2::ChunkRef{i, r});
+        seg += padded;
+        tpart += m.text_len;
+        rope_pos = std::max(rope_pos, m.et - 1 + m.text_len + 1);
+        rope_pos = std::max(rope_pos, std::max(m.eh, m.ew));
+        rope_pos = std::max(rope_pos, m.text_len);
+        plan->max_window_tokens = std::max(plan->max_window_tokens, m.n_video);
+    }
+    plan->seg_total = seg;
+    plan->text_partial_rows = tpart;
+    plan->rope_positions = rope_pos;
+    plan->num_chunks = (int)chunks.size();
+
+    // Attention items: (window, head) pairs, longest sequence first, dealt
+    // round-robin to the XCDs; the query tiles of one pair stay consecutive
+    // on one XCD so its K/V tiles are shared through that XCD's L2.
+    std::vector<std::pair<int, int> > pairs;
+    for (int i = 0; i < plan->num_windows; ++i)
+        for (int h = 0; h < heads; ++h) pairs.emplace_back(i, h);
+    std::stable_sort(pairs.begin(), pairs.end(), [&](const std::pair<int, int>& a,
+                                                     const std::pair<int, int>& b) {
+        return plan->win_meta[a.first].seq > plan->win_meta[b.first].seq;
+    });
+    std::vector<std::vector<s2::AttnItem> > lists(s2::kNumXcd);
+    std::vector<long> load(s2::kNumXcd, 0);
+    for (const auto& pr : pairs) {
+        const s2::WinMeta& m = plan->win_meta[pr.first];
+        const int tiles = (m.seq + 127) / 128;
+        // the least loaded XCD takes the next pair (LPT)
+        const int x = (int)(std::min_element(load.begin(), load.end()) - load.begin());
+        for (int t = 0; t < tiles; ++t) lists[x].push_back({pr.first, 128 * t, pr.second, 0});
+        load[x] += (long)tiles * m.seq;
+    }
+    size_t slots = 0;
+    for (const auto& l : lists) slots = std::max(slots, l.size());
+    plan->slots_per_xcd = (int)slots;
+    std::vector<s2::AttnItem> items(slots * s2::kNumXcd, s2::AttnItem{-1, 0, 0, 0});
+    for (int x = 0; x < s2::kNumXcd; ++x)
+        std::copy(lists[x].begin(), lists[x].end(), items.begin() + (size_t)x * slots);
+
+    std::vector<s2::SampleMeta> samples(batch);
+    for (int b = 0; b < batch; ++b)
+        samples[b] = {first_win[b], plan->sample_window_count[b], text_off[b], text_lengths[b],
+                      1.f / plan->sample_window_count[b]};
+    std::vector<int> text_sample(plan->text_tokens);
+    for (int b = 0; b < batch; ++b)
+        for (int t = 0; t < text_lengths[b]; ++t) text_sample[text_off[b] + t] = b;
+
+    // One device allocation for all metadata.
+    const size_t sz_w = align256(sizeof(s2::WinMeta) * plan->num_windows);
+    const size_t sz_s = align256(sizeof(s2::SampleMeta) * batch);
+    const size_t sz_t = align256(sizeof(int) * plan->text_tokens);
+    const size_t sz_c = align256(sizeof(s2::ChunkRef) * chunks.size());
+    const size_t sz_i = align256(sizeof(s2::AttnItem) * items.size());
+    std::vector<unsigned char> host(sz_w + sz_s + sz_t + sz_c + sz_i, 0);
+    size_t o = 0;
+    memcpy(host.data() + o, plan->win_meta.data(), sizeof(s2::WinMeta) * plan->num_windows);
+    o += sz_w;
+    memcpy(host.data() + o, samples.data(), sizeof(s2::SampleMeta) * batch);
+    o += sz_s;
+    memcpy(host.data() + o, text_sample.data(), sizeof(int) * plan->text_tokens);
+    o += sz_t;
+    memcpy(host.data() + o, chunks.data(), sizeof(s2::ChunkRef) * chunks.size());
+    o += sz_c;
+    memcpy(host.data() + o, items.data(), sizeof(s2::AttnItem) * items.size());
+
+    hipError_t e = hipGetDevice(&plan->device);
+    if (e == hipSuccess) e = hipMalloc(&plan->d_meta, host.size());
+    if (e == hipSuccess) e = hipMemcpy(plan->d_meta, host.data(), host.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (plan->d_meta) (void)hipFree(plan->d_meta);
+        delete plan;
+        return fail_hip(e, "plan upload");
+    }
+    unsigned char* base = (unsigned char*)plan->d_meta;
+    plan->d_wins = (s2::WinMeta*)base;
+    plan->d_samples = (s2::SampleMeta*)(base + sz_w);
+    plan->d_text_sample = (int*)(base + sz_w + sz_s);
+    plan->d_chunks = (s2::ChunkRef*)(base + sz_w + sz_s + sz_t);
+    plan->d_items = (s2::AttnItem*)(base + sz_w + sz_s + sz_t + sz_c);
+
+    // Workspace layout: Q and K [heads][seg_total][d], V^T [heads][d][seg_total]
+    // (bf16), the cos/sin table, and fp32 text partials [rows][inner].
+    const size_t qkv = align256((size_t)heads * seg * d * 2);
+    plan->off_q = 0;
+    plan->off_k = qkv;
+    plan->off_vt = 2 * qkv;
+    plan->off_rope = 3 * qkv;
+    plan->off_tpart =
+        plan->off_rope + align256(sizeof(float2) * (size_t)rope_pos * config->rope_pairs_per_axis);
+    plan->workspace_bytes = plan->off_tpart + align256(sizeof(float) * (size_t)tpart * inner);
+    *out = plan;
+    return S2_OK;
+}
+
+int s2_awa_plan_get_info(const s2_awa_plan* plan, s2_awa_plan_info* info) {
+    if (!plan || !info) return S2_ERR_INVALID;
+    info->batch = plan->batch;
+    info->num_windows = plan->num_windows;
+    info->video_tokens = plan->video_tokens;
+    info->text_tokens = plan->text_tokens;
+    info->workspace_bytes = plan->workspace_bytes;
+    return S2_OK;
+}
+
+int s2_awa_plan_get_windows(const s2_awa_plan* plan, s2_window_slice* windows, int max_windows,
+                            int* sample_window_count) {
+    if (!plan) return S2_ERR_INVALID;
+    if (windows) {
+        if (max_windows < plan->num_windows) return fail(S2_ERR_INVALID, "window buffer too small");
+        std::copy(plan->windows.begin(), plan->windows.end(), windows);
+    }
+    if (sample_window_count)
+        std::copy(plan->sample_window_count.begin(), plan->sample_window_count.end(),
+                  sample_window_count);
+    return S2_OK;
+}
+
+int s2_awa_plan_destroy(s2_awa_plan* plan) {
+    if (!plan) return S2_OK;
+    hipError_t e = hipSuccess;
+    if (plan->d_meta) e = hipFree(plan->d_meta);
+    delete plan;
+    if (e != hipSuccess) return fail_hip(e, "hipFree");
+    return S2_OK;
+}
+
+int s2_awa_plan_tables(const s2_awa_plan* plan, int* video_indices, int* inverse_video_indices,
+                       int* local_positions, s2_stream_t stream) {
+    if (!plan) return S2_ERR_INVALID;
+    S2_HIP(s2::launch_awa_plan_tables(*plan, video_indices, inverse_video_indices, local_positions,
+                                      (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const float* rope_freqs,
+                   const void* video_q, const void* video_k, const void* video_v,
+                   long video_row_stride, const void* text_q, const void* text_k,
+                   const void* text_v, long text_row_stride, s2_dtype in_dtype, void* out_video,
+                   void* out_text, s2_dtype out_dtype, void* workspace, size_t workspace_bytes,
+                   s2_stream_t stream) {
+    if (!plan || !norm_weights || !video_q || !video_k || !video_v || !text_q || !text_k ||
+        !text_v || !out_video || !out_text || !workspace)
+        return fail(S2_ERR_INVALID, "null argument");
+    if ((plan->config.rope_pairs_per_axis > 0 && !rope_freqs))
+        return fail(S2_ERR_INVALID, "missing rope frequencies");
+    if (workspace_bytes < plan->workspace_bytes) return fail(S2_ERR_INVALID, "workspace too small");
+    if ((in_dtype != S2_DTYPE_F32 && in_dtype != S2_DTYPE_BF16) ||
+        (out_dtype != S2_DTYPE_F32 && out_dtype != S2_DTYPE_BF16))
+        return fail(S2_ERR_INVALID, "unsupported dtype");
+    const int inner = plan->config.heads * plan->config.head_dim;
+    if (video_row_stride < inner || text_row_stride < inner || (video_row_stride % 8) != 0 ||
+        (text_row_stride % 8) != 0)
+        return fail(S2_ERR_INVALID, "row stride must be >= heads*head_dim and a multiple of 8");
+    const size_t elem = in_dtype == S2_DTYPE_BF16 ? 2 : 4;
+    const void* ins[6] = {video_q, video_k, video_v, text_q, text_k, text_v};
+    for (const void* p : ins)
+        if (((uintptr_t)p) % (8 * elem) != 0)
+            return fail(S2_ERR_INVALID, "inputs must be aligned to 8 elements");
+    if (((uintptr_t)workspace) % 256 != 0) return fail(S2_ERR_INVALID, "workspace alignment");
+
+    hipStream_t s = (hipStream_t)stream;
+    unsigned char* ws = (unsigned char*)workspace;
+    uint16_t* q = (uint16_t*)(ws + plan->off_q);
+    uint16_t* k = (uint16_t*)(ws + plan->off_k);
+    uint16_t* vt = (uint16_t*)(ws + plan->off_vt);
+    float2* rope = (float2*)(ws + plan->off_rope);
+    float* tpart = (float*)(ws + plan->off_tpart);
+    const bool in_bf16 = in_dtype == S2_DTYPE_BF16;
+    const bool out_bf16 = out_dtype == S2_DTYPE_BF16;
+    if (plan->config.rope_pairs_per_axis > 0)
+        S2_HIP(s2::launch_rope_table(rope_freqs, plan->config.rope_pairs_per_axis,
+                                     plan->rope_positions, rope, s));
+    S2_HIP(s2::launch_awa_prologue(*plan, video_q, video_k, video_v, video_row_stride, text_q,
+                                   text_k, text_v, text_row_stride, in_bf16, norm_weights, rope, q,
+                                   k, vt, s));
+    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, out_bf16, tpart, s));
+    S2_HIP(s2::launch_awa_text_pool(*plan, tpart, out_text, out_bf16, s));
+    return S2_OK;
+}
+
+int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream_t stream) {
+    if (count && (!src || !dst)) return S2_ERR_INVALID;
+    S2_HIP(s2::launch_cast_f32_bf16(src, dst, count, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream_t stream) {
+    if (count && (!src || !dst)) return S2_ERR_INVALID;
+    S2_HIP(s2::launch_cast_bf16_f32(src, dst, count, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
+                             s2_dtype x_dtype, const uint16_t* weight, const float* bias, int n,
+                             int k, int activation, void* y_video, void* y_text, s2_dtype y_dtype,
+                             s2_stream_t stream) {
+    if (n <= 0 || k <= 0 || m_video < 0 || m_text < 0 || !weight)
+        return fail(S2_ERR_INVALID, "invalid linear shape");
+    if ((m_video > 0 && (!x_video || !y_video)) || (m_text > 0 && (!x_text || !y_text)))
+        return fail(S2_ERR_INVALID, "null stream pointer");
+    if (k % 8 != 0) return fail(S2_ERR_INVALID, "k must be a multiple of 8");
+    if (activation != S2_ACT_NONE && activation != S2_ACT_GELU)
+        return fail(S2_ERR_INVALID, "unknown activation");
+    if ((x_dtype != S2_DTYPE_F32 && x_dtype != S2_DTYPE_BF16) ||
+        (y_dtype != S2_DTYPE_F32 && y_dtype != S2_DTYPE_BF16))
+        return fail(S2_ERR_INVALID, "unsupported dtype");
+    const size_t xe = x_dtype == S2_DTYPE_BF16 ? 2 : 4;
+    if (((uintptr_t)x_video) % (8 * xe) || ((uintptr_t)x_text) % (8 * xe) ||
+        ((uintptr_t)weight) % 16)
+        return fail(S2_ERR_INVALID, "operands must be 16-byte aligned");
+    S2_HIP(s2::launch_shared_linear(x_video, m_video, x_text, m_text, x_dtype == S2_DTYPE_BF16,
+                                    weight, bias, n, k, activation, y_video, y_text,
+                                    y_dtype == S2_DTYPE_BF16, (hipStream_t)stream));
+    return S2_OK;
+}
+
+}  // extern "C"

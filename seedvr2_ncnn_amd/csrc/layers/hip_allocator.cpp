@@ -1,0 +1,69 @@
+#include "hip_allocator.h"
+
+#include <algorithm>
+
+#include "seedvr2_hip.h"
+
+namespace seedvr2 {
+
+HipDeviceAllocator::HipDeviceAllocator(void* stream) : stream_(stream) {}
+
+HipDeviceAllocator::~HipDeviceAllocator() { clear(); }
+
+void* HipDeviceAllocator::fastMalloc(size_t) { return 0; }
+
+void HipDeviceAllocator::fastFree(void* ptr) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    std::vector<void*>::iterator it = std::find(owned_.begin(), owned_.end(), ptr);
+    if (it != owned_.end()) {
+        s2_free(ptr);
+        owned_.erase(it);
+    }
+}
+
+ncnn::Mat HipDeviceAllocator::create_blob(int w, int h, size_t elemsize) {
+    if (w <= 0 || h <= 0 || (elemsize != 2 && elemsize != 4)) return ncnn::Mat();
+    void* p = 0;
+    if (s2_malloc(&p, (size_t)w * h * elemsize) != S2_OK || !p) return ncnn::Mat();
+    {
+        std::lock_guard<std::mutex> lock(mutex_);
+        owned_.push_back(p);
+    }
+    return ncnn::Mat(w, h, p, elemsize, this);
+}
+
+ncnn::Mat HipDeviceAllocator::wrap_blob(int w, int h, void* device_data, size_t elemsize) {
+    return ncnn::Mat(w, h, device_data, elemsize, this);
+}
+
+void HipDeviceAllocator::clear() {
+    std::lock_guard<std::mutex> lock(mutex_);
+    if (!owned_.empty()) s2_stream_synchronize(stream_);
+    for (size_t i = 0; i < owned_.size(); i++) s2_free(owned_[i]);
+    owned_.clear();
+}
+
+HipDeviceAllocator* device_allocator_of(const ncnn::Mat& m) {
+    return dynamic_cast<HipDeviceAllocator*>(m.allocator);
+}
+
+DeviceBuffer::~DeviceBuffer() { release(); }
+
+int DeviceBuffer::reserve(size_t bytes) {
+    if (bytes <= bytes_) return S2_OK;
+    release();
+    void* p = 0;
+    const int ret = s2_malloc(&p, bytes);
+    if (ret != S2_OK) return ret;
+    ptr_ = p;
+    bytes_ = bytes;
+    return S2_OK;
+}
+
+void DeviceBuffer::release() {
+    if (ptr_) s2_free(ptr_);
+    ptr_ = 0;
+    bytes_ = 0;
+}
+
+}  // namespace seedvr2

@@ -1,0 +1,71 @@
+// Device-resident blobs for the MI355X layers.
+//
+// A device blob is an ncnn::Mat over external HIP device memory whose
+// `allocator` member points at a HipDeviceAllocator; the layers see that tag
+// and run zero-copy on the device, on the allocator's stream.  Blobs made by
+// create_blob() are owned by the allocator until clear() or its destruction
+// (ncnn::Mat itself never frees external data).  Host Mats (any other
+// allocator) take the staged path: upload, compute, download, synchronise.
+//
+// Never pass a HipDeviceAllocator to ncnn::Mat::create: upstream ncnn keeps
+// the reference count at the end of the data block and would write it from
+// the host into device memory.  fastMalloc therefore refuses (returns 0).
+#ifndef SEEDVR2_HIP_ALLOCATOR_H
+#define SEEDVR2_HIP_ALLOCATOR_H
+
+#include <mutex>
+#include <vector>
+
+#include <allocator.h>
+#include <mat.h>
+
+namespace seedvr2 {
+
+class HipDeviceAllocator : public ncnn::Allocator {
+public:
+    // stream: a hipStream_t (as void*), 0 = the default stream.
+    explicit HipDeviceAllocator(void* stream = 0);
+    virtual ~HipDeviceAllocator();
+
+    virtual void* fastMalloc(size_t size);
+    virtual void fastFree(void* ptr);
+
+    // Device Mat (dims 2: w x h, elemsize 4 = fp32, 2 = bf16) owned by this
+    // allocator.  Empty on allocation failure.
+    ncnn::Mat create_blob(int w, int h, size_t elemsize);
+    // Wraps caller-owned device memory as a device blob (not owned).
+    ncnn::Mat wrap_blob(int w, int h, void* device_data, size_t elemsize);
+    // Frees every blob this allocator created.
+    void clear();
+
+    void* stream() const { return stream_; }
+
+private:
+    void* stream_;
+    std::mutex mutex_;
+    std::vector<void*> owned_;
+};
+
+// True when m is a device blob (its allocator is a HipDeviceAllocator).
+HipDeviceAllocator* device_allocator_of(const ncnn::Mat& m);
+
+// Device buffer that only grows; used for layer workspaces and staging.
+class DeviceBuffer {
+public:
+    DeviceBuffer() : ptr_(0), bytes_(0) {}
+    ~DeviceBuffer();
+    int reserve(size_t bytes);   // S2_OK or S2_ERR_ALLOC / S2_ERR_DEVICE
+    void release();
+    void* get() const { return ptr_; }
+    size_t size() const { return bytes_; }
+
+private:
+    DeviceBuffer(const DeviceBuffer&);
+    DeviceBuffer& operator=(const DeviceBuffer&);
+    void* ptr_;
+    size_t bytes_;
+};
+
+}  // namespace seedvr2
+
+#endif  // SEEDVR2_HIP_ALLOCATOR_H

@@ -1,0 +1,83 @@
+// Device-side helpers shared by the gfx950 kernels: bf16 conversion, 16-byte
+// vector moves and the MFMA operand types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "awa_plan.h"
+
+namespace s2 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kWave = 64;
+
+// The reference round_bf16 (adaptive_window_attention.cpp:499-508), returning
+// the upper 16 bits: round to nearest even; for Inf/NaN the increment is
+// skipped, so a NaN whose payload sits only in the low 16 bits becomes Inf,
+// exactly as on the reference CPU path.
+__device__ __forceinline__ uint16_t round_bf16_ref_bits(float x) {
+    uint32_t b = __float_as_uint(x);
+    if ((b & 0x7f800000u) != 0x7f800000u) b += 0x7fffu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+// Storage conversion fp32 -> bf16: round to nearest even, NaN stays NaN.
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+    uint32_t b = __float_as_uint(x);
+    if ((b & 0x7f800000u) == 0x7f800000u)
+        return (uint16_t)((b >> 16) | ((b & 0xffffu) ? 0x40u : 0u));
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return (uint16_t)(b >> 16);
+}
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+    return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// Load 8 consecutive elements as fp32.
+__device__ __forceinline__ void load8(const uint16_t* p, float (&v)[8]) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        v[2 * i] = __uint_as_float(w[i] << 16);
+        v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+}
+
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ uint4 pack8_bf16(const uint16_t (&h)[8]) {
+    uint4 r;
+    r.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+    r.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+    r.z = (uint32_t)h[4] | ((uint32_t)h[5] << 16);
+    r.w = (uint32_t)h[6] | ((uint32_t)h[7] << 16);
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+// Physical workgroup id -> logical id such that consecutive logical ids run
+// on the same XCD (the hardware deals workgroups to XCDs round-robin).
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+    const int xcd = bid % kNumXcd;
+    const int idx = bid / kNumXcd;
+    const int per = nblocks / kNumXcd;
+    const int rem = nblocks % kNumXcd;
+    return xcd * per + (xcd < rem ? xcd : rem) + idx;
+}
+
+}  // namespace s2

@@ -1,0 +1,182 @@
+// Test harness: drives the ncnn-surface layers (AdaptiveWindowAttention,
+// SharedLinear) the way an ncnn Net does -- creator, load_param from a .param
+// field string, load_model from raw weight bytes, create_pipeline, forward --
+// and exposes that to the Python tests through a few extern "C" calls.
+// Test infrastructure only; built into tests/harness/liblayer_harness.so.
+#include <string.h>
+
+#include <array>
+#include <string>
+#include <vector>
+
+#include <layer.h>
+#include <modelbin.h>
+#include <paramdict.h>
+
+#include "adaptive_window_attention.h"
+#include "hip_allocator.h"
+#include "seedvr2_hip.h"
+#include "shared_linear.h"
+
+namespace {
+
+seedvr2::HipDeviceAllocator& device_allocator() {
+    static seedvr2::HipDeviceAllocator alloc(0);
+    return alloc;
+}
+
+struct Handle {
+    ncnn::Layer* layer;
+    ncnn::layer_destroyer_func destroyer;
+    seedvr2::AdaptiveWindowRuntimeState state;
+    ncnn::Option opt;
+};
+
+}  // namespace
+
+extern "C" {
+
+typedef struct h_blob {
+    int dims;       // 0 = empty blob, 1 or 2
+    int w, h;
+    int elemsize;   // 4 fp32 / int32, 2 bf16
+    int device;     // data is a device pointer
+    void* data;
+} h_blob;
+
+// type: "AdaptiveWindowAttention" or "SharedLinear"; params: the id=value
+// fields of a .param line; model: raw weight bytes (nullptr/0: skip
+// load_model).  Returns load_param's or load_model's code.
+int h_layer_create(const char* type, const char* params, const void* model, long model_bytes,
+                   void** out) {
+    *out = 0;
+    Handle* h = new Handle();
+    if (strcmp(type, "AdaptiveWindowAttention") == 0) {
+        h->layer = seedvr2::adaptive_window_attention_layer_creator(&h->state);
+        h->destroyer = seedvr2::adaptive_window_attention_layer_destroyer;
+    } else if (strcmp(type, "SharedLinear") == 0) {
+        h->layer = seedvr2::shared_linear_layer_creator(0);
+        h->destroyer = seedvr2::shared_linear_layer_destroyer;
+    } else {
+        delete h;
+        return -1;
+    }
+    h->layer->type = type;
+    ncnn::ParamDict pd;
+    int ret = pd.load_param_text(params ? params : "");
+    if (ret == 0) ret = h->layer->load_param(pd);
+    if (ret == 0 && model) {
+        ncnn::ModelBinFromMemory mb(static_cast<const unsigned char*>(model), (size_t)model_bytes);
+        ret = h->layer->load_model(mb);
+    }
+    *out = h;
+    return ret;
+}
+
+int h_layer_create_pipeline(void* handle) {
+    Handle* h = static_cast<Handle*>(handle);
+    return h->layer->create_pipeline(h->opt);
+}
+
+void h_layer_destroy(void* handle) {
+    Handle* h = static_cast<Handle*>(handle);
+    if (!h) return;
+    h->layer->destroy_pipeline(h->opt);
+    h->destroyer(h->layer, 0);
+    delete h;
+}
+
+// AdaptiveWindowAttention::set_runtime_shapes through the creator's
+// userdata (the reference's runtime_state, seedvr2_dit.cpp:724-725).
+void h_awa_set_state(void* handle, const int* shapes, const int* text_lengths, int batch) {
+    Handle* h = static_cast<Handle*>(handle);
+    h->state.video_shapes.resize(batch);
+    h->state.text_lengths.assign(text_lengths, text_lengths + batch);
+    for (int b = 0; b < batch; b++)
+        for (int a = 0; a < 3; a++) h->state.video_shapes[b][a] = shapes[3 * b + a];
+}
+
+int h_awa_configure_and_set_weights(void* handle, int heads, int head_dim, const int* target,
+                                    int shifted, float eps, int pairs, int int32_shapes,
+                                    int official_bf16, const float* vq, const float* vk,
+                                    const float* tq, const float* tk, const float* freqs) {
+    Handle* h = static_cast<Handle*>(handle);
+    seedvr2::AdaptiveWindowAttention* l = dynamic_cast<seedvr2::AdaptiveWindowAttention*>(h->layer);
+    if (!l) return -1;
+    std::array<int, 3> t = {{target[0], target[1], target[2]}};
+    l->configure(heads, head_dim, t, shifted != 0, eps, pairs, int32_shapes != 0, official_bf16 != 0);
+    return l->set_weights(std::vector<float>(vq, vq + head_dim), std::vector<float>(vk, vk + head_dim),
+                          std::vector<float>(tq, tq + head_dim), std::vector<float>(tk, tk + head_dim),
+                          std::vector<float>(freqs, freqs + pairs));
+}
+
+// forward(vector<Mat>) with host or device input blobs.  Outputs are copied
+// into the caller's buffers (host, or device when outs[i].device); their
+// shapes are reported back in outs[i].
+int h_layer_forward(void* handle, int n_in, const h_blob* ins, int n_out, h_blob* outs) {
+    Handle* h = static_cast<Handle*>(handle);
+    std::vector<ncnn::Mat> bottoms(n_in);
+    for (int i = 0; i < n_in; i++) {
+        const h_blob& b = ins[i];
+        if (b.dims == 0) continue;
+        ncnn::Allocator* alloc = b.device ? &device_allocator() : 0;
+        if (b.dims == 1)
+            bottoms[i] = ncnn::Mat(b.w, b.data, (size_t)b.elemsize, alloc);
+        else
+            bottoms[i] = ncnn::Mat(b.w, b.h, b.data, (size_t)b.elemsize, alloc);
+    }
+    std::vector<ncnn::Mat> tops(n_out);
+    int ret = h->layer->forward(bottoms, tops, h->opt);
+    if (ret != 0) return ret;
+    for (int i = 0; i < n_out; i++) {
+        h_blob& o = outs[i];
+        const ncnn::Mat& m = tops[i];
+        const size_t bytes = m.total() * m.elemsize;
+        const size_t cap = (size_t)o.w * o.h * o.elemsize;
+        o.dims = m.dims;
+        const bool src_dev = seedvr2::device_allocator_of(m) != 0;
+        if (bytes > cap) return -3;
+        o.w = m.w;
+        o.h = m.h;
+        o.elemsize = (int)m.elemsize;
+        if (bytes == 0) continue;
+        if (src_dev && o.device) ret = s2_memcpy_d2d(o.data, m.data, bytes, 0);
+        else if (src_dev) ret = s2_memcpy_d2h(o.data, m.data, bytes, 0);
+        else if (o.device) ret = s2_memcpy_h2d(o.data, m.data, bytes, 0);
+        else memcpy(o.data, m.data, bytes);
+        if (ret != 0) return ret;
+    }
+    ret = s2_stream_synchronize(0);
+    device_allocator().clear();
+    return ret;
+}
+
+// seedvr2::build_adaptive_window_plan (layer-level API) into flat arrays.
+int h_build_plan(const int* shapes, int batch, const int* target, int shifted, int max_windows,
+                 int* num_windows, int* windows, int* counts, int* indices, int* inverse,
+                 int* positions) {
+    std::vector<std::array<int, 3> > vs(batch);
+    for (int b = 0; b < batch; b++)
+        for (int a = 0; a < 3; a++) vs[b][a] = shapes[3 * b + a];
+    std::array<int, 3> t = {{target[0], target[1], target[2]}};
+    seedvr2::AdaptiveWindowPlan plan;
+    const int ret = seedvr2::build_adaptive_window_plan(vs, t, shifted != 0, plan);
+    if (ret != 0) return ret;
+    *num_windows = (int)plan.windows.size();
+    if ((int)plan.windows.size() > max_windows) return -3;
+    for (size_t i = 0; i < plan.windows.size(); i++) {
+        const seedvr2::WindowSlice& s = plan.windows[i];
+        const int f[9] = {s.sample_index, s.t0, s.t1, s.h0, s.h1, s.w0, s.w1,
+                          s.partition_offset, s.token_count};
+        memcpy(windows + 9 * i, f, sizeof(f));
+    }
+    for (int b = 0; b < batch; b++) counts[b] = plan.sample_window_count[b];
+    for (size_t p = 0; p < plan.video_indices.size(); p++) {
+        indices[p] = plan.video_indices[p];
+        inverse[p] = plan.inverse_video_indices[p];
+        for (int a = 0; a < 3; a++) positions[3 * p + a] = plan.local_positions[p][a];
+    }
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,239 @@
+"""AdaptiveWindowAttention on the GPU against the CPU oracle.
+
+Inputs are seeded N(0,1) activations (rounded to bf16 where the device path
+reads bf16, with the oracle consuming the same rounded values) and norm
+weights 1+N(0,0.02) ("peaky", a real softmax) or N(0,0.02) ("literal").
+Bar: max-abs <= 2e-2 and cosine >= 0.9999 against the fp32 oracle; window
+tables bit-exact.  The reference CPU forward restated by the oracle is
+src/seedvr2/adaptive_window_attention.cpp:764-978."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from common import (COSINE_TOL, MAX_ABS_TOL, Layer, assert_close, awa_param_string,
+                    make_awa_inputs, oracle_awa)
+from seedvr2_ncnn_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def torch_mod():
+    import torch
+    assert capi.device_count() >= 1, "no gfx950 device visible to libseedvr2_hip"
+    return torch
+
+
+def _run_capi(case, heads, d, target, shifted, pairs, shapes, text_lengths, bf16_in, out_dtype,
+              official=False, split=False, eps=1e-5):
+    torch = torch_mod()
+    inner = heads * d
+    dt = torch.bfloat16 if bf16_in else torch.float32
+    v = torch.from_numpy(case["video"]).to("cuda").to(dt)
+    t = torch.from_numpy(case["text"]).to("cuda").to(dt)
+    if split:
+        vq, vk, vv = (v[:, i * inner:(i + 1) * inner].contiguous() for i in range(3))
+        tq, tk, tv = (t[:, i * inner:(i + 1) * inner].contiguous() for i in range(3))
+    else:
+        vq, vk, vv = (v[:, i * inner:(i + 1) * inner] for i in range(3))
+        tq, tk, tv = (t[:, i * inner:(i + 1) * inner] for i in range(3))
+    norms = torch.from_numpy(case["norms"]).cuda()
+    freqs = torch.from_numpy(case["freqs"]).cuda()
+    cfg = capi.awa_config(heads, d, target, shifted, eps, pairs, official_bf16=official)
+    with capi.AwaPlan(cfg, shapes, text_lengths) as plan:
+        ov, ot = capi.awa_forward(plan, norms, freqs, vq, vk, vv, tq, tk, tv, out_dtype=out_dtype)
+        torch.cuda.synchronize()
+    return ov.float().cpu().numpy(), ot.float().cpu().numpy()
+
+
+# ---- window tables -------------------------------------------------------------------
+
+TABLE_CASES = [
+    ([(1, 32, 32)], (1, 8, 8)), ([(1, 64, 64)], (4, 3, 3)), ([(6, 45, 80)], (4, 3, 3)),
+    ([(3, 17, 29), (1, 8, 8), (7, 45, 80)], (4, 3, 3)), ([(2, 5, 3)], (2, 5, 2)),
+    ([(21, 90, 160)], (4, 3, 3)),
+]
+
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_device_window_tables_bit_exact(shifted):
+    torch = torch_mod()
+    for shapes, target in TABLE_CASES:
+        p = oracle.plan(shapes, target, shifted)
+        cfg = capi.awa_config(8, 64, target, shifted, 1e-5, 10)
+        with capi.AwaPlan(cfg, shapes, [7] * len(shapes)) as plan:
+            idx, inv, pos = plan.tables()
+            torch.cuda.synchronize()
+            wins, counts = plan.windows()
+        np.testing.assert_array_equal(np.asarray(wins, np.int32).reshape(-1, 9), p.windows)
+        np.testing.assert_array_equal(counts, p.sample_window_count)
+        np.testing.assert_array_equal(idx.cpu().numpy(), p.video_indices)
+        np.testing.assert_array_equal(inv.cpu().numpy(), p.inverse_video_indices)
+        np.testing.assert_array_equal(pos.cpu().numpy(), p.local_positions)
+
+
+# ---- committed fixture ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_tiny_fixture(shifted):
+    f = np.load(os.path.join(GOLDEN, "awa_tiny.npz"))
+    heads, d, pairs, *target = [int(x) for x in f["config"]]
+    shapes = [tuple(int(x) for x in s) for s in f["video_shapes"]]
+    tl = [int(x) for x in f["text_lengths"]]
+    case = dict(video=f["video"], text=f["text"], norms=f["norms"], freqs=f["freqs"])
+    import torch
+    ov, ot = _run_capi(case, heads, d, target, shifted, pairs, shapes, tl, False, torch.float32)
+    assert_close(ov, f[f"out_video_{shifted}"], "video")
+    assert_close(ot, f[f"out_text_{shifted}"], "text")
+
+
+# ---- single-layer configuration on the ncnn surface, fp32 host blobs ---------------
+
+def test_layer_grid_32x32_dim512_8x64_fp32_host_blobs():
+    """1x32x32 grid, D=512, 8 heads x 64, target (1,8,8): 16 windows of 8x8,
+    unshifted, fp32 host blobs through the ncnn-surface layer."""
+    torch_mod()
+    shapes, tl = [(1, 32, 32)], [64]
+    heads, d, pairs, target = 8, 64, 10, (1, 8, 8)
+    case = make_awa_inputs(101, shapes, tl, heads, d, pairs, peaky=False)
+    layer = Layer("AdaptiveWindowAttention", awa_param_string(heads, d, target, 0, 1e-5, pairs),
+                  [case["norms"][i] for i in range(4)] + [case["freqs"]])
+    assert layer.create_code == 0 and layer.create_pipeline() == 0
+    inner = heads * d
+    blobs = [case["video"], case["text"], np.asarray(shapes[0], np.float32), np.asarray(tl, np.float32)]
+    outs = [((1024, inner), np.float32), ((64, inner), np.float32)]
+    code, (ov, ot) = layer.forward(blobs, outs)
+    assert code == 0
+    rv, rt = oracle_awa(case, heads, d, target, 0, 1e-5, pairs, shapes, tl)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_layer_split_form_int32_shapes_peaky(shifted):
+    torch_mod()
+    shapes, tl = [(2, 12, 20), (1, 9, 7)], [5, 70]
+    heads, d, pairs, target = 2, 128, 21, (4, 3, 3)
+    case = make_awa_inputs(202 + shifted, shapes, tl, heads, d, pairs)
+    inner = heads * d
+    layer = Layer("AdaptiveWindowAttention",
+                  awa_param_string(heads, d, target, shifted, 1e-5, pairs, int32_shapes=True),
+                  [case["norms"][i] for i in range(4)] + [case["freqs"]])
+    assert layer.create_code == 0
+    v, t = case["video"], case["text"]
+    blobs = [v[:, :inner], v[:, inner:2 * inner], v[:, 2 * inner:],
+             t[:, :inner], t[:, inner:2 * inner], t[:, 2 * inner:],
+             np.asarray(shapes, np.int32), np.asarray(tl, np.int32)]
+    lv = sum(a * b * c for a, b, c in shapes)
+    code, (ov, ot) = layer.forward(blobs, [((lv, inner), np.float32), ((sum(tl), inner), np.float32)])
+    assert code == 0
+    rv, rt = oracle_awa(case, heads, d, target, shifted, 1e-5, pairs, shapes, tl)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+
+
+def test_layer_device_blobs_bf16_zero_copy():
+    """Device bf16 blobs (HipDeviceAllocator) run zero-copy and return bf16
+    device blobs; shapes come from the runtime state (no shape blobs)."""
+    torch = torch_mod()
+    shapes, tl = [(2, 16, 16)], [64]
+    heads, d, pairs, target = 4, 128, 21, (4, 3, 3)
+    case = make_awa_inputs(303, shapes, tl, heads, d, pairs, bf16=True)
+    inner = heads * d
+    layer = Layer("AdaptiveWindowAttention", awa_param_string(heads, d, target, 1, 1e-5, pairs),
+                  [case["norms"][i] for i in range(4)] + [case["freqs"]])
+    layer.set_state(shapes, tl)
+    v = torch.from_numpy(case["video"]).cuda().to(torch.bfloat16)
+    t = torch.from_numpy(case["text"]).cuda().to(torch.bfloat16)
+    code, (ov, ot) = layer.forward([v, t, None, None],
+                                   [((512, inner), torch.bfloat16), ((64, inner), torch.bfloat16)],
+                                   device_out=True)
+    assert code == 0
+    rv, rt = oracle_awa(case, heads, d, target, 1, 1e-5, pairs, shapes, tl)
+    assert_close(ov.float().cpu().numpy(), rv, "video")
+    assert_close(ot.float().cpu().numpy(), rt, "text")
+
+
+# ---- SeedVR2-3B shapes through the C-ABI, bf16 -------------------------------------------
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_image_grid_64x64_dim2560(shifted):
+    """One 1024x1024 image: 1x64x64 tokens, hidden 2560, 20 heads x 128."""
+    import torch
+    shapes, tl = [(1, 64, 64)], [64]
+    case = make_awa_inputs(404 + shifted, shapes, tl, 20, 128, 21, bf16=True)
+    rv, rt = oracle_awa(case, 20, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl)
+    for out_dtype in (torch.float32, torch.bfloat16):
+        ov, ot = _run_capi(case, 20, 128, (4, 3, 3), shifted, 21, shapes, tl, True, out_dtype)
+        assert_close(ov, rv, f"video {out_dtype}")
+        assert_close(ot, rt, f"text {out_dtype}")
+
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_video_grid_6x45x80_dim2560(shifted):
+    """21 frames at 1280x720: 6x45x80 = 21,600 tokens, ragged shifted windows."""
+    import torch
+    shapes, tl = [(6, 45, 80)], [64]
+    case = make_awa_inputs(505 + shifted, shapes, tl, 20, 128, 21, bf16=True)
+    ov, ot = _run_capi(case, 20, 128, (4, 3, 3), shifted, 21, shapes, tl, True, torch.bfloat16)
+    rv, rt = oracle_awa(case, 20, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl, fast=True)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+
+
+# ---- variants ------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("official", [False, True])
+def test_official_bf16_attention(official):
+    import torch
+    shapes, tl = [(3, 10, 14)], [9]
+    heads, d, pairs = 3, 128, 21
+    case = make_awa_inputs(606, shapes, tl, heads, d, pairs, bf16=True)
+    ov, ot = _run_capi(case, heads, d, (4, 3, 3), 1, pairs, shapes, tl, True, torch.float32,
+                       official=official)
+    rv, rt = oracle_awa(case, heads, d, (4, 3, 3), 1, 1e-5, pairs, shapes, tl, official_bf16=official)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+    if official:
+        # the context is rounded to bf16 before the scatter, as the reference does
+        assert np.array_equal(ov.view(np.uint32) & 0xFFFF, np.zeros_like(ov.view(np.uint32)))
+
+
+def test_literal_weights_and_fp32_inputs_split():
+    import torch
+    shapes, tl = [(4, 20, 33)], [64]
+    heads, d, pairs = 4, 128, 21
+    case = make_awa_inputs(707, shapes, tl, heads, d, pairs, peaky=False)
+    ov, ot = _run_capi(case, heads, d, (4, 3, 3), 0, pairs, shapes, tl, False, torch.float32, split=True)
+    rv, rt = oracle_awa(case, heads, d, (4, 3, 3), 0, 1e-5, pairs, shapes, tl)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+
+
+@pytest.mark.parametrize("d,pairs", [(64, 10), (64, 0), (128, 0)])
+def test_head_dims_and_rope_widths(d, pairs):
+    import torch
+    shapes, tl = [(1, 13, 9), (2, 3, 5)], [1, 130]
+    heads = 3
+    case = make_awa_inputs(808 + d + pairs, shapes, tl, heads, d, pairs)
+    if pairs == 0:
+        case["freqs"] = np.zeros(1, np.float32)   # the C-ABI ignores it
+        ref_case = dict(case, freqs=np.zeros(1, np.float32))
+    else:
+        ref_case = case
+    ov, ot = _run_capi(case, heads, d, (2, 2, 2), 1, pairs, shapes, tl, True, torch.float32)
+    rv, rt = oracle_awa(ref_case, heads, d, (2, 2, 2), 1, 1e-5, pairs, shapes, tl)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+
+
+def test_repeated_forward_is_deterministic():
+    import torch
+    shapes, tl = [(2, 30, 40)], [64]
+    case = make_awa_inputs(909, shapes, tl, 4, 128, 21, bf16=True)
+    a = _run_capi(case, 4, 128, (4, 3, 3), 1, 21, shapes, tl, True, torch.float32)
+    b = _run_capi(case, 4, 128, (4, 3, 3), 1, 21, shapes, tl, True, torch.float32)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])

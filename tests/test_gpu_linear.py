@@ -1,0 +1,133 @@
+"""SharedLinear on the GPU against the CPU oracle (src/seedvr2/shared_linear.cpp:83-96):
+y = act(x W^T + b) for the video and text streams in one grouped launch.
+
+The device computes in bf16 with fp32 accumulation: W is held in bf16, fp32
+activations are rounded to bf16 as they are staged.  Two comparisons per
+case: against the fp32 oracle on the unrounded inputs with the path's bar
+(max-abs <= 2e-2, cosine >= 0.9999), and against the oracle on the
+bf16-rounded inputs with a tight bound that isolates the kernel's own
+arithmetic (accumulation order only)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from common import Layer, assert_close, bf16_round
+from seedvr2_ncnn_amd import capi
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+THREADS = min(16, os.cpu_count() or 1)
+
+
+def _gpu_linear(xv, xt, w, b, act, x_bf16, y_bf16):
+    import torch
+    assert capi.device_count() >= 1
+    xdt = torch.bfloat16 if x_bf16 else torch.float32
+    ydt = torch.bfloat16 if y_bf16 else torch.float32
+    tv = torch.from_numpy(xv).cuda().to(xdt)
+    tt = torch.from_numpy(xt).cuda().to(xdt) if xt is not None else None
+    wb = capi.cast_f32_to_bf16(torch.from_numpy(w).cuda())
+    tb = torch.from_numpy(b).cuda() if b is not None else None
+    yv, yt = capi.shared_linear(tv, tt, wb, tb, act, out_dtype=ydt)
+    torch.cuda.synchronize()
+    return yv.float().cpu().numpy(), (yt.float().cpu().numpy() if yt is not None else None)
+
+
+def _tight(got, xr, wr, b, act, rows=None):
+    ref = oracle.linear(xr, wr, b, act, rows=rows, threads=THREADS)
+    scale = max(1.0, float(np.max(np.abs(ref))))
+    err = float(np.max(np.abs(got - ref)))
+    return err / scale
+
+
+SHAPES = [(1, 0, 8, 16), (37, 5, 24, 40), (130, 64, 72, 136), (257, 3, 2560, 96), (64, 64, 128, 2560)]
+
+
+@pytest.mark.parametrize("mv,mt,k,n", SHAPES)
+@pytest.mark.parametrize("act", [0, 1])
+def test_small_shapes(mv, mt, k, n, act):
+    g = np.random.default_rng(mv * 7 + k + act)
+    xv = g.standard_normal((mv, k)).astype(np.float32)
+    xt = g.standard_normal((mt, k)).astype(np.float32) if mt else None
+    w = (0.02 * g.standard_normal((n, k))).astype(np.float32)
+    b = (0.02 * g.standard_normal(n)).astype(np.float32) if act == 0 or k % 16 else None
+    for x_bf16, y_bf16 in ((False, False), (True, True), (True, False)):
+        yv, yt = _gpu_linear(xv, xt, w, b, act, x_bf16, y_bf16)
+        assert_close(yv, oracle.linear(xv, w, b, act, threads=THREADS), "video")
+        # kernel arithmetic: same bf16 operands, fp32 accumulation
+        tol = 1e-2 if y_bf16 else 2e-4
+        assert _tight(yv, bf16_round(xv), bf16_round(w), b, act) < tol
+        if mt:
+            assert_close(yt, oracle.linear(xt, w, b, act, threads=THREADS), "text")
+
+
+def test_tiny_fixture():
+    f = np.load(os.path.join(GOLDEN, "linear_tiny.npz"))
+    yv, yt = _gpu_linear(f["x_video"], f["x_text"], f["weight"], f["bias"], 1, False, False)
+    assert_close(yv, f["y_video"], "video")
+    assert_close(yt, f["y_text"], "text")
+
+
+# SeedVR2-3B block GEMMs at the 720p video shape: 21,600 video + 64 text tokens.
+VIDEO_GEMMS = [("qkv", 2560, 7680, 0), ("out", 2560, 2560, 0), ("mlp_up_gelu", 2560, 10240, 1),
+               ("mlp_down", 10240, 2560, 0)]
+
+
+@pytest.mark.parametrize("name,k,n,act", VIDEO_GEMMS)
+def test_video_shape_gemms(name, k, n, act):
+    import torch
+    g = np.random.default_rng(sum(map(ord, name)))
+    mv, mt = 21600, 64
+    xv = g.standard_normal((mv, k), dtype=np.float32)
+    xt = g.standard_normal((mt, k), dtype=np.float32)
+    w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
+    b = (0.02 * g.standard_normal(n)).astype(np.float32)
+    yv, yt = _gpu_linear(bf16_round(xv), bf16_round(xt), w, b, act, True, True)
+    rows = np.concatenate([np.arange(0, 3), np.arange(127, 131), g.integers(0, mv, 40),
+                           np.arange(mv - 5, mv)]).astype(np.int32)
+    assert_close(yv[rows], oracle.linear(xv, w, b, act, rows=rows, threads=THREADS), "video rows")
+    assert_close(yt, oracle.linear(xt, w, b, act, threads=THREADS), "text")
+    # whole output against torch (hipBLASLt) on the same bf16 operands
+    ref = (torch.from_numpy(bf16_round(xv)).cuda() @ torch.from_numpy(bf16_round(w)).cuda().T
+           + torch.from_numpy(b).cuda())
+    if act:
+        ref = torch.nn.functional.gelu(ref)
+    d = (torch.from_numpy(yv).cuda() - ref).abs().max().item()
+    assert d < 2e-2, d
+
+
+def test_layer_host_fp32_and_device_bf16():
+    import torch
+    g = np.random.default_rng(5)
+    k, n, mv, mt = 256, 384, 300, 64
+    w = (0.02 * g.standard_normal((n, k))).astype(np.float32)
+    b = (0.02 * g.standard_normal(n)).astype(np.float32)
+    xv = g.standard_normal((mv, k)).astype(np.float32)
+    xt = g.standard_normal((mt, k)).astype(np.float32)
+    layer = Layer("SharedLinear", f"0={n} 1={k} 2=1", [w, b])
+    assert layer.create_code == 0 and layer.create_pipeline() == 0
+    code, (yv, yt) = layer.forward([xv, xt], [((mv, n), np.float32), ((mt, n), np.float32)])
+    assert code == 0
+    assert_close(yv, oracle.linear(xv, w, b), "host video")
+    assert_close(yt, oracle.linear(xt, w, b), "host text")
+    dv = torch.from_numpy(xv).cuda().to(torch.bfloat16)
+    dt = torch.from_numpy(xt).cuda().to(torch.bfloat16)
+    code, (yv, yt) = layer.forward([dv, dt], [((mv, n), torch.bfloat16), ((mt, n), torch.bfloat16)],
+                                   device_out=True)
+    assert code == 0
+    assert_close(yv.float().cpu().numpy(), oracle.linear(xv, w, b), "device video")
+    assert_close(yt.float().cpu().numpy(), oracle.linear(xt, w, b), "device text")
+
+
+def test_layer_gelu_activation_param():
+    g = np.random.default_rng(6)
+    k, n = 64, 96
+    w = (0.1 * g.standard_normal((n, k))).astype(np.float32)
+    layer = Layer("SharedLinear", f"0={n} 1={k} 2=0 3=1", [w])
+    xv = g.standard_normal((10, k)).astype(np.float32)
+    xt = g.standard_normal((2, k)).astype(np.float32)
+    code, (yv, yt) = layer.forward([xv, xt], [((10, n), np.float32), ((2, n), np.float32)])
+    assert code == 0
+    assert_close(yv, oracle.linear(xv, w, None, 1), "video")
