@@ -27,8 +27,18 @@ __device__ __forceinline__ uint4 load_chunk(const float* p) {
     return pack8_bf16(h);
 }
 
-__device__ __forceinline__ float gelu_erf(float x) {
-    return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+// erf-GELU, 0.5 x (1 + erf(x / sqrt 2)), with erf from Abramowitz & Stegun
+// 7.1.26: 1 - erf(z) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-z^2),
+// t = 1 / (1 + p z), z >= 0, |error| <= 1.5e-7.  The negative branch uses
+// the complement directly, so small outputs keep their relative accuracy.
+__device__ __forceinline__ float gelu(float x) {
+    const float z = fabsf(x) * 0.70710678118654752f;
+    const float t = __builtin_amdgcn_rcpf(1.f + 0.3275911f * z);
+    const float poly =
+        t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f +
+                                                                          t * 1.061405429f))));
+    const float c = poly * __expf(-z * z);   // 1 - erf(|x| / sqrt 2)
+    return x >= 0.f ? x * (1.f - 0.5f * c) : 0.5f * x * c;
 }
 
 }  // namespace
@@ -161,9 +171,231 @@ __global__ __launch_bounds__(256, 2) void shared_linear_kernel(
                 const int row = row0 + wm * 64 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
                 if (row >= m) continue;
                 float v = acc[i][j][r] + b;
-                if (ACT == S2_ACT_GELU) v = gelu_erf(v);
+                if (ACT == S2_ACT_GELU) v = gelu(v);
                 if (Y_BF16)
                     ((uint16_t*)y)[(long)row * n + col] = f32_to_bf16(v);
+                else
+                    ((float*)y)[(long)row * n + col] = v;
+            }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Large-tile path for bf16 activations with k % 32 == 0.
+//
+// Block tile 256x256, four waves in a 2x2 grid of 128x128 wave tiles (4x4
+// MFMA 32x32x16 accumulators = 256 fp32 per lane, held in AGPRs): per 16-k
+// step a wave issues 8 LDS reads for 16 MFMAs.  The operands stream through
+// a ring of four 32-k LDS stages (32 KB each) filled by buffer_load_dwordx4
+// ... lds (global -> LDS, no VGPR staging), three stages ahead of the MFMAs.
+// The buffer descriptors bound each tile to its valid rows, so ragged m and
+// n read zeros.  LDS rows are 64 bytes; 16-byte chunk c of row r is stored at
+// position c ^ (((r >> 1) ^ (r >> 3)) & 3), which spreads the rows one
+// ds_read_b128 phase touches over distinct banks.  The bf16 epilogue adds the
+// bias and activation in fp32, converts with v_cvt_pk_bf16_f32, assembles the
+// 256x256 tile in LDS and writes it as 16-byte row chunks.
+namespace {
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    i32x4 r;
+    r.x = (int)(uint32_t)a;
+    r.y = (int)(uint32_t)(a >> 32);   // stride 0: raw buffer
+    r.z = (int)bytes;                 // num_records: reads past it return 0
+    r.w = 0x00020000;
+    return r;
+}
+
+// One buffer_load_dwordx4 with the lds modifier: lane i's 16 bytes land at
+// LDS address lds_addr + 16*i.  Issued through asm so that the compiler does
+// not order every later LDS read behind it; the main loop waits for the
+// stage it reads with s_waitcnt vmcnt and a barrier.  M0 is written only
+// here in this file.
+__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset,
+                                          uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
+// Waits until at most `later` stages of DMA loads (8 instructions each per
+// wave) are still in flight.
+__device__ __forceinline__ void wait_stage(int later) {
+    if (later >= 2)
+        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (later == 1)
+        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+}  // namespace
+
+template <bool Y_BF16, int ACT>
+__global__ __launch_bounds__(256, 1) void shared_linear_256_kernel(
+    const uint16_t* __restrict__ x0, int m0, const uint16_t* __restrict__ x1, int m1,
+    const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
+    void* __restrict__ y0, void* __restrict__ y1, int mt0, int mtiles, int ntiles) {
+    constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
+    constexpr int TB = BM * BK * 2;   // 16 KB per operand per stage
+    constexpr int SB = 2 * TB;        // 32 KB per stage
+    constexpr int EP = BN * 2 + 16;   // epilogue LDS row pitch (bytes)
+    constexpr int LDS_BYTES = STAGES * SB > BM * EP ? STAGES * SB : BM * EP;
+    constexpr int GROUP = 8;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int group_size = GROUP * ntiles;
+    const int first_m = (lid / group_size) * GROUP;
+    const int gm = min(mtiles - first_m, GROUP);
+    const int mt = first_m + (lid % group_size) % gm;
+    const int nt = (lid % group_size) / gm;
+    const uint16_t* x;
+    int m, row0;
+    void* y;
+    if (mt < mt0) {
+        x = x0; m = m0; y = y0; row0 = mt * BM;
+    } else {
+        x = x1; m = m1; y = y1; row0 = (mt - mt0) * BM;
+    }
+    const int col0 = nt * BN;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int wm = wave >> 1;
+    const int wn = wave & 1;
+
+    const i32x4 ra = buffer_rsrc(x + (long)row0 * k, (uint32_t)(min(m - row0, BM) * k * 2));
+    const i32x4 rb = buffer_rsrc(wgt + (long)col0 * k, (uint32_t)(min(n - col0, BN) * k * 2));
+    // DMA instruction j of a wave fills the 16 LDS rows (4 wave + j) * 16 ..:
+    // lane i takes row +i/4 and the logical chunk stored at position i%4.
+    const int lrow = lane >> 2;
+    uint32_t voff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = wave * 64 + j * 16 + lrow;
+        const int chunk = (lane & 3) ^ (((row >> 1) ^ (row >> 3)) & 3);
+        voff[j] = (uint32_t)(row * k * 2 + chunk * 16);
+    }
+    const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+    auto issue = [&](int stage, int kt) {
+        const uint32_t soff = (uint32_t)(kt * BK * 2);
+        const uint32_t st = lds_base + stage * SB + wave * 4 * 1024;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            lds_dma16(ra, __builtin_amdgcn_readfirstlane(st + j * 1024), voff[j], soff);
+            lds_dma16(rb, __builtin_amdgcn_readfirstlane(st + TB + j * 1024), voff[j], soff);
+        }
+    };
+
+    f32x16 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // fragment rows differ from l32 by multiples of 32, so their swizzle
+    // depends on l32 only
+    const int swz = ((l32 >> 1) ^ (l32 >> 3)) & 3;
+    bf16x8 a[2][4], b[2][4];
+    auto frag = [&](const uint8_t* st, int kk, int slot) {
+        const int pc = ((2 * kk + g) ^ swz) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            a[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * 64 + pc));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            b[slot][j] = as_bf16x8(*(const uint4*)(st + TB + (wn * 128 + 32 * j + l32) * 64 + pc));
+    };
+    auto mma = [&](int slot) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[slot][i], b[slot][j], acc[i][j],
+                                                                   0, 0, 0);
+    };
+
+    const int nk = k / BK;
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; ++s)
+        if (s < nk) issue(s, s);
+#pragma unroll 1
+    for (int kt = 0; kt < nk; ++kt) {
+        wait_stage(min(nk - 1, kt + STAGES - 2) - kt);
+        __syncthreads();   // stage kt visible to all waves; stage kt-1 no longer read
+        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
+        const uint8_t* st = lds + (kt % STAGES) * SB;
+        frag(st, 0, 0);
+        frag(st, 1, 1);
+        mma(0);
+        mma(1);
+        // issue order: step 0's 8 reads, then step 1's reads interleaved with
+        // step 0's first MFMAs, then the remaining MFMAs
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);
+    }
+
+    if (Y_BF16 && (n & 7) == 0) {
+        __syncthreads();   // every wave is done reading the last stage
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int cl = wn * 128 + 32 * j + l32;
+            const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    float v = acc[i][j][r] + bv;
+                    if (ACT == S2_ACT_GELU) v = gelu(v);
+                    const int rl = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                    *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
+                }
+        }
+        __syncthreads();
+        // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows t/32 + 8c
+#pragma unroll 4
+        for (int c = 0; c < 32; ++c) {
+            const int idx = c * 256 + tid;
+            const int rl = idx >> 5;
+            const int ch = idx & 31;
+            const int row = row0 + rl;
+            const int col = col0 + ch * 8;
+            if (row < m && col < n)
+                *(uint4*)((uint16_t*)y + (long)row * n + col) =
+                    *(const uint4*)(lds + rl * EP + ch * 16);
+        }
+        return;
+    }
+    // fp32 output (or a ragged n): direct stores, register r of a 32x32
+    // accumulator is row 8(r/4) + 4g + r%4, column l32
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int col = col0 + wn * 128 + 32 * j + l32;
+        if (col >= n) continue;
+        const float bv = bias ? bias[col] : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int row = row0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                if (row >= m) continue;
+                float v = acc[i][j][r] + bv;
+                if (ACT == S2_ACT_GELU) v = gelu(v);
+                if (Y_BF16)
+                    ((__bf16*)y)[(long)row * n + col] = (__bf16)v;
                 else
                     ((float*)y)[(long)row * n + col] = v;
             }
@@ -198,6 +430,19 @@ template <typename TX, bool Y_BF16, int ACT>
 static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, const uint16_t* w,
                               const float* bias, int n, int k, void* y0, void* y1,
                               hipStream_t stream) {
+    if (sizeof(TX) == 2 && k % 32 == 0 &&
+        (long)256 * k * 2 <= 0x7fffffffL) {   // buffer offsets are 32-bit
+        const int mt0 = (m0 + 255) / 256;
+        const int mt1 = (m1 + 255) / 256;
+        const int ntiles = (n + 255) / 256;
+        const int mtiles = mt0 + mt1;
+        const long blocks = (long)mtiles * ntiles;
+        if (blocks == 0) return hipSuccess;
+        shared_linear_256_kernel<Y_BF16, ACT><<<(unsigned)blocks, 256, 0, stream>>>(
+            (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mt0, mtiles,
+            ntiles);
+        return hipGetLastError();
+    }
     const int mt0 = (m0 + 127) / 128;
     const int mt1 = (m1 + 127) / 128;
     const int ntiles = (n + 127) / 128;

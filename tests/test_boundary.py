@@ -193,3 +193,18 @@ def test_param_text_parser_accepts_ncnn_fields():
     assert layer.create_code == 0
     bad = Layer("SharedLinear", "0=x")
     assert bad.create_code == -1
+
+
+def test_awa_one_dim_text_length_blob_reads_column_zero_for_every_sample():
+    # The reference reads text_lengths[sample] = read_shape_value(blob, sample, 0)
+    # (adaptive_window_attention.cpp:812, :475-485): a 1-D blob of width B
+    # answers column 0 for every sample, so batches need a [B][1] blob.
+    layer = _awa()
+    video = np.zeros((16 + 4, 3 * INNER), np.float32)
+    text = np.zeros((3 + 2, 3 * INNER), np.float32)
+    shapes = np.asarray([[1, 4, 4], [1, 2, 2]], np.float32)
+    outs = [((20, INNER), np.float32), ((5, INNER), np.float32)]
+    one_dim = layer.forward([video, text, shapes, np.asarray([3, 2], np.float32)], outs)[0]
+    assert one_dim == -1          # lengths read as (3, 3): 6 text rows expected, 5 given
+    two_dim = layer.forward([video, text, shapes, np.asarray([[3], [2]], np.float32)], outs)[0]
+    assert two_dim in (0, capi.S2_ERR_DEVICE)

@@ -126,7 +126,7 @@ def test_layer_split_form_int32_shapes_peaky(shifted):
     v, t = case["video"], case["text"]
     blobs = [v[:, :inner], v[:, inner:2 * inner], v[:, 2 * inner:],
              t[:, :inner], t[:, inner:2 * inner], t[:, 2 * inner:],
-             np.asarray(shapes, np.int32), np.asarray(tl, np.int32)]
+             np.asarray(shapes, np.int32), np.asarray(tl, np.int32).reshape(-1, 1)]
     lv = sum(a * b * c for a, b, c in shapes)
     code, (ov, ot) = layer.forward(blobs, [((lv, inner), np.float32), ((sum(tl), inner), np.float32)])
     assert code == 0

@@ -84,18 +84,24 @@ def test_video_shape_gemms(name, k, n, act):
     xt = g.standard_normal((mt, k), dtype=np.float32)
     w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
     b = (0.02 * g.standard_normal(n)).astype(np.float32)
-    yv, yt = _gpu_linear(bf16_round(xv), bf16_round(xt), w, b, act, True, True)
+    xv, xt = bf16_round(xv), bf16_round(xt)
+    # fp32 output carries the parity bar; the bf16 output must be the
+    # round-to-nearest-even of that same fp32 result (one rounding).
+    yv, yt = _gpu_linear(xv, xt, w, b, act, True, False)
+    yv16, yt16 = _gpu_linear(xv, xt, w, b, act, True, True)
+    np.testing.assert_array_equal(yv16, bf16_round(yv))
+    np.testing.assert_array_equal(yt16, bf16_round(yt))
     rows = np.concatenate([np.arange(0, 3), np.arange(127, 131), g.integers(0, mv, 40),
                            np.arange(mv - 5, mv)]).astype(np.int32)
     assert_close(yv[rows], oracle.linear(xv, w, b, act, rows=rows, threads=THREADS), "video rows")
     assert_close(yt, oracle.linear(xt, w, b, act, threads=THREADS), "text")
     # whole output against torch (hipBLASLt) on the same bf16 operands
-    ref = (torch.from_numpy(bf16_round(xv)).cuda() @ torch.from_numpy(bf16_round(w)).cuda().T
+    ref = (torch.from_numpy(xv).cuda() @ torch.from_numpy(bf16_round(w)).cuda().T
            + torch.from_numpy(b).cuda())
     if act:
         ref = torch.nn.functional.gelu(ref)
     d = (torch.from_numpy(yv).cuda() - ref).abs().max().item()
-    assert d < 2e-2, d
+    assert d < 2e-3, d
 
 
 def test_layer_host_fp32_and_device_bf16():
