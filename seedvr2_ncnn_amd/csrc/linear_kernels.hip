@@ -181,19 +181,21 @@ __global__ __launch_bounds__(256, 2) void shared_linear_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Large-tile path for bf16 activations with k % 32 == 0.
+// Large-tile path for bf16 activations with k % 64 == 0.
 //
-// Block tile 256x256, four waves in a 2x2 grid of 128x128 wave tiles (4x4
-// MFMA 32x32x16 accumulators = 256 fp32 per lane, held in AGPRs): per 16-k
-// step a wave issues 8 LDS reads for 16 MFMAs.  The operands stream through
-// a ring of four 32-k LDS stages (32 KB each) filled by buffer_load_dwordx4
-// ... lds (global -> LDS, no VGPR staging), three stages ahead of the MFMAs.
-// The buffer descriptors bound each tile to its valid rows, so ragged m and
-// n read zeros.  LDS rows are 64 bytes; 16-byte chunk c of row r is stored at
-// position c ^ (((r >> 1) ^ (r >> 3)) & 3), which spreads the rows one
-// ds_read_b128 phase touches over distinct banks.  The bf16 epilogue adds the
-// bias and activation in fp32, converts with v_cvt_pk_bf16_f32, assembles the
-// 256x256 tile in LDS and writes it as 16-byte row chunks.
+// Block tile 256x256 with eight waves, two per SIMD, in a 2 (m) x 4 (n) grid
+// of 128x64 wave tiles (4x2 MFMA 32x32x16 accumulators = 128 fp32 per lane):
+// while one wave of a SIMD waits on LDS or the stage barrier the other keeps
+// the matrix core busy.  Per 16-k step a wave issues 6 LDS reads for 8 MFMAs.
+// The operands stream through two 64-k LDS stages (64 KB each) filled by
+// buffer_load_dwordx4 ... lds (global -> LDS, no VGPR staging) one stage
+// ahead of the MFMAs.  The buffer descriptors bound each tile to its valid
+// rows, so ragged m and n read zeros.  LDS rows are 128 bytes; 16-byte chunk
+// c of row r is stored at position c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7), so
+// the rows one ds_read_b128 phase touches land on distinct banks.  The bf16
+// epilogue adds the bias and activation in fp32, converts with
+// v_cvt_pk_bf16_f32, assembles the 256x256 tile in LDS and writes it out as
+// 16-byte row chunks.
 namespace {
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
@@ -221,27 +223,19 @@ __device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t lds_addr, uint32_
                  : "memory", "m0");
 }
 
-// Waits until at most `later` stages of DMA loads (8 instructions each per
-// wave) are still in flight.
-__device__ __forceinline__ void wait_stage(int later) {
-    if (later >= 2)
-        asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
-    else if (later == 1)
-        asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
-    else
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-}
+__device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
 }  // namespace
 
 template <bool Y_BF16, int ACT>
-__global__ __launch_bounds__(256, 1) void shared_linear_256_kernel(
+__global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const uint16_t* __restrict__ x0, int m0, const uint16_t* __restrict__ x1, int m1,
     const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
     void* __restrict__ y0, void* __restrict__ y1, int mt0, int mtiles, int ntiles) {
-    constexpr int BM = 256, BN = 256, BK = 32, STAGES = 4;
-    constexpr int TB = BM * BK * 2;   // 16 KB per operand per stage
-    constexpr int SB = 2 * TB;        // 32 KB per stage
+    constexpr int BM = 256, BN = 256, BK = 64, STAGES = 2;
+    constexpr int TB = BM * BK * 2;   // 32 KB per operand per stage
+    constexpr int SB = 2 * TB;        // 64 KB per stage
+    constexpr int RB = BK * 2;        // LDS row bytes
     constexpr int EP = BN * 2 + 16;   // epilogue LDS row pitch (bytes)
     constexpr int LDS_BYTES = STAGES * SB > BM * EP ? STAGES * SB : BM * EP;
     constexpr int GROUP = 8;
@@ -267,20 +261,19 @@ __global__ __launch_bounds__(256, 1) void shared_linear_256_kernel(
     const int wave = tid >> 6;
     const int l32 = lane & 31;
     const int g = lane >> 5;
-    const int wm = wave >> 1;
-    const int wn = wave & 1;
+    const int wm = wave >> 2;
+    const int wn = wave & 3;
 
     const i32x4 ra = buffer_rsrc(x + (long)row0 * k, (uint32_t)(min(m - row0, BM) * k * 2));
     const i32x4 rb = buffer_rsrc(wgt + (long)col0 * k, (uint32_t)(min(n - col0, BN) * k * 2));
-    // DMA instruction j of a wave fills the 16 LDS rows (4 wave + j) * 16 ..:
-    // lane i takes row +i/4 and the logical chunk stored at position i%4.
-    const int lrow = lane >> 2;
+    // Wave w fills LDS rows 32w .. 32w+31 of each operand with 4 DMA
+    // instructions of 8 rows: lane i takes row +i/8 and the logical chunk
+    // stored at position i%8.
     uint32_t voff[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int row = wave * 64 + j * 16 + lrow;
-        const int chunk = (lane & 3) ^ (((row >> 1) ^ (row >> 3)) & 3);
-        voff[j] = (uint32_t)(row * k * 2 + chunk * 16);
+        const int row = wave * 32 + j * 8 + (lane >> 3);
+        voff[j] = (uint32_t)(row * k * 2 + (((lane & 7) ^ lds_swizzle(row)) * 16));
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
     auto issue = [&](int stage, int kt) {
@@ -293,66 +286,54 @@ __global__ __launch_bounds__(256, 1) void shared_linear_256_kernel(
         }
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // fragment rows differ from l32 by multiples of 32, so their swizzle
     // depends on l32 only
-    const int swz = ((l32 >> 1) ^ (l32 >> 3)) & 3;
-    bf16x8 a[2][4], b[2][4];
+    const int sw = lds_swizzle(l32);
+    bf16x8 a[2][4], b[2][2];
     auto frag = [&](const uint8_t* st, int kk, int slot) {
-        const int pc = ((2 * kk + g) ^ swz) * 16;
+        const int pc = ((2 * kk + g) ^ sw) * 16;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-            a[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * 64 + pc));
+            a[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * RB + pc));
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            b[slot][j] = as_bf16x8(*(const uint4*)(st + TB + (wn * 128 + 32 * j + l32) * 64 + pc));
-    };
-    auto mma = [&](int slot) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[slot][i], b[slot][j], acc[i][j],
-                                                                   0, 0, 0);
+        for (int j = 0; j < 2; ++j)
+            b[slot][j] = as_bf16x8(*(const uint4*)(st + TB + (wn * 64 + 32 * j + l32) * RB + pc));
     };
 
     const int nk = k / BK;
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; ++s)
-        if (s < nk) issue(s, s);
+    issue(0, 0);
 #pragma unroll 1
     for (int kt = 0; kt < nk; ++kt) {
-        wait_stage(min(nk - 1, kt + STAGES - 2) - kt);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();   // stage kt visible to all waves; stage kt-1 no longer read
-        if (kt + STAGES - 1 < nk) issue((kt + STAGES - 1) % STAGES, kt + STAGES - 1);
-        const uint8_t* st = lds + (kt % STAGES) * SB;
+        if (kt + 1 < nk) issue((kt + 1) & 1, kt + 1);
+        const uint8_t* st = lds + (kt & 1) * SB;
         frag(st, 0, 0);
-        frag(st, 1, 1);
-        mma(0);
-        mma(1);
-        // issue order: step 0's 8 reads, then step 1's reads interleaved with
-        // step 0's first MFMAs, then the remaining MFMAs
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            if (kk + 1 < BK / 16) frag(st, kk + 1, (kk + 1) & 1);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j],
+                                                                       acc[i][j], 0, 0, 0);
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);
     }
 
     if (Y_BF16 && (n & 7) == 0) {
         __syncthreads();   // every wave is done reading the last stage
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int cl = wn * 128 + 32 * j + l32;
+        for (int j = 0; j < 2; ++j) {
+            const int cl = wn * 64 + 32 * j + l32;
             const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
@@ -365,10 +346,10 @@ __global__ __launch_bounds__(256, 1) void shared_linear_256_kernel(
                 }
         }
         __syncthreads();
-        // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows t/32 + 8c
+        // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows t/32 + 16c
 #pragma unroll 4
-        for (int c = 0; c < 32; ++c) {
-            const int idx = c * 256 + tid;
+        for (int c = 0; c < 16; ++c) {
+            const int idx = c * 512 + tid;
             const int rl = idx >> 5;
             const int ch = idx & 31;
             const int row = row0 + rl;
@@ -382,8 +363,8 @@ __global__ __launch_bounds__(256, 1) void shared_linear_256_kernel(
     // fp32 output (or a ragged n): direct stores, register r of a 32x32
     // accumulator is row 8(r/4) + 4g + r%4, column l32
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int col = col0 + wn * 128 + 32 * j + l32;
+    for (int j = 0; j < 2; ++j) {
+        const int col = col0 + wn * 64 + 32 * j + l32;
         if (col >= n) continue;
         const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
@@ -430,7 +411,7 @@ template <typename TX, bool Y_BF16, int ACT>
 static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, const uint16_t* w,
                               const float* bias, int n, int k, void* y0, void* y1,
                               hipStream_t stream) {
-    if (sizeof(TX) == 2 && k % 32 == 0 &&
+    if (sizeof(TX) == 2 && k % 64 == 0 &&
         (long)256 * k * 2 <= 0x7fffffffL) {   // buffer offsets are 32-bit
         const int mt0 = (m0 + 255) / 256;
         const int mt1 = (m1 + 255) / 256;
@@ -438,7 +419,7 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
         const int mtiles = mt0 + mt1;
         const long blocks = (long)mtiles * ntiles;
         if (blocks == 0) return hipSuccess;
-        shared_linear_256_kernel<Y_BF16, ACT><<<(unsigned)blocks, 256, 0, stream>>>(
+        shared_linear_256_kernel<Y_BF16, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
             (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mt0, mtiles,
             ntiles);
         return hipGetLastError();
