@@ -81,7 +81,8 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
     const int rot_width = pairs * 6;
     const long head_rows = (long)head * seg_total + w.seg_off;
 
-#pragma unroll 1
+    // passes fully unrolled so every row's loads can be in flight together
+#pragma unroll
     for (int pass = 0; pass < CHUNK / RPP; ++pass) {
         const int rl = pass * RPP + tid / TPR;   // row within the chunk
         const int r = ch.row0 + rl;                 // row within the window sequence
@@ -189,29 +190,57 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
 // ---------------------------------------------------------------------------
 // Flash window attention.
 //
-// Four waves; wave j owns query rows q_row0 + 32j .. +31.  Each key tile of
-// 64 keys is staged in LDS (K rows and V^T rows, double buffered).  The
-// score tile is computed transposed, S^T = K Q^T, so that each lane owns one
-// query column; the probabilities then feed O^T += V^T P^T directly from the
-// accumulator registers.  For that the A-operand row R of the S^T MFMA loads
-// key pi(R) = R with bits 2 and 3 swapped: accumulator register i = 8s+j of
-// lane group g then holds key 16s + 8g + j, which is exactly the B-operand
-// slot 8g+j of the 16-key PV step s.
+// Four waves; wave j owns query rows q_row0 + 32j .. +31.  Keys stream in
+// tiles of 32 through a ring of three LDS stages, each holding the tile's K
+// rows and its V^T rows, filled by buffer_load_dwordx4 ... lds (global ->
+// LDS without VGPR staging) two tiles ahead.  At about 140 VGPRs three
+// workgroups share a CU, so three waves per SIMD hide the MFMA dependency
+// chains and the softmax VALU work of one another.
+//
+// The score tile is computed transposed, S^T = K Q^T, so that each lane owns
+// one query column; the probabilities then feed O^T += V^T P^T directly from
+// the accumulator registers.  For that the A-operand row R of the S^T MFMA
+// loads key pi(R) = R with bits 2 and 3 swapped: accumulator register
+// i = 8s+j of lane group g then holds key 16s + 8g + j, which is exactly the
+// B-operand slot 8g+j of the 16-key PV step s.
+//
+// Online softmax in the log2 domain with a lazily updated row max: the
+// running max only moves when a tile's max exceeds it by more than 8, so
+// un-normalised probabilities stay below 2^8 and the accumulator rescale is
+// skipped for the many tiles that do not raise any row max of the wave.
+// The result is the same softmax; only the reference point of the
+// exponentials changes.
+//
+// LDS swizzles (16-byte chunk c of row r stored at position c ^ f(r)) keep
+// the rows one ds_read_b128 phase reads on distinct banks:
+//   K rows (D*2 bytes):  f(r) = r & 15 for D = 128, (r ^ (r >> 3)) & 7 for D = 64
+//   V^T rows (64 bytes): f(r) = ((r >> 1) ^ (r >> 3)) & 3
 template <int D>
-__global__ __launch_bounds__(256, 2) void awa_attention_kernel(
+__device__ __forceinline__ int k_swizzle(int r) {
+    return D == 128 ? (r & 15) : ((r ^ (r >> 3)) & 7);
+}
+__device__ __forceinline__ int vt_swizzle(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+
+template <int D>
+__global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     const WinMeta* __restrict__ wins, const AttnItem* __restrict__ items, int slots_per_xcd,
     const uint16_t* __restrict__ q_in, const uint16_t* __restrict__ k_in,
     const uint16_t* __restrict__ vt_in, long seg_total, float scale_log2, int official_bf16,
     void* __restrict__ out_video, int out_bf16, int inner, float* __restrict__ text_partial) {
-    constexpr int KT = 64;            // keys per tile
-    constexpr int KP = D + 8;         // K tile LDS pitch (elements)
-    constexpr int VP = KT + 8;        // V^T tile LDS pitch
-    constexpr int NKK = D / 16;       // MFMA k-steps over the head dim
-    constexpr int NDT = D / 32;       // 32-channel output tiles
-    constexpr int K_CHUNKS = KT * D / 8 / 256;   // 16-byte loads per thread
-    constexpr int V_CHUNKS = D * KT / 8 / 256;
-    __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][KT * KP];
-    __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * VP];
+    constexpr int KT = 32;                  // keys per tile
+    constexpr int STAGES = 3;
+    constexpr int KB = KT * D * 2;          // K tile bytes
+    constexpr int VB = D * KT * 2;          // V^T tile bytes
+    constexpr int SB = KB + VB;             // stage bytes
+    constexpr int NKK = D / 16;             // MFMA k-steps over the head dim
+    constexpr int NDT = D / 32;             // 32-channel output tiles
+    constexpr int KCH = D / 8;              // 16-byte chunks per K row
+    constexpr int KRI = 1024 / (D * 2);     // K rows per DMA instruction
+    constexpr int KI_W = KB / 1024 / 4;     // K DMA instructions per wave per tile
+    constexpr int VI_W = VB / 1024 / 4;     // V^T DMA instructions per wave per tile
+    constexpr int DMA_W = KI_W + VI_W;
+    constexpr float kLazy = 8.f;            // max growth (log2) tolerated before rescaling
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * SB];
 
     const int bid = blockIdx.x;
     const AttnItem it = items[(bid % kNumXcd) * slots_per_xcd + bid / kNumXcd];
@@ -223,8 +252,7 @@ __global__ __launch_bounds__(256, 2) void awa_attention_kernel(
     const int l32 = lane & 31;
     const int g = lane >> 5;
     const long head_rows = (long)it.head * seg_total + w.seg_off;
-    const uint16_t* kbase = k_in + head_rows * D;
-    const uint16_t* vbase = vt_in + (long)it.head * D * seg_total + w.seg_off;
+    const int padded = (w.seq + kSegAlign - 1) / kSegAlign * kSegAlign;
     const int nkt = (w.seq + KT - 1) / KT;
 
     // Q fragment (B operand of S^T = K Q^T): query row l32 of this wave,
@@ -242,39 +270,35 @@ __global__ __launch_bounds__(256, 2) void awa_attention_kernel(
         }
     }
 
-    uint4 kreg[K_CHUNKS], vreg[V_CHUNKS];
-    auto load_tile = [&](int kt) {
-        const int key0 = kt * KT;
+    // DMA sources: this (window, head)'s K rows [padded][D] and V^T rows
+    // [D][seg_total] starting at the window's segment.
+    const i32x4 rk = buffer_rsrc(k_in + head_rows * D, (uint32_t)(padded * D * 2));
+    const i32x4 rv = buffer_rsrc(vt_in + (long)it.head * D * seg_total + w.seg_off,
+                                 (uint32_t)(((long)(D - 1) * seg_total + padded) * 2));
+    uint32_t koff[KI_W], voff[VI_W];
 #pragma unroll
-        for (int c = 0; c < K_CHUNKS; ++c) {
-            const int idx = tid + 256 * c;
-            const int row = idx / (D / 8);
-            const int col = (idx % (D / 8)) * 8;
-            kreg[c] = *reinterpret_cast<const uint4*>(kbase + (long)(key0 + row) * D + col);
-        }
+    for (int j = 0; j < KI_W; ++j) {
+        const int row = (wave * KI_W + j) * KRI + lane / KCH;
+        const int c = (lane % KCH) ^ k_swizzle<D>(row);
+        koff[j] = (uint32_t)((row * D + c * 8) * 2);
+    }
 #pragma unroll
-        for (int c = 0; c < V_CHUNKS; ++c) {
-            const int idx = tid + 256 * c;
-            const int d = idx / (KT / 8);
-            const int col = (idx % (KT / 8)) * 8;
-            vreg[c] = *reinterpret_cast<const uint4*>(vbase + (long)d * seg_total + key0 + col);
-        }
-    };
-    auto store_tile = [&](int buf) {
+    for (int j = 0; j < VI_W; ++j) {
+        const int d = (wave * VI_W + j) * 16 + (lane >> 2);
+        const int c = (lane & 3) ^ vt_swizzle(d);
+        voff[j] = (uint32_t)(((long)d * seg_total + c * 8) * 2);
+    }
+    const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+    auto issue = [&](int stage, int kt) {
+        const uint32_t st = lds_base + stage * SB;
 #pragma unroll
-        for (int c = 0; c < K_CHUNKS; ++c) {
-            const int idx = tid + 256 * c;
-            const int row = idx / (D / 8);
-            const int col = (idx % (D / 8)) * 8;
-            *reinterpret_cast<uint4*>(&k_lds[buf][row * KP + col]) = kreg[c];
-        }
+        for (int j = 0; j < KI_W; ++j)
+            lds_dma16(rk, __builtin_amdgcn_readfirstlane(st + (wave * KI_W + j) * 1024), koff[j],
+                      (uint32_t)(kt * KT * D * 2));
 #pragma unroll
-        for (int c = 0; c < V_CHUNKS; ++c) {
-            const int idx = tid + 256 * c;
-            const int d = idx / (KT / 8);
-            const int col = (idx % (KT / 8)) * 8;
-            *reinterpret_cast<uint4*>(&v_lds[buf][d * VP + col]) = vreg[c];
-        }
+        for (int j = 0; j < VI_W; ++j)
+            lds_dma16(rv, __builtin_amdgcn_readfirstlane(st + KB + (wave * VI_W + j) * 1024),
+                      voff[j], (uint32_t)(kt * KT * 2));
     };
 
     f32x16 o[NDT];
@@ -285,81 +309,85 @@ __global__ __launch_bounds__(256, 2) void awa_attention_kernel(
     float m_run = -INFINITY;   // running max (log2 domain), same in lanes l and l^32
     float l_run = 0.f;         // this lane's share of the running sum
 
-    // row of the S^T accumulator -> key within a 32-key subtile
+    // S^T A-operand row l32 loads key krow; its swizzle and the V^T row
+    // swizzle depend on l32 only
     const int krow = (l32 & 0x13) | ((l32 & 4) << 1) | ((l32 & 8) >> 1);
+    const int kswz = k_swizzle<D>(krow);
+    const int vswz = vt_swizzle(l32);
 
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
+    issue(0, 0);
+    if (nkt > 1) issue(1, 1);
 #pragma unroll 1
     for (int kt = 0; kt < nkt; ++kt) {
-        const int buf = kt & 1;
-        if (kt + 1 < nkt) load_tile(kt + 1);
+        if (kt + 1 < nkt) {   // stage kt+1 may stay in flight
+            if constexpr (DMA_W == 4)
+                asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+            else
+                asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+        } else {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        }
+        __syncthreads();   // tile kt visible to all waves; tile kt-1 no longer read
+        if (kt + 2 < nkt) issue((kt + 2) % STAGES, kt + 2);
+        const uint8_t* st = lds + (kt % STAGES) * SB;
 
-        f32x16 s[2];
+        f32x16 s;
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
+        for (int i = 0; i < 16; ++i) s[i] = 0.f;
+        const uint8_t* kp = st + krow * (D * 2);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) s[st][i] = 0.f;
-            const uint16_t* kp = &k_lds[buf][(32 * st + krow) * KP + 8 * g];
-#pragma unroll
-            for (int kk = 0; kk < NKK; ++kk) {
-                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(kp + 16 * kk));
-                s[st] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s[st], 0, 0, 0);
-            }
+        for (int kk = 0; kk < NKK; ++kk) {
+            const bf16x8 a = as_bf16x8(*(const uint4*)(kp + (((2 * kk + g) ^ kswz) * 16)));
+            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s, 0, 0, 0);
         }
         // keys past the window's sequence (only in the last tile) are masked
         const int key_base = kt * KT;
-        const bool tail = key_base + KT > w.seq;
-        float mx = -INFINITY;
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
+        if (key_base + KT > w.seq) {
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float x = s[st][i] * scale_log2;
-                if (tail) {
-                    // register i of lane group g holds key 16*(i/8) + 8g + (i%8)
-                    const int key = key_base + 32 * st + 16 * (i >> 3) + 8 * g + (i & 7);
-                    if (key >= w.seq) x = -INFINITY;
-                }
-                s[st][i] = x;
-                mx = fmaxf(mx, x);
+                // register i of lane group g holds key 16*(i/8) + 8g + (i%8)
+                const int key = key_base + 16 * (i >> 3) + 8 * g + (i & 7);
+                if (key >= w.seq) s[i] = -INFINITY;
             }
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = exp2f(m_run - m_new);
-        m_run = m_new;
+        }
+        float mx = s[0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+        float alpha = 1.f;
+        if (mx > m_run + kLazy) {
+            alpha = __builtin_amdgcn_exp2f(m_run - mx);   // 0 on the first tile
+            m_run = mx;
+        }
         float psum = 0.f;
-        bf16x8 pb[4];
+        bf16x8 pb[2];
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
+        for (int half = 0; half < 2; ++half) {
+            bf16x8 v;
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                uint16_t hb[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float p = exp2f(s[st][8 * half + j] - m_new);
-                    psum += p;
-                    hb[j] = f32_to_bf16(p);
-                }
-                pb[2 * st + half] = as_bf16x8(pack8_bf16(hb));
+            for (int j = 0; j < 8; ++j) {
+                const float p = __builtin_amdgcn_exp2f(fmaf(s[8 * half + j], scale_log2, -m_run));
+                psum += p;
+                v[j] = (__bf16)p;
             }
+            pb[half] = v;
+        }
         l_run = l_run * alpha + psum;
+        if (__any(alpha != 1.f)) {
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+                for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+        }
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) {
-            const uint16_t* vp = &v_lds[buf][(32 * dt + l32) * VP + 8 * g];
+            const uint8_t* vp = st + KB + (32 * dt + l32) * (KT * 2);
 #pragma unroll
-            for (int ps = 0; ps < 4; ++ps) {
-                const bf16x8 a = as_bf16x8(*reinterpret_cast<const uint4*>(vp + 16 * ps));
+            for (int ps = 0; ps < 2; ++ps) {
+                const bf16x8 a = as_bf16x8(*(const uint4*)(vp + (((2 * ps + g) ^ vswz) * 16)));
                 o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ps], o[dt], 0, 0, 0);
             }
         }
-        if (kt + 1 < nkt) store_tile(buf ^ 1);
-        __syncthreads();
     }
 
     const float l_tot = l_run + __shfl_xor(l_run, 32);

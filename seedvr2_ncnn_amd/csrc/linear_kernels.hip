@@ -198,31 +198,6 @@ __global__ __launch_bounds__(256, 2) void shared_linear_kernel(
 // 16-byte row chunks.
 namespace {
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t a = (uint64_t)base;
-    i32x4 r;
-    r.x = (int)(uint32_t)a;
-    r.y = (int)(uint32_t)(a >> 32);   // stride 0: raw buffer
-    r.z = (int)bytes;                 // num_records: reads past it return 0
-    r.w = 0x00020000;
-    return r;
-}
-
-// One buffer_load_dwordx4 with the lds modifier: lane i's 16 bytes land at
-// LDS address lds_addr + 16*i.  Issued through asm so that the compiler does
-// not order every later LDS read behind it; the main loop waits for the
-// stage it reads with s_waitcnt vmcnt and a barrier.  M0 is written only
-// here in this file.
-__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset,
-                                          uint32_t soffset) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                 :
-                 : "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset)
-                 : "memory", "m0");
-}
-
 __device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
 }  // namespace

@@ -70,6 +70,33 @@ __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
     return __builtin_bit_cast(bf16x8, v);
 }
 
+// Raw buffer descriptor over [base, base + bytes): loads past the end return
+// zero.  Word 3 is the gfx950 descriptor format for untyped dword access.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t a = (uint64_t)base;
+    i32x4 r;
+    r.x = (int)(uint32_t)a;
+    r.y = (int)(uint32_t)(a >> 32);   // stride 0: raw buffer
+    r.z = (int)bytes;                 // num_records
+    r.w = 0x00020000;
+    return r;
+}
+
+// One buffer_load_dwordx4 with the lds modifier: lane i's 16 bytes land at
+// LDS address lds_addr + 16*i (lds_addr wave-uniform).  Issued through asm
+// so that the compiler does not order every later LDS read behind it: the
+// caller waits for the data with s_waitcnt vmcnt and a barrier.  M0 is
+// written only by this helper in these kernels.
+__device__ __forceinline__ void lds_dma16(i32x4 rsrc, uint32_t lds_addr, uint32_t voffset,
+                                          uint32_t soffset) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                 :
+                 : "s"(lds_addr), "v"(voffset), "s"(rsrc), "s"(soffset)
+                 : "memory", "m0");
+}
+
 // Physical workgroup id -> logical id such that consecutive logical ids run
 // on the same XCD (the hardware deals workgroups to XCDs round-robin).
 __device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
