@@ -70,12 +70,12 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
     constexpr int TPR = D / 8;         // threads per row
     constexpr int RPP = 256 / TPR;     // rows per pass
     constexpr int CHUNK = kSegAlign;   // rows per workgroup
-    constexpr int VTP = CHUNK + 8;     // padded LDS pitch of the V^T tile
+    constexpr int VTP = CHUNK;         // LDS pitch of the V^T tile (one 128-byte row per channel)
     __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VTP];
 
-    const ChunkRef ch = chunks[blockIdx.x];
+    const ChunkRef ch = chunks[blockIdx.y];
     const WinMeta w = wins[ch.window];
-    const int head = blockIdx.y;
+    const int head = blockIdx.x;
     const int tid = threadIdx.x;
     const int d0 = (tid % TPR) * 8;
     const int rot_width = pairs * 6;
@@ -158,10 +158,10 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
                     qb[i] = round_bf16_ref_bits(q[i]);
                     kb[i] = round_bf16_ref_bits(k[i]);
                     vb[i] = round_bf16_ref_bits(v[i]);
-                } else {
-                    qb[i] = f32_to_bf16(q[i]);
-                    kb[i] = f32_to_bf16(k[i]);
-                    vb[i] = f32_to_bf16(v[i]);
+                } else {   // v_cvt_pk_bf16_f32: round to nearest even
+                    qb[i] = __builtin_bit_cast(uint16_t, (__bf16)q[i]);
+                    kb[i] = __builtin_bit_cast(uint16_t, (__bf16)k[i]);
+                    vb[i] = __builtin_bit_cast(uint16_t, (__bf16)v[i]);
                 }
             }
         } else {
@@ -173,15 +173,20 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
         const long orow = (head_rows + r) * D + d0;
         *reinterpret_cast<uint4*>(q_out + orow) = pack8_bf16(qb);
         *reinterpret_cast<uint4*>(k_out + orow) = pack8_bf16(kb);
+        // channel d0+i, key rl: 16-byte key chunk rl/8 stored at position
+        // (rl/8) ^ (channel/8 & 7), which spreads the 16 channels one store
+        // instruction writes over 8 bank groups
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vt_lds[(d0 + i) * VTP + rl] = vb[i];
+        for (int i = 0; i < 8; ++i)
+            vt_lds[(d0 + i) * VTP + ((((rl >> 3) ^ (d0 >> 3)) & 7) << 3) + (rl & 7)] = vb[i];
     }
     __syncthreads();
     // V^T rows: channel-major, the chunk's 64 keys contiguous (128 bytes).
     for (int idx = tid; idx < D * (CHUNK / 8); idx += 256) {
         const int d = idx / (CHUNK / 8);
         const int c8 = idx - d * (CHUNK / 8);
-        const uint4 val = *reinterpret_cast<const uint4*>(&vt_lds[d * VTP + c8 * 8]);
+        const uint4 val =
+            *reinterpret_cast<const uint4*>(&vt_lds[d * VTP + (((c8 ^ (d >> 3)) & 7) << 3)]);
         *reinterpret_cast<uint4*>(vt_out + ((long)head * D + d) * seg_total + w.seg_off + ch.row0 +
                                   c8 * 8) = val;
     }
@@ -508,7 +513,9 @@ static hipError_t prologue_impl(const s2_awa_plan& plan, const void* vq, const v
                                 const void* tv, long tstride, const float* norm,
                                 const float2* rope, uint16_t* q_out, uint16_t* k_out,
                                 uint16_t* vt_out, hipStream_t stream) {
-    dim3 grid(plan.num_chunks, plan.config.heads);
+    // heads vary fastest: concurrently running workgroups gather the same
+    // token rows (different head slices), which keeps DRAM rows and L2 lines hot
+    dim3 grid(plan.config.heads, plan.num_chunks);
     awa_prologue_kernel<D, TIn><<<grid, 256, 0, stream>>>(
         plan.d_wins, plan.d_chunks, (const TIn*)vq, (const TIn*)vk, (const TIn*)vv, vstride,
         (const TIn*)tq, (const TIn*)tk, (const TIn*)tv, tstride, norm, rope,
