@@ -51,6 +51,22 @@ def prologue_bytes(lv, lt):
     return 2 * (lv + lt) * 3 * HIDDEN * 2 + 16 * lv
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "shared_linear_mlp_up_720p_video_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the MLP-up GEMM from the committed rocprofv3
+    PMC summary (FETCH_SIZE + WRITE_SIZE, copy-calibrated), or None."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("TRAFFIC_BYTES_PER_LAUNCH"):
+                    return int(line.split("=")[1].strip())
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(threads, budget_s=20.0):
     """The oracle's optimised build (oracle/liboracle_fast.so, the reference's
     CPU forward restated in C) timed on a bounded sample of the same block:
@@ -109,6 +125,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run one 1 GiB device copy (a plain copy kernel of known size) so "
+                         "that PMC byte counters can be calibrated in the same profiler run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
@@ -188,6 +207,13 @@ def main():
         per_op = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(ops)}
         return total_ms / steps, per_op, wall
 
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     m = lv + lt
     gemm = {"qkv": 2 * m * HIDDEN * 3 * HIDDEN, "out": 2 * m * HIDDEN * HIDDEN,
             "mlp_up": 2 * m * HIDDEN * MLP, "mlp_down": 2 * m * MLP * HIDDEN}
@@ -243,7 +269,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(up_tf / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "wall_s_timed_region": round(wall, 3),
     }
