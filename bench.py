@@ -14,7 +14,10 @@ Algorithmic work per step: 4*H*d*sum_w (n_w+64)^2 attention FLOPs (206.45 G)
 plus 2*M*K*N per GEMM with M = 21,664 (3,407.45 G): 3.614 TFLOP.  Inputs and
 weights are resident in HBM before the timed region (seeded N(0,1)
 activations, N(0,0.02) weights).  The shifted-window block (64 ragged
-windows) is timed too and reported beside the headline.
+windows) is timed too and reported beside the headline, and so is the
+SeedVR2-7B-shaped stack of 32 blocks (hidden 3072, 24 heads x 128, MLP
+3072 -> 12288 -> 3072, regular windows in even and shifted windows in odd
+blocks, 64 text tokens projected 5120 -> 3072 once) under "stack_7b".
 
 Prints one JSON line.  `--gpus` above 1 is refused: this build measures one GPU.
 """
@@ -118,6 +121,95 @@ def cpu_baseline(threads, budget_s=20.0):
     }
 
 
+STACK_HIDDEN, STACK_HEADS, STACK_MLP, STACK_BLOCKS, STACK_TEXT_WIDTH = 3072, 24, 12288, 32, 5120
+
+
+def stack_7b(steps, warmup):
+    """SeedVR2-7B-shaped 32-block stack of the hot path at the 720p video
+    grid: per block QKV -> window attention (regular windows in even blocks,
+    shifted in odd ones) -> out -> MLP up GELU -> down, each block's output
+    feeding the next; the 64 text tokens are projected 5120 -> 3072 once per
+    stack.  Every block has its own random-init bf16 weights (7.2 GB)."""
+    import torch
+    from seedvr2_ncnn_amd import capi
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    bf = torch.bfloat16
+    D, H, F = STACK_HIDDEN, STACK_HEADS, STACK_MLP
+    lv = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2]
+    lt = TEXT_TOKENS
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32) * std).to(bf)
+
+    def bias(n):
+        return torch.randn(n, generator=gen, device=dev) * 0.02
+
+    blocks = [dict(qkv=randn(3 * D, D, std=0.02), bqkv=bias(3 * D), o=randn(D, D, std=0.02),
+                   bo=bias(D), up=randn(F, D, std=0.02), bup=bias(F), dn=randn(D, F, std=0.02),
+                   bdn=bias(D), norms=(1.0 + 0.02 * torch.randn(4, HEAD_DIM, generator=gen,
+                                                                device=dev)).contiguous())
+              for _ in range(STACK_BLOCKS)]
+    w_text, b_text = randn(D, STACK_TEXT_WIDTH, std=0.02), bias(D)
+    freqs = (10000.0 ** (-torch.arange(PAIRS, device=dev, dtype=torch.float64) / PAIRS)).float()
+    x_v0, text_in = randn(lv, D), randn(lt, STACK_TEXT_WIDTH)
+    x_v, x_t = torch.empty(lv, D, dtype=bf, device=dev), torch.empty(lt, D, dtype=bf, device=dev)
+    qkv_v = torch.empty(lv, 3 * D, dtype=bf, device=dev)
+    qkv_t = torch.empty(lt, 3 * D, dtype=bf, device=dev)
+    a_v, a_t = torch.empty_like(x_v), torch.empty_like(x_t)
+    o_v, o_t = torch.empty_like(x_v), torch.empty_like(x_t)
+    h_v = torch.empty(lv, F, dtype=bf, device=dev)
+    h_t = torch.empty(lt, F, dtype=bf, device=dev)
+    plans = {s: capi.AwaPlan(capi.awa_config(H, HEAD_DIM, TARGET, s, 1e-5, PAIRS), [VIDEO_SHAPE], [lt])
+             for s in (0, 1)}
+    ws = torch.empty(max(p.info.workspace_bytes for p in plans.values()), dtype=torch.uint8, device=dev)
+
+    def forward():
+        x_v.copy_(x_v0)
+        capi.shared_linear(text_in, None, w_text, b_text, capi.ACT_NONE, y_video=x_t)
+        for i, blk in enumerate(blocks):
+            capi.shared_linear(x_v, x_t, blk["qkv"], blk["bqkv"], capi.ACT_NONE, y_video=qkv_v,
+                               y_text=qkv_t)
+            capi.awa_forward(plans[i % 2], blk["norms"], freqs,
+                             qkv_v[:, :D], qkv_v[:, D:2 * D], qkv_v[:, 2 * D:],
+                             qkv_t[:, :D], qkv_t[:, D:2 * D], qkv_t[:, 2 * D:],
+                             workspace=ws, out_video=a_v, out_text=a_t)
+            capi.shared_linear(a_v, a_t, blk["o"], blk["bo"], capi.ACT_NONE, y_video=o_v, y_text=o_t)
+            capi.shared_linear(o_v, o_t, blk["up"], blk["bup"], capi.ACT_GELU, y_video=h_v, y_text=h_t)
+            capi.shared_linear(h_v, h_t, blk["dn"], blk["bdn"], capi.ACT_NONE, y_video=x_v, y_text=x_t)
+
+    for _ in range(warmup):
+        forward()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        forward()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    finite = bool(torch.isfinite(x_v.float()).all().item())
+
+    m = lv + lt
+    gemm = 2 * m * D * (3 * D + D + 2 * F)
+    attn = {s: sum(4 * H * HEAD_DIM * (w[8] + lt) ** 2 for w in capi.plan_windows([VIDEO_SHAPE], TARGET, s)[0])
+            for s in (0, 1)}
+    flops = (2 * lt * STACK_TEXT_WIDTH * D
+             + sum(gemm + attn[i % 2] for i in range(STACK_BLOCKS)))
+    for p in plans.values():
+        p.close()
+    del blocks
+    torch.cuda.empty_cache()
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": f"SeedVR2-7B-shaped {STACK_BLOCKS}-block stack at 6x45x80 + {lt} text tokens: "
+                        f"hidden {D}, {H}x{HEAD_DIM} heads, MLP {D}->{F} GELU ->{D}, even blocks "
+                        f"regular / odd blocks shifted windows, text {STACK_TEXT_WIDTH}->{D} once",
+            "steps": steps, "warmup": warmup, "ms_per_stack": round(ms, 3),
+            "ms_per_block": round(ms / STACK_BLOCKS, 4), "stack_tflop": round(flops / 1e12, 3),
+            "tflops": round(tf, 1), "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2),
+            "output_finite": finite}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -125,6 +217,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--no-stack", action="store_true", help="skip the 32-block 7B-shaped stack")
+    ap.add_argument("--stack-steps", type=int, default=3)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device copy (a plain copy kernel of known size) so "
                          "that PMC byte counters can be calibrated in the same profiler run")
@@ -263,7 +357,7 @@ def main():
         "kernels": kernels,
         "prologue_algorithmic_bytes": prologue_bytes(lv, lt),
         "roofline": {
-            "kernel": "shared_linear_kernel (MLP up 2560->10240 + GELU, M=21664)",
+            "kernel": "s2::shared_linear_256_kernel<true, 1> (MLP up 2560->10240 + GELU, M=21664)",
             "bound": "mfma",
             "achieved": round(up_tf, 1),
             "peak": PEAK_BF16_TFLOPS,
@@ -273,11 +367,15 @@ def main():
         },
         "wall_s_timed_region": round(wall, 3),
     }
+    for p in plans.values():
+        p.close()
+    del x_v, x_t, w_qkv, w_o, w_up, w_dn, qkv_v, qkv_t, a_v, a_t, o_v, o_t, h_v, h_t, y_v, y_t, ws
+    torch.cuda.empty_cache()
+    if not args.no_stack:
+        line["stack_7b"] = stack_7b(args.stack_steps, 1)
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         line["cpu_baseline"] = cpu_baseline(threads)
-    for p in plans.values():
-        p.close()
     print(json.dumps(line), flush=True)
 
 

@@ -184,6 +184,19 @@ def test_video_grid_6x45x80_dim2560(shifted):
     assert_close(ot, rt, "text")
 
 
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_video_grid_6x45x80_dim3072_24_heads(shifted):
+    """SeedVR2-7B attention shape: the 720p 21-frame grid, hidden 3072,
+    24 heads x 128 (one layer of the 32-block stack)."""
+    import torch
+    shapes, tl = [(6, 45, 80)], [64]
+    case = make_awa_inputs(707 + shifted, shapes, tl, 24, 128, 21, bf16=True)
+    ov, ot = _run_capi(case, 24, 128, (4, 3, 3), shifted, 21, shapes, tl, True, torch.bfloat16)
+    rv, rt = oracle_awa(case, 24, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl, fast=True)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+
+
 # ---- variants ------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("official", [False, True])

@@ -70,9 +70,12 @@ def test_tiny_fixture():
     assert_close(yt, f["y_text"], "text")
 
 
-# SeedVR2-3B block GEMMs at the 720p video shape: 21,600 video + 64 text tokens.
+# Block GEMMs at the 720p video shape, 21,600 video + 64 text tokens: the
+# SeedVR2-3B block (hidden 2560) and the SeedVR2-7B block (hidden 3072).
 VIDEO_GEMMS = [("qkv", 2560, 7680, 0), ("out", 2560, 2560, 0), ("mlp_up_gelu", 2560, 10240, 1),
-               ("mlp_down", 10240, 2560, 0)]
+               ("mlp_down", 10240, 2560, 0),
+               ("qkv_3072", 3072, 9216, 0), ("out_3072", 3072, 3072, 0),
+               ("mlp_up_gelu_3072", 3072, 12288, 1), ("mlp_down_3072", 12288, 3072, 0)]
 
 
 @pytest.mark.parametrize("name,k,n,act", VIDEO_GEMMS)
@@ -137,3 +140,17 @@ def test_layer_gelu_activation_param():
     code, (yv, yt) = layer.forward([xv, xt], [((10, n), np.float32), ((2, n), np.float32)])
     assert code == 0
     assert_close(yv, oracle.linear(xv, w, None, 1), "video")
+
+
+def test_text_projection_5120_to_3072():
+    """The 64 conditioning tokens of the 7B stack enter at the frontend text
+    width 5120 and are projected to the hidden width 3072 once; a small-M,
+    long-K GEMM (one 256-row tile)."""
+    g = np.random.default_rng(5120)
+    k, n, m = 5120, 3072, 64
+    x = bf16_round(g.standard_normal((m, k), dtype=np.float32))
+    w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
+    b = (0.02 * g.standard_normal(n)).astype(np.float32)
+    y, _ = _gpu_linear(x, None, w, b, 0, True, False)
+    assert_close(y, oracle.linear(x, w, b, threads=THREADS), "text projection")
+    assert _tight(y, x, bf16_round(w), b, 0) < 1e-4
