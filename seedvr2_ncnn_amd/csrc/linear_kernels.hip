@@ -7,6 +7,9 @@
 // unchanged.  fp32 activations are rounded to bf16 while they are staged.
 #include <math.h>
 
+#include <algorithm>
+#include <mutex>
+
 #include "awa_kernels.h"
 #include "s2_device.h"
 
@@ -196,41 +199,56 @@ __global__ __launch_bounds__(256, 2) void shared_linear_kernel(
 // epilogue adds the bias and activation in fp32, converts with
 // v_cvt_pk_bf16_f32, assembles the 256x256 tile in LDS and writes it out as
 // 16-byte row chunks.
+//
+// Tail balancing.  When the tile count leaves the last wave of workgroups
+// partly idle, the tiles of that wave are not given one workgroup each:
+// their 64-k iterations are dealt out evenly to sk_groups workgroups, each
+// taking one contiguous range of (tile, k-iteration) pairs (with sk_groups
+// a multiple of the tile count, every range lies inside one tile).  A tile finished by one workgroup takes the normal epilogue; a tile
+// split between workgroups has every part store its fp32 accumulators to a
+// per-workgroup slot and bump the tile's arrival counter, and the last part
+// to arrive sums all the slots in workgroup order (so the result does not
+// depend on which part arrives last), runs the epilogue and resets the
+// counter.  No workgroup waits on another.
 namespace {
 
 __device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
+constexpr int kSlotFloats = 128 * 512;   // one workgroup's accumulators
+
+// Cache policy of the slot stores and loads: sc0 sc1, coherent across the
+// XCDs' L2s (stores write through, loads do not hit a stale L2 line), so the
+// parts of a tile can meet without cache-wide writeback or invalidation.
+constexpr int kCoherent = 1 | 16;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
 }  // namespace
+
+struct SkTail {
+    int dp_tiles;      // tiles [0, dp_tiles): one workgroup each
+    int sk_tiles;      // tiles [dp_tiles, dp_tiles + sk_tiles): shared out along k
+    int sk_groups;     // workgroups sharing them, <= sk_tiles * (k / 64)
+    float* slots;      // [sk_groups][2][kSlotFloats] partial accumulators
+    int* counters;     // [sk_tiles] arrivals; zero between launches
+};
 
 template <bool Y_BF16, int ACT>
 __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const uint16_t* __restrict__ x0, int m0, const uint16_t* __restrict__ x1, int m1,
     const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
-    void* __restrict__ y0, void* __restrict__ y1, int mt0, int mtiles, int ntiles) {
-    constexpr int BM = 256, BN = 256, BK = 64, STAGES = 2;
+    void* __restrict__ y0, void* __restrict__ y1, int mt0, int mtiles, int ntiles, SkTail sk) {
+    constexpr int BM = 256, BN = 256, BK = 64;
     constexpr int TB = BM * BK * 2;   // 32 KB per operand per stage
     constexpr int SB = 2 * TB;        // 64 KB per stage
     constexpr int RB = BK * 2;        // LDS row bytes
     constexpr int EP = BN * 2 + 16;   // epilogue LDS row pitch (bytes)
-    constexpr int LDS_BYTES = STAGES * SB > BM * EP ? STAGES * SB : BM * EP;
+    constexpr int LDS_BYTES = 2 * SB > BM * EP ? 2 * SB : BM * EP;
     constexpr int GROUP = 8;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
+    __shared__ int arrival;
 
-    const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int group_size = GROUP * ntiles;
-    const int first_m = (lid / group_size) * GROUP;
-    const int gm = min(mtiles - first_m, GROUP);
-    const int mt = first_m + (lid % group_size) % gm;
-    const int nt = (lid % group_size) / gm;
-    const uint16_t* x;
-    int m, row0;
-    void* y;
-    if (mt < mt0) {
-        x = x0; m = m0; y = y0; row0 = mt * BM;
-    } else {
-        x = x1; m = m1; y = y1; row0 = (mt - mt0) * BM;
-    }
-    const int col0 = nt * BN;
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -238,123 +256,275 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const int g = lane >> 5;
     const int wm = wave >> 2;
     const int wn = wave & 3;
-
-    const i32x4 ra = buffer_rsrc(x + (long)row0 * k, (uint32_t)(min(m - row0, BM) * k * 2));
-    const i32x4 rb = buffer_rsrc(wgt + (long)col0 * k, (uint32_t)(min(n - col0, BN) * k * 2));
-    // Wave w fills LDS rows 32w .. 32w+31 of each operand with 4 DMA
-    // instructions of 8 rows: lane i takes row +i/8 and the logical chunk
-    // stored at position i%8.
-    uint32_t voff[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int row = wave * 32 + j * 8 + (lane >> 3);
-        voff[j] = (uint32_t)(row * k * 2 + (((lane & 7) ^ lds_swizzle(row)) * 16));
-    }
+    const int nk = k / BK;
+    const int sw = lds_swizzle(l32);   // fragment rows differ from l32 by multiples of 32
     const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
-    auto issue = [&](int stage, int kt) {
-        const uint32_t soff = (uint32_t)(kt * BK * 2);
-        const uint32_t st = lds_base + stage * SB + wave * 4 * 1024;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            lds_dma16(ra, __builtin_amdgcn_readfirstlane(st + j * 1024), voff[j], soff);
-            lds_dma16(rb, __builtin_amdgcn_readfirstlane(st + TB + j * 1024), voff[j], soff);
+
+    // the current tile
+    const uint16_t* x;
+    int m, row0, col0;
+    void* y;
+    auto set_tile = [&](int t) {
+        // grouped raster: GROUP m-tiles share each sweep over the n-tiles
+        const int group_size = GROUP * ntiles;
+        const int first_m = (t / group_size) * GROUP;
+        const int gm = min(mtiles - first_m, GROUP);
+        const int mt = first_m + (t % group_size) % gm;
+        const int nt = (t % group_size) / gm;
+        if (mt < mt0) {
+            x = x0; m = m0; y = y0; row0 = mt * BM;
+        } else {
+            x = x1; m = m1; y = y1; row0 = (mt - mt0) * BM;
         }
+        col0 = nt * BN;
     };
 
     f32x16 acc[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-
-    // fragment rows differ from l32 by multiples of 32, so their swizzle
-    // depends on l32 only
-    const int sw = lds_swizzle(l32);
     bf16x8 a[2][4], b[2][2];
-    auto frag = [&](const uint8_t* st, int kk, int slot) {
-        const int pc = ((2 * kk + g) ^ sw) * 16;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            a[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * RB + pc));
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-            b[slot][j] = as_bf16x8(*(const uint4*)(st + TB + (wn * 64 + 32 * j + l32) * RB + pc));
-    };
 
-    const int nk = k / BK;
-    issue(0, 0);
-#pragma unroll 1
-    for (int kt = 0; kt < nk; ++kt) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();   // stage kt visible to all waves; stage kt-1 no longer read
-        if (kt + 1 < nk) issue((kt + 1) & 1, kt + 1);
-        const uint8_t* st = lds + (kt & 1) * SB;
-        frag(st, 0, 0);
+    // acc = sum over 64-k iterations [kb, ke) of the current tile
+    auto mainloop = [&](int kb, int ke) {
+        // the tile is the same for every lane: keep the descriptors in SGPRs
+        const i32x4 ra =
+            wave_uniform(buffer_rsrc(x + (long)row0 * k, (uint32_t)(min(m - row0, BM) * k * 2)));
+        const i32x4 rb =
+            wave_uniform(buffer_rsrc(wgt + (long)col0 * k, (uint32_t)(min(n - col0, BN) * k * 2)));
+        // Wave w fills LDS rows 32w .. 32w+31 of each operand with 4 DMA
+        // instructions of 8 rows: lane i takes row +i/8 and the logical
+        // chunk stored at position i%8.
+        uint32_t voff[4];
 #pragma unroll
-        for (int kk = 0; kk < BK / 16; ++kk) {
-            if (kk + 1 < BK / 16) frag(st, kk + 1, (kk + 1) & 1);
+        for (int j = 0; j < 4; ++j) {
+            const int row = wave * 32 + j * 8 + (lane >> 3);
+            voff[j] = (uint32_t)(row * k * 2 + (((lane & 7) ^ lds_swizzle(row)) * 16));
+        }
+        auto issue = [&](int stage, int kt) {
+            const uint32_t soff = __builtin_amdgcn_readfirstlane((uint32_t)(kt * BK * 2));
+            const uint32_t st = lds_base + stage * SB + wave * 4 * 1024;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                lds_dma16(ra, __builtin_amdgcn_readfirstlane(st + j * 1024), voff[j], soff);
+                lds_dma16(rb, __builtin_amdgcn_readfirstlane(st + TB + j * 1024), voff[j], soff);
+            }
+        };
+        auto frag = [&](const uint8_t* st, int kk, int slot) {
+            const int pc = ((2 * kk + g) ^ sw) * 16;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
+                a[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * RB + pc));
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[kk & 1][i], b[kk & 1][j],
-                                                                       acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 2; ++j)
+                b[slot][j] = as_bf16x8(*(const uint4*)(st + TB + (wn * 64 + 32 * j + l32) * RB + pc));
+        };
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+        issue(0, kb);
+#pragma unroll 1
+        for (int kt = kb; kt < ke; ++kt) {
+            const int stage = (kt - kb) & 1;
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();   // stage kt visible to all waves; the other stage no longer read
+            if (kt + 1 < ke) issue(stage ^ 1, kt + 1);
+            const uint8_t* st = lds + stage * SB;
+            frag(st, 0, 0);
+            // The scheduling barriers keep the next slice's LDS reads ahead
+            // of this slice's MFMAs (two fragment buffers), instead of the
+            // compiler sinking each read next to its first use.
+#pragma unroll
+            for (int kk = 0; kk < BK / 16; ++kk) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (kk + 1 < BK / 16) frag(st, kk + 1, (kk + 1) & 1);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                            a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-    }
+    };
 
-    if (Y_BF16 && (n & 7) == 0) {
-        __syncthreads();   // every wave is done reading the last stage
+    // y tile = act(acc + bias)
+    auto epilogue = [&]() {
+        if (Y_BF16 && (n & 7) == 0) {
+            __syncthreads();   // every wave is done reading the last stage
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int cl = wn * 64 + 32 * j + l32;
+                const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        float v = acc[i][j][r] + bv;
+                        if (ACT == S2_ACT_GELU) v = gelu(v);
+                        const int rl = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                        *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
+                    }
+            }
+            __syncthreads();
+            // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows t/32 + 16c
+#pragma unroll 4
+            for (int c = 0; c < 16; ++c) {
+                const int idx = c * 512 + tid;
+                const int rl = idx >> 5;
+                const int ch = idx & 31;
+                const int row = row0 + rl;
+                const int col = col0 + ch * 8;
+                if (row < m && col < n)
+                    *(uint4*)((uint16_t*)y + (long)row * n + col) =
+                        *(const uint4*)(lds + rl * EP + ch * 16);
+            }
+            return;
+        }
+        // fp32 output (or a ragged n): direct stores, register r of a 32x32
+        // accumulator is row 8(r/4) + 4g + r%4, column l32
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int cl = wn * 64 + 32 * j + l32;
-            const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
+            const int col = col0 + wn * 64 + 32 * j + l32;
+            if (col >= n) continue;
+            const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
+                    const int row = row0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                    if (row >= m) continue;
                     float v = acc[i][j][r] + bv;
                     if (ACT == S2_ACT_GELU) v = gelu(v);
-                    const int rl = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                    *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
+                    if (Y_BF16)
+                        ((__bf16*)y)[(long)row * n + col] = (__bf16)v;
+                    else
+                        ((float*)y)[(long)row * n + col] = v;
                 }
         }
-        __syncthreads();
-        // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows t/32 + 16c
-#pragma unroll 4
-        for (int c = 0; c < 16; ++c) {
-            const int idx = c * 512 + tid;
-            const int rl = idx >> 5;
-            const int ch = idx & 31;
-            const int row = row0 + rl;
-            const int col = col0 + ch * 8;
-            if (row < m && col < n)
-                *(uint4*)((uint16_t*)y + (long)row * n + col) =
-                    *(const uint4*)(lds + rl * EP + ch * 16);
+    };
+
+    // Work of this workgroup as segments (tile, k-iterations [kb, ke)).  A
+    // data-parallel workgroup has one whole tile.  Stream-K workgroup s owns
+    // iterations [bound(s), bound(s + 1)) of the split tiles, iteration i
+    // being k-step i % nk of split tile i / nk.
+    const bool split = (int)blockIdx.x >= sk.dp_tiles;
+    // consecutive ranges (neighbouring tiles of the raster) on one XCD, so
+    // that they share A and B panels in its L2 (dp_tiles is a multiple of 8)
+    const int s = split ? xcd_remap(blockIdx.x - sk.dp_tiles, sk.sk_groups) : 0;
+    const long total = (long)sk.sk_tiles * nk;
+    auto bound = [&](long q) { return q * total / sk.sk_groups; };
+    // the stream-K workgroup whose range holds iteration i
+    auto owner = [&](long i) { return (int)(((i + 1) * sk.sk_groups - 1) / total); };
+    long i = split ? bound(s) : 0;
+    const long iend = split ? bound(s + 1) : nk;
+    bool first = true;
+#pragma unroll 1
+    while (i < iend) {
+        int t, kb, ke;
+        if (split) {
+            t = (int)(i / nk);
+            kb = (int)(i - (long)t * nk);
+            ke = (int)min((long)nk, kb + (iend - i));
+            set_tile(sk.dp_tiles + t);
+        } else {
+            t = 0;
+            kb = 0;
+            ke = nk;
+            set_tile(xcd_remap(blockIdx.x, sk.dp_tiles));
         }
-        return;
-    }
-    // fp32 output (or a ragged n): direct stores, register r of a 32x32
-    // accumulator is row 8(r/4) + 4g + r%4, column l32
+        if (!first) __syncthreads();   // the previous segment's LDS is no longer read
+        mainloop(kb, ke);
+        bool finish = kb == 0 && ke == nk;
+        if (!finish) {
+            // slot layout: float4 c (4 accumulator registers) of thread tid
+            // at byte (c * 512 + tid) * 16; the chunk index goes in soffset
+            const __amdgpu_buffer_rsrc_t mine = __builtin_amdgcn_make_buffer_rsrc(
+                sk.slots + ((long)s * 2 + (first ? 0 : 1)) * kSlotFloats, (short)0,
+                kSlotFloats * 4, 0x00020000);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int col = col0 + wn * 64 + 32 * j + l32;
-        if (col >= n) continue;
-        const float bv = bias ? bias[col] : 0.f;
+            for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+                for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int row = row0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                if (row >= m) continue;
-                float v = acc[i][j][r] + bv;
-                if (ACT == S2_ACT_GELU) v = gelu(v);
-                if (Y_BF16)
-                    ((__bf16*)y)[(long)row * n + col] = (__bf16)v;
-                else
-                    ((float*)y)[(long)row * n + col] = v;
+                    for (int c = 0; c < 4; ++c) {
+                        f32x4 v = {acc[ii][j][4 * c], acc[ii][j][4 * c + 1], acc[ii][j][4 * c + 2],
+                                   acc[ii][j][4 * c + 3]};
+                        __builtin_amdgcn_raw_buffer_store_b128(
+                            __builtin_bit_cast(u32x4, v), mine, tid * 16,
+                            ((ii * 2 + j) * 4 + c) * 512 * 16, kCoherent);
+                    }
+            // the slot stores write through to memory; wait for all of them
+            // before the arrival is counted
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            if (tid == 0)
+                arrival = __hip_atomic_fetch_add(&sk.counters[t], 1, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+            __syncthreads();
+            const int lo = owner((long)t * nk);
+            const int hi = owner((long)t * nk + nk - 1);
+            if (arrival == hi - lo) {
+                // sum every part, this one's included, in workgroup order so
+                // that the result does not depend on the order of arrival
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int r = 0; r < 16; ++r) acc[ii][j][r] = 0.f;
+#pragma unroll 1
+                for (int q = lo; q <= hi; ++q) {
+                    // q's segment of tile t is its first one iff its range starts in t
+                    const int qslot = (bound(q) / nk == t) ? 0 : 1;
+                    const __amdgpu_buffer_rsrc_t other = __builtin_amdgcn_make_buffer_rsrc(
+                        sk.slots + ((long)q * 2 + qslot) * kSlotFloats, (short)0, kSlotFloats * 4,
+                        0x00020000);
+                    // sixteen 16-byte loads in flight per batch (four
+                    // accumulators; the fragment registers are free here)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        __builtin_amdgcn_sched_barrier(0);
+                        f32x4 v[2][2][4];
+#pragma unroll
+                        for (int iq = 0; iq < 2; ++iq)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                                for (int c = 0; c < 4; ++c)
+                                    v[iq][j][c] = __builtin_bit_cast(
+                                        f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   other, tid * 16,
+                                                   (((2 * h + iq) * 2 + j) * 4 + c) * 512 * 16,
+                                                   kCoherent));
+#pragma unroll
+                        for (int iq = 0; iq < 2; ++iq)
+#pragma unroll
+                            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                                for (int c = 0; c < 4; ++c) {
+                                    f32x16& d = acc[2 * h + iq][j];
+                                    d[4 * c] += v[iq][j][c].x;
+                                    d[4 * c + 1] += v[iq][j][c].y;
+                                    d[4 * c + 2] += v[iq][j][c].z;
+                                    d[4 * c + 3] += v[iq][j][c].w;
+                                }
+                    }
+                }
+                if (tid == 0)
+                    __hip_atomic_store(&sk.counters[t], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                finish = true;
             }
+        }
+        if (finish) epilogue();
+        // every memory operation of this segment is complete: a real
+        // s_waitcnt (not asm) lets the compiler's wait insertion know, so
+        // it adds no vmcnt wait of its own inside the next main loop
+        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        first = false;
+        i += ke - kb;
     }
 }
 
@@ -382,6 +552,52 @@ hipError_t launch_cast_bf16_f32(const uint16_t* src, float* dst, size_t n, hipSt
     return hipGetLastError();
 }
 
+// Per-device scratch of the stream-K tail: partial-accumulator slots and
+// arrival counters, allocated on first use and kept for the process.
+namespace {
+
+struct SkScratch {
+    int groups = 0;
+    float* slots = nullptr;
+    int* counters = nullptr;
+};
+
+constexpr int kMaxDevices = 64;
+SkScratch g_sk[kMaxDevices];
+std::mutex g_sk_mutex;
+
+hipError_t sk_scratch(SkScratch** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_sk_mutex);
+    SkScratch& sc = g_sk[dev];
+    if (!sc.slots) {
+        int cus = 0;
+        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return e;
+        const int groups = cus > 0 ? cus : 256;
+        float* slots = nullptr;
+        int* counters = nullptr;
+        e = hipMalloc((void**)&slots, sizeof(float) * (size_t)groups * 2 * kSlotFloats);
+        if (e != hipSuccess) return e;
+        // the shared-out tiles number fewer than two waves of workgroups
+        e = hipMalloc((void**)&counters, sizeof(int) * (size_t)groups * 2);
+        if (e != hipSuccess) { (void)hipFree(slots); return e; }
+        e = hipMemset(counters, 0, sizeof(int) * (size_t)groups * 2);
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e != hipSuccess) { (void)hipFree(slots); (void)hipFree(counters); return e; }
+        sc.groups = groups;
+        sc.slots = slots;
+        sc.counters = counters;
+    }
+    *out = &sc;
+    return hipSuccess;
+}
+
+}  // namespace
+
 template <typename TX, bool Y_BF16, int ACT>
 static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, const uint16_t* w,
                               const float* bias, int n, int k, void* y0, void* y1,
@@ -392,11 +608,33 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
         const int mt1 = (m1 + 255) / 256;
         const int ntiles = (n + 255) / 256;
         const int mtiles = mt0 + mt1;
-        const long blocks = (long)mtiles * ntiles;
-        if (blocks == 0) return hipSuccess;
+        const long tiles = (long)mtiles * ntiles;
+        if (tiles == 0) return hipSuccess;
+        SkScratch* sc = nullptr;
+        hipError_t e = sk_scratch(&sc);
+        if (e != hipSuccess) return e;
+        const int G = sc->groups;
+        const int nk = k / 64;
+        SkTail sk{(int)tiles, 0, 0, sc->slots, sc->counters};
+        // When the last wave of tiles would leave more than 3% of the
+        // workgroup slots idle, each tile of that wave is split along k into
+        // P equal parts on P workgroups (P <= 4, at least 8 k-iterations a
+        // part): the wave then takes about 1/P of a tile's time plus the
+        // reduction of P partial tiles.
+        const long waves = (tiles + G - 1) / G;
+        const long rem = tiles % G == 0 ? G : tiles % G;
+        if ((double)tiles / (double)(waves * G) < 0.97) {
+            const long parts = std::min<long>(4, std::min<long>(G / rem, nk / 8));
+            if (parts >= 2) {
+                sk.dp_tiles = (int)(tiles - rem);
+                sk.sk_tiles = (int)rem;
+                sk.sk_groups = (int)(rem * parts);
+            }
+        }
+        const long blocks = (long)sk.dp_tiles + sk.sk_groups;
         shared_linear_256_kernel<Y_BF16, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
             (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mt0, mtiles,
-            ntiles);
+            ntiles, sk);
         return hipGetLastError();
     }
     const int mt0 = (m0 + 127) / 128;

@@ -84,6 +84,17 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
     return r;
 }
 
+// A descriptor the compiler cannot prove wave-uniform (built from values
+// that passed through control flow) moved to SGPRs; the caller guarantees
+// that every lane holds the same value.
+__device__ __forceinline__ i32x4 wave_uniform(i32x4 r) {
+    r.x = __builtin_amdgcn_readfirstlane(r.x);
+    r.y = __builtin_amdgcn_readfirstlane(r.y);
+    r.z = __builtin_amdgcn_readfirstlane(r.z);
+    r.w = __builtin_amdgcn_readfirstlane(r.w);
+    return r;
+}
+
 // One buffer_load_dwordx4 with the lds modifier: lane i's 16 bytes land at
 // LDS address lds_addr + 16*i (lds_addr wave-uniform).  Issued through asm
 // so that the compiler does not order every later LDS read behind it: the

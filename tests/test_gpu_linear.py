@@ -154,3 +154,23 @@ def test_text_projection_5120_to_3072():
     y, _ = _gpu_linear(x, None, w, b, 0, True, False)
     assert_close(y, oracle.linear(x, w, b, threads=THREADS), "text projection")
     assert _tight(y, x, bf16_round(w), b, 0) < 1e-4
+
+
+@pytest.mark.parametrize("mv,mt,k,n", [(300, 0, 2560, 2560), (1000, 64, 640, 768), (21600, 64, 2560, 2560)])
+def test_split_tail_is_deterministic(mv, mt, k, n):
+    """Tiles of a partly filled last wave are split along k between
+    workgroups and summed by whichever part finishes last; the sum runs in a
+    fixed order, so repeated calls give identical bits."""
+    g = np.random.default_rng(mv + k)
+    xv = bf16_round(g.standard_normal((mv, k), dtype=np.float32))
+    xt = bf16_round(g.standard_normal((mt, k), dtype=np.float32)) if mt else None
+    w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
+    b = (0.02 * g.standard_normal(n)).astype(np.float32)
+    outs = [_gpu_linear(xv, xt, w, b, 1, True, False) for _ in range(3)]
+    for yv, yt in outs[1:]:
+        np.testing.assert_array_equal(yv, outs[0][0])
+        if mt:
+            np.testing.assert_array_equal(yt, outs[0][1])
+    rows = np.concatenate([np.arange(0, 3), g.integers(0, mv, 20), np.arange(mv - 3, mv)]).astype(np.int32)
+    assert_close(outs[0][0][rows], oracle.linear(xv, w, b, 1, rows=rows, threads=THREADS), "video rows")
+    assert _tight(outs[0][0][rows], xv, bf16_round(w), b, 1, rows=rows) < 2e-4
