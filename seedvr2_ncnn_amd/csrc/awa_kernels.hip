@@ -55,6 +55,39 @@ __global__ void rope_table_kernel(const float* __restrict__ freqs, int pairs, in
 }
 
 // ---------------------------------------------------------------------------
+// Eight consecutive input channels held as loaded (bf16 or fp32), converted
+// to fp32 when used.
+template <typename T>
+struct Raw8;
+
+template <>
+struct Raw8<uint16_t> {
+    uint4 v;
+    __device__ __forceinline__ void load(const uint16_t* p) { v = *reinterpret_cast<const uint4*>(p); }
+    __device__ __forceinline__ void to_float(float (&f)[8]) const {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = __uint_as_float(w[i] << 16);
+            f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+};
+
+template <>
+struct Raw8<float> {
+    float4 a, b;
+    __device__ __forceinline__ void load(const float* p) {
+        a = *reinterpret_cast<const float4*>(p);
+        b = *reinterpret_cast<const float4*>(p + 4);
+    }
+    __device__ __forceinline__ void to_float(float (&f)[8]) const {
+        f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+        f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+    }
+};
+
+// ---------------------------------------------------------------------------
 // Prologue.  256 threads; each row of D channels is handled by D/8 threads
 // holding 8 consecutive channels (RoPE pairs never straddle threads).
 template <int D, typename TIn>
@@ -81,42 +114,60 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
     const int rot_width = pairs * 6;
     const long head_rows = (long)head * seg_total + w.seg_off;
 
-    // passes fully unrolled so every row's loads can be in flight together
+    constexpr int NP = CHUNK / RPP;      // rows per thread
+    // Every row's q, k and v loads are issued before any of them is used, so
+    // a thread keeps 3 * NP loads in flight; rows past the sequence (padding)
+    // read video row 0 and are zeroed afterwards.
+    Raw8<TIn> rq[NP], rk[NP], rv[NP];
+    float2 cs[NP][4];   // RoPE (cos, sin) of this thread's four channel pairs
+    // norm weights of this thread's 8 channels: video q, video k, text q, text k
+    float nw[4][8];
 #pragma unroll
-    for (int pass = 0; pass < CHUNK / RPP; ++pass) {
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) nw[t][i] = norm[t * D + d0 + i];
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
+        const int r = ch.row0 + pass * RPP + tid / TPR;   // row within the window sequence
+        const bool video = r < w.n_video;
+        const TokenCoord tc = window_token(w, video ? r : 0);
+        // window-local video position, temporal axis offset by the text
+        // length (:901-902); text position (i,i,i) (:915)
+        const int tt = r - w.n_video;
+        const int pos[3] = {video ? tc.lt + w.text_len : tt, video ? tc.lh : tt, video ? tc.lw : tt};
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+            // pair (2p, 2p+1) of axis a is rotated by pos[a] * f[p]; pairs
+            // past the rotated width are left unrotated
+            const int d = d0 + 2 * pp;
+            const int axis = d / (2 * pairs > 0 ? 2 * pairs : 1);
+            const int pair = (d - axis * 2 * pairs) >> 1;
+            const bool rot = d < rot_width && r < w.seq;
+            cs[pass][pp] = rot ? rope[pos[axis < 3 ? axis : 0] * pairs + pair] : make_float2(1.f, 0.f);
+        }
+        const long src = video ? tc.src : (long)w.text_off + tt;
+        const bool ok = r < w.seq;
+        const TIn* bq = video || !ok ? vq : tq;
+        const TIn* bk = video || !ok ? vk : tk;
+        const TIn* bv = video || !ok ? vv : tv;
+        const long row = ok ? src : 0;
+        const long stride = video || !ok ? vstride : tstride;
+        const int col = head * D + d0;
+        rq[pass].load(bq + row * stride + col);
+        rk[pass].load(bk + row * stride + col);
+        rv[pass].load(bv + row * stride + col);
+    }
+#pragma unroll
+    for (int pass = 0; pass < NP; ++pass) {
         const int rl = pass * RPP + tid / TPR;   // row within the chunk
-        const int r = ch.row0 + rl;                 // row within the window sequence
+        const int r = ch.row0 + rl;               // row within the window sequence
         uint16_t qb[8], kb[8], vb[8];
         if (r < w.seq) {
-            const TIn *sq, *sk, *sv;
-            const float *wq, *wk;
-            int pos[3];
-            if (r < w.n_video) {
-                const TokenCoord c = window_token(w, r);
-                sq = vq + c.src * vstride;
-                sk = vk + c.src * vstride;
-                sv = vv + c.src * vstride;
-                wq = norm;
-                wk = norm + D;
-                // window-local position, temporal axis offset by the text length (:901-902)
-                pos[0] = c.lt + w.text_len;
-                pos[1] = c.lh;
-                pos[2] = c.lw;
-            } else {
-                const int tt = r - w.n_video;
-                const long src = (long)w.text_off + tt;
-                sq = tq + src * tstride;
-                sk = tk + src * tstride;
-                sv = tv + src * tstride;
-                wq = norm + 2 * D;
-                wk = norm + 3 * D;
-                pos[0] = pos[1] = pos[2] = tt;     // text position (i,i,i) (:915)
-            }
-            const int col = head * D + d0;
+            const bool video = r < w.n_video;
             float q[8], k[8], v[8];
-            load8(sq + col, q);
-            load8(sk + col, k);
-            load8(sv + col, v);
+            rq[pass].to_float(q);
+            rk[pass].to_float(k);
+            rv[pass].to_float(v);
             float sq2 = 0.f, sk2 = 0.f;
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -133,23 +184,20 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
             const float inv_k = 1.f / sqrtf(sk2 / (float)D + eps);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                q[i] = q[i] * inv_q * wq[d0 + i];
-                k[i] = k[i] * inv_k * wk[d0 + i];
+                q[i] = q[i] * inv_q * (video ? nw[0][i] : nw[2][i]);
+                k[i] = k[i] * inv_k * (video ? nw[1][i] : nw[3][i]);
             }
             // apply_mm_rope (:521-543): pair (2p, 2p+1) of axis a rotated by pos[a]*f[p]
 #pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
-                const int d = d0 + 2 * pp;
-                if (d < rot_width) {
-                    const int axis = d / (2 * pairs);
-                    const int pair = (d - axis * 2 * pairs) >> 1;
-                    const float2 cs = rope[pos[axis] * pairs + pair];
+                if (d0 + 2 * pp < rot_width) {
+                    const float2 c = cs[pass][pp];
                     const float q0 = q[2 * pp], q1 = q[2 * pp + 1];
                     const float k0 = k[2 * pp], k1 = k[2 * pp + 1];
-                    q[2 * pp] = q0 * cs.x - q1 * cs.y;
-                    q[2 * pp + 1] = q0 * cs.y + q1 * cs.x;
-                    k[2 * pp] = k0 * cs.x - k1 * cs.y;
-                    k[2 * pp + 1] = k0 * cs.y + k1 * cs.x;
+                    q[2 * pp] = q0 * c.x - q1 * c.y;
+                    q[2 * pp + 1] = q0 * c.y + q1 * c.x;
+                    k[2 * pp] = k0 * c.x - k1 * c.y;
+                    k[2 * pp + 1] = k0 * c.y + k1 * c.x;
                 }
             }
 #pragma unroll
@@ -459,10 +507,13 @@ __global__ void awa_text_pool_kernel(const SampleMeta* __restrict__ samples,
     const int c = (int)(i - (long)row * q4) * 4;
     const SampleMeta sm = samples[text_sample[row]];
     const int tt = row - sm.text_off;
+    // the sample's windows hold consecutive partial blocks of text_len rows
+    const float* p = partial + ((long)wins[sm.first_window].tpart_off + tt) * inner + c;
+    const long step = (long)sm.text_len * inner;
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
     for (int k = 0; k < sm.num_windows; ++k) {
-        const int tp = wins[sm.first_window + k].tpart_off;
-        const float4 x = *reinterpret_cast<const float4*>(partial + (long)(tp + tt) * inner + c);
+        const float4 x = *reinterpret_cast<const float4*>(p + k * step);
         acc.x += x.x * sm.pool_scale;
         acc.y += x.y * sm.pool_scale;
         acc.z += x.z * sm.pool_scale;
