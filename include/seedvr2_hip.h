@@ -157,7 +157,11 @@ int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream
  * weight: device bf16 [n][k] row-major (the reference [N][K] layout,
  * :66-69); bias: device fp32 [n] or NULL (param 2).  x_*: device
  * [m_*][k] in x_dtype; y_*: device [m_*][n] in y_dtype.  Either stream may
- * have m == 0 (its pointers are then ignored).  k must be a multiple of 8. */
+ * have m == 0 (its pointers are then ignored).  k must be a multiple of 8.
+ * The first call on a device allocates that device's split-k scratch (about
+ * 128 MB of partial-tile slots and their counters), kept until the process
+ * ends; calls whose kernels overlap in time on one device (different streams)
+ * share it and must not run concurrently. */
 int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
                              s2_dtype x_dtype, const uint16_t* weight, const float* bias,
                              int n, int k, int activation,
