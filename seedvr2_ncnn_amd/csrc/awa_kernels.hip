@@ -370,75 +370,91 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
 
     issue(0, 0);
     if (nkt > 1) issue(1, 1);
+    // The tile loop is unrolled by the stage count so that every LDS
+    // address is a loop-invariant register plus a constant stage offset.
 #pragma unroll 1
-    for (int kt = 0; kt < nkt; ++kt) {
-        if (kt + 1 < nkt) {   // stage kt+1 may stay in flight
-            if constexpr (DMA_W == 4)
-                asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-            else
-                asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-        } else {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        }
-        __syncthreads();   // tile kt visible to all waves; tile kt-1 no longer read
-        if (kt + 2 < nkt) issue((kt + 2) % STAGES, kt + 2);
-        const uint8_t* st = lds + (kt % STAGES) * SB;
+    for (int kt0 = 0; kt0 < nkt; kt0 += STAGES) {
+#pragma unroll
+        for (int u = 0; u < STAGES; ++u) {
+            const int kt = kt0 + u;
+            if (kt >= nkt) break;
+            if (kt + 1 < nkt) {   // stage kt+1 may stay in flight
+                if constexpr (DMA_W == 4)
+                    asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+                else
+                    asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+            } else {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
+            __syncthreads();   // tile kt visible to all waves; tile kt-1 no longer read
+            if (kt + 2 < nkt) issue((u + 2) % STAGES, kt + 2);
+            const uint8_t* st = lds + u * SB;
 
-        f32x16 s;
+            // S^T = K Q^T as two independent MFMA chains (even and odd
+            // 16-channel slices), summed afterwards
+            f32x16 s0, s1;
+            const uint8_t* kp = st + krow * (D * 2);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = 0.f;
-        const uint8_t* kp = st + krow * (D * 2);
-#pragma unroll
-        for (int kk = 0; kk < NKK; ++kk) {
-            const bf16x8 a = as_bf16x8(*(const uint4*)(kp + (((2 * kk + g) ^ kswz) * 16)));
-            s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qf[kk], s, 0, 0, 0);
-        }
-        // keys past the window's sequence (only in the last tile) are masked
-        const int key_base = kt * KT;
-        if (key_base + KT > w.seq) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                // register i of lane group g holds key 16*(i/8) + 8g + (i%8)
-                const int key = key_base + 16 * (i >> 3) + 8 * g + (i & 7);
-                if (key >= w.seq) s[i] = -INFINITY;
+            for (int kk = 0; kk < NKK; kk += 2) {
+                const bf16x8 a0 = as_bf16x8(*(const uint4*)(kp + (((2 * kk + g) ^ kswz) * 16)));
+                const bf16x8 a1 =
+                    as_bf16x8(*(const uint4*)(kp + (((2 * kk + 2 + g) ^ kswz) * 16)));
+                if (kk == 0) {
+                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[kk], f32x16{}, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[kk + 1], f32x16{}, 0, 0, 0);
+                } else {
+                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[kk], s0, 0, 0, 0);
+                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[kk + 1], s1, 0, 0, 0);
+                }
             }
-        }
-        float mx = s[0];
+            f32x16 s = s0 + s1;
+            // keys past the window's sequence (only in the last tile) are masked
+            const int key_base = kt * KT;
+            if (key_base + KT > w.seq) {
 #pragma unroll
-        for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
-        float alpha = 1.f;
-        if (mx > m_run + kLazy) {
-            alpha = __builtin_amdgcn_exp2f(m_run - mx);   // 0 on the first tile
-            m_run = mx;
-        }
-        float psum = 0.f;
-        bf16x8 pb[2];
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            bf16x8 v;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float p = __builtin_amdgcn_exp2f(fmaf(s[8 * half + j], scale_log2, -m_run));
-                psum += p;
-                v[j] = (__bf16)p;
+                for (int i = 0; i < 16; ++i) {
+                    // register i of lane group g holds key 16*(i/8) + 8g + (i%8)
+                    const int key = key_base + 16 * (i >> 3) + 8 * g + (i & 7);
+                    if (key >= w.seq) s[i] = -INFINITY;
+                }
             }
-            pb[half] = v;
-        }
-        l_run = l_run * alpha + psum;
-        if (__any(alpha != 1.f)) {
+            float mx = s[0];
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
+            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+            float alpha = 1.f;
+            if (mx > m_run + kLazy) {
+                alpha = __builtin_amdgcn_exp2f(m_run - mx);   // 0 on the first tile
+                m_run = mx;
+            }
+            float p[16];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
-        }
+            for (int i = 0; i < 16; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(s[i], scale_log2, -m_run));
+            bf16x8 pb[2];
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-            const uint8_t* vp = st + KB + (32 * dt + l32) * (KT * 2);
+            for (int half = 0; half < 2; ++half)
 #pragma unroll
-            for (int ps = 0; ps < 2; ++ps) {
-                const bf16x8 a = as_bf16x8(*(const uint4*)(vp + (((2 * ps + g) ^ vswz) * 16)));
-                o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ps], o[dt], 0, 0, 0);
+                for (int j = 0; j < 8; ++j) pb[half][j] = (__bf16)p[8 * half + j];
+            // pairwise sum: a dependency depth of 4 instead of 16
+#pragma unroll
+            for (int w2 = 8; w2 >= 1; w2 >>= 1)
+#pragma unroll
+                for (int i = 0; i < w2; ++i) p[i] += p[i + w2];
+            l_run = l_run * alpha + p[0];
+            if (__any(alpha != 1.f)) {
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+            }
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) {
+                const uint8_t* vp = st + KB + (32 * dt + l32) * (KT * 2);
+#pragma unroll
+                for (int ps = 0; ps < 2; ++ps) {
+                    const bf16x8 a = as_bf16x8(*(const uint4*)(vp + (((2 * ps + g) ^ vswz) * 16)));
+                    o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[ps], o[dt], 0, 0, 0);
+                }
             }
         }
     }
