@@ -311,6 +311,7 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     // Q fragment (B operand of S^T = K Q^T): query row l32 of this wave,
     // channels 16kk + 8g .. +7.
     const int qrow = it.q_row0 + wave * 32 + l32;
+    const bool wave_active = it.q_row0 + wave * 32 < w.seq;
     bf16x8 qf[NKK];
     {
         const bool valid = qrow < w.seq;
@@ -392,6 +393,9 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
 
             // S^T = K Q^T as two independent MFMA chains (even and odd
             // 16-channel slices), summed afterwards
+            // a wave whose 32 query rows all lie past the sequence (the last
+            // q-tile of a window) only takes part in the DMA and barriers
+            if (!wave_active) continue;
             f32x16 s0, s1;
             const uint8_t* kp = st + krow * (D * 2);
 #pragma unroll
@@ -480,8 +484,8 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
                 }
                 if (out_bf16) {
                     uint2 pk;
-                    pk.x = (uint32_t)f32_to_bf16(vals[0]) | ((uint32_t)f32_to_bf16(vals[1]) << 16);
-                    pk.y = (uint32_t)f32_to_bf16(vals[2]) | ((uint32_t)f32_to_bf16(vals[3]) << 16);
+                    pk.x = pack2_bf16_rne(vals[0], vals[1]);
+                    pk.y = pack2_bf16_rne(vals[2], vals[3]);
                     *reinterpret_cast<uint2*>((uint16_t*)out_video + obase + ch) = pk;
                 } else {
                     *reinterpret_cast<float4*>((float*)out_video + obase + ch) =
@@ -537,8 +541,8 @@ __global__ void awa_text_pool_kernel(const SampleMeta* __restrict__ samples,
     }
     if (out_bf16) {
         uint2 pk;
-        pk.x = (uint32_t)f32_to_bf16(acc.x) | ((uint32_t)f32_to_bf16(acc.y) << 16);
-        pk.y = (uint32_t)f32_to_bf16(acc.z) | ((uint32_t)f32_to_bf16(acc.w) << 16);
+        pk.x = pack2_bf16_rne(acc.x, acc.y);
+        pk.y = pack2_bf16_rne(acc.z, acc.w);
         *reinterpret_cast<uint2*>((uint16_t*)out + (long)row * inner + c) = pk;
     } else {
         *reinterpret_cast<float4*>((float*)out + (long)row * inner + c) = acc;

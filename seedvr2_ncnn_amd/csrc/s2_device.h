@@ -35,6 +35,14 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
     return (uint16_t)(b >> 16);
 }
 
+// two floats -> packed bf16 pair (low, high) with the hardware conversion
+// (v_cvt_pk_bf16_f32, round to nearest even; equal to f32_to_bf16 for every
+// non-NaN input)
+__device__ __forceinline__ uint32_t pack2_bf16_rne(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(((uint32_t)h) << 16);
 }
