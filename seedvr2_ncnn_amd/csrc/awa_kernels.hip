@@ -29,12 +29,22 @@ struct TokenCoord {
     long src;
 };
 
+// a / b for 0 <= a < 2^22, b > 0: the fp32 quotient is within one of the
+// true one, and one correction step makes it exact (cheaper than the
+// integer division sequence)
+__device__ __forceinline__ int div_small(int a, int b) {
+    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
+    const int r = a - q * b;
+    q += (r >= b) - (r < 0);
+    return q;
+}
+
 __device__ __forceinline__ TokenCoord window_token(const WinMeta& w, int r) {
     TokenCoord c;
     const int plane = w.eh * w.ew;
-    c.lt = r / plane;
+    c.lt = div_small(r, plane);
     const int rem = r - c.lt * plane;
-    c.lh = rem / w.ew;
+    c.lh = div_small(rem, w.ew);
     c.lw = rem - c.lh * w.ew;
     c.src = (long)w.tok_off +
             ((long)(w.t0 + c.lt) * w.grid_h + (w.h0 + c.lh)) * w.grid_w + (w.w0 + c.lw);
