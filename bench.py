@@ -48,10 +48,15 @@ def attention_flops(shifted):
     return sum(4 * HEADS * HEAD_DIM * (w[8] + TEXT_TOKENS) ** 2 for w in wins)
 
 
-def prologue_bytes(lv, lt):
-    # read q,k,v bf16 once + write windowed q,k,v bf16 once + int32 index and
-    # three positions per video token
-    return 2 * (lv + lt) * 3 * HIDDEN * 2 + 16 * lv
+def prologue_bytes(shifted, hidden=HIDDEN):
+    """Algorithmic HBM bytes of the attention prologue: read the bf16 q, k, v
+    of every video and text token once, write the windowed bf16 Q, K and V^T
+    of every video token once and of the text tokens once per window.  The
+    window index math reads no tables."""
+    from seedvr2_ncnn_amd import capi
+    wins, _, _ = capi.plan_windows([VIDEO_SHAPE], TARGET, shifted)
+    lv = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2]
+    return (lv + TEXT_TOKENS) * 3 * hidden * 2 + (lv + len(wins) * TEXT_TOKENS) * 3 * hidden * 2
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "shared_linear_mlp_up_720p_video_traffic.md")
@@ -314,6 +319,33 @@ def main():
         flops = dict(gemm, attention=attention_flops(shifted))
         results[shifted] = (ms, per_op, flops, wall)
 
+    # per-kernel times of the attention forward from events the library
+    # records around its four kernels (separate runs: the timed loop above
+    # records none)
+    stages = {}
+    for shifted in (0, 1):
+        capi.awa_stage_timing(True)
+        acc = {}
+        reps = max(3, args.steps // 2)
+        for _ in range(reps):
+            step(shifted)
+            for key, v in capi.awa_stage_times().items():
+                acc[key] = acc.get(key, 0.0) + v / reps
+        capi.awa_stage_timing(False)
+        pb = prologue_bytes(shifted)
+        af = attention_flops(shifted)
+        stages["shifted" if shifted else "regular"] = {
+            "rope_table_ms": round(acc["rope_table"], 4),
+            "prologue_ms": round(acc["prologue"], 4),
+            "prologue_algorithmic_bytes": pb,
+            "prologue_gbs": round(pb / (acc["prologue"] * 1e-3) / 1e9, 1),
+            "prologue_frac_hbm_peak": round(pb / (acc["prologue"] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+            "attention_kernel_ms": round(acc["attention"], 4),
+            "attention_kernel_tflops": round(af / (acc["attention"] * 1e-3) / 1e12, 1),
+            "attention_kernel_frac_bf16_peak": round(af / (acc["attention"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "text_pool_ms": round(acc["text_pool"], 4),
+        }
+
     ms, per_op, flops, wall = results[0]
     block_flops = sum(flops.values())
     value = block_flops / (ms * 1e-3) / 1e12
@@ -352,7 +384,7 @@ def main():
         "attention_shifted": {"ms": round(per_op_s["attention"], 4),
                               "tflops": round(flops_s["attention"] / (per_op_s["attention"] * 1e-3) / 1e12, 1)},
         "kernels": kernels,
-        "prologue_algorithmic_bytes": prologue_bytes(lv, lt),
+        "attention_stages": stages,
         "roofline": {
             "kernel": "s2::shared_linear_256_kernel<true, 1> (MLP up 2560->10240 + GELU, M=21664)",
             "bound": "mfma",

@@ -15,6 +15,14 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/* Only the functions below are exported; the library is built with hidden
+ * default visibility. */
+#if defined(__GNUC__) || defined(__clang__)
+#define S2_API __attribute__((visibility("default")))
+#else
+#define S2_API
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -74,15 +82,15 @@ typedef struct s2_awa_plan_info {
 /* ---- device memory (so layer host code needs no HIP headers) ---------- */
 
 /* Number of gfx950 devices visible; 0 with S2_OK when there are none. */
-int s2_device_count(int* count);
-int s2_malloc(void** ptr, size_t bytes);
-int s2_free(void* ptr);
-int s2_memcpy_h2d(void* dst, const void* src, size_t bytes, s2_stream_t stream);
-int s2_memcpy_d2h(void* dst, const void* src, size_t bytes, s2_stream_t stream);
-int s2_memcpy_d2d(void* dst, const void* src, size_t bytes, s2_stream_t stream);
-int s2_stream_synchronize(s2_stream_t stream);
+S2_API int s2_device_count(int* count);
+S2_API int s2_malloc(void** ptr, size_t bytes);
+S2_API int s2_free(void* ptr);
+S2_API int s2_memcpy_h2d(void* dst, const void* src, size_t bytes, s2_stream_t stream);
+S2_API int s2_memcpy_d2h(void* dst, const void* src, size_t bytes, s2_stream_t stream);
+S2_API int s2_memcpy_d2d(void* dst, const void* src, size_t bytes, s2_stream_t stream);
+S2_API int s2_stream_synchronize(s2_stream_t stream);
 /* Last HIP error string recorded by this library on the calling thread. */
-const char* s2_last_error(void);
+S2_API const char* s2_last_error(void);
 
 /* ---- window plan -------------------------------------------------------- */
 
@@ -91,7 +99,7 @@ const char* s2_last_error(void);
  * (w outer, h, t inner, per sample).  video_shapes is [batch][3] (t,h,w).
  * Pass windows == NULL to query *num_windows.  sample_window_count
  * ([batch]) and video_tokens may be NULL.  Returns S2_OK or S2_ERR_INVALID. */
-int s2_awa_plan_windows(const int* video_shapes, int batch, const int target_windows[3],
+S2_API int s2_awa_plan_windows(const int* video_shapes, int batch, const int target_windows[3],
                         int shifted, s2_window_slice* windows, int max_windows,
                         int* num_windows, int* sample_window_count, int* video_tokens);
 
@@ -99,20 +107,20 @@ int s2_awa_plan_windows(const int* video_shapes, int batch, const int target_win
  * reference rebuilds its plan on every forward, :833-836 and :1116-1120; a
  * caller keeps this handle while the shapes stay the same).  text_lengths is
  * [batch], each > 0 (reference :813-814). */
-int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
+S2_API int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
                        const int* text_lengths, int batch, s2_awa_plan** plan);
-int s2_awa_plan_get_info(const s2_awa_plan* plan, s2_awa_plan_info* info);
+S2_API int s2_awa_plan_get_info(const s2_awa_plan* plan, s2_awa_plan_info* info);
 /* Copies the plan's window list / per-sample window counts to host arrays. */
-int s2_awa_plan_get_windows(const s2_awa_plan* plan, s2_window_slice* windows,
+S2_API int s2_awa_plan_get_windows(const s2_awa_plan* plan, s2_window_slice* windows,
                             int max_windows, int* sample_window_count);
-int s2_awa_plan_destroy(s2_awa_plan* plan);
+S2_API int s2_awa_plan_destroy(s2_awa_plan* plan);
 
 /* Materialises the plan's per-token tables on the device with the same
  * integer index math the forward kernels use: video_indices[L] (partition ->
  * source token), inverse_video_indices[L], local_positions[L][3]
  * (AdaptiveWindowPlan, adaptive_window_attention.h:29-36).  int32 device
  * arrays; any may be NULL. */
-int s2_awa_plan_tables(const s2_awa_plan* plan, int* video_indices,
+S2_API int s2_awa_plan_tables(const s2_awa_plan* plan, int* video_indices,
                        int* inverse_video_indices, int* local_positions,
                        s2_stream_t stream);
 
@@ -135,7 +143,7 @@ int s2_awa_plan_tables(const s2_awa_plan* plan, int* video_indices,
  * out_video [video_tokens][inner], out_text [text_tokens][inner] in out_dtype.
  * workspace: device memory of at least info.workspace_bytes, 256-byte aligned.
  * All work is enqueued on stream; nothing is synchronised. */
-int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights,
+S2_API int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights,
                    const float* rope_freqs,
                    const void* video_q, const void* video_k, const void* video_v,
                    long video_row_stride,
@@ -144,12 +152,21 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights,
                    void* out_video, void* out_text, s2_dtype out_dtype,
                    void* workspace, size_t workspace_bytes, s2_stream_t stream);
 
+/* Stage timing of s2_awa_forward, a diagnostic with no counterpart in the
+ * reference.  While enabled on the calling thread, every s2_awa_forward
+ * records HIP events on its stream around its four kernels: RoPE table,
+ * prologue (window gather, RMSNorm, RoPE), attention, text pool.
+ * s2_awa_stage_times waits for the last such forward and returns the four
+ * durations in milliseconds. */
+S2_API int s2_awa_stage_timing(int enable);
+S2_API int s2_awa_stage_times(float stage_ms[4]);
+
 /* ---- SharedLinear -------------------------------------------------------- */
 
 /* fp32 -> bf16 (round to nearest even) on the device; used to keep weights
  * resident in bf16 (SharedLinear::load_model, shared_linear.cpp:61-81). */
-int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream_t stream);
-int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream_t stream);
+S2_API int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream_t stream);
+S2_API int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream_t stream);
 
 /* SharedLinear::forward (shared_linear.cpp:83-96): one projection applied to
  * two token streams in ONE grouped launch sharing the weight:
@@ -162,7 +179,7 @@ int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream
  * 128 MB of partial-tile slots and their counters), kept until the process
  * ends; calls whose kernels overlap in time on one device (different streams)
  * share it and must not run concurrently. */
-int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
+S2_API int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
                              s2_dtype x_dtype, const uint16_t* weight, const float* bias,
                              int n, int k, int activation,
                              void* y_video, void* y_text, s2_dtype y_dtype,

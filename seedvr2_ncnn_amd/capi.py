@@ -30,7 +30,8 @@ EXPORTS = (
     "s2_memcpy_d2d", "s2_stream_synchronize", "s2_last_error", "s2_awa_plan_windows",
     "s2_awa_plan_create", "s2_awa_plan_get_info", "s2_awa_plan_get_windows",
     "s2_awa_plan_destroy", "s2_awa_plan_tables", "s2_awa_forward", "s2_cast_f32_to_bf16",
-    "s2_cast_bf16_to_f32", "s2_shared_linear_forward",
+    "s2_cast_bf16_to_f32", "s2_shared_linear_forward", "s2_awa_stage_timing",
+    "s2_awa_stage_times",
 )
 
 
@@ -98,6 +99,8 @@ def lib() -> ctypes.CDLL:
         L.s2_cast_f32_to_bf16.argtypes = [vp, vp, sz, vp]
         L.s2_cast_bf16_to_f32.argtypes = [vp, vp, sz, vp]
         L.s2_shared_linear_forward.argtypes = [vp, ci, vp, ci, ci, vp, vp, ci, ci, ci, vp, vp, ci, vp]
+        L.s2_awa_stage_timing.argtypes = [ci]
+        L.s2_awa_stage_times.argtypes = [P(ctypes.c_float)]
         _LIB = L
     return _LIB
 
@@ -259,6 +262,23 @@ def awa_forward(plan: AwaPlan, norm_weights, rope_freqs, video_q, video_k, video
                                _ptr(workspace), workspace.numel(), _stream(stream)),
           "s2_awa_forward")
     return out_video, out_text
+
+
+AWA_STAGES = ("rope_table", "prologue", "attention", "text_pool")
+
+
+def awa_stage_timing(enable: bool) -> None:
+    """s2_awa_stage_timing: record events around the four kernels of every
+    awa_forward on this thread (a diagnostic)."""
+    check(lib().s2_awa_stage_timing(1 if enable else 0), "s2_awa_stage_timing")
+
+
+def awa_stage_times() -> dict:
+    """s2_awa_stage_times: milliseconds of the last timed awa_forward's
+    RoPE table, prologue, attention and text-pool kernels."""
+    out = (ctypes.c_float * 4)()
+    check(lib().s2_awa_stage_times(out), "s2_awa_stage_times")
+    return dict(zip(AWA_STAGES, (float(v) for v in out)))
 
 
 def cast_f32_to_bf16(src, dst=None, stream=None):

@@ -250,6 +250,19 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
     }
 }
 
+// v_permlane32_swap with the same value in both operands leaves, in every
+// lane, the pair {x[lane], x[lane ^ 32]} in its two results (a VALU op, no
+// LDS round trip as with a shuffle).
+__device__ __forceinline__ float max_with_lane_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float sum_with_lane_xor32(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // ---------------------------------------------------------------------------
 // Flash window attention.
 //
@@ -435,7 +448,7 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
             float mx = s[0];
 #pragma unroll
             for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
-            mx = fmaxf(mx, __shfl_xor(mx, 32)) * scale_log2;
+            mx = max_with_lane_xor32(mx) * scale_log2;
             float alpha = 1.f;
             if (mx > m_run + kLazy) {
                 alpha = __builtin_amdgcn_exp2f(m_run - mx);   // 0 on the first tile
@@ -473,7 +486,7 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
         }
     }
 
-    const float l_tot = l_run + __shfl_xor(l_run, 32);
+    const float l_tot = sum_with_lane_xor32(l_run);
     const float inv_l = 1.f / l_tot;
     if (qrow >= w.seq) return;
     // O^T register i of tile dt: channel 32dt + 8(i/4) + 4g + (i%4), query l32

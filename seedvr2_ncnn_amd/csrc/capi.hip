@@ -40,6 +40,23 @@ bool valid_config(const s2_awa_config* c) {
 
 }  // namespace
 
+namespace {
+
+// Per-thread stage timing of s2_awa_forward (s2_awa_stage_timing).
+struct StageTimer {
+    bool on = false;
+    bool created = false;
+    bool recorded = false;
+    hipEvent_t ev[5] = {};
+};
+
+StageTimer& stage_timer() {
+    thread_local StageTimer t;
+    return t;
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* s2_last_error(void) { return g_last_error.c_str(); }
@@ -352,14 +369,43 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
     float* tpart = (float*)(ws + plan->off_tpart);
     const bool in_bf16 = in_dtype == S2_DTYPE_BF16;
     const bool out_bf16 = out_dtype == S2_DTYPE_BF16;
+    StageTimer& tm = stage_timer();
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[0], s));
     if (plan->config.rope_pairs_per_axis > 0)
         S2_HIP(s2::launch_rope_table(rope_freqs, plan->config.rope_pairs_per_axis,
                                      plan->rope_positions, rope, s));
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[1], s));
     S2_HIP(s2::launch_awa_prologue(*plan, video_q, video_k, video_v, video_row_stride, text_q,
                                    text_k, text_v, text_row_stride, in_bf16, norm_weights, rope, q,
                                    k, vt, s));
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[2], s));
     S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, out_bf16, tpart, s));
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[3], s));
     S2_HIP(s2::launch_awa_text_pool(*plan, tpart, out_text, out_bf16, s));
+    if (tm.on) {
+        S2_HIP(hipEventRecord(tm.ev[4], s));
+        tm.recorded = true;
+    }
+    return S2_OK;
+}
+
+int s2_awa_stage_timing(int enable) {
+    StageTimer& tm = stage_timer();
+    if (enable && !tm.created) {
+        for (hipEvent_t& e : tm.ev) S2_HIP(hipEventCreate(&e));
+        tm.created = true;
+    }
+    tm.on = enable != 0;
+    tm.recorded = false;
+    return S2_OK;
+}
+
+int s2_awa_stage_times(float stage_ms[4]) {
+    if (!stage_ms) return fail(S2_ERR_INVALID, "null argument");
+    StageTimer& tm = stage_timer();
+    if (!tm.created || !tm.recorded) return fail(S2_ERR_INVALID, "no timed forward recorded");
+    S2_HIP(hipEventSynchronize(tm.ev[4]));
+    for (int i = 0; i < 4; ++i) S2_HIP(hipEventElapsedTime(&stage_ms[i], tm.ev[i], tm.ev[i + 1]));
     return S2_OK;
 }
 

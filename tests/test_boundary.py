@@ -29,6 +29,19 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(L, name), name
 
 
+def test_library_exports_only_declared_functions():
+    """libseedvr2_hip.so is built with hidden visibility: its dynamic symbol
+    table holds the functions of include/seedvr2_hip.h and no internals."""
+    import shutil
+    import subprocess
+    if shutil.which("nm") is None:
+        pytest.skip("nm not available")
+    out = subprocess.run(["nm", "-D", "--defined-only", capi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    funcs = sorted(line.split()[-1] for line in out.splitlines() if line.split()[1:2] == ["T"])
+    assert funcs == _declared_symbols()
+
+
 def test_layers_library_loads():
     ctypes.CDLL(capi.LAYERS_PATH)
 
