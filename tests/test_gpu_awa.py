@@ -185,6 +185,20 @@ def test_video_grid_6x45x80_dim2560(shifted):
 
 
 @pytest.mark.parametrize("shifted", [0, 1])
+def test_batch_of_video_image_and_ragged_samples_dim2560(shifted):
+    """Three samples in one call (720p video, one 1024x1024 image, a ragged
+    3x17x29 grid) with different text lengths: windows never mix samples and
+    every sample pools its own text over its own windows (:963-974)."""
+    import torch
+    shapes, tl = [(6, 45, 80), (1, 64, 64), (3, 17, 29)], [64, 32, 77]
+    case = make_awa_inputs(909 + shifted, shapes, tl, 20, 128, 21, bf16=True)
+    ov, ot = _run_capi(case, 20, 128, (4, 3, 3), shifted, 21, shapes, tl, True, torch.float32)
+    rv, rt = oracle_awa(case, 20, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl, fast=True)
+    assert_close(ov, rv, "video")
+    assert_close(ot, rt, "text")
+
+
+@pytest.mark.parametrize("shifted", [0, 1])
 def test_video_grid_6x45x80_dim3072_24_heads(shifted):
     """SeedVR2-7B attention shape: the 720p 21-frame grid, hidden 3072,
     24 heads x 128 (one layer of the 32-block stack)."""

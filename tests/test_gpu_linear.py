@@ -174,3 +174,20 @@ def test_split_tail_is_deterministic(mv, mt, k, n):
     rows = np.concatenate([np.arange(0, 3), g.integers(0, mv, 20), np.arange(mv - 3, mv)]).astype(np.int32)
     assert_close(outs[0][0][rows], oracle.linear(xv, w, b, 1, rows=rows, threads=THREADS), "video rows")
     assert _tight(outs[0][0][rows], xv, bf16_round(w), b, 1, rows=rows) < 2e-4
+
+
+def test_fp32_activations_medium_shape():
+    """fp32 activations take the 128x128-tile path (rounded to bf16 while
+    staged): a 4,100-row, K = 2560 -> N = 2560 projection with GELU."""
+    g = np.random.default_rng(4100)
+    mv, mt, k, n = 4036, 64, 2560, 2560
+    xv = g.standard_normal((mv, k), dtype=np.float32)
+    xt = g.standard_normal((mt, k), dtype=np.float32)
+    w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
+    b = (0.02 * g.standard_normal(n)).astype(np.float32)
+    yv, yt = _gpu_linear(xv, xt, w, b, 1, False, False)
+    rows = np.concatenate([np.arange(0, 4), g.integers(0, mv, 40), np.arange(mv - 4, mv)]).astype(np.int32)
+    assert_close(yv[rows], oracle.linear(xv, w, b, 1, rows=rows, threads=THREADS), "video rows")
+    assert_close(yt, oracle.linear(xt, w, b, 1, threads=THREADS), "text")
+    assert _tight(yv[rows], bf16_round(xv), bf16_round(w), b, 1, rows=rows) < 2e-4
+
