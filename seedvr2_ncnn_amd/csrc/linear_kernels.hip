@@ -30,18 +30,23 @@ __device__ __forceinline__ uint4 load_chunk(const float* p) {
     return pack8_bf16(h);
 }
 
-// erf-GELU, 0.5 x (1 + erf(x / sqrt 2)), with erf from Abramowitz & Stegun
-// 7.1.26: 1 - erf(z) = (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) e^(-z^2),
-// t = 1 / (1 + p z), z >= 0, |error| <= 1.5e-7.  The negative branch uses
-// the complement directly, so small outputs keep their relative accuracy.
+// erf-GELU, 0.5 x (1 + erf(x / sqrt 2)) = max(x, 0) - |x| Q(|x|) with
+// Q(a) = 0.5 erfc(a / sqrt 2): both signs reduce to one fma, and for x < 0
+// the result is the product -|x| Q directly, without cancellation.  erfc is
+// Abramowitz & Stegun 7.1.26, erfc(z) = (a1 t + ... + a5 t^5) e^(-z^2),
+// t = 1 / (1 + p z), |error| <= 1.5e-7; the factor 0.5 is folded into a1..a5
+// and e^(-z^2) = 2^(-w^2) with w = z sqrt(log2 e).
 __device__ __forceinline__ float gelu(float x) {
-    const float z = fabsf(x) * 0.70710678118654752f;
-    const float t = __builtin_amdgcn_rcpf(1.f + 0.3275911f * z);
+    constexpr float kSqrtLog2e = 1.2011224087864498f;
+    const float ax = fabsf(x);
+    const float w = ax * (0.70710678118654752f * kSqrtLog2e);
+    const float t = __builtin_amdgcn_rcpf(fmaf(w, 0.3275911f / kSqrtLog2e, 1.f));
     const float poly =
-        t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f +
-                                                                          t * 1.061405429f))));
-    const float c = poly * __expf(-z * z);   // 1 - erf(|x| / sqrt 2)
-    return x >= 0.f ? x * (1.f - 0.5f * c) : 0.5f * x * c;
+        t * (0.5f * 0.254829592f +
+             t * (0.5f * -0.284496736f +
+                  t * (0.5f * 1.421413741f + t * (0.5f * -1.453152027f + t * (0.5f * 1.061405429f)))));
+    const float q = poly * __builtin_amdgcn_exp2f(-w * w);   // Q(|x|)
+    return fmaf(-ax, q, fmaxf(x, 0.f));
 }
 
 }  // namespace
@@ -238,7 +243,7 @@ template <bool Y_BF16, int ACT>
 __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const uint16_t* __restrict__ x0, int m0, const uint16_t* __restrict__ x1, int m1,
     const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
-    void* __restrict__ y0, void* __restrict__ y1, int mt0, int mtiles, int ntiles, SkTail sk) {
+    void* __restrict__ y0, void* __restrict__ y1, int mv, int mtiles, int ntiles, SkTail sk) {
     constexpr int BM = 256, BN = 256, BK = 64;
     constexpr int TB = BM * BK * 2;   // 32 KB per operand per stage
     constexpr int SB = 2 * TB;        // 64 KB per stage
@@ -260,10 +265,11 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const int sw = lds_swizzle(l32);   // fragment rows differ from l32 by multiples of 32
     const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
 
-    // the current tile
-    const uint16_t* x;
-    int m, row0, col0;
-    void* y;
+    // The two token streams share one row space: video row r is row r, text
+    // row r is row mv + r (mv = m0 rounded up to a multiple of 8), so the
+    // tile holding the video tail also holds the first text rows.  Every
+    // 8-row DMA group lies in one stream.
+    int row0, col0;   // the current tile
     auto set_tile = [&](int t) {
         // grouped raster: GROUP m-tiles share each sweep over the n-tiles
         const int group_size = GROUP * ntiles;
@@ -271,12 +277,15 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         const int gm = min(mtiles - first_m, GROUP);
         const int mt = first_m + (t % group_size) % gm;
         const int nt = (t % group_size) / gm;
-        if (mt < mt0) {
-            x = x0; m = m0; y = y0; row0 = mt * BM;
-        } else {
-            x = x1; m = m1; y = y1; row0 = (mt - mt0) * BM;
-        }
+        row0 = mt * BM;
         col0 = nt * BN;
+    };
+    // output row of tile row rl, or null past either stream
+    auto out_row = [&](int rl) -> void* {
+        const int r = row0 + rl;
+        if (r < m0) return (char*)y0 + (long)r * n * (Y_BF16 ? 2 : 4);
+        if (r >= mv && r < mv + m1) return (char*)y1 + (long)(r - mv) * n * (Y_BF16 ? 2 : 4);
+        return nullptr;
     };
 
     f32x16 acc[4][2];
@@ -284,9 +293,15 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 
     // acc = sum over 64-k iterations [kb, ke) of the current tile
     auto mainloop = [&](int kb, int ke) {
-        // the tile is the same for every lane: keep the descriptors in SGPRs
-        const i32x4 ra =
-            wave_uniform(buffer_rsrc(x + (long)row0 * k, (uint32_t)(min(m - row0, BM) * k * 2)));
+        // the tile is the same for every lane: keep the descriptors in SGPRs.
+        // Both A descriptors address tile row r at byte r * k * 2; each only
+        // covers its own stream's rows (the text one starts at row mv).
+        const i32x4 rav = wave_uniform(
+            buffer_rsrc(x0 + (long)row0 * k, (uint32_t)(max(min(m0 - row0, BM), 0) * k * 2)));
+        const i32x4 rat = wave_uniform(
+            buffer_rsrc(x1 + (long)(row0 - mv) * k,
+                        (uint32_t)(row0 + BM > mv ? min(mv + m1 - row0, BM) * k * 2 : 0)));
+        const int wrow = __builtin_amdgcn_readfirstlane(row0 + wave * 32);
         const i32x4 rb =
             wave_uniform(buffer_rsrc(wgt + (long)col0 * k, (uint32_t)(min(n - col0, BN) * k * 2)));
         // Wave w fills LDS rows 32w .. 32w+31 of each operand with 4 DMA
@@ -303,7 +318,8 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             const uint32_t st = lds_base + stage * SB + wave * 4 * 1024;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                lds_dma16(ra, __builtin_amdgcn_readfirstlane(st + j * 1024), voff[j], soff);
+                lds_dma16(wrow + j * 8 < mv ? rav : rat,
+                          __builtin_amdgcn_readfirstlane(st + j * 1024), voff[j], soff);
                 lds_dma16(rb, __builtin_amdgcn_readfirstlane(st + TB + j * 1024), voff[j], soff);
             }
         };
@@ -375,11 +391,9 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 const int idx = c * 512 + tid;
                 const int rl = idx >> 5;
                 const int ch = idx & 31;
-                const int row = row0 + rl;
                 const int col = col0 + ch * 8;
-                if (row < m && col < n)
-                    *(uint4*)((uint16_t*)y + (long)row * n + col) =
-                        *(const uint4*)(lds + rl * EP + ch * 16);
+                uint16_t* yr = (uint16_t*)out_row(rl);
+                if (yr && col < n) *(uint4*)(yr + col) = *(const uint4*)(lds + rl * EP + ch * 16);
             }
             return;
         }
@@ -394,14 +408,14 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int row = row0 + wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                    if (row >= m) continue;
+                    void* yr = out_row(wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3));
+                    if (!yr) continue;
                     float v = acc[i][j][r] + bv;
                     if (ACT == S2_ACT_GELU) v = gelu(v);
                     if (Y_BF16)
-                        ((__bf16*)y)[(long)row * n + col] = (__bf16)v;
+                        ((__bf16*)yr)[col] = (__bf16)v;
                     else
-                        ((float*)y)[(long)row * n + col] = v;
+                        ((float*)yr)[col] = v;
                 }
         }
     };
@@ -604,10 +618,9 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
                               hipStream_t stream) {
     if (sizeof(TX) == 2 && k % 64 == 0 &&
         (long)256 * k * 2 <= 0x7fffffffL) {   // buffer offsets are 32-bit
-        const int mt0 = (m0 + 255) / 256;
-        const int mt1 = (m1 + 255) / 256;
+        const int mv = (m0 + 7) / 8 * 8;   // first text row in the joint row space
         const int ntiles = (n + 255) / 256;
-        const int mtiles = mt0 + mt1;
+        const int mtiles = (mv + m1 + 255) / 256;
         const long tiles = (long)mtiles * ntiles;
         if (tiles == 0) return hipSuccess;
         SkScratch* sc = nullptr;
@@ -633,7 +646,7 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
         }
         const long blocks = (long)sk.dp_tiles + sk.sk_groups;
         shared_linear_256_kernel<Y_BF16, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
-            (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mt0, mtiles,
+            (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mv, mtiles,
             ntiles, sk);
         return hipGetLastError();
     }

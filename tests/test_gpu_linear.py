@@ -42,7 +42,11 @@ def _tight(got, xr, wr, b, act, rows=None):
     return err / scale
 
 
-SHAPES = [(1, 0, 8, 16), (37, 5, 24, 40), (130, 64, 72, 136), (257, 3, 2560, 96), (64, 64, 128, 2560)]
+# the last three put video and text rows in one 256-row tile: the video tail
+# ends off (257, 300) or on (250 -> 256) an 8-row boundary, and n = 260 takes
+# the direct-store epilogue
+SHAPES = [(1, 0, 8, 16), (37, 5, 24, 40), (130, 64, 72, 136), (64, 64, 128, 2560),
+          (257, 3, 2560, 96), (300, 40, 128, 260), (250, 70, 192, 512)]
 
 
 @pytest.mark.parametrize("mv,mt,k,n", SHAPES)
