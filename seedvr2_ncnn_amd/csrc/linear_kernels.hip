@@ -385,7 +385,9 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                     }
             }
             __syncthreads();
-            // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows t/32 + 16c
+            // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows
+            // t/32 + 16c.  The output is not read again by this launch: the
+            // stores are non-temporal, leaving the L2 to the operand tiles.
 #pragma unroll 4
             for (int c = 0; c < 16; ++c) {
                 const int idx = c * 512 + tid;
@@ -393,7 +395,9 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 const int ch = idx & 31;
                 const int col = col0 + ch * 8;
                 uint16_t* yr = (uint16_t*)out_row(rl);
-                if (yr && col < n) *(uint4*)(yr + col) = *(const uint4*)(lds + rl * EP + ch * 16);
+                if (yr && col < n)
+                    __builtin_nontemporal_store(*(const u32x4*)(lds + rl * EP + ch * 16),
+                                                (u32x4*)(yr + col));
             }
             return;
         }
