@@ -394,6 +394,12 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
 
     issue(0, 0);
     if (nkt > 1) issue(1, 1);
+    // The Q loads must be complete before the loop in a way the compiler
+    // sees: its wait insertion does not track the DMA asm, and with Q loads
+    // possibly outstanding at the loop header it would put a vmcnt(0) before
+    // the first MFMA of every tile, which also waits for the DMA issued two
+    // tiles ahead.  The first tile needs its DMA anyway.
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
     // The tile loop is unrolled by the stage count so that every LDS
     // address is a loop-invariant register plus a constant stage offset.
 #pragma unroll 1
