@@ -427,18 +427,28 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
             if (!wave_active) continue;
             f32x16 s0, s1;
             const uint8_t* kp = st + krow * (D * 2);
+            auto kfrag = [&](int kk) {
+                return as_bf16x8(*(const uint4*)(kp + (((2 * kk + g) ^ kswz) * 16)));
+            };
+            // K fragments are read two slices ahead of their MFMA (the
+            // scheduling barriers keep the compiler from sinking each read
+            // next to its use, which would expose the LDS latency per slice)
+            bf16x8 kf[NKK];
+            kf[0] = kfrag(0);
+            kf[1] = kfrag(1);
 #pragma unroll
-            for (int kk = 0; kk < NKK; kk += 2) {
-                const bf16x8 a0 = as_bf16x8(*(const uint4*)(kp + (((2 * kk + g) ^ kswz) * 16)));
-                const bf16x8 a1 =
-                    as_bf16x8(*(const uint4*)(kp + (((2 * kk + 2 + g) ^ kswz) * 16)));
-                if (kk == 0) {
-                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[kk], f32x16{}, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[kk + 1], f32x16{}, 0, 0, 0);
-                } else {
-                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, qf[kk], s0, 0, 0, 0);
-                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, qf[kk + 1], s1, 0, 0, 0);
-                }
+            for (int kk = 0; kk < NKK; ++kk) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (kk + 2 < NKK) kf[kk + 2] = kfrag(kk + 2);
+                __builtin_amdgcn_sched_barrier(0);
+                if (kk == 0)
+                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], f32x16{}, 0, 0, 0);
+                else if (kk == 1)
+                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1], qf[1], f32x16{}, 0, 0, 0);
+                else if (kk & 1)
+                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s1, 0, 0, 0);
+                else
+                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s0, 0, 0, 0);
             }
             f32x16 s = s0 + s1;
             // keys past the window's sequence (only in the last tile) are masked
