@@ -420,12 +420,11 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
             if (kt + 2 < nkt) issue((u + 2) % STAGES, kt + 2);
             const uint8_t* st = lds + u * SB;
 
-            // S^T = K Q^T as two independent MFMA chains (even and odd
-            // 16-channel slices), summed afterwards
+            // S^T = K Q^T
             // a wave whose 32 query rows all lie past the sequence (the last
             // q-tile of a window) only takes part in the DMA and barriers
             if (!wave_active) continue;
-            f32x16 s0, s1;
+            f32x16 s;
             const uint8_t* kp = st + krow * (D * 2);
             auto kfrag = [&](int kk) {
                 return as_bf16x8(*(const uint4*)(kp + (((2 * kk + g) ^ kswz) * 16)));
@@ -441,16 +440,13 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
                 __builtin_amdgcn_sched_barrier(0);
                 if (kk + 2 < NKK) kf[kk + 2] = kfrag(kk + 2);
                 __builtin_amdgcn_sched_barrier(0);
+                // one accumulation chain: back-to-back dependent MFMAs of
+                // the same shape accumulate without extra wait states
                 if (kk == 0)
-                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], f32x16{}, 0, 0, 0);
-                else if (kk == 1)
-                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[1], qf[1], f32x16{}, 0, 0, 0);
-                else if (kk & 1)
-                    s1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s1, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], f32x16{}, 0, 0, 0);
                 else
-                    s0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s0, 0, 0, 0);
+                    s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s, 0, 0, 0);
             }
-            f32x16 s = s0 + s1;
             // keys past the window's sequence (only in the last tile) are masked
             const int key_base = kt * KT;
             if (key_base + KT > w.seq) {
