@@ -253,9 +253,15 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
 // v_permlane32_swap with the same value in both operands leaves, in every
 // lane, the pair {x[lane], x[lane ^ 32]} in its two results (a VALU op, no
 // LDS round trip as with a shuffle).
+// Maxima of attention scores with the NaN-propagating maximum (v_maximum3 on
+// gfx950), which needs no quieting of its operands first, unlike fmaxf
+__device__ __forceinline__ float max3_scores(float a, float b, float c) {
+    return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+
 __device__ __forceinline__ float max_with_lane_xor32(float x) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    return __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
 __device__ __forceinline__ float sum_with_lane_xor32(float x) {
@@ -457,9 +463,10 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
                     if (key >= w.seq) s[i] = -INFINITY;
                 }
             }
-            float mx = s[0];
+            float mx = max3_scores(s[0], s[1], s[2]);
 #pragma unroll
-            for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+            for (int i = 3; i < 15; i += 2) mx = max3_scores(mx, s[i], s[i + 1]);
+            mx = max3_scores(mx, mx, s[15]);
             mx = max_with_lane_xor32(mx) * scale_log2;
             float alpha = 1.f;
             if (mx > m_run + kLazy) {
