@@ -250,7 +250,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     constexpr int RB = BK * 2;        // LDS row bytes
     constexpr int EP = BN * 2 + 16;   // epilogue LDS row pitch (bytes)
     constexpr int LDS_BYTES = 2 * SB > BM * EP ? 2 * SB : BM * EP;
-    constexpr int GROUP = 8;
+    constexpr int GROUP = 4;   // row-tiles per raster group (4 measured 1-3% faster than 8 or 16)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     __shared__ int arrival;
 
