@@ -1,7 +1,7 @@
 """ctypes wrapper of the CPU oracle (oracle.c) -- TEST INFRASTRUCTURE.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this module, and only as the checker or the timed CPU baseline.  The product
+this module, and only as the reference result or the timed CPU baseline.  The product
 path (seedvr2_ncnn_amd) never imports it.
 
 The C code restates the reference CPU forward of AdaptiveWindowAttention

@@ -1,7 +1,7 @@
 /*
  * CPU oracle for the SeedVR2 window-attention hot path -- TEST INFRASTRUCTURE.
  * Used only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
- * always as the checker or the CPU baseline, never as the product.
+ * always as the reference result or the CPU baseline, never as the product.
  * See oracle.h for the pinning of each function.
  */
 #include "oracle.h"

@@ -2,8 +2,8 @@
  * CPU oracle for the SeedVR2 window-attention hot path.
  *
  * TEST INFRASTRUCTURE ONLY.  This is a plain-C restatement of the reference
- * layers' CPU forward (Chisato623/seedvr2_ncnn), used as the checker by the
- * test suite, by __graft_entry__.smoke() and by bench.py's cpu_baseline leg.
+ * layers' CPU forward (Chisato623/seedvr2_ncnn), the reference result of the
+ * test suite and of __graft_entry__.smoke(), and bench.py's cpu_baseline leg.
  * Nothing in the product path (seedvr2_ncnn_amd/) may link, load or call it.
  *
  * Every function names the reference file:line it restates.  Floating-point
