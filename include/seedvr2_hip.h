@@ -35,9 +35,13 @@ extern "C" {
 
 typedef void* s2_stream_t;
 
+/* Element types of activations.  The 16-bit ones are the two storage types
+ * of the reference's Vulkan path (adaptive_window_attention.cpp:1082-1087,
+ * 1141: blobs of elembits 16, fp16 or bf16 by ncnn's storage options). */
 typedef enum s2_dtype {
     S2_DTYPE_F32 = 0,
-    S2_DTYPE_BF16 = 1
+    S2_DTYPE_BF16 = 1,
+    S2_DTYPE_F16 = 2   /* IEEE binary16 */
 } s2_dtype;
 
 typedef enum s2_activation {
@@ -139,7 +143,7 @@ S2_API int s2_awa_plan_tables(const s2_awa_plan* plan, int* video_indices,
  *   video_row_stride elements: the fused [L][3*inner] blob gives
  *   (base, base+inner, base+2*inner, 3*inner), the split blobs give three
  *   pointers with stride inner (reference 4- and 8-input forms, :768-797).
- * in_dtype: F32 or BF16 for all six inputs.
+ * in_dtype: F32, BF16 or F16 for all six inputs.
  * out_video [video_tokens][inner], out_text [text_tokens][inner] in out_dtype.
  * workspace: device memory of at least info.workspace_bytes, 256-byte aligned.
  * All work is enqueued on stream; nothing is synchronised. */
@@ -173,8 +177,10 @@ S2_API int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2
  *   y_video = act(x_video W^T + b),  y_text = act(x_text W^T + b).
  * weight: device bf16 [n][k] row-major (the reference [N][K] layout,
  * :66-69); bias: device fp32 [n] or NULL (param 2).  x_*: device
- * [m_*][k] in x_dtype; y_*: device [m_*][n] in y_dtype.  Either stream may
- * have m == 0 (its pointers are then ignored).  k must be a multiple of 8.
+ * [m_*][k] in x_dtype; y_*: device [m_*][n] in y_dtype.  The MFMAs take bf16
+ * operands: fp32 and fp16 activations are rounded to bf16 (nearest even) as
+ * they are staged.  Either stream may have m == 0 (its pointers are then
+ * ignored).  k must be a multiple of 8; x, y and weight 16-byte aligned.
  * The first call on a device allocates that device's split-k scratch (about
  * 128 MB of partial-tile slots and their counters), kept until the process
  * ends; calls whose kernels overlap in time on one device (different streams)

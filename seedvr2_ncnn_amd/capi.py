@@ -21,6 +21,7 @@ S2_ERR_DEVICE = -200
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
+DTYPE_F16 = 2
 ACT_NONE = 0
 ACT_GELU = 1
 
@@ -226,6 +227,8 @@ def _dtype_code(t):
     import torch
     if t.dtype == torch.bfloat16:
         return DTYPE_BF16
+    if t.dtype == torch.float16:
+        return DTYPE_F16
     if t.dtype == torch.float32:
         return DTYPE_F32
     raise TypeError(f"unsupported dtype {t.dtype}")

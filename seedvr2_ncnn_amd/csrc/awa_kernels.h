@@ -5,28 +5,30 @@
 
 #include "awa_plan.h"
 
+// Activation element types (in_kind, out_kind, x_kind, y_kind) are the
+// s2_dtype values: 0 fp32, 1 bf16, 2 fp16.
 namespace s2 {
 
 hipError_t launch_rope_table(const float* freqs, int pairs, int positions, float2* table,
                              hipStream_t stream);
 hipError_t launch_awa_prologue(const s2_awa_plan& plan, const void* vq, const void* vk,
                                const void* vv, long vstride, const void* tq, const void* tk,
-                               const void* tv, long tstride, bool in_bf16, const float* norm,
+                               const void* tv, long tstride, int in_kind, const float* norm,
                                const float2* rope, uint16_t* q_out, uint16_t* k_out,
                                uint16_t* vt_out, hipStream_t stream);
 hipError_t launch_awa_attention(const s2_awa_plan& plan, const uint16_t* q, const uint16_t* k,
-                                const uint16_t* vt, void* out_video, bool out_bf16,
+                                const uint16_t* vt, void* out_video, int out_kind,
                                 float* text_partial, hipStream_t stream);
 hipError_t launch_awa_text_pool(const s2_awa_plan& plan, const float* partial, void* out_text,
-                                bool out_bf16, hipStream_t stream);
+                                int out_kind, hipStream_t stream);
 hipError_t launch_awa_plan_tables(const s2_awa_plan& plan, int* indices, int* inverse,
                                   int* positions, hipStream_t stream);
 
 hipError_t launch_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream);
 hipError_t launch_cast_bf16_f32(const uint16_t* src, float* dst, size_t n, hipStream_t stream);
 // Grouped y_s = act(x_s W^T + b) over the video and text streams.
-hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, bool x_bf16,
+hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, int x_kind,
                                 const uint16_t* w, const float* bias, int n, int k, int act,
-                                void* y0, void* y1, bool y_bf16, hipStream_t stream);
+                                void* y0, void* y1, int y_kind, hipStream_t stream);
 
 }  // namespace s2

@@ -17,6 +17,8 @@
 // and the Vulkan path :1059-1270 with its shaders :21-409.
 #include <math.h>
 
+#include <type_traits>
+
 #include "awa_kernels.h"
 #include "s2_device.h"
 
@@ -65,8 +67,13 @@ __global__ void rope_table_kernel(const float* __restrict__ freqs, int pairs, in
 }
 
 // ---------------------------------------------------------------------------
-// Eight consecutive input channels held as loaded (bf16 or fp32), converted
-// to fp32 when used.
+// Eight consecutive input channels held as loaded (bf16, fp16 or fp32),
+// converted to fp32 when used.
+template <typename T>
+struct type_tag {
+    using type = T;
+};
+
 template <typename T>
 struct Raw8;
 
@@ -80,6 +87,20 @@ struct Raw8<uint16_t> {
         for (int i = 0; i < 4; ++i) {
             f[2 * i] = __uint_as_float(w[i] << 16);
             f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+        }
+    }
+};
+
+template <>
+struct Raw8<_Float16> {
+    uint4 v;
+    __device__ __forceinline__ void load(const _Float16* p) { v = *reinterpret_cast<const uint4*>(p); }
+    __device__ __forceinline__ void to_float(float (&f)[8]) const {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            f[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu));
+            f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
         }
     }
 };
@@ -308,7 +329,7 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     const WinMeta* __restrict__ wins, const AttnItem* __restrict__ items, int slots_per_xcd,
     const uint16_t* __restrict__ q_in, const uint16_t* __restrict__ k_in,
     const uint16_t* __restrict__ vt_in, long seg_total, float scale_log2, int official_bf16,
-    void* __restrict__ out_video, int out_bf16, int inner, float* __restrict__ text_partial) {
+    void* __restrict__ out_video, int out_kind, int inner, float* __restrict__ text_partial) {
     constexpr int KT = 32;                  // keys per tile
     constexpr int STAGES = 3;
     constexpr int KB = KT * D * 2;          // K tile bytes
@@ -524,15 +545,7 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
                     if (official_bf16) x = bf16_to_f32(round_bf16_ref_bits(x));
                     vals[e] = x;
                 }
-                if (out_bf16) {
-                    uint2 pk;
-                    pk.x = pack2_bf16_rne(vals[0], vals[1]);
-                    pk.y = pack2_bf16_rne(vals[2], vals[3]);
-                    *reinterpret_cast<uint2*>((uint16_t*)out_video + obase + ch) = pk;
-                } else {
-                    *reinterpret_cast<float4*>((float*)out_video + obase + ch) =
-                        make_float4(vals[0], vals[1], vals[2], vals[3]);
-                }
+                store4(out_video, obase + ch, vals[0], vals[1], vals[2], vals[3], out_kind);
             }
     } else {
         const long obase = (long)(w.tpart_off + qrow - w.n_video) * inner + (long)it.head * D;
@@ -561,7 +574,7 @@ __global__ void awa_text_pool_kernel(const SampleMeta* __restrict__ samples,
                                      const int* __restrict__ text_sample,
                                      const WinMeta* __restrict__ wins,
                                      const float* __restrict__ partial, int text_tokens,
-                                     int inner, void* __restrict__ out, int out_bf16) {
+                                     int inner, void* __restrict__ out, int out_kind) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;   // float4 index
     const int q4 = inner / 4;
     if (i >= (long)text_tokens * q4) return;
@@ -581,14 +594,7 @@ __global__ void awa_text_pool_kernel(const SampleMeta* __restrict__ samples,
         acc.z += x.z * sm.pool_scale;
         acc.w += x.w * sm.pool_scale;
     }
-    if (out_bf16) {
-        uint2 pk;
-        pk.x = pack2_bf16_rne(acc.x, acc.y);
-        pk.y = pack2_bf16_rne(acc.z, acc.w);
-        *reinterpret_cast<uint2*>((uint16_t*)out + (long)row * inner + c) = pk;
-    } else {
-        *reinterpret_cast<float4*>((float*)out + (long)row * inner + c) = acc;
-    }
+    store4(out, (long)row * inner + c, acc.x, acc.y, acc.z, acc.w, out_kind);
 }
 
 // ---------------------------------------------------------------------------
@@ -639,25 +645,28 @@ static hipError_t prologue_impl(const s2_awa_plan& plan, const void* vq, const v
 
 hipError_t launch_awa_prologue(const s2_awa_plan& plan, const void* vq, const void* vk,
                                const void* vv, long vstride, const void* tq, const void* tk,
-                               const void* tv, long tstride, bool in_bf16, const float* norm,
+                               const void* tv, long tstride, int in_kind, const float* norm,
                                const float2* rope, uint16_t* q_out, uint16_t* k_out,
                                uint16_t* vt_out, hipStream_t stream) {
     const int d = plan.config.head_dim;
-    if (d == 128)
-        return in_bf16 ? prologue_impl<128, uint16_t>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
-                                                      norm, rope, q_out, k_out, vt_out, stream)
-                       : prologue_impl<128, float>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
-                                                   norm, rope, q_out, k_out, vt_out, stream);
-    if (d == 64)
-        return in_bf16 ? prologue_impl<64, uint16_t>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
-                                                     norm, rope, q_out, k_out, vt_out, stream)
-                       : prologue_impl<64, float>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride,
-                                                  norm, rope, q_out, k_out, vt_out, stream);
+    auto run = [&](auto dtag, auto ttag) {
+        constexpr int DD = decltype(dtag)::value;
+        using T = typename decltype(ttag)::type;
+        return prologue_impl<DD, T>(plan, vq, vk, vv, vstride, tq, tk, tv, tstride, norm, rope,
+                                    q_out, k_out, vt_out, stream);
+    };
+    auto by_type = [&](auto dtag) {
+        if (in_kind == 1) return run(dtag, type_tag<uint16_t>{});
+        if (in_kind == 2) return run(dtag, type_tag<_Float16>{});
+        return run(dtag, type_tag<float>{});
+    };
+    if (d == 128) return by_type(std::integral_constant<int, 128>{});
+    if (d == 64) return by_type(std::integral_constant<int, 64>{});
     return hipErrorInvalidValue;
 }
 
 hipError_t launch_awa_attention(const s2_awa_plan& plan, const uint16_t* q, const uint16_t* k,
-                                const uint16_t* vt, void* out_video, bool out_bf16,
+                                const uint16_t* vt, void* out_video, int out_kind,
                                 float* text_partial, hipStream_t stream) {
     const int d = plan.config.head_dim;
     const int inner = plan.config.heads * d;
@@ -667,24 +676,24 @@ hipError_t launch_awa_attention(const s2_awa_plan& plan, const uint16_t* q, cons
     if (d == 128)
         awa_attention_kernel<128><<<grid, 256, 0, stream>>>(
             plan.d_wins, plan.d_items, plan.slots_per_xcd, q, k, vt, plan.seg_total, scale_log2,
-            plan.config.official_bf16_attention, out_video, out_bf16 ? 1 : 0, inner, text_partial);
+            plan.config.official_bf16_attention, out_video, out_kind, inner, text_partial);
     else if (d == 64)
         awa_attention_kernel<64><<<grid, 256, 0, stream>>>(
             plan.d_wins, plan.d_items, plan.slots_per_xcd, q, k, vt, plan.seg_total, scale_log2,
-            plan.config.official_bf16_attention, out_video, out_bf16 ? 1 : 0, inner, text_partial);
+            plan.config.official_bf16_attention, out_video, out_kind, inner, text_partial);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();
 }
 
 hipError_t launch_awa_text_pool(const s2_awa_plan& plan, const float* partial, void* out_text,
-                                bool out_bf16, hipStream_t stream) {
+                                int out_kind, hipStream_t stream) {
     const int inner = plan.config.heads * plan.config.head_dim;
     const long n = (long)plan.text_tokens * (inner / 4);
     if (n == 0) return hipSuccess;
     awa_text_pool_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
         plan.d_samples, plan.d_text_sample, plan.d_wins, partial, plan.text_tokens, inner,
-        out_text, out_bf16 ? 1 : 0);
+        out_text, out_kind);
     return hipGetLastError();
 }
 

@@ -55,6 +55,9 @@ StageTimer& stage_timer() {
     return t;
 }
 
+bool dtype_ok(s2_dtype t) { return t == S2_DTYPE_F32 || t == S2_DTYPE_BF16 || t == S2_DTYPE_F16; }
+size_t dtype_bytes(s2_dtype t) { return t == S2_DTYPE_F32 ? 4 : 2; }
+
 }  // namespace
 
 extern "C" {
@@ -346,18 +349,18 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
     if ((plan->config.rope_pairs_per_axis > 0 && !rope_freqs))
         return fail(S2_ERR_INVALID, "missing rope frequencies");
     if (workspace_bytes < plan->workspace_bytes) return fail(S2_ERR_INVALID, "workspace too small");
-    if ((in_dtype != S2_DTYPE_F32 && in_dtype != S2_DTYPE_BF16) ||
-        (out_dtype != S2_DTYPE_F32 && out_dtype != S2_DTYPE_BF16))
-        return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
     const int inner = plan->config.heads * plan->config.head_dim;
     if (video_row_stride < inner || text_row_stride < inner || (video_row_stride % 8) != 0 ||
         (text_row_stride % 8) != 0)
         return fail(S2_ERR_INVALID, "row stride must be >= heads*head_dim and a multiple of 8");
-    const size_t elem = in_dtype == S2_DTYPE_BF16 ? 2 : 4;
+    const size_t elem = dtype_bytes(in_dtype);
     const void* ins[6] = {video_q, video_k, video_v, text_q, text_k, text_v};
     for (const void* p : ins)
         if (((uintptr_t)p) % (8 * elem) != 0)
             return fail(S2_ERR_INVALID, "inputs must be aligned to 8 elements");
+    if (((uintptr_t)out_video) % 16 != 0 || ((uintptr_t)out_text) % 16 != 0)
+        return fail(S2_ERR_INVALID, "outputs must be 16-byte aligned");
     if (((uintptr_t)workspace) % 256 != 0) return fail(S2_ERR_INVALID, "workspace alignment");
 
     hipStream_t s = (hipStream_t)stream;
@@ -367,8 +370,6 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
     uint16_t* vt = (uint16_t*)(ws + plan->off_vt);
     float2* rope = (float2*)(ws + plan->off_rope);
     float* tpart = (float*)(ws + plan->off_tpart);
-    const bool in_bf16 = in_dtype == S2_DTYPE_BF16;
-    const bool out_bf16 = out_dtype == S2_DTYPE_BF16;
     StageTimer& tm = stage_timer();
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[0], s));
     if (plan->config.rope_pairs_per_axis > 0)
@@ -376,12 +377,12 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
                                      plan->rope_positions, rope, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[1], s));
     S2_HIP(s2::launch_awa_prologue(*plan, video_q, video_k, video_v, video_row_stride, text_q,
-                                   text_k, text_v, text_row_stride, in_bf16, norm_weights, rope, q,
+                                   text_k, text_v, text_row_stride, (int)in_dtype, norm_weights, rope, q,
                                    k, vt, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[2], s));
-    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, out_bf16, tpart, s));
+    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[3], s));
-    S2_HIP(s2::launch_awa_text_pool(*plan, tpart, out_text, out_bf16, s));
+    S2_HIP(s2::launch_awa_text_pool(*plan, tpart, out_text, (int)out_dtype, s));
     if (tm.on) {
         S2_HIP(hipEventRecord(tm.ev[4], s));
         tm.recorded = true;
@@ -432,16 +433,14 @@ int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_tex
     if (k % 8 != 0) return fail(S2_ERR_INVALID, "k must be a multiple of 8");
     if (activation != S2_ACT_NONE && activation != S2_ACT_GELU)
         return fail(S2_ERR_INVALID, "unknown activation");
-    if ((x_dtype != S2_DTYPE_F32 && x_dtype != S2_DTYPE_BF16) ||
-        (y_dtype != S2_DTYPE_F32 && y_dtype != S2_DTYPE_BF16))
-        return fail(S2_ERR_INVALID, "unsupported dtype");
-    const size_t xe = x_dtype == S2_DTYPE_BF16 ? 2 : 4;
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    const size_t xe = dtype_bytes(x_dtype);
     if (((uintptr_t)x_video) % (8 * xe) || ((uintptr_t)x_text) % (8 * xe) ||
-        ((uintptr_t)weight) % 16)
+        ((uintptr_t)weight) % 16 || ((uintptr_t)y_video) % 16 || ((uintptr_t)y_text) % 16)
         return fail(S2_ERR_INVALID, "operands must be 16-byte aligned");
-    S2_HIP(s2::launch_shared_linear(x_video, m_video, x_text, m_text, x_dtype == S2_DTYPE_BF16,
-                                    weight, bias, n, k, activation, y_video, y_text,
-                                    y_dtype == S2_DTYPE_BF16, (hipStream_t)stream));
+    S2_HIP(s2::launch_shared_linear(x_video, m_video, x_text, m_text, (int)x_dtype, weight, bias,
+                                    n, k, activation, y_video, y_text, (int)y_dtype,
+                                    (hipStream_t)stream));
     return S2_OK;
 }
 

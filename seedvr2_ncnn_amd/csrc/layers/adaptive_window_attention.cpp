@@ -331,7 +331,7 @@ int AdaptiveWindowAttention::forward(const std::vector<ncnn::Mat>& bottom_blobs,
     const int inner_dim = heads * head_dim;
 
     // Host blobs must be fp32 (as the reference CPU path); device blobs may
-    // be fp32 or bf16 but must agree.
+    // be fp32, bf16 or fp16 (device_blob_dtype) but must agree.
     HipDeviceAllocator* device = device_allocator_of(video_qkv);
     const size_t elemsize = video_qkv.elemsize;
     const int n_data = split_qkv ? 6 : 2;
@@ -461,7 +461,7 @@ int AdaptiveWindowAttention::forward(const std::vector<ncnn::Mat>& bottom_blobs,
         const void* tk = split_qkv ? bottom_blobs[4].data : t + inner_dim * elemsize;
         const void* tv = split_qkv ? bottom_blobs[5].data : t + 2 * inner_dim * elemsize;
         const long vstride = split_qkv ? inner_dim : 3 * inner_dim;
-        const s2_dtype dtype = elemsize == 2 ? S2_DTYPE_BF16 : S2_DTYPE_F32;
+        const s2_dtype dtype = device_blob_dtype(elemsize, opt);
         return s2_awa_forward(plan, norms, freqs, vq, vk, vv, vstride, tq, tk, tv, vstride, dtype,
                               top_blobs[0].data, top_blobs[1].data, dtype, workspace.get(),
                               workspace.size(), device->stream());

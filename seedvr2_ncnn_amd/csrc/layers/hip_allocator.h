@@ -18,6 +18,9 @@
 
 #include <allocator.h>
 #include <mat.h>
+#include <option.h>
+
+#include "seedvr2_hip.h"
 
 namespace seedvr2 {
 
@@ -30,8 +33,8 @@ public:
     virtual void* fastMalloc(size_t size);
     virtual void fastFree(void* ptr);
 
-    // Device Mat (dims 2: w x h, elemsize 4 = fp32, 2 = bf16) owned by this
-    // allocator.  Empty on allocation failure.
+    // Device Mat (dims 2: w x h, elemsize 4 = fp32, 2 = bf16 or fp16, see
+    // device_blob_dtype) owned by this allocator.  Empty on allocation failure.
     ncnn::Mat create_blob(int w, int h, size_t elemsize);
     // Wraps caller-owned device memory as a device blob (not owned).
     ncnn::Mat wrap_blob(int w, int h, void* device_data, size_t elemsize);
@@ -48,6 +51,17 @@ private:
 
 // True when m is a device blob (its allocator is a HipDeviceAllocator).
 HipDeviceAllocator* device_allocator_of(const ncnn::Mat& m);
+
+// Element type of a device blob: elemsize 4 is fp32; elemsize 2 follows
+// ncnn's 16-bit storage options, as the reference Vulkan path's blobs of
+// elembits 16 do (adaptive_window_attention.cpp:1082-1087): fp16 when only
+// use_fp16_storage is set, bf16 otherwise (use_bf16_storage, or neither).
+inline s2_dtype device_blob_dtype(size_t elemsize, const ncnn::Option& opt)
+{
+    if (elemsize == 4)
+        return S2_DTYPE_F32;
+    return opt.use_fp16_storage && !opt.use_bf16_storage ? S2_DTYPE_F16 : S2_DTYPE_BF16;
+}
 
 // Device buffer that only grows; used for layer workspaces and staging.
 class DeviceBuffer {

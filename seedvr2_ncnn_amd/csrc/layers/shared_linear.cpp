@@ -152,7 +152,7 @@ int SharedLinear::forward(const std::vector<ncnn::Mat>& bottom_blobs,
         top_blobs[1] = out_alloc->create_blob(num_output, m1, elemsize);
         if ((m0 > 0 && top_blobs[0].empty()) || (m1 > 0 && top_blobs[1].empty()))
             return -100;
-        const s2_dtype dtype = elemsize == 2 ? S2_DTYPE_BF16 : S2_DTYPE_F32;
+        const s2_dtype dtype = device_blob_dtype(elemsize, opt);
         return s2_shared_linear_forward(bottom_blobs[0].data, m0, bottom_blobs[1].data, m1, dtype,
                                         static_cast<const uint16_t*>(weight_gpu.get()), bias,
                                         num_output, num_input, activation, top_blobs[0].data,

@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "awa_kernels.h"
 #include "s2_device.h"
@@ -19,6 +20,29 @@ namespace {
 
 __device__ __forceinline__ uint4 load_chunk(const uint16_t* p) {
     return *reinterpret_cast<const uint4*>(p);
+}
+
+__device__ __forceinline__ uint4 load_chunk(const _Float16* p) {
+    const uint4 raw = *reinterpret_cast<const uint4*>(p);
+    const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+    uint16_t h[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        h[2 * i] = f32_to_bf16((float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xffffu)));
+        h[2 * i + 1] = f32_to_bf16((float)__builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16)));
+    }
+    return pack8_bf16(h);
+}
+
+// one output element of type YK (0 fp32, 1 bf16, 2 fp16)
+template <int YK>
+__device__ __forceinline__ void store1(void* y, long idx, float v) {
+    if (YK == 1)
+        ((uint16_t*)y)[idx] = f32_to_bf16(v);
+    else if (YK == 2)
+        ((_Float16*)y)[idx] = (_Float16)v;
+    else
+        ((float*)y)[idx] = v;
 }
 
 __device__ __forceinline__ uint4 load_chunk(const float* p) {
@@ -54,7 +78,7 @@ __device__ __forceinline__ float gelu(float x) {
 // Block tile 128x128, k-step 64, four waves in a 2x2 grid of 64x64 wave tiles
 // (2x2 MFMA 32x32 accumulators per wave).  LDS double buffered, rows padded
 // by 16 bytes against bank conflicts.
-template <typename TX, bool Y_BF16, int ACT>
+template <typename TX, int YK, int ACT>
 __global__ __launch_bounds__(256, 2) void shared_linear_kernel(
     const TX* __restrict__ x0, int m0, const TX* __restrict__ x1, int m1,
     const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
@@ -180,10 +204,7 @@ __global__ __launch_bounds__(256, 2) void shared_linear_kernel(
                 if (row >= m) continue;
                 float v = acc[i][j][r] + b;
                 if (ACT == S2_ACT_GELU) v = gelu(v);
-                if (Y_BF16)
-                    ((uint16_t*)y)[(long)row * n + col] = f32_to_bf16(v);
-                else
-                    ((float*)y)[(long)row * n + col] = v;
+                store1<YK>(y, (long)row * n + col, v);
             }
     }
 }
@@ -239,7 +260,7 @@ struct SkTail {
     int* counters;     // [sk_tiles] arrivals; zero between launches
 };
 
-template <bool Y_BF16, int ACT>
+template <int YK, int ACT>
 __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const uint16_t* __restrict__ x0, int m0, const uint16_t* __restrict__ x1, int m1,
     const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
@@ -283,8 +304,8 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     // output row of tile row rl, or null past either stream
     auto out_row = [&](int rl) -> void* {
         const int r = row0 + rl;
-        if (r < m0) return (char*)y0 + (long)r * n * (Y_BF16 ? 2 : 4);
-        if (r >= mv && r < mv + m1) return (char*)y1 + (long)(r - mv) * n * (Y_BF16 ? 2 : 4);
+        if (r < m0) return (char*)y0 + (long)r * n * (YK ? 2 : 4);
+        if (r >= mv && r < mv + m1) return (char*)y1 + (long)(r - mv) * n * (YK ? 2 : 4);
         return nullptr;
     };
 
@@ -368,7 +389,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 
     // y tile = act(acc + bias)
     auto epilogue = [&]() {
-        if (Y_BF16 && (n & 7) == 0) {
+        if (YK && (n & 7) == 0) {
             __syncthreads();   // every wave is done reading the last stage
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
@@ -381,7 +402,10 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                         float v = acc[i][j][r] + bv;
                         if (ACT == S2_ACT_GELU) v = gelu(v);
                         const int rl = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-                        *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
+                        if (YK == 2)
+                            *(_Float16*)(lds + rl * EP + cl * 2) = (_Float16)v;
+                        else
+                            *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
                     }
             }
             __syncthreads();
@@ -416,10 +440,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                     if (!yr) continue;
                     float v = acc[i][j][r] + bv;
                     if (ACT == S2_ACT_GELU) v = gelu(v);
-                    if (Y_BF16)
-                        ((__bf16*)yr)[col] = (__bf16)v;
-                    else
-                        ((float*)yr)[col] = v;
+                    store1<YK>(yr, col, v);
                 }
         }
     };
@@ -616,11 +637,13 @@ hipError_t sk_scratch(SkScratch** out) {
 
 }  // namespace
 
-template <typename TX, bool Y_BF16, int ACT>
+template <typename TX, int YK, int ACT>
 static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, const uint16_t* w,
                               const float* bias, int n, int k, void* y0, void* y1,
                               hipStream_t stream) {
-    if (sizeof(TX) == 2 && k % 64 == 0 &&
+    // bf16 activations (the operand type of the MFMAs) go straight to LDS;
+    // fp32 and fp16 ones are rounded to bf16 while staged by the 128 kernel
+    if (std::is_same<TX, uint16_t>::value && k % 64 == 0 &&
         (long)256 * k * 2 <= 0x7fffffffL) {   // buffer offsets are 32-bit
         const int mv = (m0 + 7) / 8 * 8;   // first text row in the joint row space
         const int ntiles = (n + 255) / 256;
@@ -649,7 +672,7 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
             }
         }
         const long blocks = (long)sk.dp_tiles + sk.sk_groups;
-        shared_linear_256_kernel<Y_BF16, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
+        shared_linear_256_kernel<YK, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
             (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mv, mtiles,
             ntiles, sk);
         return hipGetLastError();
@@ -660,28 +683,37 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
     const int mtiles = mt0 + mt1;
     const long blocks = (long)mtiles * ntiles;
     if (blocks == 0) return hipSuccess;
-    shared_linear_kernel<TX, Y_BF16, ACT><<<(unsigned)blocks, 256, 0, stream>>>(
+    shared_linear_kernel<TX, YK, ACT><<<(unsigned)blocks, 256, 0, stream>>>(
         (const TX*)x0, m0, (const TX*)x1, m1, w, bias, n, k, y0, y1, mt0, mtiles, ntiles);
     return hipGetLastError();
 }
 
-template <typename TX, bool Y_BF16>
+template <typename TX, int YK>
 static hipError_t linear_act(int act, const void* x0, int m0, const void* x1, int m1,
                              const uint16_t* w, const float* bias, int n, int k, void* y0,
                              void* y1, hipStream_t stream) {
     if (act == S2_ACT_GELU)
-        return linear_impl<TX, Y_BF16, S2_ACT_GELU>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
-    return linear_impl<TX, Y_BF16, S2_ACT_NONE>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+        return linear_impl<TX, YK, S2_ACT_GELU>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+    return linear_impl<TX, YK, S2_ACT_NONE>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
 }
 
-hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, bool x_bf16,
+template <typename TX>
+static hipError_t linear_out(int y_kind, int act, const void* x0, int m0, const void* x1, int m1,
+                             const uint16_t* w, const float* bias, int n, int k, void* y0,
+                             void* y1, hipStream_t stream) {
+    if (y_kind == 1) return linear_act<TX, 1>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+    if (y_kind == 2) return linear_act<TX, 2>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+    return linear_act<TX, 0>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+}
+
+hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, int x_kind,
                                 const uint16_t* w, const float* bias, int n, int k, int act,
-                                void* y0, void* y1, bool y_bf16, hipStream_t stream) {
-    if (x_bf16)
-        return y_bf16 ? linear_act<uint16_t, true>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream)
-                      : linear_act<uint16_t, false>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
-    return y_bf16 ? linear_act<float, true>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream)
-                  : linear_act<float, false>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+                                void* y0, void* y1, int y_kind, hipStream_t stream) {
+    if (x_kind == 1)
+        return linear_out<uint16_t>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+    if (x_kind == 2)
+        return linear_out<_Float16>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+    return linear_out<float>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
 }
 
 }  // namespace s2

@@ -43,6 +43,27 @@ __device__ __forceinline__ uint32_t pack2_bf16_rne(float lo, float hi) {
            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
 }
 
+// two floats -> packed fp16 pair (low, high), round to nearest even
+__device__ __forceinline__ uint32_t pack2_f16_rne(float lo, float hi) {
+    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+}
+
+// Four consecutive floats stored at element `idx` of an activation buffer of
+// element type `kind` (0 fp32, 1 bf16, 2 fp16; the s2_dtype values).
+__device__ __forceinline__ void store4(void* base, long idx, float a, float b, float c, float d,
+                                       int kind) {
+    if (kind == 1) {
+        *reinterpret_cast<uint2*>((uint16_t*)base + idx) =
+            make_uint2(pack2_bf16_rne(a, b), pack2_bf16_rne(c, d));
+    } else if (kind == 2) {
+        *reinterpret_cast<uint2*>((uint16_t*)base + idx) =
+            make_uint2(pack2_f16_rne(a, b), pack2_f16_rne(c, d));
+    } else {
+        *reinterpret_cast<float4*>((float*)base + idx) = make_float4(a, b, c, d);
+    }
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
     return __uint_as_float(((uint32_t)h) << 16);
 }

@@ -50,12 +50,12 @@ def rope_freqs(pairs):
 
 
 def make_awa_inputs(seed, video_shapes, text_lengths, heads, head_dim, pairs, bf16=False,
-                    peaky=True, shared_norm=False):
+                    peaky=True, shared_norm=False, fp16=False):
     """Seeded synthetic inputs of the layer: fused video_qkv [Lv, 3*inner] and
     text_qkv [Lt, 3*inner] ~ N(0,1); norm weights N(0,0.02) ("literal") or
     1+N(0,0.02) ("peaky", which makes the softmax far from uniform).  With
-    bf16=True the activations are rounded to bf16 and the oracle consumes the
-    same rounded values."""
+    bf16=True (fp16=True) the activations are rounded to bf16 (fp16) and the
+    oracle consumes the same rounded values."""
     g = np.random.default_rng(seed)
     inner = heads * head_dim
     lv = int(sum(t * h * w for t, h, w in video_shapes))
@@ -64,6 +64,9 @@ def make_awa_inputs(seed, video_shapes, text_lengths, heads, head_dim, pairs, bf
     text = g.standard_normal((lt, 3 * inner), dtype=np.float32)
     if bf16:
         video, text = bf16_round(video), bf16_round(text)
+    if fp16:
+        video = video.astype(np.float16).astype(np.float32)
+        text = text.astype(np.float16).astype(np.float32)
     base = 1.0 if peaky else 0.0
     norms = (base + 0.02 * g.standard_normal((4, head_dim))).astype(np.float32)
     if shared_norm:
@@ -111,6 +114,7 @@ def harness():
         L.h_awa_configure_and_set_weights.argtypes = [vp, ci, ci, P(ci), ci, cf, ci, ci, ci,
                                                       P(cf), P(cf), P(cf), P(cf), P(cf)]
         L.h_layer_forward.argtypes = [vp, ci, P(HBlob), ci, P(HBlob)]
+        L.h_layer_set_storage.argtypes = [vp, ci, ci]
         L.h_build_plan.argtypes = [P(ci), ci, P(ci), ci, ci, P(ci), P(ci), P(ci), P(ci), P(ci), P(ci)]
         _H = L
     return _H
@@ -141,6 +145,10 @@ class Layer:
 
     def create_pipeline(self):
         return harness().h_layer_create_pipeline(self.h)
+
+    def set_storage(self, fp16, bf16):
+        """ncnn Option use_fp16_storage / use_bf16_storage for forward."""
+        harness().h_layer_set_storage(self.h, int(bool(fp16)), int(bool(bf16)))
 
     def set_state(self, video_shapes, text_lengths):
         s = np.ascontiguousarray(np.asarray(video_shapes, np.int32).ravel())

@@ -39,7 +39,7 @@ extern "C" {
 typedef struct h_blob {
     int dims;       // 0 = empty blob, 1 or 2
     int w, h;
-    int elemsize;   // 4 fp32 / int32, 2 bf16
+    int elemsize;   // 4 fp32 / int32, 2 bf16 or fp16
     int device;     // data is a device pointer
     void* data;
 } h_blob;
@@ -108,6 +108,14 @@ int h_awa_configure_and_set_weights(void* handle, int heads, int head_dim, const
     return l->set_weights(std::vector<float>(vq, vq + head_dim), std::vector<float>(vk, vk + head_dim),
                           std::vector<float>(tq, tq + head_dim), std::vector<float>(tk, tk + head_dim),
                           std::vector<float>(freqs, freqs + pairs));
+}
+
+// ncnn's 16-bit storage options of the Option passed to forward: they pick
+// fp16 or bf16 for device blobs of elemsize 2.
+void h_layer_set_storage(void* handle, int use_fp16_storage, int use_bf16_storage) {
+    Handle* h = static_cast<Handle*>(handle);
+    h->opt.use_fp16_storage = use_fp16_storage != 0;
+    h->opt.use_bf16_storage = use_bf16_storage != 0;
 }
 
 // forward(vector<Mat>) with host or device input blobs.  Outputs are copied

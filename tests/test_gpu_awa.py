@@ -28,10 +28,10 @@ def torch_mod():
 
 
 def _run_capi(case, heads, d, target, shifted, pairs, shapes, text_lengths, bf16_in, out_dtype,
-              official=False, split=False, eps=1e-5):
+              official=False, split=False, eps=1e-5, in_dtype=None):
     torch = torch_mod()
     inner = heads * d
-    dt = torch.bfloat16 if bf16_in else torch.float32
+    dt = in_dtype or (torch.bfloat16 if bf16_in else torch.float32)
     v = torch.from_numpy(case["video"]).to("cuda").to(dt)
     t = torch.from_numpy(case["text"]).to("cuda").to(dt)
     if split:
@@ -157,6 +157,29 @@ def test_layer_device_blobs_bf16_zero_copy():
     assert_close(ot.float().cpu().numpy(), rt, "text")
 
 
+def test_layer_device_blobs_fp16_zero_copy():
+    """Device blobs of elemsize 2 under ncnn's use_fp16_storage are fp16: they
+    run zero-copy and return fp16 device blobs."""
+    torch = torch_mod()
+    shapes, tl = [(2, 16, 16)], [64]
+    heads, d, pairs, target = 4, 128, 21, (4, 3, 3)
+    case = make_awa_inputs(313, shapes, tl, heads, d, pairs, fp16=True)
+    inner = heads * d
+    layer = Layer("AdaptiveWindowAttention", awa_param_string(heads, d, target, 1, 1e-5, pairs),
+                  [case["norms"][i] for i in range(4)] + [case["freqs"]])
+    layer.set_storage(fp16=True, bf16=False)
+    layer.set_state(shapes, tl)
+    v = torch.from_numpy(case["video"]).cuda().to(torch.float16)
+    t = torch.from_numpy(case["text"]).cuda().to(torch.float16)
+    code, (ov, ot) = layer.forward([v, t, None, None],
+                                   [((512, inner), torch.float16), ((64, inner), torch.float16)],
+                                   device_out=True)
+    assert code == 0
+    rv, rt = oracle_awa(case, heads, d, target, 1, 1e-5, pairs, shapes, tl)
+    assert_close(ov.float().cpu().numpy(), rv, "video")
+    assert_close(ot.float().cpu().numpy(), rt, "text")
+
+
 # ---- SeedVR2-3B shapes through the C-ABI, bf16 -------------------------------------------
 
 @pytest.mark.parametrize("shifted", [0, 1])
@@ -168,6 +191,21 @@ def test_image_grid_64x64_dim2560(shifted):
     rv, rt = oracle_awa(case, 20, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl)
     for out_dtype in (torch.float32, torch.bfloat16):
         ov, ot = _run_capi(case, 20, 128, (4, 3, 3), shifted, 21, shapes, tl, True, out_dtype)
+        assert_close(ov, rv, f"video {out_dtype}")
+        assert_close(ot, rt, f"text {out_dtype}")
+
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_image_grid_64x64_dim2560_fp16(shifted):
+    """The same image in fp16 storage (the reference Vulkan path's usual 16-bit
+    blobs): fp16 inputs, fp16 and fp32 outputs."""
+    import torch
+    shapes, tl = [(1, 64, 64)], [64]
+    case = make_awa_inputs(414 + shifted, shapes, tl, 20, 128, 21, fp16=True)
+    rv, rt = oracle_awa(case, 20, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl)
+    for out_dtype in (torch.float16, torch.float32):
+        ov, ot = _run_capi(case, 20, 128, (4, 3, 3), shifted, 21, shapes, tl, False, out_dtype,
+                           in_dtype=torch.float16)
         assert_close(ov, rv, f"video {out_dtype}")
         assert_close(ot, rt, f"text {out_dtype}")
 

@@ -180,6 +180,32 @@ def test_split_tail_is_deterministic(mv, mt, k, n):
     assert _tight(outs[0][0][rows], xv, bf16_round(w), b, 1, rows=rows) < 2e-4
 
 
+@pytest.mark.parametrize("mv,mt,k,n", [(300, 40, 128, 260), (1000, 64, 640, 768)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_fp16_activations(mv, mt, k, n, act):
+    """fp16 activations (rounded to bf16, the MFMA operand type, while staged)
+    with fp16 and fp32 outputs."""
+    import torch
+    g = np.random.default_rng(mv + k + 7 * act)
+    xv = g.standard_normal((mv, k)).astype(np.float16).astype(np.float32)
+    xt = g.standard_normal((mt, k)).astype(np.float16).astype(np.float32)
+    w = (0.02 * g.standard_normal((n, k))).astype(np.float32)
+    b = (0.02 * g.standard_normal(n)).astype(np.float32)
+    tv = torch.from_numpy(xv).cuda().to(torch.float16)
+    tt = torch.from_numpy(xt).cuda().to(torch.float16)
+    wb = capi.cast_f32_to_bf16(torch.from_numpy(w).cuda())
+    tb = torch.from_numpy(b).cuda()
+    for odt in (torch.float16, torch.float32):
+        yv, yt = capi.shared_linear(tv, tt, wb, tb, act, out_dtype=odt)
+        torch.cuda.synchronize()
+        assert yv.dtype == odt and yt.dtype == odt
+        assert_close(yv.float().cpu().numpy(), oracle.linear(xv, w, b, act, threads=THREADS), "video")
+        assert_close(yt.float().cpu().numpy(), oracle.linear(xt, w, b, act, threads=THREADS), "text")
+        # kernel arithmetic: the same bf16 operands, fp32 accumulation
+        tol = 1e-2 if odt == torch.float16 else 2e-4
+        assert _tight(yv.float().cpu().numpy(), bf16_round(xv), bf16_round(w), b, act) < tol
+
+
 def test_fp32_activations_medium_shape():
     """fp32 activations take the 128x128-tile path (rounded to bf16 while
     staged): a 4,100-row, K = 2560 -> N = 2560 projection with GELU."""
