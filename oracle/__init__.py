@@ -68,6 +68,12 @@ def lib(fast: bool = False) -> ctypes.CDLL:
                                       P(cf), P(cf), P(cf), ctypes.c_long,
                                       P(cf), P(cf), P(ci), ci, ci]
         L.orc_linear.argtypes = [P(cf), ci, ci, P(cf), P(cf), ci, ci, P(cf), P(ci), ci, ci]
+        cl = ctypes.c_long
+        L.orc_patchify_video.argtypes = [P(cf), cl, P(ci), ci, P(cf)]
+        L.orc_timestep_embedding.argtypes = [P(cf), ci, P(cf)]
+        L.orc_unpatchify_prediction.argtypes = [P(cf), cl, P(ci), ci, P(cf)]
+        L.orc_apply_cfg.argtypes = [P(cf), P(cf), cl, cf, cf, P(cf)]
+        L.orc_euler_step.argtypes = [P(cf), cl, P(cf), cl, cf]
         _LIBS[name] = L
     return _LIBS[name]
 
@@ -229,3 +235,55 @@ def linear(x, w, bias=None, activation=0, rows=None, threads=1, fast=False) -> n
                  y.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), pr, nr if rows is not None else 0,
                  threads)
     return y
+
+
+# ---- DiT frontend and tail ---------------------------------------------------------
+
+def patchify_video(source, video_shapes):
+    """seedvr2_dit.cpp:167-230: [tokens][33] -> [patches][132]; (code, out)."""
+    src, ps = _f32(source)
+    shapes, pshp = _i32(np.asarray(video_shapes).reshape(-1, 3))
+    patches = int(sum(int(t) * (int(h) // 2) * (int(w) // 2) for t, h, w in shapes))
+    out = np.zeros((patches, 132), np.float32)
+    code = lib().orc_patchify_video(ps, src.shape[0], pshp, shapes.shape[0],
+                                    out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return code, out
+
+
+def timestep_embedding(timesteps):
+    """seedvr2_dit.cpp:232-253: [count][256]."""
+    ts, pt = _f32(np.asarray(timesteps, np.float32).ravel())
+    out = np.zeros((ts.shape[0], 256), np.float32)
+    lib().orc_timestep_embedding(pt, ts.shape[0], out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return out
+
+
+def unpatchify_prediction(source, video_shapes):
+    """seedvr2_dit.cpp:255-326: [patches][64] -> [tokens][16]; (code, out)."""
+    src, ps = _f32(source)
+    shapes, pshp = _i32(np.asarray(video_shapes).reshape(-1, 3))
+    tokens = int(sum(int(t) * int(h) * int(w) for t, h, w in shapes))
+    out = np.zeros((tokens, 16), np.float32)
+    code = lib().orc_unpatchify_prediction(ps, src.shape[0], pshp, shapes.shape[0],
+                                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return code, out
+
+
+def apply_cfg(positive, negative, scale, rescale):
+    """seedvr2_pipeline.cpp:171-210."""
+    pos, pp = _f32(np.ravel(positive))
+    neg, pn = _f32(np.ravel(negative))
+    out = np.zeros_like(pos)
+    lib().orc_apply_cfg(pp, pn, pos.shape[0], float(scale), float(rescale),
+                        out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return out.reshape(np.shape(positive))
+
+
+def euler_step(latent, prediction, delta):
+    """seedvr2_pipeline.cpp:575-588 on a copy of latent [16][stride] (the
+    first tokens entries of each channel row are the tokens)."""
+    lat = np.array(latent, dtype=np.float32, copy=True, order="C")
+    pred, pp = _f32(prediction)
+    lib().orc_euler_step(lat.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), lat.shape[1], pp,
+                         pred.shape[0], float(delta))
+    return lat

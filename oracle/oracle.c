@@ -488,3 +488,126 @@ void orc_linear(const float* x, int m, int k, const float* w, const float* bias,
     }
     (void)num_threads;
 }
+
+/* ---- DiT frontend and tail -------------------------------------------------- */
+
+/* seedvr2_dit.cpp:167-230 */
+int orc_patchify_video(const float* source, long tokens, const int* shapes, int batch,
+                       float* destination)
+{
+    long expected = 0;
+    for (int b = 0; b < batch; b++) {
+        const int t = shapes[3 * b], h = shapes[3 * b + 1], w = shapes[3 * b + 2];
+        if (t <= 0 || h <= 0 || w <= 0 || h % 2 != 0 || w % 2 != 0)
+            return -1;
+        expected += (long)t * h * w;
+    }
+    if (expected != tokens)
+        return -1;
+    long in_off = 0, out_row = 0;
+    for (int b = 0; b < batch; b++) {
+        const int t = shapes[3 * b], h = shapes[3 * b + 1], w = shapes[3 * b + 2];
+        for (int f = 0; f < t; f++)
+            for (int py = 0; py < h / 2; py++)
+                for (int px = 0; px < w / 2; px++) {
+                    float* out = destination + (out_row++) * 132;
+                    for (int y = 0; y < 2; y++)
+                        for (int x = 0; x < 2; x++) {
+                            const long tok = in_off + ((long)f * h + py * 2 + y) * w + px * 2 + x;
+                            memcpy(out + (y * 2 + x) * 33, source + tok * 33, 33 * sizeof(float));
+                        }
+                }
+        in_off += (long)t * h * w;
+    }
+    return 0;
+}
+
+/* seedvr2_dit.cpp:232-253 */
+void orc_timestep_embedding(const float* timesteps, int count, float* embedding)
+{
+    const int half_dim = 128;
+    for (int s = 0; s < count; s++) {
+        float* out = embedding + (long)s * 2 * half_dim;
+        for (int i = 0; i < half_dim; i++) {
+            const float exponent = -logf(10000.f) * i / half_dim;
+            const float phase = timesteps[s] * expf(exponent);
+            out[i] = sinf(phase);
+            out[i + half_dim] = cosf(phase);
+        }
+    }
+}
+
+/* seedvr2_dit.cpp:255-326 */
+int orc_unpatchify_prediction(const float* source, long patches, const int* shapes, int batch,
+                              float* destination)
+{
+    long expected = 0;
+    for (int b = 0; b < batch; b++) {
+        const int t = shapes[3 * b], h = shapes[3 * b + 1], w = shapes[3 * b + 2];
+        if (t <= 0 || h <= 0 || w <= 0 || h % 2 != 0 || w % 2 != 0)
+            return -1;
+        expected += (long)t * (h / 2) * (w / 2);
+    }
+    if (expected != patches)
+        return -1;
+    long patch_off = 0, out_off = 0;
+    for (int b = 0; b < batch; b++) {
+        const int t = shapes[3 * b], h = shapes[3 * b + 1], w = shapes[3 * b + 2];
+        const int ph = h / 2, pw = w / 2;
+        for (int f = 0; f < t; f++)
+            for (int py = 0; py < ph; py++)
+                for (int px = 0; px < pw; px++) {
+                    const float* in = source + (patch_off + ((long)f * ph + py) * pw + px) * 64;
+                    for (int y = 0; y < 2; y++)
+                        for (int x = 0; x < 2; x++) {
+                            const long tok = out_off + ((long)f * h + py * 2 + y) * w + px * 2 + x;
+                            memcpy(destination + tok * 16, in + (y * 2 + x) * 16, 16 * sizeof(float));
+                        }
+                }
+        patch_off += (long)t * ph * pw;
+        out_off += (long)t * h * w;
+    }
+    return 0;
+}
+
+/* seedvr2_pipeline.cpp:171-210 */
+void orc_apply_cfg(const float* positive, const float* negative, long count, float scale,
+                   float rescale, float* output)
+{
+    for (long i = 0; i < count; i++)
+        output[i] = negative[i] + scale * (positive[i] - negative[i]);
+    if (rescale == 0.f || count < 2)
+        return;
+    double pos_mean = 0.0, cfg_mean = 0.0;
+    for (long i = 0; i < count; i++) {
+        pos_mean += positive[i];
+        cfg_mean += output[i];
+    }
+    pos_mean /= count;
+    cfg_mean /= count;
+    double pos_var = 0.0, cfg_var = 0.0;
+    for (long i = 0; i < count; i++) {
+        const double p = positive[i] - pos_mean;
+        const double c = output[i] - cfg_mean;
+        pos_var += p * p;
+        cfg_var += c * c;
+    }
+    const double pos_std = sqrt(pos_var / (count - 1));
+    const double cfg_std = sqrt(cfg_var / (count - 1));
+    if (cfg_std == 0.0)
+        return;
+    const float factor = (float)(rescale * pos_std / cfg_std + (1.f - rescale));
+    for (long i = 0; i < count; i++)
+        output[i] *= factor;
+}
+
+/* seedvr2_pipeline.cpp:575-588 */
+void orc_euler_step(float* latent, long channel_stride, const float* prediction, long tokens,
+                    float delta)
+{
+    for (long t = 0; t < tokens; t++)
+        for (int c = 0; c < 16; c++) {
+            const float step = delta * prediction[t * 16 + c];
+            latent[c * channel_stride + t] += step;
+        }
+}

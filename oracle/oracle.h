@@ -23,6 +23,13 @@
  *   orc_linear        torch matmul in float64; GELU vs torch erf-GELU.
  *   orc_awa_forward   an independent torch float64 implementation of the
  *                     layer semantics; single-window pooling identity.
+ *   orc_patchify_video, orc_unpatchify_prediction
+ *                     numpy reshape/transpose of the (t, h, w) grids;
+ *                     unpatchify of a patchified grid returns its tokens.
+ *   orc_timestep_embedding  float64 closed form; t = 0 gives sin 0, cos 1.
+ *   orc_apply_cfg     float64 numpy closed form; scale 1 gives pos; zero
+ *                     spread keeps the unrescaled result.
+ *   orc_euler_step    numpy closed form with a strided channel layout.
  */
 #ifndef SEEDVR2_ORACLE_H
 #define SEEDVR2_ORACLE_H
@@ -112,6 +119,39 @@ int orc_awa_forward(const orc_awa_params* params,
  * (num_rows of them, Y then holds num_rows rows in that order). */
 void orc_linear(const float* x, int m, int k, const float* w, const float* bias, int n,
                 int activation, float* y, const int* rows, int num_rows, int num_threads);
+
+/* ---- DiT frontend and tail (the steps either side of the block stack) ---- */
+
+/* patchify_video (seedvr2_dit.cpp:167-230): source [tokens][33] of samples
+ * with video shapes (t, h, w), h and w even, -> destination
+ * [sum t*(h/2)*(w/2)][132]; patch (f, py, px) holds the 2x2 tokens
+ * (f, 2py+y, 2px+x) at feature offset (2y+x)*33.  Returns 0 or -1. */
+int orc_patchify_video(const float* source, long tokens, const int* shapes, int batch,
+                       float* destination);
+
+/* make_timestep_embedding (seedvr2_dit.cpp:232-253): [count][256],
+ * sin(t * exp(-log(10000) * i / 128)) at i, the cos at i + 128, fp32. */
+void orc_timestep_embedding(const float* timesteps, int count, float* embedding);
+
+/* unpatchify_prediction (seedvr2_dit.cpp:255-326): source [patches][64] ->
+ * destination [tokens][16]; token (f, 2py+y, 2px+x) takes features
+ * (2y+x)*16 .. +15 of patch (f, py, px).  shapes are the unpatchified
+ * (t, h, w), h and w even.  Returns 0 or -1. */
+int orc_unpatchify_prediction(const float* source, long patches, const int* shapes, int batch,
+                              float* destination);
+
+/* apply_cfg (seedvr2_pipeline.cpp:171-210): out = neg + scale*(pos - neg) in
+ * fp32; with rescale != 0 and count >= 2 it is then multiplied by
+ * float(rescale * std(pos) / std(out) + (1 - rescale)), the means and the
+ * (count - 1)-normalised deviations in double, unless std(out) is 0. */
+void orc_apply_cfg(const float* positive, const float* negative, long count, float scale,
+                   float rescale, float* output);
+
+/* Euler update of SeedVR2Pipeline::denoise (seedvr2_pipeline.cpp:575-588):
+ * latent channel c (channel_stride floats apart) at token t
+ * += delta * prediction[t][c], c < 16, as a product then a sum. */
+void orc_euler_step(float* latent, long channel_stride, const float* prediction, long tokens,
+                    float delta);
 
 #ifdef __cplusplus
 }
