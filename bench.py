@@ -17,7 +17,9 @@ activations, N(0,0.02) weights).  The shifted-window block (64 ragged
 windows) is timed too and reported beside the headline, and so is the
 SeedVR2-7B-shaped stack of 32 blocks (hidden 3072, 24 heads x 128, MLP
 3072 -> 12288 -> 3072, regular windows in even and shifted windows in odd
-blocks, 64 text tokens projected 5120 -> 3072 once) under "stack_7b".
+blocks, 64 text tokens projected 5120 -> 3072 once) under "stack_7b".  The
+frontend/tail kernels (patchify, unpatchify, CFG, Euler update) at the 720p
+latent are timed under "sampler_tail".
 
 Prints one JSON line.  `--gpus` above 1 is refused: this build measures one GPU.
 """
@@ -123,6 +125,86 @@ def cpu_baseline(threads, gemm_rows=2048):
     }
 
 
+LATENT_SHAPE = (6, 90, 160)    # 720p latent: 21 frames -> 6, 720/8, 1280/8
+
+
+def sampler_tail(reps=50):
+    """The frontend and tail kernels around the block stack at the 720p
+    latent (6x90x160 = 86,400 tokens, 21,600 patches), each timed over
+    `reps` back-to-back launches with HIP events on the launching stream.
+    Algorithmic bytes: every input element read once, every output element
+    written once (fp32); the Euler update reads and writes the 16 latent
+    planes.  Also times the oracle's serial CPU restatement of one denoise
+    step's tail (unpatchify twice, CFG with rescale, Euler) on one core."""
+    import numpy as np
+    import torch
+    import oracle
+    from seedvr2_ncnn_amd import capi
+
+    t, h, w = LATENT_SHAPE
+    tokens, patches = t * h * w, t * h * w // 4
+    stride = tokens
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(99)
+
+    def randn(*shape):
+        return torch.randn(*shape, generator=gen, device=dev, dtype=torch.float32)
+
+    lat, cond = randn(16, stride), randn(16, stride)
+    video, pos, neg = randn(tokens, 33), randn(patches, 64), randn(patches, 64)
+    pp, pn = torch.empty(tokens, 16, device=dev), torch.empty(tokens, 16, device=dev)
+    out132 = torch.empty(patches, 132, device=dev)
+    cfg_out = torch.empty(tokens, 16, device=dev)
+    f4 = 4
+    pl = tokens * 16 * f4          # one prediction / one set of 16 planes
+    cases = {
+        "latent_patches": (lambda: capi.latent_patches(lat, cond, t, h, w, stride, patches=out132),
+                           2 * pl + patches * 132 * f4),
+        "patchify": (lambda: capi.patchify_video(video, [LATENT_SHAPE], patches=out132),
+                     2 * tokens * 33 * f4),
+        "unpatchify": (lambda: capi.unpatchify_prediction(pos, [LATENT_SHAPE], prediction=pp), 2 * pl),
+        "apply_cfg_rescale": (lambda: capi.apply_cfg(pp, pn, 6.5, 0.7, output=cfg_out), 3 * pl),
+        "euler_step": (lambda: capi.euler_step(lat, stride, cfg_out, 0.0), 3 * pl),
+        "denoise_update_cfg_rescale": (
+            lambda: capi.denoise_update(pos, neg, t, h, w, 6.5, 0.7, 0.0, lat, stride), 4 * pl),
+    }
+    capi.unpatchify_prediction(neg, [LATENT_SHAPE], prediction=pn)
+    out = {}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(5):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        out[name] = {"us": round(ms * 1e3, 2), "algorithmic_bytes": nbytes,
+                     "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                     "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+    unfused = sum(out[k]["us"] for k in ("unpatchify", "apply_cfg_rescale", "euler_step")) + out["unpatchify"]["us"]
+    out["step_tail_unfused_us"] = round(unfused, 2)
+    out["step_tail_fused_us"] = out["denoise_update_cfg_rescale"]["us"]
+
+    g = np.random.default_rng(5)
+    h_pos = g.standard_normal((patches, 64), dtype=np.float32)
+    h_neg = g.standard_normal((patches, 64), dtype=np.float32)
+    h_lat = g.standard_normal((16, stride), dtype=np.float32)
+    t0 = time.perf_counter()
+    _, a = oracle.unpatchify_prediction(h_pos, [LATENT_SHAPE])
+    _, b = oracle.unpatchify_prediction(h_neg, [LATENT_SHAPE])
+    guided = oracle.apply_cfg(a.ravel(), b.ravel(), 6.5, 0.7).reshape(a.shape)
+    oracle.euler_step(h_lat, guided, -0.02)
+    out["cpu_step_tail_ms"] = round((time.perf_counter() - t0) * 1e3, 2)
+    out["workload"] = (f"720p latent {t}x{h}x{w} = {tokens} tokens, {patches} patches; "
+                       "fp32; CFG scale 6.5, rescale 0.7")
+    del lat, cond, video, pos, neg, pp, pn, out132, cfg_out
+    torch.cuda.empty_cache()
+    return out
+
+
 STACK_HIDDEN, STACK_HEADS, STACK_MLP, STACK_BLOCKS, STACK_TEXT_WIDTH = 3072, 24, 12288, 32, 5120
 
 
@@ -221,6 +303,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-stack", action="store_true", help="skip the 32-block 7B-shaped stack")
     ap.add_argument("--stack-steps", type=int, default=3)
+    ap.add_argument("--no-tail", action="store_true",
+                    help="skip the frontend/tail kernels at the 720p latent")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device copy (a plain copy kernel of known size) so "
                          "that PMC byte counters can be calibrated in the same profiler run")
@@ -402,6 +486,8 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_stack:
         line["stack_7b"] = stack_7b(args.stack_steps, 1)
+    if not args.no_tail:
+        line["sampler_tail"] = sampler_tail()
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         line["cpu_baseline"] = cpu_baseline(threads)

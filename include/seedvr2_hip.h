@@ -191,6 +191,77 @@ S2_API int s2_shared_linear_forward(const void* x_video, int m_video, const void
                              void* y_video, void* y_text, s2_dtype y_dtype,
                              s2_stream_t stream);
 
+/* ---- DiT frontend and tail, sampler step -------------------------------- */
+/* The steps either side of the block stack, on device fp32 buffers.  A video
+ * sample is a (frames, height, width) token grid; shapes are int[3] per
+ * sample.  Returns S2_ERR_INVALID where the reference returns -1: a
+ * non-positive extent, an odd height or width, or sizes that do not match. */
+
+/* patchify_video (src/seedvr2/seedvr2_dit.cpp:167-230): tokens [tokens][33]
+ * -> patches [sum t*(h/2)*(w/2)][132]; patch (f, py, px) is the four tokens
+ * (2py+y, 2px+x), y outer, each 33 wide.  video_shapes: int[batch][3] on the
+ * host.  Both buffers 8-byte aligned. */
+S2_API int s2_patchify_video(const float* video, long tokens, const int* video_shapes, int batch,
+                             float* patches, s2_stream_t stream);
+
+/* The video tokens SeedVR2Pipeline::predict assembles from the latent and
+ * the condition (src/seedvr2/seedvr2_pipeline.cpp:296-317: token t is
+ * [latent[0..15][t] | condition[0..15][t] | 1]) and patchifies in
+ * SeedVR2DiT::forward (seedvr2_dit.cpp:1224), in one pass without the
+ * [tokens][33] intermediate.  latent, condition: 16 channel planes of one
+ * sample, plane c at c * channel_stride floats (an ncnn Mat's cstep). */
+S2_API int s2_latent_patches(const float* latent, const float* condition, long channel_stride,
+                             int frames, int height, int width, float* patches,
+                             s2_stream_t stream);
+
+/* make_timestep_embedding (src/seedvr2/seedvr2_dit.cpp:232-253): count
+ * timesteps (HOST memory, like the reference's std::vector<float>) ->
+ * device [count][256], row s = [sin(t_s f_i) | cos(t_s f_i)],
+ * f_i = exp(-ln(10000) i / 128).  Values are the correctly rounded sin/cos of
+ * the reference's fp32 phase (within 1 ulp of a C library's sinf/cosf). */
+S2_API int s2_timestep_embedding(const float* timesteps, int count, float* embedding,
+                                 s2_stream_t stream);
+
+/* unpatchify_prediction (src/seedvr2/seedvr2_dit.cpp:255-326): patches
+ * [sum t*(h/2)*(w/2)][64] -> prediction [sum t*h*w][16], the inverse token
+ * order of patchify with 16 channels per token.  The patchified shapes are
+ * (t, h/2, w/2) of video_shapes.  Both buffers 16-byte aligned. */
+S2_API int s2_unpatchify_prediction(const float* patches, long patch_count,
+                                    const int* video_shapes, int batch, float* prediction,
+                                    s2_stream_t stream);
+
+/* apply_cfg (src/seedvr2/seedvr2_pipeline.cpp:171-210): output = negative +
+ * scale (positive - negative), each operation rounded to fp32; when
+ * rescale != 0 and count >= 2, output *= (float)(rescale std(positive) /
+ * std(output) + (1 - rescale)) (sample standard deviations, accumulated in
+ * fp64), unless std(output) is 0.  16-byte aligned operands.  The rescale
+ * uses a per-device statistics scratch (40 KB, allocated by the first such
+ * call on a device and kept until the process ends); calls whose kernels
+ * overlap in time on one device must not both rescale. */
+S2_API int s2_apply_cfg(const float* positive, const float* negative, long count, float scale,
+                        float rescale, float* output, s2_stream_t stream);
+
+/* The Euler update of SeedVR2Pipeline::denoise (src/seedvr2/
+ * seedvr2_pipeline.cpp:575-588): latent[c][t] += delta * prediction[t][c]
+ * for c < 16, t < tokens, the product rounded before the sum.  latent: 16
+ * planes at channel_stride floats; prediction [tokens][16], 16-byte
+ * aligned. */
+S2_API int s2_euler_step(float* latent, long channel_stride, const float* prediction, long tokens,
+                         float delta, s2_stream_t stream);
+
+/* One sampler step after the predictions (src/seedvr2/
+ * seedvr2_pipeline.cpp:553-588 with the unpatchify of seedvr2_dit.cpp:1492),
+ * straight from the patchified predictions [t*(h/2)*(w/2)][64] of one sample:
+ * negative_patches NULL takes the positive prediction as is (the reference's
+ * cfg_scale == 1 branch); otherwise apply_cfg(positive, negative, cfg_scale,
+ * cfg_rescale).  Then the Euler update of the latent planes.  Equal to
+ * s2_unpatchify_prediction, s2_apply_cfg and s2_euler_step in sequence;
+ * shares s2_apply_cfg's statistics scratch. */
+S2_API int s2_denoise_update(const float* positive_patches, const float* negative_patches,
+                             int frames, int height, int width, float cfg_scale,
+                             float cfg_rescale, float delta, float* latent, long channel_stride,
+                             s2_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,7 @@ def lib(fast: bool = False) -> ctypes.CDLL:
         L.orc_unpatchify_prediction.argtypes = [P(cf), cl, P(ci), ci, P(cf)]
         L.orc_apply_cfg.argtypes = [P(cf), P(cf), cl, cf, cf, P(cf)]
         L.orc_euler_step.argtypes = [P(cf), cl, P(cf), cl, cf]
+        L.orc_video_tokens.argtypes = [P(cf), P(cf), cl, cl, P(cf)]
         _LIBS[name] = L
     return _LIBS[name]
 
@@ -287,3 +288,14 @@ def euler_step(latent, prediction, delta):
     lib().orc_euler_step(lat.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), lat.shape[1], pp,
                          pred.shape[0], float(delta))
     return lat
+
+
+def video_tokens(latent, condition, tokens):
+    """seedvr2_pipeline.cpp:296-317: planes [16][stride] x2 -> [tokens][33]."""
+    lat, pl = _f32(latent)
+    cond, pc = _f32(condition)
+    assert lat.shape == cond.shape and lat.shape[0] == 16 and lat.shape[1] >= tokens
+    out = np.zeros((tokens, 33), np.float32)
+    lib().orc_video_tokens(pl, pc, lat.shape[1], tokens,
+                           out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return out

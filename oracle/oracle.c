@@ -611,3 +611,17 @@ void orc_euler_step(float* latent, long channel_stride, const float* prediction,
             latent[c * channel_stride + t] += step;
         }
 }
+
+/* seedvr2_pipeline.cpp:296-317 */
+void orc_video_tokens(const float* latent, const float* condition, long channel_stride,
+                      long tokens, float* destination)
+{
+    for (long t = 0; t < tokens; t++) {
+        float* row = destination + t * 33;
+        for (int c = 0; c < 16; c++) {
+            row[c] = latent[c * channel_stride + t];
+            row[c + 16] = condition[c * channel_stride + t];
+        }
+        row[32] = 1.f;
+    }
+}

@@ -27,9 +27,12 @@
  *                     numpy reshape/transpose of the (t, h, w) grids;
  *                     unpatchify of a patchified grid returns its tokens.
  *   orc_timestep_embedding  float64 closed form; t = 0 gives sin 0, cos 1.
- *   orc_apply_cfg     float64 numpy closed form; scale 1 gives pos; zero
- *                     spread keeps the unrescaled result.
+ *   orc_apply_cfg     without rescale bit-exact against numpy fp32 (each
+ *                     operation rounded); with it, the float64 numpy closed
+ *                     form; scale 0 gives neg; zero spread keeps the
+ *                     unrescaled result.
  *   orc_euler_step    numpy closed form with a strided channel layout.
+ *   orc_video_tokens  numpy transpose of the channel planes.
  */
 #ifndef SEEDVR2_ORACLE_H
 #define SEEDVR2_ORACLE_H
@@ -152,6 +155,12 @@ void orc_apply_cfg(const float* positive, const float* negative, long count, flo
  * += delta * prediction[t][c], c < 16, as a product then a sum. */
 void orc_euler_step(float* latent, long channel_stride, const float* prediction, long tokens,
                     float delta);
+
+/* The video tokens of SeedVR2Pipeline::predict (seedvr2_pipeline.cpp:296-317):
+ * row t of destination [tokens][33] is latent channel 0..15 at t, condition
+ * channel 0..15 at t, then 1.  Channels are channel_stride floats apart. */
+void orc_video_tokens(const float* latent, const float* condition, long channel_stride,
+                      long tokens, float* destination);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,8 @@ EXPORTS = (
     "s2_awa_plan_create", "s2_awa_plan_get_info", "s2_awa_plan_get_windows",
     "s2_awa_plan_destroy", "s2_awa_plan_tables", "s2_awa_forward", "s2_cast_f32_to_bf16",
     "s2_cast_bf16_to_f32", "s2_shared_linear_forward", "s2_awa_stage_timing",
-    "s2_awa_stage_times",
+    "s2_awa_stage_times", "s2_patchify_video", "s2_latent_patches", "s2_timestep_embedding",
+    "s2_unpatchify_prediction", "s2_apply_cfg", "s2_euler_step", "s2_denoise_update",
 )
 
 
@@ -102,6 +103,13 @@ def lib() -> ctypes.CDLL:
         L.s2_shared_linear_forward.argtypes = [vp, ci, vp, ci, ci, vp, vp, ci, ci, ci, vp, vp, ci, vp]
         L.s2_awa_stage_timing.argtypes = [ci]
         L.s2_awa_stage_times.argtypes = [P(ctypes.c_float)]
+        L.s2_patchify_video.argtypes = [vp, cl, P(ci), ci, vp, vp]
+        L.s2_latent_patches.argtypes = [vp, vp, cl, ci, ci, ci, vp, vp]
+        L.s2_timestep_embedding.argtypes = [P(cf), ci, vp, vp]
+        L.s2_unpatchify_prediction.argtypes = [vp, cl, P(ci), ci, vp, vp]
+        L.s2_apply_cfg.argtypes = [vp, vp, cl, cf, cf, vp, vp]
+        L.s2_euler_step.argtypes = [vp, cl, vp, cl, cf, vp]
+        L.s2_denoise_update.argtypes = [vp, vp, ci, ci, ci, cf, cf, cf, vp, cl, vp]
         _LIB = L
     return _LIB
 
@@ -315,3 +323,87 @@ def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, 
                                          _dtype_code(y_video), _stream(stream)),
           "s2_shared_linear_forward")
     return y_video, y_text
+
+
+# ---- DiT frontend and tail, sampler step -------------------------------------
+
+def _shape_ints(video_shapes):
+    flat = [int(x) for s in video_shapes for x in s]
+    return _ints(flat), len(flat) // 3
+
+
+def patchify_video(video, video_shapes, patches=None, stream=None):
+    """s2_patchify_video: [tokens, 33] fp32 -> [patches, 132]."""
+    import torch
+    shapes, batch = _shape_ints(video_shapes)
+    n = sum(int(t) * (int(h) // 2) * (int(w) // 2) for t, h, w in video_shapes)
+    if patches is None:
+        patches = torch.empty((n, 132), dtype=torch.float32, device=video.device)
+    check(lib().s2_patchify_video(_ptr(video), video.shape[0], shapes, batch, _ptr(patches),
+                                  _stream(stream)), "s2_patchify_video")
+    return patches
+
+
+def latent_patches(latent, condition, frames, height, width, channel_stride, patches=None,
+                   stream=None):
+    """s2_latent_patches: 16-plane latent and condition -> [patches, 132]."""
+    import torch
+    if patches is None:
+        patches = torch.empty((frames * (height // 2) * (width // 2), 132), dtype=torch.float32,
+                              device=latent.device)
+    check(lib().s2_latent_patches(_ptr(latent), _ptr(condition), channel_stride, frames, height,
+                                  width, _ptr(patches), _stream(stream)), "s2_latent_patches")
+    return patches
+
+
+def timestep_embedding(timesteps, device="cuda", embedding=None, stream=None):
+    """s2_timestep_embedding: host timesteps -> device [count, 256]."""
+    import torch
+    ts = [float(t) for t in timesteps]
+    if embedding is None:
+        embedding = torch.empty((len(ts), 256), dtype=torch.float32, device=device)
+    arr = (ctypes.c_float * max(1, len(ts)))(*ts)
+    check(lib().s2_timestep_embedding(arr, len(ts), _ptr(embedding), _stream(stream)),
+          "s2_timestep_embedding")
+    return embedding
+
+
+def unpatchify_prediction(patches, video_shapes, prediction=None, stream=None):
+    """s2_unpatchify_prediction: [patches, 64] -> [tokens, 16]."""
+    import torch
+    shapes, batch = _shape_ints(video_shapes)
+    n = sum(int(t) * int(h) * int(w) for t, h, w in video_shapes)
+    if prediction is None:
+        prediction = torch.empty((n, 16), dtype=torch.float32, device=patches.device)
+    check(lib().s2_unpatchify_prediction(_ptr(patches), patches.shape[0], shapes, batch,
+                                         _ptr(prediction), _stream(stream)),
+          "s2_unpatchify_prediction")
+    return prediction
+
+
+def apply_cfg(positive, negative, scale, rescale, output=None, stream=None):
+    """s2_apply_cfg over all elements of positive/negative (contiguous fp32)."""
+    import torch
+    if output is None:
+        output = torch.empty_like(positive)
+    check(lib().s2_apply_cfg(_ptr(positive), _ptr(negative), positive.numel(), float(scale),
+                             float(rescale), _ptr(output), _stream(stream)), "s2_apply_cfg")
+    return output
+
+
+def euler_step(latent, channel_stride, prediction, delta, stream=None):
+    """s2_euler_step: latent planes += delta * prediction^T, in place."""
+    check(lib().s2_euler_step(_ptr(latent), channel_stride, _ptr(prediction),
+                              prediction.shape[0], float(delta), _stream(stream)),
+          "s2_euler_step")
+    return latent
+
+
+def denoise_update(positive_patches, negative_patches, frames, height, width, cfg_scale,
+                   cfg_rescale, delta, latent, channel_stride, stream=None):
+    """s2_denoise_update: one sampler step from patchified predictions, in place."""
+    check(lib().s2_denoise_update(_ptr(positive_patches), _ptr(negative_patches), frames, height,
+                                  width, float(cfg_scale), float(cfg_rescale), float(delta),
+                                  _ptr(latent), channel_stride, _stream(stream)),
+          "s2_denoise_update")
+    return latent

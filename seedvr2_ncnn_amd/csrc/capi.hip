@@ -8,6 +8,7 @@
 
 #include "awa_kernels.h"
 #include "awa_plan.h"
+#include "pipeline_kernels.h"
 #include "seedvr2_hip.h"
 
 namespace {
@@ -57,6 +58,25 @@ StageTimer& stage_timer() {
 
 bool dtype_ok(s2_dtype t) { return t == S2_DTYPE_F32 || t == S2_DTYPE_BF16 || t == S2_DTYPE_F16; }
 size_t dtype_bytes(s2_dtype t) { return t == S2_DTYPE_F32 ? 4 : 2; }
+
+bool aligned(const void* p, size_t a) { return ((uintptr_t)p) % a == 0; }
+
+// Validates video sample shapes as the reference's patchify/unpatchify do
+// (seedvr2_dit.cpp:181-191, 270-283): positive, even height and width.
+// Returns the token and patch totals.
+bool video_shapes_ok(const int* shapes, int batch, long* tokens, long* patches) {
+    if (!shapes || batch <= 0) return false;
+    long nt = 0, np = 0;
+    for (int b = 0; b < batch; ++b) {
+        const int t = shapes[3 * b], h = shapes[3 * b + 1], w = shapes[3 * b + 2];
+        if (t <= 0 || h <= 0 || w <= 0 || h % 2 != 0 || w % 2 != 0) return false;
+        nt += (long)t * h * w;
+        np += (long)t * (h / 2) * (w / 2);
+    }
+    *tokens = nt;
+    *patches = np;
+    return true;
+}
 
 }  // namespace
 
@@ -441,6 +461,105 @@ int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_tex
     S2_HIP(s2::launch_shared_linear(x_video, m_video, x_text, m_text, (int)x_dtype, weight, bias,
                                     n, k, activation, y_video, y_text, (int)y_dtype,
                                     (hipStream_t)stream));
+    return S2_OK;
+}
+
+/* ---- DiT frontend and tail, sampler step ---------------------------------- */
+
+int s2_patchify_video(const float* video, long tokens, const int* video_shapes, int batch,
+                      float* patches, s2_stream_t stream) {
+    long nt = 0, np = 0;
+    if (!video_shapes_ok(video_shapes, batch, &nt, &np) || nt != tokens)
+        return fail(S2_ERR_INVALID, "video shapes do not match the token count");
+    if (!video || !patches) return fail(S2_ERR_INVALID, "null pointer");
+    if (!aligned(video, 8) || !aligned(patches, 8))
+        return fail(S2_ERR_INVALID, "video and patches must be 8-byte aligned");
+    long in_off = 0, out_off = 0;
+    for (int b = 0; b < batch; ++b) {
+        const int t = video_shapes[3 * b], h = video_shapes[3 * b + 1], w = video_shapes[3 * b + 2];
+        S2_HIP(s2::launch_patchify(video + in_off * 33, t, h, w, patches + out_off * 132,
+                                   (hipStream_t)stream));
+        in_off += (long)t * h * w;
+        out_off += (long)t * (h / 2) * (w / 2);
+    }
+    return S2_OK;
+}
+
+int s2_latent_patches(const float* latent, const float* condition, long channel_stride,
+                      int frames, int height, int width, float* patches, s2_stream_t stream) {
+    const int shape[3] = {frames, height, width};
+    long nt = 0, np = 0;
+    if (!video_shapes_ok(shape, 1, &nt, &np)) return fail(S2_ERR_INVALID, "invalid latent shape");
+    if (channel_stride < nt) return fail(S2_ERR_INVALID, "channel stride below the token count");
+    if (!latent || !condition || !patches) return fail(S2_ERR_INVALID, "null pointer");
+    S2_HIP(s2::launch_latent_patches(latent, condition, channel_stride, frames, height, width,
+                                     patches, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_timestep_embedding(const float* timesteps, int count, float* embedding,
+                          s2_stream_t stream) {
+    if (count <= 0 || !timesteps) return fail(S2_ERR_INVALID, "no timesteps");
+    if (!embedding) return fail(S2_ERR_INVALID, "null pointer");
+    S2_HIP(s2::launch_timestep_embedding(timesteps, count, embedding, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_unpatchify_prediction(const float* patches, long patch_count, const int* video_shapes,
+                             int batch, float* prediction, s2_stream_t stream) {
+    long nt = 0, np = 0;
+    if (!video_shapes_ok(video_shapes, batch, &nt, &np) || np != patch_count)
+        return fail(S2_ERR_INVALID, "video shapes do not match the patch count");
+    if (!patches || !prediction) return fail(S2_ERR_INVALID, "null pointer");
+    if (!aligned(patches, 16) || !aligned(prediction, 16))
+        return fail(S2_ERR_INVALID, "patches and prediction must be 16-byte aligned");
+    long in_off = 0, out_off = 0;
+    for (int b = 0; b < batch; ++b) {
+        const int t = video_shapes[3 * b], h = video_shapes[3 * b + 1], w = video_shapes[3 * b + 2];
+        S2_HIP(s2::launch_unpatchify(patches + in_off * 64, t, h, w, prediction + out_off * 16,
+                                     (hipStream_t)stream));
+        in_off += (long)t * (h / 2) * (w / 2);
+        out_off += (long)t * h * w;
+    }
+    return S2_OK;
+}
+
+int s2_apply_cfg(const float* positive, const float* negative, long count, float scale,
+                 float rescale, float* output, s2_stream_t stream) {
+    if (count < 0) return fail(S2_ERR_INVALID, "negative count");
+    if (count == 0) return S2_OK;
+    if (!positive || !negative || !output) return fail(S2_ERR_INVALID, "null pointer");
+    if (!aligned(positive, 16) || !aligned(negative, 16) || !aligned(output, 16))
+        return fail(S2_ERR_INVALID, "operands must be 16-byte aligned");
+    S2_HIP(s2::launch_cfg(positive, negative, count, scale, rescale, output, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_euler_step(float* latent, long channel_stride, const float* prediction, long tokens,
+                  float delta, s2_stream_t stream) {
+    if (tokens < 0 || channel_stride < tokens)
+        return fail(S2_ERR_INVALID, "token count exceeds the channel stride");
+    if (tokens == 0) return S2_OK;
+    if (!latent || !prediction) return fail(S2_ERR_INVALID, "null pointer");
+    if (!aligned(prediction, 16)) return fail(S2_ERR_INVALID, "prediction must be 16-byte aligned");
+    S2_HIP(s2::launch_euler(latent, channel_stride, prediction, tokens, delta,
+                            (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_denoise_update(const float* positive_patches, const float* negative_patches, int frames,
+                      int height, int width, float cfg_scale, float cfg_rescale, float delta,
+                      float* latent, long channel_stride, s2_stream_t stream) {
+    const int shape[3] = {frames, height, width};
+    long nt = 0, np = 0;
+    if (!video_shapes_ok(shape, 1, &nt, &np)) return fail(S2_ERR_INVALID, "invalid latent shape");
+    if (channel_stride < nt) return fail(S2_ERR_INVALID, "channel stride below the token count");
+    if (!positive_patches || !latent) return fail(S2_ERR_INVALID, "null pointer");
+    if (!aligned(positive_patches, 16) || !aligned(negative_patches, 16))
+        return fail(S2_ERR_INVALID, "patches must be 16-byte aligned");
+    S2_HIP(s2::launch_denoise_update(positive_patches, negative_patches, frames, height, width,
+                                     cfg_scale, cfg_rescale, delta, latent, channel_stride,
+                                     (hipStream_t)stream));
     return S2_OK;
 }
 

@@ -1,0 +1,57 @@
+"""Argument checks of the DiT frontend/tail entry points, which return
+S2_ERR_INVALID (the reference's -1, src/seedvr2/seedvr2_dit.cpp:173-191,
+262-283) before any device work, so they run without a GPU."""
+import ctypes
+
+import pytest
+
+from seedvr2_ncnn_amd import capi
+
+INVALID = capi.S2_ERR_INVALID
+FAKE = ctypes.c_void_p(0x10000)   # never dereferenced: the checks fail first
+
+
+def _shapes(*s):
+    flat = [x for t in s for x in t]
+    return (ctypes.c_int * len(flat))(*flat)
+
+
+@pytest.fixture(scope="module")
+def L():
+    return capi.lib()
+
+
+def test_patchify_rejects_bad_shapes(L):
+    assert L.s2_patchify_video(FAKE, 24, _shapes((2, 3, 4)), 1, FAKE, None) == INVALID   # odd h
+    assert L.s2_patchify_video(FAKE, 24, _shapes((2, 4, 3)), 1, FAKE, None) == INVALID   # odd w
+    assert L.s2_patchify_video(FAKE, 24, _shapes((0, 4, 4)), 1, FAKE, None) == INVALID
+    assert L.s2_patchify_video(FAKE, 31, _shapes((2, 4, 4)), 1, FAKE, None) == INVALID   # count
+    assert L.s2_patchify_video(FAKE, 0, None, 0, FAKE, None) == INVALID                  # empty
+    assert L.s2_patchify_video(None, 32, _shapes((2, 4, 4)), 1, FAKE, None) == INVALID
+    assert L.s2_patchify_video(ctypes.c_void_p(0x10004), 32, _shapes((2, 4, 4)), 1, FAKE,
+                               None) == INVALID                                           # align
+
+
+def test_unpatchify_rejects_bad_shapes(L):
+    assert L.s2_unpatchify_prediction(FAKE, 7, _shapes((2, 4, 4)), 1, FAKE, None) == INVALID
+    assert L.s2_unpatchify_prediction(FAKE, 8, _shapes((2, 4, 5)), 1, FAKE, None) == INVALID
+    assert L.s2_unpatchify_prediction(FAKE, 8, _shapes((2, 4, 4)), 1, ctypes.c_void_p(0x10008),
+                                      None) == INVALID
+
+
+def test_latent_patches_and_steps_reject_bad_arguments(L):
+    assert L.s2_latent_patches(FAKE, FAKE, 31, 2, 4, 4, FAKE, None) == INVALID   # stride < tokens
+    assert L.s2_latent_patches(FAKE, FAKE, 32, 2, 4, 5, FAKE, None) == INVALID
+    assert L.s2_latent_patches(FAKE, None, 32, 2, 4, 4, FAKE, None) == INVALID
+    assert L.s2_timestep_embedding(None, 1, FAKE, None) == INVALID
+    ts = (ctypes.c_float * 1)(1.0)
+    assert L.s2_timestep_embedding(ts, 0, FAKE, None) == INVALID
+    assert L.s2_apply_cfg(FAKE, FAKE, -1, 2.0, 0.0, FAKE, None) == INVALID
+    assert L.s2_apply_cfg(FAKE, FAKE, 0, 2.0, 0.0, FAKE, None) == capi.S2_OK    # nothing to do
+    assert L.s2_apply_cfg(FAKE, ctypes.c_void_p(0x10004), 8, 2.0, 0.0, FAKE, None) == INVALID
+    assert L.s2_euler_step(FAKE, 9, FAKE, 10, 0.1, None) == INVALID
+    assert L.s2_euler_step(FAKE, 10, FAKE, 0, 0.1, None) == capi.S2_OK
+    assert L.s2_denoise_update(FAKE, None, 2, 4, 4, 1.0, 0.0, 0.1, FAKE, 31, None) == INVALID
+    assert L.s2_denoise_update(FAKE, None, 2, 3, 4, 1.0, 0.0, 0.1, FAKE, 32, None) == INVALID
+    assert L.s2_denoise_update(FAKE, ctypes.c_void_p(0x10004), 2, 4, 4, 1.0, 0.0, 0.1, FAKE, 32,
+                               None) == INVALID

@@ -114,3 +114,13 @@ def test_euler_step_closed_form():
     ref = lat.copy()
     ref[:, :tokens] = lat[:, :tokens] + (delta * pred.T)
     assert np.array_equal(out, ref)
+
+
+def test_video_tokens_transpose_of_planes():
+    g = np.random.default_rng(6)
+    tokens, stride = 300, 304
+    lat = g.standard_normal((16, stride)).astype(np.float32)
+    cond = g.standard_normal((16, stride)).astype(np.float32)
+    out = oracle.video_tokens(lat, cond, tokens)
+    ref = np.concatenate([lat[:, :tokens].T, cond[:, :tokens].T, np.ones((tokens, 1), np.float32)], 1)
+    assert np.array_equal(out, ref)
