@@ -20,6 +20,24 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIBS: dict = {}
 
 
+class Conv3dConfig(ctypes.Structure):
+    """The 16 DecomposedConv3D configuration values (decomposed_conv3d.cpp:422-441)."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "num_output", "num_input", "kernel_w", "kernel_h", "kernel_t", "stride_t", "dilation_t",
+        "head_frames", "stride_w", "stride_h", "dilation_w", "dilation_h", "pad_w", "pad_h",
+        "groups", "bias_term")]
+
+
+def conv3d_config(**kw):
+    c = Conv3dConfig()
+    defaults = dict(stride_t=1, dilation_t=1, head_frames=0, stride_w=1, stride_h=1,
+                    dilation_w=1, dilation_h=1, pad_w=0, pad_h=0, groups=1, bias_term=0)
+    defaults.update(kw)
+    for name, _ in Conv3dConfig._fields_:
+        setattr(c, name, int(defaults[name]))
+    return c
+
+
 class Slice(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "sample_index", "t0", "t1", "h0", "h1", "w0", "w1",
@@ -75,6 +93,8 @@ def lib(fast: bool = False) -> ctypes.CDLL:
         L.orc_apply_cfg.argtypes = [P(cf), P(cf), cl, cf, cf, P(cf)]
         L.orc_euler_step.argtypes = [P(cf), cl, P(cf), cl, cf]
         L.orc_video_tokens.argtypes = [P(cf), P(cf), cl, cl, P(cf)]
+        L.orc_decomposed_conv3d.argtypes = [P(Conv3dConfig), P(cf), ci, ci, ci, cl, P(cf), ci, cl,
+                                            P(cf), P(cf), P(cf), cl, P(cf), cl, ci]
         _LIBS[name] = L
     return _LIBS[name]
 
@@ -299,3 +319,54 @@ def video_tokens(latent, condition, tokens):
     lib().orc_video_tokens(pl, pc, lat.shape[1], tokens,
                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
     return out
+
+
+def _planar(a, pad):
+    """[C, F, H, W] -> [C, F*H*W + pad] (channel stride with padding)."""
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    c = a.shape[0]
+    flat = a.reshape(c, -1)
+    if pad:
+        flat = np.concatenate([flat, np.full((c, pad), np.nan, np.float32)], axis=1)
+    return np.ascontiguousarray(flat)
+
+
+def decomposed_conv3d(cfg, x, weights, bias=None, memory=None, want_memory=False, threads=8,
+                      cstep_pad=0):
+    """decomposed_conv3d.cpp:605-755.  x [Cin, F, H, W]; weights [kt, Cout,
+    Cin, kh, kw]; memory [Cin, M, H, W] or None.  Returns (out_t or -1,
+    out [Cout, To, Ho, Wo], next_memory [Cin, kt - st, H, W] or None)."""
+    cin, frames, h, w = x.shape
+    xin = _planar(x, cstep_pad)
+    pxin = xin.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+    mem = None
+    pm, mframes, mcs = None, 0, 0
+    if memory is not None:
+        mem = _planar(memory, cstep_pad)
+        pm, mframes, mcs = mem.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), memory.shape[1], mem.shape[1]
+    wts, pw_ = _f32(weights)
+    pb = None
+    if bias is not None:
+        b, pb = _f32(bias)
+    prefix = mframes if mframes else cfg.head_frames
+    extent = cfg.dilation_t * (cfg.kernel_t - 1) + 1
+    out_t = max((frames + prefix - extent) // cfg.stride_t + 1, 1)
+    ow = (w + 2 * cfg.pad_w - cfg.dilation_w * (cfg.kernel_w - 1) - 1) // cfg.stride_w + 1
+    oh = (h + 2 * cfg.pad_h - cfg.dilation_h * (cfg.kernel_h - 1) - 1) // cfg.stride_h + 1
+    out = np.zeros((cfg.num_output, max(out_t * oh * ow, 1)), np.float32)
+    cache = cfg.kernel_t - cfg.stride_t
+    nxt = None
+    pn, ncs = None, 0
+    if want_memory and cache > 0:
+        nxt = np.zeros((cin, cache * h * w), np.float32)
+        pn, ncs = nxt.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), nxt.shape[1]
+    code = lib().orc_decomposed_conv3d(ctypes.byref(cfg), pxin, frames, h, w, xin.shape[1], pm,
+                                       mframes, mcs, pw_, pb,
+                                       out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                       out.shape[1], pn, ncs, threads)
+    if code < 0:
+        return code, None, None
+    out = out[:, :code * oh * ow].reshape(cfg.num_output, code, oh, ow)
+    if nxt is not None:
+        nxt = nxt.reshape(cin, cache, h, w)
+    return code, out, nxt

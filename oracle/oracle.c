@@ -625,3 +625,111 @@ void orc_video_tokens(const float* latent, const float* condition, long channel_
         row[32] = 1.f;
     }
 }
+
+/* decomposed_conv3d.cpp:605-755: padded frame p of the sequence [prefix |
+ * input] comes from the memory (p < memory_frames), from input frame 0
+ * (p < head_frames without memory) or from input frame p - prefix. */
+static const float* conv3d_source_frame(const float* input, long in_cstep, int frames,
+                                        const float* memory, int memory_frames, long mem_cstep,
+                                        int prefix, int padded_index, int plane, long* cstep)
+{
+    if (memory && padded_index < prefix) {
+        if (padded_index >= memory_frames)
+            return NULL;
+        *cstep = mem_cstep;
+        return memory + (long)padded_index * plane;
+    }
+    const int source = padded_index < prefix ? 0 : padded_index - prefix;
+    if (source < 0 || source >= frames)
+        return NULL;
+    *cstep = in_cstep;
+    return input + (long)source * plane;
+}
+
+int orc_decomposed_conv3d(const orc_conv3d* cfg, const float* input, int frames, int height,
+                          int width, long in_cstep, const float* memory, int memory_frames,
+                          long mem_cstep, const float* weights, const float* bias, float* output,
+                          long out_cstep, float* next_memory, long next_cstep, int num_threads)
+{
+    const orc_conv3d c = *cfg;
+    if (c.num_output <= 0 || c.num_input <= 0 || c.kernel_w <= 0 || c.kernel_h <= 0 ||
+        c.kernel_t <= 0 || c.stride_t <= 0 || c.dilation_t <= 0 || c.stride_w <= 0 ||
+        c.stride_h <= 0 || c.dilation_w <= 0 || c.dilation_h <= 0 || c.groups != 1 ||
+        c.head_frames < 0 || frames <= 0)
+        return -1;
+    const int use_memory = memory != NULL && memory_frames > 0;
+    const int prefix = use_memory ? memory_frames : c.head_frames;
+    const int padded_t = frames + prefix;
+    const int extent = c.dilation_t * (c.kernel_t - 1) + 1;
+    if (padded_t < extent)
+        return -1;
+    const int out_t = (padded_t - extent) / c.stride_t + 1;
+    const int ow = (width + 2 * c.pad_w - c.dilation_w * (c.kernel_w - 1) - 1) / c.stride_w + 1;
+    const int oh = (height + 2 * c.pad_h - c.dilation_h * (c.kernel_h - 1) - 1) / c.stride_h + 1;
+    if (ow <= 0 || oh <= 0)
+        return -1;
+    const int plane = height * width, oplane = oh * ow;
+    const long wtap = (long)c.num_output * c.num_input * c.kernel_h * c.kernel_w;
+    const float* mem = use_memory ? memory : NULL;
+    for (int o = 0; o < out_t; o++)
+        for (int tap = 0; tap < c.kernel_t; tap++) {
+            long cs = 0;
+            if (!conv3d_source_frame(input, in_cstep, frames, mem, memory_frames, mem_cstep,
+                                     prefix, o * c.stride_t + tap * c.dilation_t, plane, &cs))
+                return -1;
+        }
+    for (int co = 0; co < c.num_output; co++)
+        for (int o = 0; o < out_t; o++)
+            memset(output + co * out_cstep + (long)o * oplane, 0, sizeof(float) * oplane);
+#pragma omp parallel for schedule(dynamic, 1) num_threads(num_threads > 0 ? num_threads : 1)
+    for (int co = 0; co < c.num_output; co++) {
+        for (int o = 0; o < out_t; o++) {
+            float* out = output + co * out_cstep + (long)o * oplane;
+            for (int tap = 0; tap < c.kernel_t; tap++) {
+                long cs = 0;
+                const float* src = conv3d_source_frame(input, in_cstep, frames, mem, memory_frames,
+                                                       mem_cstep, prefix,
+                                                       o * c.stride_t + tap * c.dilation_t,
+                                                       plane, &cs);
+                const float* wt = weights + tap * wtap + (long)co * c.num_input * c.kernel_h * c.kernel_w;
+                for (int y = 0; y < oh; y++)
+                    for (int x = 0; x < ow; x++) {
+                        /* the tap's ncnn Convolution: bias (tap 0 only) plus
+                         * the zero-padded window sum */
+                        double acc = (tap == 0 && bias) ? bias[co] : 0.0;
+                        for (int ci = 0; ci < c.num_input; ci++)
+                            for (int ky = 0; ky < c.kernel_h; ky++) {
+                                const int yi = y * c.stride_h + ky * c.dilation_h - c.pad_h;
+                                if (yi < 0 || yi >= height)
+                                    continue;
+                                for (int kx = 0; kx < c.kernel_w; kx++) {
+                                    const int xi = x * c.stride_w + kx * c.dilation_w - c.pad_w;
+                                    if (xi < 0 || xi >= width)
+                                        continue;
+                                    acc += (double)wt[((long)ci * c.kernel_h + ky) * c.kernel_w + kx] *
+                                           src[ci * cs + (long)yi * width + xi];
+                                }
+                            }
+                        out[(long)y * ow + x] += (float)acc;
+                    }
+            }
+        }
+    }
+    const int cache = c.kernel_t - c.stride_t;
+    if (next_memory && cache > 0) {
+        if (cache > padded_t)
+            return -1;
+        for (int f = 0; f < cache; f++) {
+            long cs = 0;
+            const float* src = conv3d_source_frame(input, in_cstep, frames, mem, memory_frames,
+                                                   mem_cstep, prefix, padded_t - cache + f, plane,
+                                                   &cs);
+            if (!src)
+                return -1;
+            for (int ci = 0; ci < c.num_input; ci++)
+                memcpy(next_memory + ci * next_cstep + (long)f * plane, src + ci * cs,
+                       sizeof(float) * plane);
+        }
+    }
+    return out_t;
+}

@@ -33,6 +33,10 @@
  *                     unrescaled result.
  *   orc_euler_step    numpy closed form with a strided channel layout.
  *   orc_video_tokens  numpy transpose of the channel planes.
+ *   orc_decomposed_conv3d  torch float64 conv3d over the temporally padded
+ *                     input (frame 0 replicated head_frames times); a run
+ *                     split into slices chained through the memory equals
+ *                     the unsplit run; a 1x1x1 kernel is a per-pixel matmul.
  */
 #ifndef SEEDVR2_ORACLE_H
 #define SEEDVR2_ORACLE_H
@@ -161,6 +165,31 @@ void orc_euler_step(float* latent, long channel_stride, const float* prediction,
  * channel 0..15 at t, then 1.  Channels are channel_stride floats apart. */
 void orc_video_tokens(const float* latent, const float* condition, long channel_stride,
                       long tokens, float* destination);
+
+/* The 16 configuration values of DecomposedConv3D, in the order of its
+ * config blob (decomposed_conv3d.cpp:422-441). */
+typedef struct orc_conv3d {
+    int num_output, num_input, kernel_w, kernel_h, kernel_t, stride_t, dilation_t, head_frames;
+    int stride_w, stride_h, dilation_w, dilation_h, pad_w, pad_h, groups, bias_term;
+} orc_conv3d;
+
+/* DecomposedConv3D::forward (decomposed_conv3d.cpp:605-755).  input: planar
+ * [num_input][frames][height][width], channel stride in_cstep.  memory:
+ * planar [num_input][memory_frames][height][width] (channel stride
+ * mem_cstep) of the previous slice, or NULL: then the temporal prefix is
+ * head_frames copies of input frame 0.  weights: [kernel_t][num_output]
+ * [num_input][kernel_h][kernel_w] (one ncnn Convolution weight per temporal
+ * tap); bias [num_output] or NULL.  output: planar [num_output][out_t][oh]
+ * [ow], channel stride out_cstep.  Each tap's 2-D convolution is evaluated
+ * in fp64 and rounded to fp32, then the taps are added in tap order in fp32.
+ * next_memory (or NULL): planar [num_input][kernel_t - stride_t][height]
+ * [width], channel stride next_cstep: the last kernel_t - stride_t frames of
+ * the padded input.  Returns out_t, or -1 (bad configuration, groups != 1,
+ * too few frames). */
+int orc_decomposed_conv3d(const orc_conv3d* cfg, const float* input, int frames, int height,
+                          int width, long in_cstep, const float* memory, int memory_frames,
+                          long mem_cstep, const float* weights, const float* bias, float* output,
+                          long out_cstep, float* next_memory, long next_cstep, int num_threads);
 
 #ifdef __cplusplus
 }
