@@ -262,6 +262,63 @@ S2_API int s2_denoise_update(const float* positive_patches, const float* negativ
                              float cfg_rescale, float delta, float* latent, long channel_stride,
                              s2_stream_t stream);
 
+/* ---- DecomposedConv3D (VAE) ---------------------------------------------- */
+/* The causal 3-D convolution of the VAE (src/seedvr2/decomposed_conv3d.h:33-88,
+ * decomposed_conv3d.cpp:605-755) as one implicit GEMM on the matrix cores:
+ * bf16 operands, fp32 accumulation over the whole kt x kh x kw x num_input
+ * window. */
+
+/* The 16 values of the layer's config blob, in blob order
+ * (decomposed_conv3d.cpp:422-441). */
+typedef struct s2_conv3d_config {
+    int num_output, num_input, kernel_w, kernel_h, kernel_t, stride_t, dilation_t, head_frames;
+    int stride_w, stride_h, dilation_w, dilation_h, pad_w, pad_h, groups, bias_term;
+} s2_conv3d_config;
+
+/* Output (frames, height, width) of a forward over `frames` input frames
+ * with `memory_frames` cached frames (0: the prefix is head_frames copies of
+ * frame 0), by the reference's arithmetic (:621-634) and ncnn Convolution's
+ * output size.  S2_ERR_INVALID where the reference returns -1, including
+ * groups != 1 (the reference hands the weights of a grouped configuration to
+ * an ungrouped ncnn Convolution). */
+S2_API int s2_conv3d_output_shape(const s2_conv3d_config* config, int frames, int height,
+                                  int width, int memory_frames, int out_shape[3]);
+
+/* Device weights in the kernel's layout: bf16 [num_output][kernel_t]
+ * [kernel_h][kernel_w][cpad], cpad = num_input rounded up to 64.  `weights`
+ * is the reference's per-tap ncnn Convolution weights, device fp32
+ * [kernel_t][num_output][num_input][kernel_h][kernel_w] (load_model,
+ * :457-471). */
+S2_API int s2_conv3d_packed_weight_bytes(const s2_conv3d_config* config, size_t* bytes);
+S2_API int s2_conv3d_pack_weights(const s2_conv3d_config* config, const float* weights,
+                                  void* packed, s2_stream_t stream);
+
+/* The temporal memory (:727-755): the last kernel_t - stride_t frames of the
+ * padded input, kept in this library's staged layout (bf16 channel-last);
+ * only s2_conv3d_forward reads or writes it.  *frames = kernel_t - stride_t
+ * (0: the layer keeps no memory). */
+S2_API int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, int width,
+                                  size_t* bytes, int* frames);
+S2_API int s2_conv3d_workspace_bytes(const s2_conv3d_config* config, int frames, int height,
+                                     int width, int memory_frames, size_t* bytes);
+
+/* DecomposedConv3D::forward (decomposed_conv3d.cpp:605-755).  input: device
+ * planar [num_input][frames][height][width] in in_dtype, channel stride
+ * in_cstep elements (an ncnn Mat's cstep; a multiple of 4, 16-byte aligned
+ * base).  memory: the memory a previous forward wrote (memory_frames
+ * frames), or NULL: the prefix is then head_frames copies of frame 0.
+ * output: planar [num_output][out frames][out h][out w], channel stride
+ * out_cstep, out_dtype.  next_memory (or NULL): receives the new memory
+ * (s2_conv3d_memory_bytes); it may be the same buffer as memory.  bias:
+ * device fp32 [num_output] or NULL.  workspace: s2_conv3d_workspace_bytes,
+ * 256-byte aligned. */
+S2_API int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_weights,
+                             const float* bias, const void* input, s2_dtype in_dtype, int frames,
+                             int height, int width, long in_cstep, const void* memory,
+                             int memory_frames, void* output, s2_dtype out_dtype, long out_cstep,
+                             void* next_memory, void* workspace, size_t workspace_bytes,
+                             s2_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

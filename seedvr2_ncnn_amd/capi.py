@@ -34,6 +34,8 @@ EXPORTS = (
     "s2_cast_bf16_to_f32", "s2_shared_linear_forward", "s2_awa_stage_timing",
     "s2_awa_stage_times", "s2_patchify_video", "s2_latent_patches", "s2_timestep_embedding",
     "s2_unpatchify_prediction", "s2_apply_cfg", "s2_euler_step", "s2_denoise_update",
+    "s2_conv3d_output_shape", "s2_conv3d_packed_weight_bytes", "s2_conv3d_pack_weights",
+    "s2_conv3d_memory_bytes", "s2_conv3d_workspace_bytes", "s2_conv3d_forward",
 )
 
 
@@ -59,6 +61,24 @@ class AwaConfig(ctypes.Structure):
         ("shared_norm", ctypes.c_int),
         ("official_bf16_attention", ctypes.c_int),
     ]
+
+
+class Conv3dConfig(ctypes.Structure):
+    """s2_conv3d_config: the 16 DecomposedConv3D config values in blob order."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "num_output", "num_input", "kernel_w", "kernel_h", "kernel_t", "stride_t", "dilation_t",
+        "head_frames", "stride_w", "stride_h", "dilation_w", "dilation_h", "pad_w", "pad_h",
+        "groups", "bias_term")]
+
+
+def conv3d_config(**kw) -> Conv3dConfig:
+    c = Conv3dConfig()
+    values = dict(stride_t=1, dilation_t=1, head_frames=0, stride_w=1, stride_h=1, dilation_w=1,
+                  dilation_h=1, pad_w=0, pad_h=0, groups=1, bias_term=0)
+    values.update(kw)
+    for name, _ in Conv3dConfig._fields_:
+        setattr(c, name, int(values[name]))
+    return c
 
 
 class PlanInfo(ctypes.Structure):
@@ -110,6 +130,14 @@ def lib() -> ctypes.CDLL:
         L.s2_apply_cfg.argtypes = [vp, vp, cl, cf, cf, vp, vp]
         L.s2_euler_step.argtypes = [vp, cl, vp, cl, cf, vp]
         L.s2_denoise_update.argtypes = [vp, vp, ci, ci, ci, cf, cf, cf, vp, cl, vp]
+        C3 = P(Conv3dConfig)
+        L.s2_conv3d_output_shape.argtypes = [C3, ci, ci, ci, ci, P(ci)]
+        L.s2_conv3d_packed_weight_bytes.argtypes = [C3, P(sz)]
+        L.s2_conv3d_pack_weights.argtypes = [C3, vp, vp, vp]
+        L.s2_conv3d_memory_bytes.argtypes = [C3, ci, ci, P(sz), P(ci)]
+        L.s2_conv3d_workspace_bytes.argtypes = [C3, ci, ci, ci, ci, P(sz)]
+        L.s2_conv3d_forward.argtypes = [C3, vp, vp, vp, ci, ci, ci, ci, cl, vp, ci, vp, ci, cl, vp,
+                                        vp, sz, vp]
         _LIB = L
     return _LIB
 
@@ -407,3 +435,63 @@ def denoise_update(positive_patches, negative_patches, frames, height, width, cf
                                   _ptr(latent), channel_stride, _stream(stream)),
           "s2_denoise_update")
     return latent
+
+
+# ---- DecomposedConv3D ------------------------------------------------------------
+
+class Conv3d:
+    """Device state of one DecomposedConv3D: packed bf16 weights, bias and the
+    temporal memory (s2_conv3d_*)."""
+
+    def __init__(self, config: Conv3dConfig, weights, bias=None, stream=None):
+        import torch
+        self.config = config
+        n = ctypes.c_size_t()
+        check(lib().s2_conv3d_packed_weight_bytes(ctypes.byref(config), ctypes.byref(n)),
+              "s2_conv3d_packed_weight_bytes")
+        self.packed = torch.empty(n.value // 2, dtype=torch.int16, device=weights.device)
+        check(lib().s2_conv3d_pack_weights(ctypes.byref(config), _ptr(weights.contiguous()),
+                                           _ptr(self.packed), _stream(stream)),
+              "s2_conv3d_pack_weights")
+        self.bias = bias
+        self.memory = None
+        self.memory_frames = 0
+
+    def output_shape(self, frames, height, width, memory_frames=0):
+        out = (ctypes.c_int * 3)()
+        check(lib().s2_conv3d_output_shape(ctypes.byref(self.config), frames, height, width,
+                                           memory_frames, out), "s2_conv3d_output_shape")
+        return tuple(out)
+
+    def forward(self, x, frames, height, width, cstep=None, use_memory=False, keep_memory=False,
+                out_dtype=None, out_cstep=None, stream=None):
+        """x: device [num_input, cstep] planar (cstep >= frames*height*width).
+        Returns the output as [num_output, out_cstep]."""
+        import torch
+        cfg = self.config
+        mem = self.memory if use_memory and self.memory is not None else None
+        mframes = self.memory_frames if mem is not None else 0
+        to, ho, wo = self.output_shape(frames, height, width, mframes)
+        odt = out_dtype or x.dtype
+        ocs = out_cstep or to * ho * wo
+        out = torch.empty((cfg.num_output, ocs), dtype=odt, device=x.device)
+        ws_n = ctypes.c_size_t()
+        check(lib().s2_conv3d_workspace_bytes(ctypes.byref(cfg), frames, height, width, mframes,
+                                              ctypes.byref(ws_n)), "s2_conv3d_workspace_bytes")
+        ws = torch.empty(ws_n.value, dtype=torch.uint8, device=x.device)
+        nxt = None
+        if keep_memory:
+            nb, nf = ctypes.c_size_t(), ctypes.c_int()
+            check(lib().s2_conv3d_memory_bytes(ctypes.byref(cfg), height, width, ctypes.byref(nb),
+                                               ctypes.byref(nf)), "s2_conv3d_memory_bytes")
+            if nf.value > 0:
+                nxt = torch.empty(nb.value, dtype=torch.uint8, device=x.device)
+        check(lib().s2_conv3d_forward(ctypes.byref(cfg), _ptr(self.packed), _ptr(self.bias), _ptr(x),
+                                      _dtype_code(x), frames, height, width,
+                                      cstep or x.shape[1], _ptr(mem), mframes, _ptr(out),
+                                      _dtype_code(out), ocs, _ptr(nxt), _ptr(ws), ws.numel(),
+                                      _stream(stream)), "s2_conv3d_forward")
+        if keep_memory:
+            self.memory = nxt
+            self.memory_frames = cfg.kernel_t - cfg.stride_t if nxt is not None else 0
+        return out, (to, ho, wo)

@@ -8,6 +8,7 @@
 
 #include "awa_kernels.h"
 #include "awa_plan.h"
+#include "conv3d_kernels.h"
 #include "pipeline_kernels.h"
 #include "seedvr2_hip.h"
 
@@ -60,6 +61,50 @@ bool dtype_ok(s2_dtype t) { return t == S2_DTYPE_F32 || t == S2_DTYPE_BF16 || t 
 size_t dtype_bytes(s2_dtype t) { return t == S2_DTYPE_F32 ? 4 : 2; }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p) % a == 0; }
+
+// DecomposedConv3D configuration checks of the reference load_model
+// (decomposed_conv3d.cpp:442-446), plus groups == 1.
+bool conv3d_config_ok(const s2_conv3d_config* c) {
+    return c && c->num_output > 0 && c->num_input > 0 && c->kernel_w > 0 && c->kernel_h > 0 &&
+           c->kernel_t > 0 && c->stride_t > 0 && c->dilation_t > 0 && c->stride_w > 0 &&
+           c->stride_h > 0 && c->dilation_w > 0 && c->dilation_h > 0 && c->groups == 1 &&
+           c->head_frames >= 0 && c->pad_w >= 0 && c->pad_h >= 0;
+}
+
+s2::Conv3dShape conv3d_shape(const s2_conv3d_config* c) {
+    s2::Conv3dShape s;
+    s.cin = c->num_input;
+    s.cout = c->num_output;
+    s.cpad = s2::conv3d_cpad(c->num_input);
+    s.kt = c->kernel_t;
+    s.kh = c->kernel_h;
+    s.kw = c->kernel_w;
+    s.st = c->stride_t;
+    s.sh = c->stride_h;
+    s.sw = c->stride_w;
+    s.dt = c->dilation_t;
+    s.dh = c->dilation_h;
+    s.dw = c->dilation_w;
+    s.ph = c->pad_h;
+    s.pw = c->pad_w;
+    return s;
+}
+
+// Output extent of forward (decomposed_conv3d.cpp:621-634); false where the
+// reference returns -1.
+bool conv3d_out(const s2_conv3d_config* c, int frames, int height, int width, int memory_frames,
+                int* to, int* ho, int* wo) {
+    if (!conv3d_config_ok(c) || frames <= 0 || height <= 0 || width <= 0 || memory_frames < 0)
+        return false;
+    const int prefix = memory_frames > 0 ? memory_frames : c->head_frames;
+    const long padded = (long)frames + prefix;
+    const long extent = (long)c->dilation_t * (c->kernel_t - 1) + 1;
+    if (padded < extent) return false;
+    *to = (int)((padded - extent) / c->stride_t + 1);
+    *ho = (height + 2 * c->pad_h - c->dilation_h * (c->kernel_h - 1) - 1) / c->stride_h + 1;
+    *wo = (width + 2 * c->pad_w - c->dilation_w * (c->kernel_w - 1) - 1) / c->stride_w + 1;
+    return *ho > 0 && *wo > 0;
+}
 
 // Validates video sample shapes as the reference's patchify/unpatchify do
 // (seedvr2_dit.cpp:181-191, 270-283): positive, even height and width.
@@ -560,6 +605,121 @@ int s2_denoise_update(const float* positive_patches, const float* negative_patch
     S2_HIP(s2::launch_denoise_update(positive_patches, negative_patches, frames, height, width,
                                      cfg_scale, cfg_rescale, delta, latent, channel_stride,
                                      (hipStream_t)stream));
+    return S2_OK;
+}
+
+/* ---- DecomposedConv3D ---------------------------------------------------- */
+
+int s2_conv3d_output_shape(const s2_conv3d_config* config, int frames, int height, int width,
+                           int memory_frames, int out_shape[3]) {
+    int to = 0, ho = 0, wo = 0;
+    if (!out_shape || !conv3d_out(config, frames, height, width, memory_frames, &to, &ho, &wo))
+        return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
+    out_shape[0] = to;
+    out_shape[1] = ho;
+    out_shape[2] = wo;
+    return S2_OK;
+}
+
+int s2_conv3d_packed_weight_bytes(const s2_conv3d_config* config, size_t* bytes) {
+    if (!bytes || !conv3d_config_ok(config)) return fail(S2_ERR_INVALID, "invalid configuration");
+    const s2::Conv3dShape s = conv3d_shape(config);
+    *bytes = (size_t)s.cout * s.kt * s.kh * s.kw * s.cpad * 2;
+    return S2_OK;
+}
+
+int s2_conv3d_pack_weights(const s2_conv3d_config* config, const float* weights, void* packed,
+                           s2_stream_t stream) {
+    if (!conv3d_config_ok(config)) return fail(S2_ERR_INVALID, "invalid configuration");
+    if (!weights || !packed) return fail(S2_ERR_INVALID, "null pointer");
+    S2_HIP(s2::launch_conv3d_pack_weights(weights, conv3d_shape(config), (uint16_t*)packed,
+                                          (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, int width, size_t* bytes,
+                           int* frames) {
+    if (!bytes || !frames || !conv3d_config_ok(config) || height <= 0 || width <= 0)
+        return fail(S2_ERR_INVALID, "invalid configuration");
+    const int cache = std::max(config->kernel_t - config->stride_t, 0);
+    *frames = cache;
+    *bytes = (size_t)cache * height * width * s2::conv3d_cpad(config->num_input) * 2;
+    return S2_OK;
+}
+
+int s2_conv3d_workspace_bytes(const s2_conv3d_config* config, int frames, int height, int width,
+                              int memory_frames, size_t* bytes) {
+    int to, ho, wo;
+    if (!bytes || !conv3d_out(config, frames, height, width, memory_frames, &to, &ho, &wo))
+        return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
+    *bytes = align256((size_t)(frames + memory_frames) * height * width *
+                      s2::conv3d_cpad(config->num_input) * 2);
+    return S2_OK;
+}
+
+int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_weights,
+                      const float* bias, const void* input, s2_dtype in_dtype, int frames,
+                      int height, int width, long in_cstep, const void* memory, int memory_frames,
+                      void* output, s2_dtype out_dtype, long out_cstep, void* next_memory,
+                      void* workspace, size_t workspace_bytes, s2_stream_t stream) {
+    const int mem = memory ? memory_frames : 0;
+    int to, ho, wo;
+    if (!conv3d_out(config, frames, height, width, mem, &to, &ho, &wo))
+        return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
+    if (memory && memory_frames <= 0) return fail(S2_ERR_INVALID, "memory without frames");
+    if (!packed_weights || !input || !output || !workspace) return fail(S2_ERR_INVALID, "null pointer");
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    const long plane_in = (long)height * width;
+    if (in_cstep < (long)frames * plane_in || in_cstep % 4 != 0 || !aligned(input, 16))
+        return fail(S2_ERR_INVALID, "input channel stride or alignment");
+    if (out_cstep < (long)to * ho * wo) return fail(S2_ERR_INVALID, "output channel stride");
+    if (!aligned(workspace, 256)) return fail(S2_ERR_INVALID, "workspace alignment");
+    const s2::Conv3dShape s = conv3d_shape(config);
+    const size_t frame_elems = (size_t)plane_in * s.cpad;
+    const size_t frame_bytes = frame_elems * 2;
+    const int staged_frames = mem + frames;
+    if ((size_t)staged_frames * frame_bytes > workspace_bytes)
+        return fail(S2_ERR_INVALID, "workspace too small");
+    const int prefix = mem > 0 ? mem : config->head_frames;
+    const int padded = frames + prefix;
+    const int cache = config->kernel_t - config->stride_t;
+    if (next_memory && cache > padded) return fail(S2_ERR_INVALID, "too few frames for the memory");
+    hipStream_t st = (hipStream_t)stream;
+    uint16_t* staged = (uint16_t*)workspace;
+    if (mem > 0) S2_HIP(hipMemcpyAsync(staged, memory, (size_t)mem * frame_bytes,
+                                       hipMemcpyDeviceToDevice, st));
+    S2_HIP(s2::launch_conv3d_stage(input, (int)in_dtype, in_cstep, s.cin, (long)frames * plane_in,
+                                   s.cpad, staged + (size_t)mem * frame_elems, st));
+    // padded frame p is staged frame max(p - shift, 0)
+    const int shift = prefix - mem;
+    auto staged_frame = [&](long p) { return (int)std::max(p - shift, 0L); };
+    const long max_span = (long)(0x7fffffffL / (long)frame_bytes);
+    if (max_span < (long)(config->kernel_t - 1) * config->dilation_t + 1)
+        return fail(S2_ERR_INVALID, "one output frame reads more than 2 GiB of staged input");
+    for (int t0 = 0; t0 < to;) {
+        // as many output frames as keep the staged frames they read under 2 GiB
+        const int first = staged_frame((long)t0 * config->stride_t);
+        int n = 1;
+        while (t0 + n < to &&
+               staged_frame((long)(t0 + n) * config->stride_t +
+                            (long)(config->kernel_t - 1) * config->dilation_t) - first + 1 <= max_span)
+            ++n;
+        const int last = staged_frame((long)(t0 + n - 1) * config->stride_t +
+                                      (long)(config->kernel_t - 1) * config->dilation_t);
+        S2_HIP(s2::launch_conv3d(s, staged + (size_t)first * frame_elems,
+                                 (size_t)(last - first + 1) * frame_bytes, first, shift, height,
+                                 width, ho, wo, t0, n, (const uint16_t*)packed_weights, bias, output,
+                                 (int)out_dtype, out_cstep, st));
+        t0 += n;
+    }
+    if (next_memory && cache > 0) {
+        for (int f = 0; f < cache; ++f) {
+            const int sf = staged_frame((long)padded - cache + f);
+            S2_HIP(hipMemcpyAsync((uint8_t*)next_memory + (size_t)f * frame_bytes,
+                                  staged + (size_t)sf * frame_elems, frame_bytes,
+                                  hipMemcpyDeviceToDevice, st));
+        }
+    }
     return S2_OK;
 }
 

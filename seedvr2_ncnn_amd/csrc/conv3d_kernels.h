@@ -1,0 +1,42 @@
+// Host launchers of the DecomposedConv3D kernels (conv3d_kernels.hip).
+//
+// The convolution runs as an implicit GEMM over a staged copy of its input:
+// the temporally padded frames in channel-last bf16, [frame][y][x][cpad]
+// with cpad = num_input rounded up to 64 (zero channels above num_input).
+// Weights are packed once to bf16 [num_output][kt][kh][kw][cpad], the same k
+// order, so both MFMA operands are k-contiguous.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace s2 {
+
+struct Conv3dShape {
+    int cin, cout, cpad;
+    int kt, kh, kw;
+    int st, sh, sw;
+    int dt, dh, dw;
+    int ph, pw;
+};
+
+inline int conv3d_cpad(int cin) { return (cin + 63) / 64 * 64; }
+
+// planar input [cin][frames*H*W] (channel stride in_cstep; element type
+// in_kind: 0 fp32, 1 bf16, 2 fp16) -> staged [frames*H*W][cpad] bf16
+hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, int cin,
+                               long pixels, int cpad, uint16_t* staged, hipStream_t stream);
+// fp32 [kt][cout][cin][kh][kw] -> bf16 [cout][kt][kh][kw][cpad]
+hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s,
+                                      uint16_t* packed, hipStream_t stream);
+// Output frames [t0, t0 + frames_out) of the convolution.  Padded frame p
+// (p = t*st + tap*dt) is staged frame max(p - shift, 0) - frame_base of
+// `staged` (which must hold every frame these outputs read, < 2 GiB).
+// out: planar [cout][...], element (co, t, y, x) at co*out_cstep +
+// (t*Ho + y)*Wo + x, type out_kind; bias fp32 [cout] or null.
+hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* staged, size_t staged_bytes,
+                         int frame_base, int shift, int height, int width, int ho, int wo,
+                         int t0, int frames_out, const uint16_t* packed, const float* bias,
+                         void* out, int out_kind, long out_cstep, hipStream_t stream);
+
+}  // namespace s2

@@ -1,0 +1,411 @@
+// gfx950 kernels of DecomposedConv3D (src/seedvr2/decomposed_conv3d.cpp:605-755):
+// a causal 3-D convolution whose temporal prefix is either head_frames
+// copies of the first frame or the cached last frames of the previous slice.
+//
+// The reference gathers one input frame per temporal tap, runs an ncnn 2-D
+// Convolution on it and adds the frame results.  Here the whole
+// kt x kh x kw window is one implicit GEMM on the matrix cores:
+//   rows    M = output pixels (t, y, x) of the launch,
+//   columns N = output channels,
+//   depth   K = (tap, ky, kx, ci), ci fastest,
+// A[m][k] = staged[frame(t, tap)][y*sh + ky*dh - ph][x*sw + kx*dw - pw][ci]
+// (zero outside the image), B[n][k] = packed weights.  The staged input is
+// channel-last bf16, so for one window position the 64 channels of a k-step
+// are one 128-byte run of a pixel: the A tile streams into LDS with the
+// same buffer_load ... lds DMA as the SharedLinear GEMM, each row from its
+// own pixel, and a row whose pixel falls in the zero padding gets an offset
+// past the end of the buffer, which the hardware returns as zeros.
+#include <limits.h>
+
+#include "conv3d_kernels.h"
+#include "s2_device.h"
+
+namespace s2 {
+namespace {
+
+constexpr int kStageThreads = 256;
+
+__device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
+// ---- staging: planar -> channel-last bf16 ------------------------------------
+
+template <int KIND>
+__device__ __forceinline__ float load_elem(const void* p, long i) {
+    if (KIND == 1) return __builtin_bit_cast(float, (uint32_t)((const uint16_t*)p)[i] << 16);
+    if (KIND == 2) return (float)((const _Float16*)p)[i];
+    return ((const float*)p)[i];
+}
+
+template <int KIND>
+__device__ __forceinline__ void load_elem4(const void* p, long i, float (&v)[4]) {
+    if (KIND == 0) {
+        const float4 f = *reinterpret_cast<const float4*>((const float*)p + i);
+        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+    } else {
+        const uint2 u = *reinterpret_cast<const uint2*>((const uint16_t*)p + i);
+        const uint32_t w[2] = {u.x, u.y};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+            v[e] = KIND == 1 ? __builtin_bit_cast(float, (uint32_t)h << 16)
+                             : (float)__builtin_bit_cast(_Float16, h);
+        }
+    }
+}
+
+// One block moves 64 pixels x 64 channels: 64 channel rows of 64 pixels are
+// read as 16-byte runs, transposed in LDS (row pitch 65 floats: conflict-free
+// both ways) and written as 64 pixel rows of 128 bytes.  Channels at or
+// above cin are written as zeros.
+template <int KIND>
+__global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
+    const void* __restrict__ in, long cstep, int cin, long pixels, int cpad,
+    uint16_t* __restrict__ staged) {
+    __shared__ float tile[64 * 65];
+    const long q0 = (long)blockIdx.x * 64;
+    const int c0 = blockIdx.y * 64;
+    const int t = threadIdx.x;
+    const int q4 = (t & 15) * 4;
+    const bool full = q0 + 64 <= pixels;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int cl = (t >> 4) + 16 * i;
+        const int c = c0 + cl;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (c < cin) {
+            const long base = (long)c * cstep + q0 + q4;
+            if (full) {
+                load_elem4<KIND>(in, base, v);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (q0 + q4 + e < pixels) v[e] = load_elem<KIND>(in, base + e);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tile[cl * 65 + q4 + e] = v[e];
+    }
+    __syncthreads();
+    const int q = t >> 2, part = t & 3;
+    if (q0 + q >= pixels) return;
+    uint16_t h[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) h[i] = f32_to_bf16(tile[(part * 16 + i) * 65 + q]);
+    uint4* dst = reinterpret_cast<uint4*>(staged + (q0 + q) * cpad + c0 + part * 16);
+    uint16_t lo[8], hi[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) lo[i] = h[i], hi[i] = h[8 + i];
+    dst[0] = pack8_bf16(lo);
+    dst[1] = pack8_bf16(hi);
+}
+
+// ---- weights: [kt][cout][cin][kh][kw] fp32 -> [cout][kt][kh][kw][cpad] bf16 --
+
+__global__ __launch_bounds__(256) void conv3d_pack_kernel(const float* __restrict__ w,
+                                                          Conv3dShape s, long total,
+                                                          uint16_t* __restrict__ out) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int ci = (int)(i % s.cpad);
+    long r = i / s.cpad;
+    const int kx = (int)(r % s.kw);
+    r /= s.kw;
+    const int ky = (int)(r % s.kh);
+    r /= s.kh;
+    const int tap = (int)(r % s.kt);
+    const int co = (int)(r / s.kt);
+    float v = 0.f;
+    if (ci < s.cin)
+        v = w[(((long)tap * s.cout + co) * s.cin + ci) * s.kh * s.kw + ky * s.kw + kx];
+    out[i] = f32_to_bf16(v);
+}
+
+// ---- the implicit GEMM ---------------------------------------------------------
+
+struct ConvArgs {
+    const uint16_t* staged;
+    uint32_t staged_bytes;
+    const uint16_t* packed;
+    int kp;   // packed row length: kt*kh*kw*cpad
+    const float* bias;
+    void* out;
+    long out_cstep;
+    long out_off;
+    int out_kind;
+    int vec_ok;   // 4-pixel vector stores are aligned
+    int H, W, Ho, Wo, M;
+    int cpad, cout;
+    int kh, kw, st, dt, sh, sw, dh, dw, ph, pw;
+    int shift, fbase, t0;
+    int mtiles, ntiles;
+};
+
+// Eight waves in a (BM/128) x (BN/64) grid of 128x64 wave tiles (4x2 MFMA
+// 32x32x16 accumulators, 128 fp32 per lane), as in the SharedLinear GEMM:
+// BN = 256 gives 256x256 block tiles, BN = 128 (output channels <= 128)
+// gives 512x128 tiles.  Two 64-k LDS stages of (BM + BN) x 128 bytes (64 KB
+// or 80 KB) are filled by DMA one stage ahead of the MFMAs; LDS rows use the
+// GEMM's chunk swizzle.  Wave w loads A rows [w*BM/8, (w+1)*BM/8) and B rows
+// [w*BN/8, (w+1)*BN/8), 8 rows per DMA instruction.
+template <int BN>
+__global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
+    constexpr int BM = BN == 128 ? 512 : 256;
+    constexpr int BK = 64, RB = BK * 2;
+    constexpr int WN = BN / 64;
+    constexpr int TA = BM * RB, SB = TA + BN * RB;
+    constexpr int ARPW = BM / 8, AJ = ARPW / 8;
+    constexpr int BRPW = BN / 8, BJ = BRPW / 8;
+    constexpr int GROUP = 4;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+    const int sw = lds_swizzle(l32);
+    const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+
+    // grouped, XCD-aware raster: GROUP m-tiles share each sweep over the n-tiles
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int group_size = GROUP * a.ntiles;
+    const int first_m = (lid / group_size) * GROUP;
+    const int gm = min(a.mtiles - first_m, GROUP);
+    const int mt = first_m + (lid % group_size) % gm;
+    const int nt = (lid % group_size) / gm;
+    const int row0 = mt * BM;
+    const int col0 = nt * BN;
+
+    // geometry of the A rows this lane loads: padded frame of tap 0, and the
+    // input y, x of window position (0, 0); a negative frame marks a row past M
+    const int hw = a.Ho * a.Wo;
+    int rpf[AJ], ryb[AJ], rxb[AJ];
+    uint32_t chk[AJ];
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+        const int row = wave * ARPW + j * 8 + (lane >> 3);
+        const int m = row0 + row;
+        chk[j] = (uint32_t)(((lane & 7) ^ lds_swizzle(row)) * 16);
+        rpf[j] = INT_MIN / 2;
+        ryb[j] = rxb[j] = 0;
+        if (m < a.M) {
+            const int to = m / hw;
+            const int rem = m - to * hw;
+            const int yo = rem / a.Wo;
+            const int xo = rem - yo * a.Wo;
+            rpf[j] = (a.t0 + to) * a.st;
+            ryb[j] = yo * a.sh - a.ph;
+            rxb[j] = xo * a.sw - a.pw;
+        }
+    }
+    uint32_t voffb[BJ];
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+        const int row = wave * BRPW + j * 8 + (lane >> 3);
+        voffb[j] = (uint32_t)(row * a.kp * 2 + (((lane & 7) ^ lds_swizzle(row)) * 16));
+    }
+    const i32x4 ra = wave_uniform(buffer_rsrc(a.staged, a.staged_bytes));
+    const i32x4 rb = wave_uniform(buffer_rsrc(
+        a.packed + (long)col0 * a.kp, (uint32_t)(min(a.cout - col0, BN) * a.kp * 2)));
+    const uint32_t pix_bytes = (uint32_t)(a.cpad * 2);
+
+    uint32_t voffa[AJ];
+    // A offsets of window position pos = (tap, ky, kx)
+    auto set_pos = [&](int pos) {
+        const int kx = pos % a.kw;
+        const int rest = pos / a.kw;
+        const int ky = rest % a.kh;
+        const int tap = rest / a.kh;
+        const int dtap = tap * a.dt, dy = ky * a.dh, dx = kx * a.dw;
+#pragma unroll
+        for (int j = 0; j < AJ; ++j) {
+            const int sf = max(rpf[j] + dtap - a.shift, 0) - a.fbase;
+            const int yi = ryb[j] + dy, xi = rxb[j] + dx;
+            const bool ok = rpf[j] >= 0 && sf >= 0 && (unsigned)yi < (unsigned)a.H &&
+                            (unsigned)xi < (unsigned)a.W;
+            voffa[j] = ok ? (uint32_t)((sf * a.H + yi) * a.W + xi) * pix_bytes + chk[j]
+                          : 0x80000000u;
+        }
+    };
+    const int cpc = a.cpad / 64;   // k-steps per window position
+    const int nk = a.kp / 64;
+    auto issue = [&](int stage, int ks) {
+        const uint32_t soffa = __builtin_amdgcn_readfirstlane((uint32_t)((ks % cpc) * RB));
+        const uint32_t soffb = __builtin_amdgcn_readfirstlane((uint32_t)(ks * RB));
+        const uint32_t st = lds_base + stage * SB;
+#pragma unroll
+        for (int j = 0; j < AJ; ++j)
+            lds_dma16(ra, __builtin_amdgcn_readfirstlane(st + (wave * ARPW + j * 8) * RB),
+                      voffa[j], soffa);
+#pragma unroll
+        for (int j = 0; j < BJ; ++j)
+            lds_dma16(rb, __builtin_amdgcn_readfirstlane(st + TA + (wave * BRPW + j * 8) * RB),
+                      voffb[j], soffb);
+    };
+
+    f32x16 acc[4][2];
+    bf16x8 fa[2][4], fb[2][2];
+    auto frag = [&](const uint8_t* st, int kk, int slot) {
+        const int pc = ((2 * kk + g) ^ sw) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            fa[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * RB + pc));
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            fb[slot][j] = as_bf16x8(*(const uint4*)(st + TA + (wn * 64 + 32 * j + l32) * RB + pc));
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    set_pos(0);
+    issue(0, 0);
+#pragma unroll 1
+    for (int ks = 0; ks < nk; ++ks) {
+        const int stage = ks & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();   // stage ks visible to all waves; the other stage no longer read
+        if (ks + 1 < nk) {
+            if ((ks + 1) % cpc == 0) set_pos((ks + 1) / cpc);
+            issue(stage ^ 1, ks + 1);
+        }
+        const uint8_t* st = lds + stage * SB;
+        frag(st, 0, 0);
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (kk + 1 < BK / 16) frag(st, kk + 1, (kk + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Epilogue: register r of a 32x32 accumulator is row 8(r/4) + 4g + r%4,
+    // column l32, so each lane holds 4 consecutive output pixels of one
+    // output channel: one 16-byte (fp32) or 8-byte store into that plane.
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int col = col0 + wn * 64 + 32 * j + l32;
+        if (col >= a.cout) continue;
+        const float bv = a.bias ? a.bias[col] : 0.f;
+        const long cbase = (long)col * a.out_cstep + a.out_off;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int m = row0 + wm * 128 + 32 * i + 8 * rg + 4 * g;
+                const float v0 = acc[i][j][4 * rg] + bv, v1 = acc[i][j][4 * rg + 1] + bv;
+                const float v2 = acc[i][j][4 * rg + 2] + bv, v3 = acc[i][j][4 * rg + 3] + bv;
+                if (a.vec_ok && m + 3 < a.M) {
+                    store4(a.out, cbase + m, v0, v1, v2, v3, a.out_kind);
+                } else {
+                    const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (m + e >= a.M) continue;
+                        const long idx = cbase + m + e;
+                        if (a.out_kind == 1)
+                            ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
+                        else if (a.out_kind == 2)
+                            ((_Float16*)a.out)[idx] = (_Float16)v[e];
+                        else
+                            ((float*)a.out)[idx] = v[e];
+                    }
+                }
+            }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, int cin,
+                               long pixels, int cpad, uint16_t* staged, hipStream_t stream) {
+    if (pixels <= 0) return hipSuccess;
+    const dim3 grid((unsigned)((pixels + 63) / 64), (unsigned)(cpad / 64));
+    if (in_kind == 1)
+        conv3d_stage_kernel<1><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
+                                                                     cpad, staged);
+    else if (in_kind == 2)
+        conv3d_stage_kernel<2><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
+                                                                     cpad, staged);
+    else
+        conv3d_stage_kernel<0><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
+                                                                     cpad, staged);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s,
+                                      uint16_t* packed, hipStream_t stream) {
+    const long total = (long)s.cout * s.kt * s.kh * s.kw * s.cpad;
+    if (total <= 0) return hipSuccess;
+    conv3d_pack_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(weights, s, total,
+                                                                            packed);
+    return hipGetLastError();
+}
+
+hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* staged, size_t staged_bytes,
+                         int frame_base, int shift, int height, int width, int ho, int wo,
+                         int t0, int frames_out, const uint16_t* packed, const float* bias,
+                         void* out, int out_kind, long out_cstep, hipStream_t stream) {
+    if (frames_out <= 0) return hipSuccess;
+    const long m = (long)frames_out * ho * wo;
+    const long kp = (long)s.kt * s.kh * s.kw * s.cpad;
+    if (m > INT_MAX || staged_bytes >= 0x80000000ull || kp * 2 * s.cout >= 0x80000000l ||
+        s.cpad % 64 != 0)
+        return hipErrorInvalidValue;
+    ConvArgs a;
+    a.staged = staged;
+    a.staged_bytes = (uint32_t)staged_bytes;
+    a.packed = packed;
+    a.kp = (int)kp;
+    a.bias = bias;
+    a.out = out;
+    a.out_cstep = out_cstep;
+    a.out_off = (long)t0 * ho * wo;
+    a.out_kind = out_kind;
+    const size_t esz = out_kind == 0 ? 4 : 2;
+    a.vec_ok = out_cstep % 4 == 0 && a.out_off % 4 == 0 && ((uintptr_t)out % (4 * esz)) == 0;
+    a.H = height;
+    a.W = width;
+    a.Ho = ho;
+    a.Wo = wo;
+    a.M = (int)m;
+    a.cpad = s.cpad;
+    a.cout = s.cout;
+    a.kh = s.kh;
+    a.kw = s.kw;
+    a.st = s.st;
+    a.dt = s.dt;
+    a.sh = s.sh;
+    a.sw = s.sw;
+    a.dh = s.dh;
+    a.dw = s.dw;
+    a.ph = s.ph;
+    a.pw = s.pw;
+    a.shift = shift;
+    a.fbase = frame_base;
+    a.t0 = t0;
+    if (s.cout <= 128) {
+        a.mtiles = (int)((m + 511) / 512);
+        a.ntiles = (s.cout + 127) / 128;
+        conv3d_kernel<128><<<(unsigned)(a.mtiles * a.ntiles), 512, 0, stream>>>(a);
+    } else {
+        a.mtiles = (int)((m + 255) / 256);
+        a.ntiles = (s.cout + 255) / 256;
+        conv3d_kernel<256><<<(unsigned)(a.mtiles * a.ntiles), 512, 0, stream>>>(a);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace s2

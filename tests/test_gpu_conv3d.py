@@ -1,0 +1,132 @@
+"""DecomposedConv3D on the GPU (src/seedvr2/decomposed_conv3d.cpp:605-755) against
+the CPU oracle.
+
+The device multiplies bf16 operands (inputs and weights rounded to nearest
+even as they are staged and packed) with fp32 accumulation over the whole
+kt x kh x kw x num_input window.  Two comparisons per case: against the
+oracle on the unrounded fp32 operands with the path's bar (max-abs <= 2e-2,
+cosine >= 0.9999), and against the oracle on the bf16-rounded operands with
+a tight bound (1e-4 of the output scale) that isolates the kernel's own
+arithmetic (summation order only)."""
+import numpy as np
+import pytest
+
+import oracle
+from common import assert_close, bf16_round
+from seedvr2_ncnn_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+
+def _cfg(cin, cout, k=(3, 3, 3), s=(1, 1, 1), d=(1, 1, 1), p=(1, 1), head=2, bias=True):
+    kw = dict(num_output=cout, num_input=cin, kernel_t=k[0], kernel_h=k[1], kernel_w=k[2],
+              stride_t=s[0], stride_h=s[1], stride_w=s[2], dilation_t=d[0], dilation_h=d[1],
+              dilation_w=d[2], pad_h=p[0], pad_w=p[1], head_frames=head, bias_term=int(bias))
+    return capi.conv3d_config(**kw), oracle.conv3d_config(**kw)
+
+
+def _case(cin, cout, frames, h, w, cfgs, seed):
+    g = np.random.default_rng(seed)
+    cfg = cfgs[1]
+    x = g.standard_normal((cin, frames, h, w)).astype(np.float32)
+    fan_in = cin * cfg.kernel_t * cfg.kernel_h * cfg.kernel_w
+    wts = (g.standard_normal((cfg.kernel_t, cout, cin, cfg.kernel_h, cfg.kernel_w)) /
+           np.sqrt(fan_in)).astype(np.float32)
+    bias = (0.1 * g.standard_normal(cout)).astype(np.float32) if cfg.bias_term else None
+    return x, wts, bias
+
+
+def _device(cfg, wts, bias):
+    import torch
+    return capi.Conv3d(cfg, torch.from_numpy(wts).cuda(),
+                       torch.from_numpy(bias).cuda() if bias is not None else None)
+
+
+def _run(conv, x, cstep_pad=0, dtype=None, out_dtype=None, **kw):
+    import torch
+    cin, frames, h, w = x.shape
+    flat = x.reshape(cin, -1)
+    # an ncnn cstep: the channel rounded up to 16 bytes (8 elements covers
+    # the 16-bit blobs too), plus any extra padding under test
+    pad = (-flat.shape[1]) % 8 + cstep_pad
+    if pad:
+        flat = np.concatenate([flat, np.zeros((cin, pad), np.float32)], 1)
+    t = torch.from_numpy(np.ascontiguousarray(flat)).cuda()
+    if dtype is not None:
+        t = t.to(dtype)
+    out, (to, ho, wo) = conv.forward(t, frames, h, w, out_dtype=out_dtype, **kw)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()[:, :to * ho * wo].reshape(-1, to, ho, wo)
+
+
+def _check(got, x, wts, bias, cfg_o, memory=None):
+    _, ref, _ = oracle.decomposed_conv3d(cfg_o, x, wts, bias, memory=memory)
+    assert got.shape == ref.shape
+    assert_close(got, ref)
+    _, tight, _ = oracle.decomposed_conv3d(cfg_o, bf16_round(x), bf16_round(wts), bias,
+                                           memory=None if memory is None else bf16_round(memory))
+    scale = max(1.0, float(np.max(np.abs(tight))))
+    assert float(np.max(np.abs(got - tight))) <= 1e-4 * scale
+
+
+SHAPES = [
+    # cin, cout, frames, h, w, kwargs
+    (128, 128, 3, 12, 20, {}),                         # 512x128 tiles, partial last tile
+    (64, 256, 2, 9, 13, {}),                           # 256x256 tiles
+    (16, 320, 2, 6, 10, {}),                           # cin < 64 (zero channels), ragged n
+    (3, 128, 5, 16, 16, dict(s=(1, 2, 2))),            # RGB input, spatial stride 2
+    (96, 72, 4, 7, 9, dict(k=(3, 1, 3), p=(0, 1))),    # ragged k window, cin not a multiple of 64
+    (256, 256, 1, 8, 8, dict(k=(1, 1, 1), p=(0, 0), head=0)),   # pointwise
+    (32, 40, 6, 5, 6, dict(s=(2, 1, 1), d=(2, 1, 2), p=(1, 2), head=4)),
+]
+
+
+@pytest.mark.parametrize("cin,cout,frames,h,w,kw", SHAPES)
+def test_conv3d_matches_oracle(cin, cout, frames, h, w, kw):
+    cfgs = _cfg(cin, cout, **kw)
+    x, wts, bias = _case(cin, cout, frames, h, w, cfgs, cin + cout + frames)
+    got = _run(_device(cfgs[0], wts, bias), x)
+    _check(got, x, wts, bias, cfgs[1])
+
+
+@pytest.mark.parametrize("in_dtype,out_dtype", [("bf16", "bf16"), ("f16", "f32"), ("f32", "f16")])
+def test_conv3d_16bit_blobs_and_padded_cstep(in_dtype, out_dtype):
+    import torch
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+    cfgs = _cfg(64, 128)
+    x, wts, bias = _case(64, 128, 2, 10, 12, cfgs, 7)
+    if in_dtype != "f32":
+        x = torch.from_numpy(x).to(dt[in_dtype]).float().numpy()    # the stored values
+    got = _run(_device(cfgs[0], wts, bias), x, cstep_pad=8, dtype=dt[in_dtype],
+               out_dtype=dt[out_dtype])
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("split", [1, 2])
+def test_conv3d_memory_chains_slices(split):
+    cfgs = _cfg(64, 128)
+    x, wts, bias = _case(64, 128, 5, 6, 10, cfgs, 11)
+    conv = _device(cfgs[0], wts, bias)
+    a = _run(conv, x[:, :split], keep_memory=True)
+    b = _run(conv, x[:, split:], use_memory=True, keep_memory=True)
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)   # the unsplit run
+    got = np.concatenate([a, b], axis=1)
+    assert_close(got, ref)
+    _, tight, _ = oracle.decomposed_conv3d(cfgs[1], bf16_round(x), bf16_round(wts), bias)
+    assert float(np.max(np.abs(got - tight))) <= 1e-4 * max(1.0, float(np.max(np.abs(tight))))
+
+
+def test_conv3d_larger_frame_against_torch():
+    """A VAE-shaped layer (128 -> 128, 3x3x3) on 2 frames of 90x160 against
+    torch's fp32 conv3d on the CPU over the same bf16-rounded operands."""
+    import torch
+    cfgs = _cfg(128, 128)
+    x, wts, bias = _case(128, 128, 2, 90, 160, cfgs, 3)
+    got = _run(_device(cfgs[0], wts, bias), x)
+    xp = np.concatenate([np.repeat(bf16_round(x)[:, :1], 2, axis=1), bf16_round(x)], axis=1)
+    ref = torch.nn.functional.conv3d(
+        torch.from_numpy(xp)[None], torch.from_numpy(bf16_round(wts)).permute(1, 2, 0, 3, 4),
+        torch.from_numpy(bias), padding=(0, 1, 1))[0].numpy()
+    assert got.shape == ref.shape
+    assert float(np.max(np.abs(got - ref))) <= 1e-4 * max(1.0, float(np.max(np.abs(ref))))
