@@ -464,9 +464,10 @@ class Conv3d:
         return tuple(out)
 
     def forward(self, x, frames, height, width, cstep=None, use_memory=False, keep_memory=False,
-                out_dtype=None, out_cstep=None, stream=None):
+                out_dtype=None, out_cstep=None, reuse_memory_buffer=False, stream=None):
         """x: device [num_input, cstep] planar (cstep >= frames*height*width).
-        Returns the output as [num_output, out_cstep]."""
+        Returns the output as [num_output, out_cstep].  reuse_memory_buffer
+        writes the new memory over the one this call reads."""
         import torch
         cfg = self.config
         mem = self.memory if use_memory and self.memory is not None else None
@@ -485,7 +486,10 @@ class Conv3d:
             check(lib().s2_conv3d_memory_bytes(ctypes.byref(cfg), height, width, ctypes.byref(nb),
                                                ctypes.byref(nf)), "s2_conv3d_memory_bytes")
             if nf.value > 0:
-                nxt = torch.empty(nb.value, dtype=torch.uint8, device=x.device)
+                if reuse_memory_buffer and mem is not None and mem.numel() == nb.value:
+                    nxt = mem
+                else:
+                    nxt = torch.empty(nb.value, dtype=torch.uint8, device=x.device)
         check(lib().s2_conv3d_forward(ctypes.byref(cfg), _ptr(self.packed), _ptr(self.bias), _ptr(x),
                                       _dtype_code(x), frames, height, width,
                                       cstep or x.shape[1], _ptr(mem), mframes, _ptr(out),

@@ -63,12 +63,14 @@ size_t dtype_bytes(s2_dtype t) { return t == S2_DTYPE_F32 ? 4 : 2; }
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p) % a == 0; }
 
 // DecomposedConv3D configuration checks of the reference load_model
-// (decomposed_conv3d.cpp:442-446), plus groups == 1.
+// (decomposed_conv3d.cpp:442-446), plus groups == 1 and a spatial window of
+// at most 32 positions (the kernel keeps one bit per position).
 bool conv3d_config_ok(const s2_conv3d_config* c) {
     return c && c->num_output > 0 && c->num_input > 0 && c->kernel_w > 0 && c->kernel_h > 0 &&
            c->kernel_t > 0 && c->stride_t > 0 && c->dilation_t > 0 && c->stride_w > 0 &&
            c->stride_h > 0 && c->dilation_w > 0 && c->dilation_h > 0 && c->groups == 1 &&
-           c->head_frames >= 0 && c->pad_w >= 0 && c->pad_h >= 0;
+           c->head_frames >= 0 && c->pad_w >= 0 && c->pad_h >= 0 &&
+           c->kernel_w * c->kernel_h <= 32;
 }
 
 s2::Conv3dShape conv3d_shape(const s2_conv3d_config* c) {
@@ -677,47 +679,68 @@ int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_weights
     const s2::Conv3dShape s = conv3d_shape(config);
     const size_t frame_elems = (size_t)plane_in * s.cpad;
     const size_t frame_bytes = frame_elems * 2;
-    const int staged_frames = mem + frames;
-    if ((size_t)staged_frames * frame_bytes > workspace_bytes)
+    if ((size_t)(mem + frames) * frame_bytes > workspace_bytes)
         return fail(S2_ERR_INVALID, "workspace too small");
     const int prefix = mem > 0 ? mem : config->head_frames;
     const int padded = frames + prefix;
     const int cache = config->kernel_t - config->stride_t;
-    if (next_memory && cache > padded) return fail(S2_ERR_INVALID, "too few frames for the memory");
-    hipStream_t st = (hipStream_t)stream;
-    uint16_t* staged = (uint16_t*)workspace;
-    if (mem > 0) S2_HIP(hipMemcpyAsync(staged, memory, (size_t)mem * frame_bytes,
-                                       hipMemcpyDeviceToDevice, st));
-    S2_HIP(s2::launch_conv3d_stage(input, (int)in_dtype, in_cstep, s.cin, (long)frames * plane_in,
-                                   s.cpad, staged + (size_t)mem * frame_elems, st));
-    // padded frame p is staged frame max(p - shift, 0)
-    const int shift = prefix - mem;
-    auto staged_frame = [&](long p) { return (int)std::max(p - shift, 0L); };
+    const bool want_memory = next_memory && cache > 0;
+    if (want_memory && cache > padded) return fail(S2_ERR_INVALID, "too few frames for the memory");
     const long max_span = (long)(0x7fffffffL / (long)frame_bytes);
     if (max_span < (long)(config->kernel_t - 1) * config->dilation_t + 1)
         return fail(S2_ERR_INVALID, "one output frame reads more than 2 GiB of staged input");
+    hipStream_t st = (hipStream_t)stream;
+
+    // Padded frame p is frame v = max(p - shift, 0) of [memory | input].  The
+    // kernel reads the memory frames straight from `memory` when each 8-row
+    // DMA group stays inside one output frame; otherwise they are copied in
+    // front of the staged input.
+    const int shift = prefix - mem;
+    const bool direct = mem > 0 && ((long)ho * wo) % 8 == 0 && (long)mem <= max_span;
+    const int kmem = direct ? mem : 0;
+    const int lead = mem - kmem;
+    uint16_t* staged = (uint16_t*)workspace;
+    if (lead > 0)
+        S2_HIP(hipMemcpyAsync(staged, memory, (size_t)lead * frame_bytes, hipMemcpyDeviceToDevice, st));
+    // The next memory is the last `cache` padded frames.  When they are all
+    // input frames the staging pass writes them as well, unless the kernel
+    // still has to read `memory` and next_memory overlaps it.
+    const uint8_t* mlo = (const uint8_t*)memory;
+    const uint8_t* nlo = (const uint8_t*)next_memory;
+    const bool overlap = memory && next_memory && nlo < mlo + (size_t)mem * frame_bytes &&
+                         mlo < nlo + (size_t)std::max(cache, 0) * frame_bytes;
+    const bool tail_in_stage = want_memory && frames >= cache && (kmem == 0 || !overlap);
+    S2_HIP(s2::launch_conv3d_stage(input, (int)in_dtype, in_cstep, s.cin, (long)frames * plane_in,
+                                   s.cpad, staged + (size_t)lead * frame_elems,
+                                   tail_in_stage ? (uint16_t*)next_memory : nullptr,
+                                   (long)(frames - cache) * plane_in, st));
+    auto vframe = [&](long p) { return (int)std::max(p - shift, 0L); };
+    const long reach = (long)(config->kernel_t - 1) * config->dilation_t;
     for (int t0 = 0; t0 < to;) {
         // as many output frames as keep the staged frames they read under 2 GiB
-        const int first = staged_frame((long)t0 * config->stride_t);
+        const int lo = std::max(vframe((long)t0 * config->stride_t) - kmem, 0);
         int n = 1;
         while (t0 + n < to &&
-               staged_frame((long)(t0 + n) * config->stride_t +
-                            (long)(config->kernel_t - 1) * config->dilation_t) - first + 1 <= max_span)
+               vframe((long)(t0 + n) * config->stride_t + reach) - kmem - lo + 1 <= max_span)
             ++n;
-        const int last = staged_frame((long)(t0 + n - 1) * config->stride_t +
-                                      (long)(config->kernel_t - 1) * config->dilation_t);
-        S2_HIP(s2::launch_conv3d(s, staged + (size_t)first * frame_elems,
-                                 (size_t)(last - first + 1) * frame_bytes, first, shift, height,
-                                 width, ho, wo, t0, n, (const uint16_t*)packed_weights, bias, output,
+        const int hi = vframe((long)(t0 + n - 1) * config->stride_t + reach) - kmem;
+        const size_t span = hi >= lo ? (size_t)(hi - lo + 1) * frame_bytes : 0;
+        S2_HIP(s2::launch_conv3d(s, (const uint16_t*)memory, kmem, (size_t)kmem * frame_bytes,
+                                 staged + (size_t)lo * frame_elems, span, lo, shift, height, width,
+                                 ho, wo, t0, n, (const uint16_t*)packed_weights, bias, output,
                                  (int)out_dtype, out_cstep, st));
         t0 += n;
     }
-    if (next_memory && cache > 0) {
+    if (want_memory && !tail_in_stage) {
+        // frames in ascending order: frame f comes from v >= f, so a memory
+        // buffer reused as next_memory is read before it is overwritten
         for (int f = 0; f < cache; ++f) {
-            const int sf = staged_frame((long)padded - cache + f);
-            S2_HIP(hipMemcpyAsync((uint8_t*)next_memory + (size_t)f * frame_bytes,
-                                  staged + (size_t)sf * frame_elems, frame_bytes,
-                                  hipMemcpyDeviceToDevice, st));
+            const int v = vframe((long)padded - cache + f);
+            const uint8_t* src = v < kmem ? mlo + (size_t)v * frame_bytes
+                                          : (const uint8_t*)(staged + (size_t)(v - kmem) * frame_elems);
+            uint8_t* dst = (uint8_t*)next_memory + (size_t)f * frame_bytes;
+            if (src != dst)
+                S2_HIP(hipMemcpyAsync(dst, src, frame_bytes, hipMemcpyDeviceToDevice, st));
         }
     }
     return S2_OK;

@@ -23,18 +23,24 @@ struct Conv3dShape {
 inline int conv3d_cpad(int cin) { return (cin + 63) / 64 * 64; }
 
 // planar input [cin][frames*H*W] (channel stride in_cstep; element type
-// in_kind: 0 fp32, 1 bf16, 2 fp16) -> staged [frames*H*W][cpad] bf16
+// in_kind: 0 fp32, 1 bf16, 2 fp16) -> staged [frames*H*W][cpad] bf16.  When
+// tail is non-null, pixels tail_q0.. are also written to tail (the next
+// temporal memory).
 hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, int cin,
-                               long pixels, int cpad, uint16_t* staged, hipStream_t stream);
+                               long pixels, int cpad, uint16_t* staged, uint16_t* tail,
+                               long tail_q0, hipStream_t stream);
 // fp32 [kt][cout][cin][kh][kw] -> bf16 [cout][kt][kh][kw][cpad]
 hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s,
                                       uint16_t* packed, hipStream_t stream);
 // Output frames [t0, t0 + frames_out) of the convolution.  Padded frame p
-// (p = t*st + tap*dt) is staged frame max(p - shift, 0) - frame_base of
-// `staged` (which must hold every frame these outputs read, < 2 GiB).
-// out: planar [cout][...], element (co, t, y, x) at co*out_cstep +
-// (t*Ho + y)*Wo + x, type out_kind; bias fp32 [cout] or null.
-hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* staged, size_t staged_bytes,
+// (p = t*st + tap*dt) is frame v = max(p - shift, 0) of [memory | input]:
+// memory frame v when v < mem (memory holds mem frames, memory_bytes), else
+// input frame v - mem, at frame v - mem - frame_base of `staged` (which must
+// hold every input frame these outputs read).  Both buffers < 2 GiB; mem > 0
+// needs ho*wo % 8 == 0.  out: planar [cout][...], element (co, t, y, x) at
+// co*out_cstep + (t*Ho + y)*Wo + x, type out_kind; bias fp32 [cout] or null.
+hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
+                         size_t memory_bytes, const uint16_t* staged, size_t staged_bytes,
                          int frame_base, int shift, int height, int width, int ho, int wo,
                          int t0, int frames_out, const uint16_t* packed, const float* bias,
                          void* out, int out_kind, long out_cstep, hipStream_t stream);

@@ -60,7 +60,7 @@ __device__ __forceinline__ void load_elem4(const void* p, long i, float (&v)[4])
 template <int KIND>
 __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
     const void* __restrict__ in, long cstep, int cin, long pixels, int cpad,
-    uint16_t* __restrict__ staged) {
+    uint16_t* __restrict__ staged, uint16_t* __restrict__ tail, long tail_q0) {
     __shared__ float tile[64 * 65];
     const long q0 = (long)blockIdx.x * 64;
     const int c0 = blockIdx.y * 64;
@@ -91,12 +91,19 @@ __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
     uint16_t h[16];
 #pragma unroll
     for (int i = 0; i < 16; ++i) h[i] = f32_to_bf16(tile[(part * 16 + i) * 65 + q]);
-    uint4* dst = reinterpret_cast<uint4*>(staged + (q0 + q) * cpad + c0 + part * 16);
     uint16_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) lo[i] = h[i], hi[i] = h[8 + i];
-    dst[0] = pack8_bf16(lo);
-    dst[1] = pack8_bf16(hi);
+    const uint4 vlo = pack8_bf16(lo), vhi = pack8_bf16(hi);
+    uint4* dst = reinterpret_cast<uint4*>(staged + (q0 + q) * cpad + c0 + part * 16);
+    dst[0] = vlo;
+    dst[1] = vhi;
+    // pixels from tail_q0 on are the next temporal memory as well
+    if (tail && q0 + q >= tail_q0) {
+        uint4* t2 = reinterpret_cast<uint4*>(tail + (q0 + q - tail_q0) * cpad + c0 + part * 16);
+        t2[0] = vlo;
+        t2[1] = vhi;
+    }
 }
 
 // ---- weights: [kt][cout][cin][kh][kw] fp32 -> [cout][kt][kh][kw][cpad] bf16 --
@@ -123,8 +130,11 @@ __global__ __launch_bounds__(256) void conv3d_pack_kernel(const float* __restric
 // ---- the implicit GEMM ---------------------------------------------------------
 
 struct ConvArgs {
-    const uint16_t* staged;
+    const uint16_t* staged;   // input frames fbase.. (staged layout)
     uint32_t staged_bytes;
+    const uint16_t* memory;   // memory frames 0..mem-1 (staged layout)
+    uint32_t memory_bytes;
+    int mem;
     const uint16_t* packed;
     int kp;   // packed row length: kt*kh*kw*cpad
     const float* bias;
@@ -146,8 +156,16 @@ struct ConvArgs {
 // gives 512x128 tiles.  Two 64-k LDS stages of (BM + BN) x 128 bytes (64 KB
 // or 80 KB) are filled by DMA one stage ahead of the MFMAs; LDS rows use the
 // GEMM's chunk swizzle.  Wave w loads A rows [w*BM/8, (w+1)*BM/8) and B rows
-// [w*BN/8, (w+1)*BN/8), 8 rows per DMA instruction.
-template <int BN>
+// [w*BN/8, (w+1)*BN/8), 8 rows per DMA instruction.  OK is the output type
+// (0 fp32, 1 bf16, 2 fp16).
+//
+// The im2col addressing costs a few VALU operations per row and window
+// position: each A row keeps the byte offset of its window origin
+// (rpix), a bit mask of the (ky, kx) positions that fall inside the image
+// (rmask), and the offset of its current temporal tap's frame (rbase,
+// refreshed when the tap changes).  A position then adds one scalar offset.
+// The k-steps walk (tap, ky, kx, channel chunk) with scalar counters.
+template <int BN, int OK>
 __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     constexpr int BM = BN == 128 ? 512 : 256;
     constexpr int BK = 64, RB = BK * 2;
@@ -160,7 +178,8 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    // the wave index is uniform; saying so keeps the DMA's LDS addresses in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int l32 = lane & 31;
     const int g = lane >> 5;
     const int wm = wave / WN;
@@ -178,26 +197,36 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     const int row0 = mt * BM;
     const int col0 = nt * BN;
 
-    // geometry of the A rows this lane loads: padded frame of tap 0, and the
-    // input y, x of window position (0, 0); a negative frame marks a row past M
+    const uint32_t pix = (uint32_t)(a.cpad * 2);
+    const uint32_t frame_bytes = (uint32_t)(a.H * a.W) * pix;
+    // A rows of this lane: padded frame of tap 0 (negative past M), window
+    // origin offset (mod 2^32: the origin may lie in the padding), and mask
     const int hw = a.Ho * a.Wo;
-    int rpf[AJ], ryb[AJ], rxb[AJ];
-    uint32_t chk[AJ];
+    int rpf[AJ];
+    uint32_t rpix[AJ], rmask[AJ];
 #pragma unroll
     for (int j = 0; j < AJ; ++j) {
         const int row = wave * ARPW + j * 8 + (lane >> 3);
         const int m = row0 + row;
-        chk[j] = (uint32_t)(((lane & 7) ^ lds_swizzle(row)) * 16);
+        const uint32_t chk = (uint32_t)(((lane & 7) ^ lds_swizzle(row)) * 16);
         rpf[j] = INT_MIN / 2;
-        ryb[j] = rxb[j] = 0;
+        rpix[j] = chk;
+        rmask[j] = 0;
         if (m < a.M) {
             const int to = m / hw;
             const int rem = m - to * hw;
             const int yo = rem / a.Wo;
             const int xo = rem - yo * a.Wo;
+            const int yb = yo * a.sh - a.ph, xb = xo * a.sw - a.pw;
             rpf[j] = (a.t0 + to) * a.st;
-            ryb[j] = yo * a.sh - a.ph;
-            rxb[j] = xo * a.sw - a.pw;
+            rpix[j] = (uint32_t)(yb * a.W + xb) * pix + chk;
+            uint32_t mk = 0;
+            for (int ky = 0; ky < a.kh; ++ky) {
+                if ((unsigned)(yb + ky * a.dh) >= (unsigned)a.H) continue;
+                for (int kx = 0; kx < a.kw; ++kx)
+                    if ((unsigned)(xb + kx * a.dw) < (unsigned)a.W) mk |= 1u << (ky * a.kw + kx);
+            }
+            rmask[j] = mk;
         }
     }
     uint32_t voffb[BJ];
@@ -207,42 +236,47 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
         voffb[j] = (uint32_t)(row * a.kp * 2 + (((lane & 7) ^ lds_swizzle(row)) * 16));
     }
     const i32x4 ra = wave_uniform(buffer_rsrc(a.staged, a.staged_bytes));
+    const i32x4 rm = wave_uniform(buffer_rsrc(a.memory, a.memory_bytes));
     const i32x4 rb = wave_uniform(buffer_rsrc(
         a.packed + (long)col0 * a.kp, (uint32_t)(min(a.cout - col0, BN) * a.kp * 2)));
-    const uint32_t pix_bytes = (uint32_t)(a.cpad * 2);
 
-    uint32_t voffa[AJ];
-    // A offsets of window position pos = (tap, ky, kx)
-    auto set_pos = [&](int pos) {
-        const int kx = pos % a.kw;
-        const int rest = pos / a.kw;
-        const int ky = rest % a.kh;
-        const int tap = rest / a.kh;
-        const int dtap = tap * a.dt, dy = ky * a.dh, dx = kx * a.dw;
+    // Temporal tap: padded frame p is frame v = max(p - shift, 0) of
+    // [memory | input]; v < mem reads the memory buffer, otherwise input
+    // frame v - mem of the staged buffer (based at input frame fbase).  The 8
+    // rows of one DMA instruction lie in one output frame (the host passes
+    // mem > 0 only when Ho*Wo % 8 == 0), so the buffer is the same for all.
+    uint32_t rbase[AJ];
+    int memsel[AJ];
+    auto set_tap = [&](int tap) {
+        const int dtap = tap * a.dt - a.shift;
 #pragma unroll
         for (int j = 0; j < AJ; ++j) {
-            const int sf = max(rpf[j] + dtap - a.shift, 0) - a.fbase;
-            const int yi = ryb[j] + dy, xi = rxb[j] + dx;
-            const bool ok = rpf[j] >= 0 && sf >= 0 && (unsigned)yi < (unsigned)a.H &&
-                            (unsigned)xi < (unsigned)a.W;
-            voffa[j] = ok ? (uint32_t)((sf * a.H + yi) * a.W + xi) * pix_bytes + chk[j]
-                          : 0x80000000u;
+            const int v = max(rpf[j] + dtap, 0);
+            const bool fm = v < a.mem;
+            const int sf = fm ? v : v - a.mem - a.fbase;
+            rbase[j] = (uint32_t)sf * frame_bytes + rpix[j];
+            memsel[j] = __builtin_amdgcn_readfirstlane((int)fm);
         }
+    };
+    uint32_t voffa[AJ];
+    auto set_pos = [&](int ky, int kx) {
+        const uint32_t koff = (uint32_t)(ky * a.dh * a.W + kx * a.dw) * pix;
+        const uint32_t bit = 1u << (ky * a.kw + kx);
+#pragma unroll
+        for (int j = 0; j < AJ; ++j) voffa[j] = (rmask[j] & bit) ? rbase[j] + koff : 0x80000000u;
     };
     const int cpc = a.cpad / 64;   // k-steps per window position
     const int nk = a.kp / 64;
-    auto issue = [&](int stage, int ks) {
-        const uint32_t soffa = __builtin_amdgcn_readfirstlane((uint32_t)((ks % cpc) * RB));
-        const uint32_t soffb = __builtin_amdgcn_readfirstlane((uint32_t)(ks * RB));
+    auto issue = [&](int stage, int ks, int cc) {
+        const uint32_t soffa = (uint32_t)(cc * RB);
+        const uint32_t soffb = (uint32_t)(ks * RB);
         const uint32_t st = lds_base + stage * SB;
 #pragma unroll
         for (int j = 0; j < AJ; ++j)
-            lds_dma16(ra, __builtin_amdgcn_readfirstlane(st + (wave * ARPW + j * 8) * RB),
-                      voffa[j], soffa);
+            lds_dma16(memsel[j] ? rm : ra, st + (wave * ARPW + j * 8) * RB, voffa[j], soffa);
 #pragma unroll
         for (int j = 0; j < BJ; ++j)
-            lds_dma16(rb, __builtin_amdgcn_readfirstlane(st + TA + (wave * BRPW + j * 8) * RB),
-                      voffb[j], soffb);
+            lds_dma16(rb, st + TA + (wave * BRPW + j * 8) * RB, voffb[j], soffb);
     };
 
     f32x16 acc[4][2];
@@ -263,16 +297,29 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    set_pos(0);
-    issue(0, 0);
+    // window position and channel chunk of the next k-step to issue
+    int tap = 0, ky = 0, kx = 0, cc = 0;
+    set_tap(0);
+    set_pos(0, 0);
+    issue(0, 0, 0);
 #pragma unroll 1
     for (int ks = 0; ks < nk; ++ks) {
         const int stage = ks & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();   // stage ks visible to all waves; the other stage no longer read
         if (ks + 1 < nk) {
-            if ((ks + 1) % cpc == 0) set_pos((ks + 1) / cpc);
-            issue(stage ^ 1, ks + 1);
+            if (++cc == cpc) {
+                cc = 0;
+                if (++kx == a.kw) {
+                    kx = 0;
+                    if (++ky == a.kh) {
+                        ky = 0;
+                        set_tap(++tap);
+                    }
+                }
+                set_pos(ky, kx);
+            }
+            issue(stage ^ 1, ks + 1, cc);
         }
         const uint8_t* st = lds + stage * SB;
         frag(st, 0, 0);
@@ -308,16 +355,16 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
                 const float v0 = acc[i][j][4 * rg] + bv, v1 = acc[i][j][4 * rg + 1] + bv;
                 const float v2 = acc[i][j][4 * rg + 2] + bv, v3 = acc[i][j][4 * rg + 3] + bv;
                 if (a.vec_ok && m + 3 < a.M) {
-                    store4(a.out, cbase + m, v0, v1, v2, v3, a.out_kind);
+                    store4(a.out, cbase + m, v0, v1, v2, v3, OK);
                 } else {
                     const float v[4] = {v0, v1, v2, v3};
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         if (m + e >= a.M) continue;
                         const long idx = cbase + m + e;
-                        if (a.out_kind == 1)
+                        if (OK == 1)
                             ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
-                        else if (a.out_kind == 2)
+                        else if (OK == 2)
                             ((_Float16*)a.out)[idx] = (_Float16)v[e];
                         else
                             ((float*)a.out)[idx] = v[e];
@@ -327,21 +374,33 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     }
 }
 
+template <int BN>
+void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
+    const unsigned grid = (unsigned)(a.mtiles * a.ntiles);
+    if (a.out_kind == 1)
+        conv3d_kernel<BN, 1><<<grid, 512, 0, stream>>>(a);
+    else if (a.out_kind == 2)
+        conv3d_kernel<BN, 2><<<grid, 512, 0, stream>>>(a);
+    else
+        conv3d_kernel<BN, 0><<<grid, 512, 0, stream>>>(a);
+}
+
 }  // namespace
 
 hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, int cin,
-                               long pixels, int cpad, uint16_t* staged, hipStream_t stream) {
+                               long pixels, int cpad, uint16_t* staged, uint16_t* tail,
+                               long tail_q0, hipStream_t stream) {
     if (pixels <= 0) return hipSuccess;
     const dim3 grid((unsigned)((pixels + 63) / 64), (unsigned)(cpad / 64));
     if (in_kind == 1)
         conv3d_stage_kernel<1><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
-                                                                     cpad, staged);
+                                                                     cpad, staged, tail, tail_q0);
     else if (in_kind == 2)
         conv3d_stage_kernel<2><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
-                                                                     cpad, staged);
+                                                                     cpad, staged, tail, tail_q0);
     else
         conv3d_stage_kernel<0><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
-                                                                     cpad, staged);
+                                                                     cpad, staged, tail, tail_q0);
     return hipGetLastError();
 }
 
@@ -354,19 +413,24 @@ hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s
     return hipGetLastError();
 }
 
-hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* staged, size_t staged_bytes,
+hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
+                         size_t memory_bytes, const uint16_t* staged, size_t staged_bytes,
                          int frame_base, int shift, int height, int width, int ho, int wo,
                          int t0, int frames_out, const uint16_t* packed, const float* bias,
                          void* out, int out_kind, long out_cstep, hipStream_t stream) {
     if (frames_out <= 0) return hipSuccess;
     const long m = (long)frames_out * ho * wo;
     const long kp = (long)s.kt * s.kh * s.kw * s.cpad;
-    if (m > INT_MAX || staged_bytes >= 0x80000000ull || kp * 2 * s.cout >= 0x80000000l ||
-        s.cpad % 64 != 0)
+    if (m > INT_MAX || staged_bytes >= 0x80000000ull || memory_bytes >= 0x80000000ull ||
+        kp * 2 * s.cout >= 0x80000000l || s.cpad % 64 != 0 || s.kh * s.kw > 32 ||
+        (mem > 0 && ((long)ho * wo) % 8 != 0))
         return hipErrorInvalidValue;
     ConvArgs a;
     a.staged = staged;
     a.staged_bytes = (uint32_t)staged_bytes;
+    a.memory = mem > 0 ? memory : staged;
+    a.memory_bytes = mem > 0 ? (uint32_t)memory_bytes : 0u;
+    a.mem = mem;
     a.packed = packed;
     a.kp = (int)kp;
     a.bias = bias;
@@ -399,11 +463,11 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* staged, size_t st
     if (s.cout <= 128) {
         a.mtiles = (int)((m + 511) / 512);
         a.ntiles = (s.cout + 127) / 128;
-        conv3d_kernel<128><<<(unsigned)(a.mtiles * a.ntiles), 512, 0, stream>>>(a);
+        launch_conv3d_kernel<128>(a, stream);
     } else {
         a.mtiles = (int)((m + 255) / 256);
         a.ntiles = (s.cout + 255) / 256;
-        conv3d_kernel<256><<<(unsigned)(a.mtiles * a.ntiles), 512, 0, stream>>>(a);
+        launch_conv3d_kernel<256>(a, stream);
     }
     return hipGetLastError();
 }

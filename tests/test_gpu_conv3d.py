@@ -103,18 +103,26 @@ def test_conv3d_16bit_blobs_and_padded_cstep(in_dtype, out_dtype):
     assert_close(got, ref)
 
 
+# 6x10 frames copy the memory in front of the staged input (a DMA group of
+# 8 rows can straddle two frames); 8x10 frames read it in place
 @pytest.mark.parametrize("split", [1, 2])
-def test_conv3d_memory_chains_slices(split):
+@pytest.mark.parametrize("hw", [(6, 10), (8, 10)])
+@pytest.mark.parametrize("reuse", [False, True])
+def test_conv3d_memory_chains_slices(split, hw, reuse):
     cfgs = _cfg(64, 128)
-    x, wts, bias = _case(64, 128, 5, 6, 10, cfgs, 11)
+    x, wts, bias = _case(64, 128, 5, hw[0], hw[1], cfgs, 11)
     conv = _device(cfgs[0], wts, bias)
     a = _run(conv, x[:, :split], keep_memory=True)
-    b = _run(conv, x[:, split:], use_memory=True, keep_memory=True)
+    b = _run(conv, x[:, split:], use_memory=True, keep_memory=True, reuse_memory_buffer=reuse)
     _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)   # the unsplit run
     got = np.concatenate([a, b], axis=1)
     assert_close(got, ref)
     _, tight, _ = oracle.decomposed_conv3d(cfgs[1], bf16_round(x), bf16_round(wts), bias)
     assert float(np.max(np.abs(got - tight))) <= 1e-4 * max(1.0, float(np.max(np.abs(tight))))
+    # a third slice of one frame: its memory mixes the old memory and the input
+    c = _run(conv, x[:, 4:], use_memory=True, keep_memory=True, reuse_memory_buffer=reuse)
+    _, ref3, _ = oracle.decomposed_conv3d(cfgs[1], np.concatenate([x, x[:, 4:]], 1), wts, bias)
+    assert_close(c, ref3[:, 5:])
 
 
 def test_conv3d_larger_frame_against_torch():
