@@ -2,8 +2,9 @@
 
   seedvr2_ncnn_amd/lib/libseedvr2_hip.so     HIP kernels + the C-ABI (include/seedvr2_hip.h)
   seedvr2_ncnn_amd/lib/libseedvr2_layers.so  ncnn-surface layers (AdaptiveWindowAttention,
-                                             SharedLinear) over the C-ABI, with the
-                                             ncnn-compatible Mat/Layer subset
+                                             SharedLinear, DecomposedConv3D) over the
+                                             C-ABI, with the ncnn-compatible Mat/Layer
+                                             subset
 
 Every HIP file is compiled for gfx950 only, with packed-fp32 instruction
 selection disabled.  Usage: python -m seedvr2_ncnn_amd.build [--force]
@@ -35,7 +36,8 @@ CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I" + INCLUDE,
 HIP_SOURCES = ["awa_kernels.hip", "linear_kernels.hip", "pipeline_kernels.hip",
                "conv3d_kernels.hip", "capi.hip", "awa_plan.cpp"]
 LAYER_SOURCES = ["ncnn/mat.cpp", "ncnn/layer.cpp", "layers/hip_allocator.cpp",
-                 "layers/adaptive_window_attention.cpp", "layers/shared_linear.cpp"]
+                 "layers/adaptive_window_attention.cpp", "layers/shared_linear.cpp",
+                 "layers/decomposed_conv3d.cpp"]
 
 HIP_LIB = os.path.join(LIB, "libseedvr2_hip.so")
 LAYER_LIB = os.path.join(LIB, "libseedvr2_layers.so")

@@ -36,6 +36,23 @@ ncnn::Mat HipDeviceAllocator::wrap_blob(int w, int h, void* device_data, size_t 
     return ncnn::Mat(w, h, device_data, elemsize, this);
 }
 
+ncnn::Mat HipDeviceAllocator::create_blob(int w, int h, int d, int c, size_t elemsize) {
+    if (w <= 0 || h <= 0 || d <= 0 || c <= 0 || (elemsize != 2 && elemsize != 4)) return ncnn::Mat();
+    ncnn::Mat shape(w, h, d, c, (void*)0, elemsize, this);
+    void* p = 0;
+    if (s2_malloc(&p, shape.cstep * c * elemsize) != S2_OK || !p) return ncnn::Mat();
+    {
+        std::lock_guard<std::mutex> lock(mutex_);
+        owned_.push_back(p);
+    }
+    return ncnn::Mat(w, h, d, c, p, elemsize, this);
+}
+
+ncnn::Mat HipDeviceAllocator::wrap_blob(int w, int h, int d, int c, void* device_data,
+                                        size_t elemsize) {
+    return ncnn::Mat(w, h, d, c, device_data, elemsize, this);
+}
+
 void HipDeviceAllocator::clear() {
     std::lock_guard<std::mutex> lock(mutex_);
     if (!owned_.empty()) s2_stream_synchronize(stream_);

@@ -36,8 +36,12 @@ public:
     // Device Mat (dims 2: w x h, elemsize 4 = fp32, 2 = bf16 or fp16, see
     // device_blob_dtype) owned by this allocator.  Empty on allocation failure.
     ncnn::Mat create_blob(int w, int h, size_t elemsize);
+    // 4-D device Mat (w, h, d, c) with ncnn's channel stride (each channel
+    // rounded up to 16 bytes), owned by this allocator.
+    ncnn::Mat create_blob(int w, int h, int d, int c, size_t elemsize);
     // Wraps caller-owned device memory as a device blob (not owned).
     ncnn::Mat wrap_blob(int w, int h, void* device_data, size_t elemsize);
+    ncnn::Mat wrap_blob(int w, int h, int d, int c, void* device_data, size_t elemsize);
     // Frees every blob this allocator created.
     void clear();
 

@@ -55,6 +55,12 @@ Mat::Mat(int _w, int _h, int _c, void* _data, size_t _elemsize, Allocator* _allo
     cstep = alignSize((size_t)w * h * elemsize, 16) / elemsize;
 }
 
+Mat::Mat(int _w, int _h, int _d, int _c, void* _data, size_t _elemsize, Allocator* _allocator)
+    : data(_data), refcount(0), elemsize(_elemsize), elempack(1), allocator(_allocator), dims(4),
+      w(_w), h(_h), d(_d), c(_c) {
+    cstep = alignSize((size_t)w * h * d * elemsize, 16) / elemsize;
+}
+
 Mat::~Mat() { release(); }
 
 Mat& Mat::operator=(const Mat& m) {

@@ -26,6 +26,7 @@ public:
     Mat(int w, void* data, size_t elemsize = 4u, Allocator* allocator = 0);
     Mat(int w, int h, void* data, size_t elemsize = 4u, Allocator* allocator = 0);
     Mat(int w, int h, int c, void* data, size_t elemsize = 4u, Allocator* allocator = 0);
+    Mat(int w, int h, int d, int c, void* data, size_t elemsize = 4u, Allocator* allocator = 0);
     ~Mat();
 
     Mat& operator=(const Mat& m);

@@ -99,6 +99,17 @@ class HBlob(ctypes.Structure):
 _H = None
 
 
+class HBlob4(ctypes.Structure):
+    _fields_ = [("w", ctypes.c_int), ("h", ctypes.c_int), ("d", ctypes.c_int), ("c", ctypes.c_int),
+                ("cstep", ctypes.c_long), ("elemsize", ctypes.c_int), ("device", ctypes.c_int),
+                ("data", ctypes.c_void_p)]
+
+
+def ncnn_cstep(w, h, d, elemsize):
+    """ncnn's channel stride of a 4-D Mat: a channel rounded up to 16 bytes."""
+    return ((w * h * d * elemsize + 15) // 16 * 16) // elemsize
+
+
 def harness():
     global _H
     if _H is None:
@@ -116,6 +127,9 @@ def harness():
         L.h_layer_forward.argtypes = [vp, ci, P(HBlob), ci, P(HBlob)]
         L.h_layer_set_storage.argtypes = [vp, ci, ci]
         L.h_build_plan.argtypes = [P(ci), ci, P(ci), ci, ci, P(ci), P(ci), P(ci), P(ci), P(ci), P(ci)]
+        L.h_set_vae_memory_state.argtypes = [ci]
+        L.h_conv_memory.argtypes = [vp, ci]
+        L.h_layer_forward4.argtypes = [vp, P(HBlob4), P(HBlob4)]
         _H = L
     return _H
 
@@ -149,6 +163,41 @@ class Layer:
     def set_storage(self, fp16, bf16):
         """ncnn Option use_fp16_storage / use_bf16_storage for forward."""
         harness().h_layer_set_storage(self.h, int(bool(fp16)), int(bool(bf16)))
+
+    def forward_planar(self, x, dims, out_dims, device=False, dtype=None):
+        """One-blob forward over 4-D blobs.  x: numpy [c, d, h, w] (fp32
+        values); dims = (w, h, d, c); out_dims = (w, h, d, c) expected.  With
+        device=True the blob is a device Mat of the given torch dtype
+        (elemsize 4 or 2).  Returns (code, numpy [c, d, h, w] fp32)."""
+        import torch
+        w, h, d, c = dims
+        es = 4 if dtype in (None, torch.float32) else 2
+        cs = ncnn_cstep(w, h, d, es)
+        flat = np.zeros((c, cs), np.float32)
+        flat[:, :w * h * d] = np.asarray(x, np.float32).reshape(c, -1)
+        ow, oh, od, oc = out_dims
+        ocs = ncnn_cstep(ow, oh, od, es)
+        bi, bo = HBlob4(), HBlob4()
+        bi.w, bi.h, bi.d, bi.c, bi.cstep, bi.elemsize = w, h, d, c, cs, es
+        bo.w, bo.h, bo.d, bo.c, bo.cstep, bo.elemsize = ow, oh, od, oc, ocs, es
+        if device:
+            tin = torch.from_numpy(flat).cuda().to(dtype or torch.float32)
+            tout = torch.zeros((oc, ocs), dtype=dtype or torch.float32, device="cuda")
+            bi.device = bo.device = 1
+            bi.data, bo.data = tin.data_ptr(), tout.data_ptr()
+        else:
+            hout = np.zeros((oc, ocs), np.float32)
+            bi.device = bo.device = 0
+            bi.data, bo.data = flat.ctypes.data, hout.ctypes.data
+        code = harness().h_layer_forward4(self.h, ctypes.byref(bi), ctypes.byref(bo))
+        if code != 0:
+            return code, None
+        res = tout.float().cpu().numpy() if device else hout
+        assert (bo.w, bo.h, bo.d, bo.c) == (ow, oh, od, oc)
+        return 0, res[:, :ow * oh * od].reshape(oc, od, oh, ow)
+
+    def conv_memory(self, reset):
+        return harness().h_conv_memory(self.h, int(bool(reset)))
 
     def set_state(self, video_shapes, text_lengths):
         s = np.ascontiguousarray(np.asarray(video_shapes, np.int32).ravel())
@@ -236,3 +285,8 @@ def harness_plan(video_shapes, target, shifted):
     if code != 0:
         raise ValueError(code)
     return wins[:9 * n.value].reshape(-1, 9), counts, idx, inv, pos.reshape(-1, 3)
+
+
+def set_vae_memory_state(state):
+    """seedvr2::set_vae_memory_state: 0 DISABLED, 1 INITIALIZING, 2 ACTIVE."""
+    harness().h_set_vae_memory_state(int(state))

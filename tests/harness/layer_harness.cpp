@@ -1,5 +1,5 @@
 // Test harness: drives the ncnn-surface layers (AdaptiveWindowAttention,
-// SharedLinear) the way an ncnn Net does -- creator, load_param from a .param
+// SharedLinear, DecomposedConv3D) the way an ncnn Net does -- creator, load_param from a .param
 // field string, load_model from raw weight bytes, create_pipeline, forward --
 // and exposes that to the Python tests through a few extern "C" calls.
 // Test infrastructure only; built into tests/harness/liblayer_harness.so.
@@ -14,6 +14,7 @@
 #include <paramdict.h>
 
 #include "adaptive_window_attention.h"
+#include "decomposed_conv3d.h"
 #include "hip_allocator.h"
 #include "seedvr2_hip.h"
 #include "shared_linear.h"
@@ -57,6 +58,9 @@ int h_layer_create(const char* type, const char* params, const void* model, long
     } else if (strcmp(type, "SharedLinear") == 0) {
         h->layer = seedvr2::shared_linear_layer_creator(0);
         h->destroyer = seedvr2::shared_linear_layer_destroyer;
+    } else if (strcmp(type, "DecomposedConv3d") == 0) {
+        h->layer = seedvr2::decomposed_conv3d_layer_creator(0);
+        h->destroyer = seedvr2::decomposed_conv3d_layer_destroyer;
     } else {
         delete h;
         return -1;
@@ -155,6 +159,60 @@ int h_layer_forward(void* handle, int n_in, const h_blob* ins, int n_out, h_blob
         if (ret != 0) return ret;
     }
     ret = s2_stream_synchronize(0);
+    device_allocator().clear();
+    return ret;
+}
+
+// A 4-D blob (w, h, d, c) with ncnn's channel stride cstep.
+typedef struct h_blob4 {
+    int w, h, d, c;
+    long cstep;
+    int elemsize;
+    int device;
+    void* data;
+} h_blob4;
+
+// seedvr2::set_vae_memory_state on the calling thread: 0 DISABLED,
+// 1 INITIALIZING, 2 ACTIVE.
+void h_set_vae_memory_state(int state) {
+    seedvr2::set_vae_memory_state(static_cast<seedvr2::MemoryState>(state));
+}
+
+// DecomposedConv3D::reset_temporal_memory / release_completed_temporal_memory
+int h_conv_memory(void* handle, int reset) {
+    Handle* h = static_cast<Handle*>(handle);
+    seedvr2::DecomposedConv3D* l = dynamic_cast<seedvr2::DecomposedConv3D*>(h->layer);
+    if (!l) return -1;
+    if (reset) l->reset_temporal_memory();
+    else l->release_completed_temporal_memory();
+    return 0;
+}
+
+// forward(Mat, Mat) of a one-blob layer over 4-D blobs.  The output is
+// copied into out->data (host, or device when out->device), whose capacity
+// is out->cstep * out->c elements; its shape is reported back in *out.
+int h_layer_forward4(void* handle, const h_blob4* in, h_blob4* out) {
+    Handle* h = static_cast<Handle*>(handle);
+    ncnn::Allocator* alloc = in->device ? &device_allocator() : 0;
+    ncnn::Mat bottom(in->w, in->h, in->d, in->c, in->data, (size_t)in->elemsize, alloc);
+    if ((long)bottom.cstep != in->cstep) return -4;
+    ncnn::Mat top;
+    int ret = h->layer->forward(bottom, top, h->opt);
+    if (ret != 0) return ret;
+    const size_t bytes = top.total() * top.elemsize;
+    if (bytes > (size_t)out->cstep * out->c * out->elemsize) return -3;
+    const bool src_dev = seedvr2::device_allocator_of(top) != 0;
+    if (src_dev && out->device) ret = s2_memcpy_d2d(out->data, top.data, bytes, 0);
+    else if (src_dev) ret = s2_memcpy_d2h(out->data, top.data, bytes, 0);
+    else if (out->device) ret = s2_memcpy_h2d(out->data, top.data, bytes, 0);
+    else memcpy(out->data, top.data, bytes);
+    out->w = top.w;
+    out->h = top.h;
+    out->d = top.d;
+    out->c = top.c;
+    out->cstep = (long)top.cstep;
+    out->elemsize = (int)top.elemsize;
+    if (ret == 0) ret = s2_stream_synchronize(0);
     device_allocator().clear();
     return ret;
 }

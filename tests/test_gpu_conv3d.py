@@ -138,3 +138,73 @@ def test_conv3d_larger_frame_against_torch():
         torch.from_numpy(bias), padding=(0, 1, 1))[0].numpy()
     assert got.shape == ref.shape
     assert float(np.max(np.abs(got - ref))) <= 1e-4 * max(1.0, float(np.max(np.abs(ref))))
+
+
+# ---- the ncnn-surface layer (decomposed_conv3d.h:29-88) ------------------------
+
+def _layer(cfg_o, wts, bias):
+    from common import Layer
+    fields = [getattr(cfg_o, n) for n, _ in oracle.Conv3dConfig._fields_]
+    params = " ".join(f"{i}={v}" for i, v in enumerate(fields))
+    blobs = [np.asarray(fields, np.float32)] + ([bias] if bias is not None else []) + [wts]
+    layer = Layer("DecomposedConv3d", params, weights=blobs)
+    assert layer.create_code == 0
+    assert layer.create_pipeline() == 0
+    return layer
+
+
+@pytest.mark.parametrize("device", [False, True])
+def test_layer_forward_host_and_device_blobs(device):
+    import torch
+    from common import set_vae_memory_state
+    cfgs = _cfg(64, 128)
+    x, wts, bias = _case(64, 128, 3, 10, 12, cfgs, 21)
+    layer = _layer(cfgs[1], wts, bias)
+    set_vae_memory_state(0)
+    dt = torch.bfloat16 if device else None
+    xin = torch.from_numpy(x).to(torch.bfloat16).float().numpy() if device else x
+    code, got = layer.forward_planar(xin, (12, 10, 3, 64), (12, 10, 3, 128), device=device, dtype=dt)
+    assert code == 0
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], xin, wts, bias)
+    assert_close(got, ref)
+
+
+def test_layer_memory_states_chain_slices():
+    from common import set_vae_memory_state
+    cfgs = _cfg(32, 64)
+    x, wts, bias = _case(32, 64, 6, 8, 8, cfgs, 5)
+    layer = _layer(cfgs[1], wts, bias)
+    _, full, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)
+    outs = []
+    # the VAE driver's sequence: a first slice that starts the memory, then
+    # slices that continue it (seedvr2_vae.cpp:424-447)
+    for i, (a, b) in enumerate([(0, 2), (2, 3), (3, 6)]):
+        set_vae_memory_state(1 if i == 0 else 2)
+        code, out = layer.forward_planar(x[:, a:b], (8, 8, b - a, 32), (8, 8, b - a, 64))
+        assert code == 0
+        outs.append(out)
+    assert_close(np.concatenate(outs, axis=1), full)
+    # DISABLED forgets the memory: the prefix is head frames again
+    set_vae_memory_state(0)
+    code, out = layer.forward_planar(x[:, 3:6], (8, 8, 3, 32), (8, 8, 3, 64))
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x[:, 3:6], wts, bias)
+    assert code == 0
+    assert_close(out, ref)
+
+
+def test_layer_rejects_mismatched_blobs():
+    from common import set_vae_memory_state
+    cfgs = _cfg(32, 64)
+    x, wts, bias = _case(32, 64, 2, 8, 8, cfgs, 9)
+    layer = _layer(cfgs[1], wts, bias)
+    set_vae_memory_state(0)
+    code, _ = layer.forward_planar(x[:16], (8, 8, 2, 16), (8, 8, 2, 64))   # wrong channels
+    assert code == -1
+    set_vae_memory_state(1)
+    assert layer.forward_planar(x, (8, 8, 2, 32), (8, 8, 2, 64))[0] == 0
+    set_vae_memory_state(2)   # the memory holds 8x8 frames: a 6x8 slice is refused
+    code, _ = layer.forward_planar(x[:, :, :6], (8, 6, 2, 32), (8, 6, 2, 64))
+    assert code == -1
+    assert layer.conv_memory(reset=True) == 0
+    assert layer.forward_planar(x[:, :, :6], (8, 6, 2, 32), (8, 6, 2, 64))[0] == 0
+    set_vae_memory_state(0)
