@@ -19,7 +19,8 @@ SeedVR2-7B-shaped stack of 32 blocks (hidden 3072, 24 heads x 128, MLP
 3072 -> 12288 -> 3072, regular windows in even and shifted windows in odd
 blocks, 64 text tokens projected 5120 -> 3072 once) under "stack_7b".  The
 frontend/tail kernels (patchify, unpatchify, CFG, Euler update) at the 720p
-latent are timed under "sampler_tail".
+latent are timed under "sampler_tail", and the VAE decoder's DecomposedConv3D
+layers under "vae_conv3d".
 
 Prints one JSON line.  `--gpus` above 1 is refused: this build measures one GPU.
 """
@@ -205,6 +206,87 @@ def sampler_tail(reps=50):
     return out
 
 
+# VAE decoder DecomposedConv3D layers (3x3x3, pad 1, causal 2-frame memory)
+# at 720p: one temporal slice of 4 output frames at each resolution level
+VAE_CONV_LAYERS = [
+    ("full_res_128", 128, 128, 4, 720, 1280),
+    ("half_res_256", 256, 256, 4, 360, 640),
+    ("quarter_res_512", 512, 512, 1, 180, 320),
+]
+
+
+def vae_conv3d(reps=5, cpu_threads=16, cpu=True):
+    """DecomposedConv3D at the VAE decoder's layer shapes.  Each forward
+    continues a 2-frame temporal memory (the decoder's slices after the first,
+    seedvr2_vae.cpp:424-447), so every output frame is a full 3x3x3 window:
+    algorithmic FLOPs 2 * out_pixels * cout * cin * 27.  Timed end to end
+    (staging + implicit GEMM) with HIP events over `reps` forwards, bf16
+    device blobs, and fp32 blobs for the full-resolution layer.  The CPU
+    baseline is the oracle's fp64-accumulating restatement (liboracle_fast)
+    on a band of 64 output rows of one output frame of the full-resolution
+    layer, scaled to the whole slice."""
+    import numpy as np
+    import torch
+    from seedvr2_ncnn_amd import capi
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(7)
+    out = {}
+    for name, cin, cout, frames, h, w in VAE_CONV_LAYERS:
+        cfg = capi.conv3d_config(num_output=cout, num_input=cin, kernel_t=3, kernel_h=3,
+                                 kernel_w=3, pad_h=1, pad_w=1, head_frames=2, bias_term=1)
+        wts = torch.randn(3, cout, cin, 3, 3, generator=gen, device=dev) / (cin * 27) ** 0.5
+        conv = capi.Conv3d(cfg, wts, torch.randn(cout, generator=gen, device=dev) * 0.1)
+        flops = 2.0 * frames * h * w * cout * cin * 27
+        dtypes = (torch.bfloat16, torch.float32) if name == "full_res_128" else (torch.bfloat16,)
+        for dt in dtypes:
+            x = torch.randn(cin, frames * h * w, generator=gen, device=dev).to(dt)
+            conv.forward(x, frames, h, w, keep_memory=True)
+            for _ in range(2):
+                conv.forward(x, frames, h, w, use_memory=True, keep_memory=True)
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(reps):
+                y, _ = conv.forward(x, frames, h, w, use_memory=True, keep_memory=True)
+            b.record()
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / reps
+            key = f"{name}_{'bf16' if dt == torch.bfloat16 else 'fp32'}"
+            out[key] = {"shape": f"{cin}->{cout} 3x3x3, {frames} frames {h}x{w} + 2 cached",
+                        "ms": round(ms, 3), "tflop": round(flops / 1e12, 3),
+                        "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+                        "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+            del x, y
+        del conv, wts
+        torch.cuda.empty_cache()
+    if cpu:
+        import oracle
+        rows = 64
+        g = np.random.default_rng(1)
+        cfg_o = oracle.conv3d_config(num_output=128, num_input=128, kernel_t=3, kernel_h=3,
+                                     kernel_w=3, pad_h=1, pad_w=0, head_frames=2, bias_term=1)
+        # 1 output frame of a band of `rows` output rows (rows + 2 input rows,
+        # the left/right padding applied by hand), 3 input frames via the memory
+        x = g.standard_normal((128, 1, rows + 2, 1282), dtype=np.float32)
+        x[:, :, :, 0] = x[:, :, :, -1] = 0
+        mem = g.standard_normal((128, 2, rows + 2, 1282), dtype=np.float32)
+        wt = (g.standard_normal((3, 128, 128, 3, 3), dtype=np.float32) / 60).astype(np.float32)
+        cfg_o.pad_h = 0
+        t0 = time.perf_counter()
+        code, _, _ = oracle.decomposed_conv3d(cfg_o, x, wt, np.zeros(128, np.float32), memory=mem,
+                                              threads=cpu_threads, fast=True)
+        dt = time.perf_counter() - t0
+        band = 2.0 * rows * 1280 * 128 * 128 * 27
+        full = 2.0 * 4 * 720 * 1280 * 128 * 128 * 27
+        out["cpu_baseline_full_res_128"] = {
+            "value": round(band / dt / 1e12, 6), "unit": "TFLOP/s", "cores": cpu_threads,
+            "kind": "port", "ms_per_slice": round(dt * full / band * 1e3, 1),
+            "sample": f"oracle (liboracle_fast) on 1 output frame x {rows} rows x 1280 of the "
+                      f"128->128 layer ({band / 1e9:.1f} GFLOP, {dt:.1f} s), scaled to 4x720x1280"}
+    return out
+
+
 STACK_HIDDEN, STACK_HEADS, STACK_MLP, STACK_BLOCKS, STACK_TEXT_WIDTH = 3072, 24, 12288, 32, 5120
 
 
@@ -305,6 +387,10 @@ def main():
     ap.add_argument("--stack-steps", type=int, default=3)
     ap.add_argument("--no-tail", action="store_true",
                     help="skip the frontend/tail kernels at the 720p latent")
+    ap.add_argument("--no-vae", action="store_true",
+                    help="skip the VAE DecomposedConv3D layers")
+    ap.add_argument("--vae-only", action="store_true",
+                    help="time only the VAE DecomposedConv3D layers (one JSON object)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device copy (a plain copy kernel of known size) so "
                          "that PMC byte counters can be calibrated in the same profiler run")
@@ -320,6 +406,11 @@ def main():
     assert torch.cuda.is_available() and capi.device_count() >= 1, "needs a gfx950 GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.vae_only:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        print(json.dumps({"vae_conv3d": vae_conv3d(cpu_threads=threads,
+                                                   cpu=not args.no_cpu_baseline)}), flush=True)
+        return
     gen = torch.Generator(device=dev).manual_seed(20240601)
     bf = torch.bfloat16
     lv = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2]
@@ -488,6 +579,9 @@ def main():
         line["stack_7b"] = stack_7b(args.stack_steps, 1)
     if not args.no_tail:
         line["sampler_tail"] = sampler_tail()
+    if not args.no_vae:
+        line["vae_conv3d"] = vae_conv3d(cpu_threads=args.cpu_threads or min(16, os.cpu_count() or 1),
+                                        cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         line["cpu_baseline"] = cpu_baseline(threads)

@@ -332,7 +332,7 @@ def _planar(a, pad):
 
 
 def decomposed_conv3d(cfg, x, weights, bias=None, memory=None, want_memory=False, threads=8,
-                      cstep_pad=0):
+                      cstep_pad=0, fast=False):
     """decomposed_conv3d.cpp:605-755.  x [Cin, F, H, W]; weights [kt, Cout,
     Cin, kh, kw]; memory [Cin, M, H, W] or None.  Returns (out_t or -1,
     out [Cout, To, Ho, Wo], next_memory [Cin, kt - st, H, W] or None)."""
@@ -360,7 +360,7 @@ def decomposed_conv3d(cfg, x, weights, bias=None, memory=None, want_memory=False
     if want_memory and cache > 0:
         nxt = np.zeros((cin, cache * h * w), np.float32)
         pn, ncs = nxt.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), nxt.shape[1]
-    code = lib().orc_decomposed_conv3d(ctypes.byref(cfg), pxin, frames, h, w, xin.shape[1], pm,
+    code = lib(fast).orc_decomposed_conv3d(ctypes.byref(cfg), pxin, frames, h, w, xin.shape[1], pm,
                                        mframes, mcs, pw_, pb,
                                        out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
                                        out.shape[1], pn, ncs, threads)
