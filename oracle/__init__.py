@@ -93,6 +93,8 @@ def lib(fast: bool = False) -> ctypes.CDLL:
         L.orc_apply_cfg.argtypes = [P(cf), P(cf), cl, cf, cf, P(cf)]
         L.orc_euler_step.argtypes = [P(cf), cl, P(cf), cl, cf]
         L.orc_video_tokens.argtypes = [P(cf), P(cf), cl, cl, P(cf)]
+        L.orc_mha.argtypes = [P(cf), ci, ci, ci, ci, cf, P(cf), P(cf), P(cf), P(cf), P(cf), P(cf),
+                              P(cf), P(cf), P(ci), ci, P(cf), ci]
         L.orc_decomposed_conv3d.argtypes = [P(Conv3dConfig), P(cf), ci, ci, ci, cl, P(cf), ci, cl,
                                             P(cf), P(cf), P(cf), cl, P(cf), cl, ci]
         _LIBS[name] = L
@@ -370,3 +372,23 @@ def decomposed_conv3d(cfg, x, weights, bias=None, memory=None, want_memory=False
     if nxt is not None:
         nxt = nxt.reshape(cin, cache, h, w)
     return code, out, nxt
+
+
+def mha(x, heads, wq, bq, wk, bk, wv, bv, wo, bo, scale=None, rows=None, threads=8, fast=False):
+    """vae_chunked_mha.cpp:223-235 (ncnn MultiHeadAttention, self attention).
+    x [seq][qdim]; wq/wk/wv [embed][qdim]; wo [qdim][embed].  Returns
+    [seq or len(rows)][qdim]."""
+    xs, px = _f32(x)
+    seq, qdim = xs.shape
+    embed = np.asarray(wq).shape[0]
+    if scale is None:
+        scale = 1.0 / float(np.sqrt(np.float32(embed // heads)))
+    arrs = [_f32(a) for a in (wq, bq, wk, bk, wv, bv, wo, bo)]
+    pr, n = None, seq
+    if rows is not None:
+        r, pr = _i32(np.asarray(rows))
+        n = r.shape[0]
+    out = np.zeros((n, qdim), np.float32)
+    lib(fast).orc_mha(px, seq, qdim, embed, heads, float(scale), *[a[1] for a in arrs], pr, n,
+                      out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), threads)
+    return out

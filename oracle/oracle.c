@@ -733,3 +733,72 @@ int orc_decomposed_conv3d(const orc_conv3d* cfg, const float* input, int frames,
     }
     return out_t;
 }
+
+/* vae_chunked_mha.cpp:223-235 with ncnn MultiHeadAttention's semantics */
+void orc_mha(const float* x, int seq, int qdim, int embed, int heads, float scale,
+             const float* wq, const float* bq, const float* wk, const float* bk, const float* wv,
+             const float* bv, const float* wo, const float* bo, const int* rows, int count,
+             float* out, int num_threads)
+{
+    const int d = embed / heads;
+    double* k = (double*)malloc(sizeof(double) * (size_t)seq * embed);
+    double* v = (double*)malloc(sizeof(double) * (size_t)seq * embed);
+#pragma omp parallel for schedule(static) num_threads(num_threads > 0 ? num_threads : 1)
+    for (int t = 0; t < seq; t++)
+        for (int e = 0; e < embed; e++) {
+            double sk = bk[e], sv = bv[e];
+            for (int c = 0; c < qdim; c++) {
+                sk += (double)wk[(size_t)e * qdim + c] * x[(size_t)t * qdim + c];
+                sv += (double)wv[(size_t)e * qdim + c] * x[(size_t)t * qdim + c];
+            }
+            k[(size_t)t * embed + e] = sk;
+            v[(size_t)t * embed + e] = sv;
+        }
+    const int n = rows ? count : seq;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(num_threads > 0 ? num_threads : 1)
+    for (int i = 0; i < n; i++) {
+        const int r = rows ? rows[i] : i;
+        double* q = (double*)malloc(sizeof(double) * embed);
+        double* o = (double*)malloc(sizeof(double) * embed);
+        double* p = (double*)malloc(sizeof(double) * seq);
+        for (int e = 0; e < embed; e++) {
+            double s = bq[e];
+            for (int c = 0; c < qdim; c++)
+                s += (double)wq[(size_t)e * qdim + c] * x[(size_t)r * qdim + c];
+            q[e] = s;
+        }
+        for (int h = 0; h < heads; h++) {
+            double mx = -INFINITY;
+            for (int t = 0; t < seq; t++) {
+                double s = 0.0;
+                for (int j = 0; j < d; j++)
+                    s += q[h * d + j] * k[(size_t)t * embed + h * d + j];
+                p[t] = s * scale;
+                if (p[t] > mx)
+                    mx = p[t];
+            }
+            double sum = 0.0;
+            for (int t = 0; t < seq; t++) {
+                p[t] = exp(p[t] - mx);
+                sum += p[t];
+            }
+            for (int j = 0; j < d; j++) {
+                double acc = 0.0;
+                for (int t = 0; t < seq; t++)
+                    acc += p[t] * v[(size_t)t * embed + h * d + j];
+                o[h * d + j] = acc / sum;
+            }
+        }
+        for (int c = 0; c < qdim; c++) {
+            double s = bo[c];
+            for (int e = 0; e < embed; e++)
+                s += (double)wo[(size_t)c * embed + e] * o[e];
+            out[(size_t)i * qdim + c] = (float)s;
+        }
+        free(q);
+        free(o);
+        free(p);
+    }
+    free(k);
+    free(v);
+}

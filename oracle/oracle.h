@@ -33,6 +33,9 @@
  *                     unrescaled result.
  *   orc_euler_step    numpy closed form with a strided channel layout.
  *   orc_video_tokens  numpy transpose of the channel planes.
+ *   orc_mha           torch float64 multi_head_attention_forward (self
+ *                     attention, default and explicit scale); a subset of
+ *                     query rows equals the same rows of the full run.
  *   orc_decomposed_conv3d  torch float64 conv3d over the temporally padded
  *                     input (frame 0 replicated head_frames times); a run
  *                     split into slices chained through the memory equals
@@ -165,6 +168,19 @@ void orc_euler_step(float* latent, long channel_stride, const float* prediction,
  * channel 0..15 at t, then 1.  Channels are channel_stride floats apart. */
 void orc_video_tokens(const float* latent, const float* condition, long channel_stride,
                       long tokens, float* destination);
+
+/* VAEChunkedMHA::forward (vae_chunked_mha.cpp:223-235): ncnn
+ * MultiHeadAttention over one blob (self attention).  x [seq][qdim];
+ * wq, wk, wv [embed][qdim] and bq, bk, bv [embed]; wo [qdim][embed], bo
+ * [qdim] (the load_model order, :138-152).  Per head h of d = embed / heads:
+ * softmax(scale q_h k_h^T) v_h, heads concatenated, then the output
+ * projection.  Evaluated in fp64, rounded once to fp32.  rows (or NULL):
+ * only the query rows listed (count of them) are computed; out then holds
+ * those rows in that order. */
+void orc_mha(const float* x, int seq, int qdim, int embed, int heads, float scale,
+             const float* wq, const float* bq, const float* wk, const float* bk, const float* wv,
+             const float* bv, const float* wo, const float* bo, const int* rows, int count,
+             float* out, int num_threads);
 
 /* The 16 configuration values of DecomposedConv3D, in the order of its
  * config blob (decomposed_conv3d.cpp:422-441). */
