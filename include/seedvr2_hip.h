@@ -319,6 +319,43 @@ S2_API int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_
                              void* next_memory, void* workspace, size_t workspace_bytes,
                              s2_stream_t stream);
 
+/* ---- VAEChunkedMHA (VAE) -------------------------------------------------- */
+/* ncnn MultiHeadAttention over one blob (self attention), the CPU forward of
+ * VAEChunkedMHA (src/seedvr2/vae_chunked_mha.cpp:223-235; the Vulkan forward
+ * :247-281 computes the same in query chunks of param 20).  Per head h of
+ * d = embed_dim / num_heads: softmax(scale q_h k_h^T) v_h with q = x Wq^T +
+ * bq (likewise k, v), heads concatenated, then out = o Wo^T + bo.  The
+ * projections and both attention products run on the matrix cores in bf16
+ * with fp32 accumulation; the scores are kept in fp32 until the softmax. */
+
+/* ParamDict ids 0, 1 and 6 of the reference load_param (:116-129); qdim =
+ * weight_data_size / embed_dim (the input width).  kdim and vdim equal qdim
+ * in the layer's self attention. */
+typedef struct s2_mha_config {
+    int embed_dim;
+    int num_heads;
+    int qdim;
+    float scale;
+} s2_mha_config;
+
+/* Device weights in the kernels' form (bf16 matrices, fp32 biases, the scale
+ * folded into the query projection).  The inputs are the reference's
+ * load_model blobs (:131-152) as device fp32: wq, wk, wv [embed_dim][qdim],
+ * bq, bk, bv [embed_dim], wo [qdim][embed_dim], bo [qdim]. */
+S2_API int s2_mha_weight_bytes(const s2_mha_config* config, size_t* bytes);
+S2_API int s2_mha_prepare_weights(const s2_mha_config* config, const float* wq, const float* bq,
+                                  const float* wk, const float* bk, const float* wv,
+                                  const float* bv, const float* wo, const float* bo,
+                                  void* prepared, s2_stream_t stream);
+/* Workspace of a forward over seq tokens: about seq^2 * 6 bytes (the fp32
+ * scores and bf16 probabilities of one head) plus the projections. */
+S2_API int s2_mha_workspace_bytes(const s2_mha_config* config, int seq, size_t* bytes);
+/* x: device [seq][qdim] in in_dtype; out: device [seq][qdim] in out_dtype;
+ * 16-byte aligned rows (qdim a multiple of 8); workspace 256-byte aligned. */
+S2_API int s2_mha_forward(const s2_mha_config* config, const void* prepared, const void* x,
+                          s2_dtype in_dtype, int seq, void* out, s2_dtype out_dtype,
+                          void* workspace, size_t workspace_bytes, s2_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

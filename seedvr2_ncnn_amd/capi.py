@@ -36,6 +36,7 @@ EXPORTS = (
     "s2_unpatchify_prediction", "s2_apply_cfg", "s2_euler_step", "s2_denoise_update",
     "s2_conv3d_output_shape", "s2_conv3d_packed_weight_bytes", "s2_conv3d_pack_weights",
     "s2_conv3d_memory_bytes", "s2_conv3d_workspace_bytes", "s2_conv3d_forward",
+    "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
 )
 
 
@@ -79,6 +80,12 @@ def conv3d_config(**kw) -> Conv3dConfig:
     for name, _ in Conv3dConfig._fields_:
         setattr(c, name, int(values[name]))
     return c
+
+
+class MhaConfig(ctypes.Structure):
+    """s2_mha_config: VAEChunkedMHA's embed_dim, num_heads, qdim and scale."""
+    _fields_ = [("embed_dim", ctypes.c_int), ("num_heads", ctypes.c_int), ("qdim", ctypes.c_int),
+                ("scale", ctypes.c_float)]
 
 
 class PlanInfo(ctypes.Structure):
@@ -136,6 +143,11 @@ def lib() -> ctypes.CDLL:
         L.s2_conv3d_pack_weights.argtypes = [C3, vp, vp, vp]
         L.s2_conv3d_memory_bytes.argtypes = [C3, ci, ci, P(sz), P(ci)]
         L.s2_conv3d_workspace_bytes.argtypes = [C3, ci, ci, ci, ci, P(sz)]
+        M3 = P(MhaConfig)
+        L.s2_mha_weight_bytes.argtypes = [M3, P(sz)]
+        L.s2_mha_prepare_weights.argtypes = [M3, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
+        L.s2_mha_workspace_bytes.argtypes = [M3, ci, P(sz)]
+        L.s2_mha_forward.argtypes = [M3, vp, vp, ci, ci, vp, ci, vp, sz, vp]
         L.s2_conv3d_forward.argtypes = [C3, vp, vp, vp, ci, ci, ci, ci, cl, vp, ci, vp, ci, cl, vp,
                                         vp, sz, vp]
         _LIB = L
@@ -499,3 +511,39 @@ class Conv3d:
             self.memory = nxt
             self.memory_frames = cfg.kernel_t - cfg.stride_t if nxt is not None else 0
         return out, (to, ho, wo)
+
+
+# ---- VAEChunkedMHA -------------------------------------------------------------
+
+class Mha:
+    """Device weights of one VAEChunkedMHA (s2_mha_*).  Weights are device
+    fp32 tensors in the reference load_model order."""
+
+    def __init__(self, heads, wq, bq, wk, bk, wv, bv, wo, bo, scale=None, stream=None):
+        import math
+        import torch
+        embed, qdim = wq.shape
+        self.config = MhaConfig(embed, heads, qdim,
+                                scale if scale is not None else 1.0 / math.sqrt(embed // heads))
+        n = ctypes.c_size_t()
+        check(lib().s2_mha_weight_bytes(ctypes.byref(self.config), ctypes.byref(n)),
+              "s2_mha_weight_bytes")
+        self.prepared = torch.empty(n.value, dtype=torch.uint8, device=wq.device)
+        ws = [t.contiguous() for t in (wq, bq, wk, bk, wv, bv, wo, bo)]
+        check(lib().s2_mha_prepare_weights(ctypes.byref(self.config), *[_ptr(t) for t in ws],
+                                           _ptr(self.prepared), _stream(stream)),
+              "s2_mha_prepare_weights")
+
+    def forward(self, x, out_dtype=None, stream=None):
+        """x: device [seq, qdim]; returns [seq, qdim]."""
+        import torch
+        seq = x.shape[0]
+        n = ctypes.c_size_t()
+        check(lib().s2_mha_workspace_bytes(ctypes.byref(self.config), seq, ctypes.byref(n)),
+              "s2_mha_workspace_bytes")
+        ws = torch.empty(n.value, dtype=torch.uint8, device=x.device)
+        out = torch.empty((seq, self.config.qdim), dtype=out_dtype or x.dtype, device=x.device)
+        check(lib().s2_mha_forward(ctypes.byref(self.config), _ptr(self.prepared), _ptr(x),
+                                   _dtype_code(x), seq, _ptr(out), _dtype_code(out), _ptr(ws),
+                                   ws.numel(), _stream(stream)), "s2_mha_forward")
+        return out

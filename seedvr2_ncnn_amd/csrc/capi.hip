@@ -9,6 +9,7 @@
 #include "awa_kernels.h"
 #include "awa_plan.h"
 #include "conv3d_kernels.h"
+#include "mha_kernels.h"
 #include "pipeline_kernels.h"
 #include "seedvr2_hip.h"
 
@@ -61,6 +62,56 @@ bool dtype_ok(s2_dtype t) { return t == S2_DTYPE_F32 || t == S2_DTYPE_BF16 || t 
 size_t dtype_bytes(s2_dtype t) { return t == S2_DTYPE_F32 ? 4 : 2; }
 
 bool aligned(const void* p, size_t a) { return ((uintptr_t)p) % a == 0; }
+
+// VAEChunkedMHA configuration checks of the reference load_param
+// (vae_chunked_mha.cpp:124-128); the GEMMs need 16-byte operand rows.
+bool mha_config_ok(const s2_mha_config* c) {
+    return c && c->embed_dim > 0 && c->num_heads > 0 && c->embed_dim % c->num_heads == 0 &&
+           c->qdim > 0 && c->qdim % 8 == 0 && (c->embed_dim / c->num_heads) % 8 == 0;
+}
+
+// Byte layout of the prepared MHA weights: bf16 wq (scaled), wk, wv, wo,
+// then fp32 bq (scaled), bk, bv, bo, each 256-byte aligned.
+struct MhaWeights {
+    size_t wq, wk, wv, wo, bq, bk, bv, bo, total;
+};
+
+MhaWeights mha_layout(const s2_mha_config* c) {
+    MhaWeights m;
+    const size_t mat = align256((size_t)c->embed_dim * c->qdim * 2);
+    m.wq = 0;
+    m.wk = m.wq + mat;
+    m.wv = m.wk + mat;
+    m.wo = m.wv + mat;
+    m.bq = m.wo + mat;
+    m.bk = m.bq + align256((size_t)c->embed_dim * 4);
+    m.bv = m.bk + align256((size_t)c->embed_dim * 4);
+    m.bo = m.bv + align256((size_t)c->embed_dim * 4);
+    m.total = m.bo + align256((size_t)c->qdim * 4);
+    return m;
+}
+
+// Workspace of a forward: staged x and the per-head buffers.
+struct MhaWork {
+    int lp;   // seq rounded up to 64: the k extent of the P V product
+    size_t xp, q, k, vt, s, p, oh, o, total;
+};
+
+MhaWork mha_work(const s2_mha_config* c, int seq) {
+    MhaWork w;
+    const int d = c->embed_dim / c->num_heads;
+    w.lp = (seq + 63) / 64 * 64;
+    w.xp = 0;
+    w.q = w.xp + align256((size_t)w.lp * c->qdim * 2);
+    w.k = w.q + align256((size_t)w.lp * d * 2);
+    w.vt = w.k + align256((size_t)w.lp * d * 2);
+    w.s = w.vt + align256((size_t)d * w.lp * 2);
+    w.p = w.s + align256((size_t)seq * seq * 4);
+    w.oh = w.p + align256((size_t)seq * w.lp * 2);
+    w.o = w.oh + align256((size_t)seq * d * 2);
+    w.total = w.o + (c->num_heads > 1 ? align256((size_t)seq * c->embed_dim * 2) : 0);
+    return w;
+}
 
 // DecomposedConv3D configuration checks of the reference load_model
 // (decomposed_conv3d.cpp:442-446), plus groups == 1 and a spatial window of
@@ -743,6 +794,104 @@ int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_weights
                 S2_HIP(hipMemcpyAsync(dst, src, frame_bytes, hipMemcpyDeviceToDevice, st));
         }
     }
+    return S2_OK;
+}
+
+/* ---- VAEChunkedMHA ------------------------------------------------------- */
+
+int s2_mha_weight_bytes(const s2_mha_config* config, size_t* bytes) {
+    if (!bytes || !mha_config_ok(config)) return fail(S2_ERR_INVALID, "invalid MHA configuration");
+    *bytes = mha_layout(config).total;
+    return S2_OK;
+}
+
+int s2_mha_prepare_weights(const s2_mha_config* config, const float* wq, const float* bq,
+                           const float* wk, const float* bk, const float* wv, const float* bv,
+                           const float* wo, const float* bo, void* prepared,
+                           s2_stream_t stream) {
+    if (!mha_config_ok(config)) return fail(S2_ERR_INVALID, "invalid MHA configuration");
+    if (!wq || !bq || !wk || !bk || !wv || !bv || !wo || !bo || !prepared)
+        return fail(S2_ERR_INVALID, "null pointer");
+    if (!aligned(prepared, 256)) return fail(S2_ERR_INVALID, "prepared weights alignment");
+    const MhaWeights m = mha_layout(config);
+    uint8_t* base = (uint8_t*)prepared;
+    hipStream_t st = (hipStream_t)stream;
+    const long mat = (long)config->embed_dim * config->qdim;
+    S2_HIP(s2::launch_mha_weight(wq, mat, config->scale, (uint16_t*)(base + m.wq), st));
+    S2_HIP(s2::launch_mha_weight(wk, mat, 1.f, (uint16_t*)(base + m.wk), st));
+    S2_HIP(s2::launch_mha_weight(wv, mat, 1.f, (uint16_t*)(base + m.wv), st));
+    S2_HIP(s2::launch_mha_weight(wo, mat, 1.f, (uint16_t*)(base + m.wo), st));
+    S2_HIP(s2::launch_mha_bias(bq, config->embed_dim, config->scale, (float*)(base + m.bq), st));
+    S2_HIP(s2::launch_mha_bias(bk, config->embed_dim, 1.f, (float*)(base + m.bk), st));
+    S2_HIP(s2::launch_mha_bias(bv, config->embed_dim, 1.f, (float*)(base + m.bv), st));
+    S2_HIP(s2::launch_mha_bias(bo, config->qdim, 1.f, (float*)(base + m.bo), st));
+    return S2_OK;
+}
+
+int s2_mha_workspace_bytes(const s2_mha_config* config, int seq, size_t* bytes) {
+    if (!bytes || !mha_config_ok(config) || seq <= 0)
+        return fail(S2_ERR_INVALID, "invalid MHA configuration or sequence");
+    *bytes = mha_work(config, seq).total;
+    return S2_OK;
+}
+
+int s2_mha_forward(const s2_mha_config* config, const void* prepared, const void* x,
+                   s2_dtype in_dtype, int seq, void* out, s2_dtype out_dtype, void* workspace,
+                   size_t workspace_bytes, s2_stream_t stream) {
+    if (!mha_config_ok(config) || seq <= 0)
+        return fail(S2_ERR_INVALID, "invalid MHA configuration or sequence");
+    if (!prepared || !x || !out || !workspace) return fail(S2_ERR_INVALID, "null pointer");
+    if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (!aligned(x, 16) || !aligned(out, 16) || !aligned(workspace, 256) || !aligned(prepared, 256))
+        return fail(S2_ERR_INVALID, "operand alignment");
+    const MhaWork w = mha_work(config, seq);
+    if (workspace_bytes < w.total) return fail(S2_ERR_INVALID, "workspace too small");
+    const MhaWeights m = mha_layout(config);
+    const int E = config->embed_dim, H = config->num_heads, D = E / H, Q = config->qdim;
+    const uint8_t* wb = (const uint8_t*)prepared;
+    uint8_t* ws = (uint8_t*)workspace;
+    const uint16_t* wq = (const uint16_t*)(wb + m.wq);
+    const uint16_t* wk = (const uint16_t*)(wb + m.wk);
+    const uint16_t* wv = (const uint16_t*)(wb + m.wv);
+    const uint16_t* wo = (const uint16_t*)(wb + m.wo);
+    const float* bq = (const float*)(wb + m.bq);
+    const float* bk = (const float*)(wb + m.bk);
+    const float* bv = (const float*)(wb + m.bv);
+    const float* bo = (const float*)(wb + m.bo);
+    uint16_t* xp = (uint16_t*)(ws + w.xp);
+    uint16_t* q = (uint16_t*)(ws + w.q);
+    uint16_t* k = (uint16_t*)(ws + w.k);
+    uint16_t* vt = (uint16_t*)(ws + w.vt);
+    float* sc = (float*)(ws + w.s);
+    uint16_t* p = (uint16_t*)(ws + w.p);
+    uint16_t* oh = (uint16_t*)(ws + w.oh);
+    uint16_t* o = H > 1 ? (uint16_t*)(ws + w.o) : oh;
+    hipStream_t st = (hipStream_t)stream;
+    constexpr int kBF = (int)S2_DTYPE_BF16, kF32 = (int)S2_DTYPE_F32;
+    // x as bf16 rows, padded with zero rows to the 64-multiple extent of P V
+    S2_HIP(s2::launch_mha_stage(x, (int)in_dtype, seq, w.lp, Q, xp, st));
+    for (int h = 0; h < H; ++h) {
+        const long wo_h = (long)h * D * Q;
+        // q_h = x Wq_h^T + bq_h (scale folded in), k_h likewise: [lp][D]
+        S2_HIP(s2::launch_shared_linear(xp, w.lp, nullptr, 0, kBF, wq + wo_h, bq + h * D, D, Q,
+                                        S2_ACT_NONE, q, nullptr, kBF, st));
+        S2_HIP(s2::launch_shared_linear(xp, w.lp, nullptr, 0, kBF, wk + wo_h, bk + h * D, D, Q,
+                                        S2_ACT_NONE, k, nullptr, kBF, st));
+        // v_h^T without its bias = Wv_h x^T: [D][lp], zero columns past seq
+        S2_HIP(s2::launch_shared_linear(wv + wo_h, D, nullptr, 0, kBF, xp, nullptr, w.lp, Q,
+                                        S2_ACT_NONE, vt, nullptr, kBF, st));
+        // S = q_h k_h^T (already scaled): [seq][seq] fp32
+        S2_HIP(s2::launch_shared_linear(q, seq, nullptr, 0, kBF, k, nullptr, seq, D, S2_ACT_NONE,
+                                        sc, nullptr, kF32, st));
+        S2_HIP(s2::launch_mha_softmax(sc, seq, seq, seq, w.lp, p, st));
+        // o_h = P v_h + bv_h (the rows of P sum to one): [seq][D]
+        S2_HIP(s2::launch_shared_linear(p, seq, nullptr, 0, kBF, vt, bv + h * D, D, w.lp,
+                                        S2_ACT_NONE, oh, nullptr, kBF, st));
+        if (H > 1) S2_HIP(s2::launch_mha_interleave(oh, seq, D, E, h, o, st));
+    }
+    // out = o Wo^T + bo: [seq][qdim]
+    S2_HIP(s2::launch_shared_linear(o, seq, nullptr, 0, kBF, wo, bo, Q, E, S2_ACT_NONE, out,
+                                    nullptr, (int)out_dtype, st));
     return S2_OK;
 }
 

@@ -1,0 +1,74 @@
+"""VAEChunkedMHA on the GPU (src/seedvr2/vae_chunked_mha.cpp:223-281: ncnn
+MultiHeadAttention over one blob) against the CPU oracle.
+
+The device runs the projections and both attention products in bf16 with
+fp32 accumulation (scores stay fp32 until the softmax, probabilities are
+rounded to bf16).  The bar is the path's: max-abs <= 2e-2 and cosine >=
+0.9999 against the fp32-input oracle.  Sequences of VAE size are checked on
+a spread of query rows (the oracle computes only those rows)."""
+import numpy as np
+import pytest
+
+import oracle
+from common import assert_close
+from seedvr2_ncnn_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(g, qdim, embed):
+    w = lambda *s: (g.standard_normal(s) / np.sqrt(s[-1])).astype(np.float32)
+    b = lambda n: (0.1 * g.standard_normal(n)).astype(np.float32)
+    return [w(embed, qdim), b(embed), w(embed, qdim), b(embed), w(embed, qdim), b(embed),
+            w(qdim, embed), b(qdim)]
+
+
+def _device(heads, ws, scale=None):
+    import torch
+    return capi.Mha(heads, *[torch.from_numpy(a).cuda() for a in ws], scale=scale)
+
+
+def _run(mha, x, dtype=None, out_dtype=None):
+    import torch
+    t = torch.from_numpy(x).cuda()
+    if dtype is not None:
+        t = t.to(dtype)
+    y = mha.forward(t, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    return y.float().cpu().numpy()
+
+
+@pytest.mark.parametrize("seq,qdim,heads", [(1, 64, 1), (37, 64, 2), (200, 128, 4), (1000, 512, 1),
+                                            (333, 256, 2)])
+def test_mha_matches_oracle(seq, qdim, heads):
+    g = np.random.default_rng(seq + qdim)
+    x = g.standard_normal((seq, qdim)).astype(np.float32)
+    ws = _weights(g, qdim, qdim)
+    got = _run(_device(heads, ws), x)
+    ref = oracle.mha(x, heads, *ws, threads=16)
+    assert_close(got, ref)
+
+
+def test_mha_explicit_scale_and_16bit_blobs():
+    import torch
+    g = np.random.default_rng(2)
+    x = g.standard_normal((300, 128)).astype(np.float32)
+    ws = _weights(g, 128, 128)
+    mha = _device(2, ws, scale=0.3)
+    for dt, odt in ((torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)):
+        xs = torch.from_numpy(x).to(dt).float().numpy()    # the stored values
+        got = _run(mha, xs, dtype=dt, out_dtype=odt)
+        assert_close(got, oracle.mha(xs, 2, *ws, scale=0.3, threads=16))
+
+
+def test_mha_vae_frame_rows():
+    """One 720p latent frame (90 x 160 = 14,400 tokens, 512 channels, one
+    head): 64 query rows spread over the sequence against the oracle."""
+    g = np.random.default_rng(9)
+    seq, qdim = 14400, 512
+    x = g.standard_normal((seq, qdim)).astype(np.float32)
+    ws = _weights(g, qdim, qdim)
+    got = _run(_device(1, ws), x)
+    rows = np.linspace(0, seq - 1, 64).astype(np.int32)
+    ref = oracle.mha(x, 1, *ws, rows=rows, threads=16, fast=True)
+    assert_close(got[rows], ref)
