@@ -130,6 +130,7 @@ def harness():
         L.h_set_vae_memory_state.argtypes = [ci]
         L.h_conv_memory.argtypes = [vp, ci]
         L.h_layer_forward4.argtypes = [vp, P(HBlob4), P(HBlob4)]
+        L.h_layer_forward1.argtypes = [vp, P(HBlob), P(HBlob)]
         _H = L
     return _H
 
@@ -195,6 +196,31 @@ class Layer:
         res = tout.float().cpu().numpy() if device else hout
         assert (bo.w, bo.h, bo.d, bo.c) == (ow, oh, od, oc)
         return 0, res[:, :ow * oh * od].reshape(oc, od, oh, ow)
+
+    def forward_rows(self, x, out_w, device=False, dtype=None):
+        """One-blob forward over a 2-D blob x [h][w] (numpy fp32 values); with
+        device=True a device Mat of the given torch dtype.  Returns (code,
+        numpy [h][out_w] fp32)."""
+        import torch
+        h, w = x.shape
+        es = 4 if dtype in (None, torch.float32) else 2
+        bi, bo = HBlob(), HBlob()
+        bi.dims, bi.w, bi.h, bi.elemsize = 2, w, h, es
+        bo.dims, bo.w, bo.h, bo.elemsize = 2, out_w, h, es
+        if device:
+            tin = torch.from_numpy(np.ascontiguousarray(x, np.float32)).cuda().to(dtype or torch.float32)
+            tout = torch.zeros((h, out_w), dtype=dtype or torch.float32, device="cuda")
+            bi.device = bo.device = 1
+            bi.data, bo.data = tin.data_ptr(), tout.data_ptr()
+        else:
+            xin = np.ascontiguousarray(x, np.float32)
+            hout = np.zeros((h, out_w), np.float32)
+            bi.device = bo.device = 0
+            bi.data, bo.data = xin.ctypes.data, hout.ctypes.data
+        code = harness().h_layer_forward1(self.h, ctypes.byref(bi), ctypes.byref(bo))
+        if code != 0:
+            return code, None
+        return 0, (tout.float().cpu().numpy() if device else hout)
 
     def conv_memory(self, reset):
         return harness().h_conv_memory(self.h, int(bool(reset)))

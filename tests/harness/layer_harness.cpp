@@ -1,5 +1,5 @@
 // Test harness: drives the ncnn-surface layers (AdaptiveWindowAttention,
-// SharedLinear, DecomposedConv3D) the way an ncnn Net does -- creator, load_param from a .param
+// SharedLinear, DecomposedConv3D, VAEChunkedMHA) the way an ncnn Net does -- creator, load_param from a .param
 // field string, load_model from raw weight bytes, create_pipeline, forward --
 // and exposes that to the Python tests through a few extern "C" calls.
 // Test infrastructure only; built into tests/harness/liblayer_harness.so.
@@ -18,6 +18,7 @@
 #include "hip_allocator.h"
 #include "seedvr2_hip.h"
 #include "shared_linear.h"
+#include "vae_chunked_mha.h"
 
 namespace {
 
@@ -58,6 +59,9 @@ int h_layer_create(const char* type, const char* params, const void* model, long
     } else if (strcmp(type, "SharedLinear") == 0) {
         h->layer = seedvr2::shared_linear_layer_creator(0);
         h->destroyer = seedvr2::shared_linear_layer_destroyer;
+    } else if (strcmp(type, "SeedVR2ChunkedMHA") == 0) {
+        h->layer = seedvr2::vae_chunked_mha_layer_creator(0);
+        h->destroyer = seedvr2::vae_chunked_mha_layer_destroyer;
     } else if (strcmp(type, "DecomposedConv3d") == 0) {
         h->layer = seedvr2::decomposed_conv3d_layer_creator(0);
         h->destroyer = seedvr2::decomposed_conv3d_layer_destroyer;
@@ -211,6 +215,31 @@ int h_layer_forward4(void* handle, const h_blob4* in, h_blob4* out) {
     out->d = top.d;
     out->c = top.c;
     out->cstep = (long)top.cstep;
+    out->elemsize = (int)top.elemsize;
+    if (ret == 0) ret = s2_stream_synchronize(0);
+    device_allocator().clear();
+    return ret;
+}
+
+// forward(Mat, Mat) of a one-blob layer over 2-D blobs; the output is copied
+// into out->data (capacity out->w * out->h elements) and its shape reported.
+int h_layer_forward1(void* handle, const h_blob* in, h_blob* out) {
+    Handle* h = static_cast<Handle*>(handle);
+    ncnn::Allocator* alloc = in->device ? &device_allocator() : 0;
+    ncnn::Mat bottom(in->w, in->h, in->data, (size_t)in->elemsize, alloc);
+    ncnn::Mat top;
+    int ret = h->layer->forward(bottom, top, h->opt);
+    if (ret != 0) return ret;
+    const size_t bytes = top.total() * top.elemsize;
+    if (bytes > (size_t)out->w * out->h * out->elemsize) return -3;
+    const bool src_dev = seedvr2::device_allocator_of(top) != 0;
+    if (src_dev && out->device) ret = s2_memcpy_d2d(out->data, top.data, bytes, 0);
+    else if (src_dev) ret = s2_memcpy_d2h(out->data, top.data, bytes, 0);
+    else if (out->device) ret = s2_memcpy_h2d(out->data, top.data, bytes, 0);
+    else memcpy(out->data, top.data, bytes);
+    out->dims = top.dims;
+    out->w = top.w;
+    out->h = top.h;
     out->elemsize = (int)top.elemsize;
     if (ret == 0) ret = s2_stream_synchronize(0);
     device_allocator().clear();

@@ -72,3 +72,63 @@ def test_mha_vae_frame_rows():
     rows = np.linspace(0, seq - 1, 64).astype(np.int32)
     ref = oracle.mha(x, 1, *ws, rows=rows, threads=16, fast=True)
     assert_close(got[rows], ref)
+
+
+# ---- the ncnn-surface layer (vae_chunked_mha.h:12-50) --------------------------
+
+FP16_TAG = np.frombuffer(np.uint32(0x01306B47).tobytes(), np.float32)
+
+
+def _fp16_blob(a):
+    """ncnn's tagged fp16 weight: the tag, then the halves padded to 4 bytes."""
+    h = np.asarray(a, np.float16).ravel()
+    if h.size % 2:
+        h = np.concatenate([h, np.zeros(1, np.float16)])
+    return np.concatenate([FP16_TAG, h.view(np.float32)])
+
+
+def _layer(embed, heads, qdim, ws, scale=None, fp16_out_weight=False):
+    from common import Layer
+    wq, bq, wk, bk, wv, bv, wo, bo = ws
+    params = f"0={embed} 1={heads} 2={embed * qdim} 3={qdim} 4={qdim} 20=64"
+    if scale is not None:
+        params += f" 6={scale}"
+    tag0 = np.zeros(1, np.float32)   # raw fp32 tag of a type-0 blob
+    out_w = _fp16_blob(wo) if fp16_out_weight else np.concatenate([tag0, wo.ravel()])
+    blobs = [tag0, wq, bq, tag0, wk, bk, tag0, wv, bv, out_w, bo]
+    layer = Layer("SeedVR2ChunkedMHA", params, weights=blobs)
+    assert layer.create_code == 0
+    assert layer.create_pipeline() == 0
+    return layer
+
+
+@pytest.mark.parametrize("device", [False, True])
+def test_layer_forward(device):
+    import torch
+    g = np.random.default_rng(12)
+    x = g.standard_normal((500, 128)).astype(np.float32)
+    ws = _weights(g, 128, 128)
+    layer = _layer(128, 2, 128, ws)
+    dt = torch.bfloat16 if device else None
+    xs = torch.from_numpy(x).to(torch.bfloat16).float().numpy() if device else x
+    code, got = layer.forward_rows(xs, 128, device=device, dtype=dt)
+    assert code == 0
+    assert_close(got, oracle.mha(xs, 2, *ws, threads=16))
+
+
+def test_layer_fp16_weights_and_scale():
+    g = np.random.default_rng(13)
+    x = g.standard_normal((64, 64)).astype(np.float32)
+    ws = _weights(g, 64, 64)
+    ws[6] = ws[6].astype(np.float16).astype(np.float32)   # what the fp16 blob stores
+    layer = _layer(64, 1, 64, ws, scale=0.2, fp16_out_weight=True)
+    code, got = layer.forward_rows(x, 64)
+    assert code == 0
+    assert_close(got, oracle.mha(x, 1, *ws, scale=0.2, threads=16))
+
+
+def test_layer_rejects_wrong_width():
+    g = np.random.default_rng(14)
+    ws = _weights(g, 64, 64)
+    layer = _layer(64, 1, 64, ws)
+    assert layer.forward_rows(np.zeros((8, 32), np.float32), 32)[0] == -1
