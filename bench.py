@@ -19,8 +19,8 @@ SeedVR2-7B-shaped stack of 32 blocks (hidden 3072, 24 heads x 128, MLP
 3072 -> 12288 -> 3072, regular windows in even and shifted windows in odd
 blocks, 64 text tokens projected 5120 -> 3072 once) under "stack_7b".  The
 frontend/tail kernels (patchify, unpatchify, CFG, Euler update) at the 720p
-latent are timed under "sampler_tail", and the VAE decoder's DecomposedConv3D
-layers under "vae_conv3d".
+latent are timed under "sampler_tail", the VAE decoder's DecomposedConv3D
+layers under "vae_conv3d" and its VAEChunkedMHA under "vae_mha".
 
 Prints one JSON line.  `--gpus` above 1 is refused: this build measures one GPU.
 """
@@ -287,6 +287,64 @@ def vae_conv3d(reps=5, cpu_threads=16, cpu=True):
     return out
 
 
+def vae_mha(reps=5, cpu_threads=16, cpu=True):
+    """VAEChunkedMHA at one 720p latent frame: 90 x 160 = 14,400 tokens of
+    width 512, one head.  Algorithmic FLOPs: the q, k, v and out
+    projections 4 * 2 * seq * 512^2 plus the two attention products
+    2 * 2 * seq^2 * 512.  Timed end to end with HIP events over `reps`
+    forwards (bf16 device blobs).  The CPU baseline is the oracle (fp64,
+    liboracle_fast): its k/v projections, then 64 query rows, scaled to all
+    rows."""
+    import numpy as np
+    import torch
+    from seedvr2_ncnn_amd import capi
+
+    seq, e = 14400, 512
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(11)
+    w = [torch.randn(e, e, generator=gen, device=dev) / e ** 0.5 for _ in range(4)]
+    b = [torch.randn(e, generator=gen, device=dev) * 0.1 for _ in range(4)]
+    mha = capi.Mha(1, w[0], b[0], w[1], b[1], w[2], b[2], w[3], b[3])
+    x = torch.randn(seq, e, generator=gen, device=dev).to(torch.bfloat16)
+    for _ in range(2):
+        mha.forward(x)
+    torch.cuda.synchronize()
+    a, z = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        y = mha.forward(x)
+    z.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(z) / reps
+    flops = 4 * 2.0 * seq * e * e + 2 * 2.0 * seq * seq * e
+    out = {"shape": f"{seq} tokens x {e}, 1 head (one 90x160 latent frame)", "ms": round(ms, 3),
+           "gflop": round(flops / 1e9, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+           "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    del mha, x, y
+    torch.cuda.empty_cache()
+    if cpu:
+        import oracle
+        g = np.random.default_rng(2)
+        xs = g.standard_normal((seq, e), dtype=np.float32)
+        ws = [g.standard_normal((e, e), dtype=np.float32) / 23 for _ in range(4)]
+        bs = [np.zeros(e, np.float32) for _ in range(4)]
+        args = (ws[0], bs[0], ws[1], bs[1], ws[2], bs[2], ws[3], bs[3])
+        t0 = time.perf_counter()
+        oracle.mha(xs, 1, *args, rows=np.zeros(0, np.int32), threads=cpu_threads, fast=True)
+        t_kv = time.perf_counter() - t0
+        rows = np.linspace(0, seq - 1, 64).astype(np.int32)
+        t0 = time.perf_counter()
+        oracle.mha(xs, 1, *args, rows=rows, threads=cpu_threads, fast=True)
+        t_rows = time.perf_counter() - t0 - t_kv
+        full = t_kv + t_rows * seq / len(rows)
+        out["cpu_baseline"] = {
+            "value": round(flops / full / 1e12, 6), "unit": "TFLOP/s", "cores": cpu_threads,
+            "kind": "port", "ms": round(full * 1e3, 1),
+            "sample": f"oracle (liboracle_fast): k/v projections ({t_kv:.1f} s) and 64 of "
+                      f"{seq} query rows ({t_rows:.1f} s), scaled to all rows"}
+    return out
+
+
 STACK_HIDDEN, STACK_HEADS, STACK_MLP, STACK_BLOCKS, STACK_TEXT_WIDTH = 3072, 24, 12288, 32, 5120
 
 
@@ -388,9 +446,10 @@ def main():
     ap.add_argument("--no-tail", action="store_true",
                     help="skip the frontend/tail kernels at the 720p latent")
     ap.add_argument("--no-vae", action="store_true",
-                    help="skip the VAE DecomposedConv3D layers")
+                    help="skip the VAE DecomposedConv3D and VAEChunkedMHA layers")
     ap.add_argument("--vae-only", action="store_true",
-                    help="time only the VAE DecomposedConv3D layers (one JSON object)")
+                    help="time only the VAE DecomposedConv3D and VAEChunkedMHA layers "
+                         "(one JSON object)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run one 1 GiB device copy (a plain copy kernel of known size) so "
                          "that PMC byte counters can be calibrated in the same profiler run")
@@ -409,7 +468,9 @@ def main():
     if args.vae_only:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         print(json.dumps({"vae_conv3d": vae_conv3d(cpu_threads=threads,
-                                                   cpu=not args.no_cpu_baseline)}), flush=True)
+                                                   cpu=not args.no_cpu_baseline),
+                          "vae_mha": vae_mha(cpu_threads=threads, cpu=not args.no_cpu_baseline)}),
+              flush=True)
         return
     gen = torch.Generator(device=dev).manual_seed(20240601)
     bf = torch.bfloat16
@@ -580,8 +641,9 @@ def main():
     if not args.no_tail:
         line["sampler_tail"] = sampler_tail()
     if not args.no_vae:
-        line["vae_conv3d"] = vae_conv3d(cpu_threads=args.cpu_threads or min(16, os.cpu_count() or 1),
-                                        cpu=not args.no_cpu_baseline)
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        line["vae_conv3d"] = vae_conv3d(cpu_threads=threads, cpu=not args.no_cpu_baseline)
+        line["vae_mha"] = vae_mha(cpu_threads=threads, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         line["cpu_baseline"] = cpu_baseline(threads)

@@ -425,8 +425,49 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             }
             return;
         }
-        // fp32 output (or a ragged n): direct stores, register r of a 32x32
-        // accumulator is row 8(r/4) + 4g + r%4, column l32
+        if (!YK && (n & 3) == 0) {
+            // fp32: the same LDS staging in two halves of 128 rows (1 KB
+            // rows); the waves of row half h (wm == h) fill it, then all
+            // store 16-byte row chunks
+            constexpr int EF = BN * 4 + 16;   // fp32 row pitch (bytes)
+            static_assert(128 * EF <= LDS_BYTES, "fp32 half tile exceeds the LDS");
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                __syncthreads();   // the stage (h = 0) or the previous half is no longer read
+                if (wm == h) {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int cl = wn * 64 + 32 * j + l32;
+                        const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                float v = acc[i][j][r] + bv;
+                                if (ACT == S2_ACT_GELU) v = gelu(v);
+                                const int rl = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                                *(float*)(lds + rl * EF + cl * 4) = v;
+                            }
+                    }
+                }
+                __syncthreads();
+                // 128 rows x 1024 bytes: thread t stores chunk t%64 of rows
+                // t/64 + 8c
+#pragma unroll 4
+                for (int c = 0; c < 16; ++c) {
+                    const int rl = (tid >> 6) + 8 * c;
+                    const int ch = tid & 63;
+                    const int col = col0 + ch * 4;
+                    float* yr = (float*)out_row(h * 128 + rl);
+                    if (yr && col < n)
+                        __builtin_nontemporal_store(*(const u32x4*)(lds + rl * EF + ch * 16),
+                                                    (u32x4*)(yr + col));
+                }
+            }
+            return;
+        }
+        // ragged n: direct stores, register r of a 32x32 accumulator is row
+        // 8(r/4) + 4g + r%4, column l32
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int col = col0 + wn * 64 + 32 * j + l32;

@@ -100,6 +100,66 @@ __global__ __launch_bounds__(256) void mha_softmax_kernel(const float* __restric
                           : (uint16_t)0;
 }
 
+// The same softmax with the row held in registers: thread t owns the float4
+// groups t, t + 256, ... (NV of them, so rows up to NV * 1024 columns).  All
+// loads are issued at once and the row is read from HBM once.  VEC: the row
+// stride and the row start allow 16-byte loads.
+template <int NV, bool VEC>
+__global__ __launch_bounds__(256) void mha_softmax_reg_kernel(const float* __restrict__ s,
+                                                              long ld_s, int cols, int ld_p,
+                                                              uint16_t* __restrict__ p) {
+    constexpr float kLog2e = 1.4426950408889634f;
+    __shared__ float red[4];
+    const float* row = s + (long)blockIdx.x * ld_s;
+    uint16_t* out = p + (long)blockIdx.x * ld_p;
+    const int t = threadIdx.x;
+    float v[NV][4];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (i * 256 + t) * 4;
+        if (VEC && c + 3 < cols) {
+            const float4 f = *reinterpret_cast<const float4*>(row + c);
+            v[i][0] = f.x, v[i][1] = f.y, v[i][2] = f.z, v[i][3] = f.w;
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[i][e] = c + e < cols ? row[c + e] : -INFINITY;
+        }
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = fmaxf(m, v[i][e]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if ((t & 63) == 0) red[t >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();   // red is reused for the sums
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[i][e] = __builtin_amdgcn_exp2f((v[i][e] - m) * kLog2e);   // -inf -> 0
+            sum += v[i][e];
+        }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
+    if ((t & 63) == 0) red[t >> 6] = sum;
+    __syncthreads();
+    const float inv = 1.f / ((red[0] + red[1]) + (red[2] + red[3]));
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        const int c = (i * 256 + t) * 4;
+        if (c >= ld_p) continue;
+        // columns past `cols` hold exp(-inf) = 0; ld_p is a multiple of 4
+        *reinterpret_cast<uint2*>(out + c) =
+            make_uint2(pack2_bf16_rne(v[i][0] * inv, v[i][1] * inv),
+                       pack2_bf16_rne(v[i][2] * inv, v[i][3] * inv));
+    }
+}
+
 // head h's output [rows][d] (bf16) into columns [h*d, (h+1)*d) of O [rows][embed]
 __global__ __launch_bounds__(256) void mha_interleave_kernel(const uint16_t* __restrict__ oh,
                                                              int rows, int d, int embed, int h,
@@ -140,10 +200,31 @@ hipError_t launch_mha_bias(const float* b, int n, float scale, float* out, hipSt
     return hipGetLastError();
 }
 
+template <int NV>
+static void softmax_reg(const float* s, long ld_s, int rows, int cols, int ld_p, uint16_t* p,
+                        hipStream_t stream) {
+    if (ld_s % 4 == 0 && ((uintptr_t)s % 16) == 0)
+        mha_softmax_reg_kernel<NV, true><<<(unsigned)rows, 256, 0, stream>>>(s, ld_s, cols, ld_p, p);
+    else
+        mha_softmax_reg_kernel<NV, false><<<(unsigned)rows, 256, 0, stream>>>(s, ld_s, cols, ld_p, p);
+}
+
 hipError_t launch_mha_softmax(const float* s, long ld_s, int rows, int cols, int ld_p,
                               uint16_t* p, hipStream_t stream) {
     if (rows <= 0) return hipSuccess;
-    mha_softmax_kernel<<<(unsigned)rows, 256, 0, stream>>>(s, ld_s, cols, ld_p, p);
+    // rows of up to 16,384 columns live in registers (up to 64 floats per
+    // thread); longer rows take the streaming kernel
+    const int groups = (ld_p + 1023) / 1024;   // float4 groups per thread
+    if (ld_p % 4 != 0 || groups > 16)
+        mha_softmax_kernel<<<(unsigned)rows, 256, 0, stream>>>(s, ld_s, cols, ld_p, p);
+    else if (groups <= 2)
+        softmax_reg<2>(s, ld_s, rows, cols, ld_p, p, stream);
+    else if (groups <= 4)
+        softmax_reg<4>(s, ld_s, rows, cols, ld_p, p, stream);
+    else if (groups <= 8)
+        softmax_reg<8>(s, ld_s, rows, cols, ld_p, p, stream);
+    else
+        softmax_reg<16>(s, ld_s, rows, cols, ld_p, p, stream);
     return hipGetLastError();
 }
 
