@@ -319,6 +319,31 @@ S2_API int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_
                              void* next_memory, void* workspace, size_t workspace_bytes,
                              s2_stream_t stream);
 
+/* s2_conv3d_forward over the input padded with pad_right zero columns and
+ * pad_bottom zero rows: VAEDownsample3D's padding (vae_downsample3d.cpp:145-172)
+ * without materialising it.  The output extent is s2_conv3d_output_shape of
+ * (height + pad_bottom, width + pad_right); the memory and the workspace are
+ * those of the unpadded frames. */
+S2_API int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_weights,
+                                    const float* bias, const void* input, s2_dtype in_dtype,
+                                    int frames, int height, int width, long in_cstep,
+                                    int pad_right, int pad_bottom, const void* memory,
+                                    int memory_frames, void* output, s2_dtype out_dtype,
+                                    long out_cstep, void* next_memory, void* workspace,
+                                    size_t workspace_bytes, s2_stream_t stream);
+
+/* VAEUpsample3D's depth-to-space shuffle (vae_upsample3d.cpp:270-318): packed
+ * [channels * tr * sr * sr][frames][height][width] (channel stride
+ * packed_cstep) -> output [channels][frames * tr - remove_head][height * sr]
+ * [width * sr] (channel stride out_cstep), both in dtype.  Packed channel
+ * ((yo * sr + xo) * tr + z) * channels + c of frame f goes to channel c, time
+ * f * tr + z (one less after the removed time 1 when remove_head), pixel
+ * (y * sr + yo, x * sr + xo). */
+S2_API int s2_vae_pixel_shuffle(const void* packed, s2_dtype dtype, int channels, int frames,
+                                int height, int width, long packed_cstep, int temporal_ratio,
+                                int spatial_ratio, int remove_head, void* output,
+                                long out_cstep, s2_stream_t stream);
+
 /* ---- VAEChunkedMHA (VAE) -------------------------------------------------- */
 /* ncnn MultiHeadAttention over one blob (self attention), the CPU forward of
  * VAEChunkedMHA (src/seedvr2/vae_chunked_mha.cpp:223-235; the Vulkan forward

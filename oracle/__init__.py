@@ -95,6 +95,7 @@ def lib(fast: bool = False) -> ctypes.CDLL:
         L.orc_video_tokens.argtypes = [P(cf), P(cf), cl, cl, P(cf)]
         L.orc_mha.argtypes = [P(cf), ci, ci, ci, ci, cf, P(cf), P(cf), P(cf), P(cf), P(cf), P(cf),
                               P(cf), P(cf), P(ci), ci, P(cf), ci]
+        L.orc_vae_pixel_shuffle.argtypes = [P(cf), ci, ci, ci, ci, cl, ci, ci, ci, P(cf), cl]
         L.orc_decomposed_conv3d.argtypes = [P(Conv3dConfig), P(cf), ci, ci, ci, cl, P(cf), ci, cl,
                                             P(cf), P(cf), P(cf), cl, P(cf), cl, ci]
         _LIBS[name] = L
@@ -391,4 +392,41 @@ def mha(x, heads, wq, bq, wk, bk, wv, bv, wo, bo, scale=None, rows=None, threads
     out = np.zeros((n, qdim), np.float32)
     lib(fast).orc_mha(px, seq, qdim, embed, heads, float(scale), *[a[1] for a in arrs], pr, n,
                       out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), threads)
+    return out
+
+
+def vae_pixel_shuffle(packed, channels, tr, sr, remove_head):
+    """vae_upsample3d.cpp:270-318.  packed [channels*tr*sr*sr, F, H, W] ->
+    [channels, F*tr - remove_head, H*sr, W*sr]."""
+    pk = np.ascontiguousarray(packed, np.float32)
+    _, frames, h, w = pk.shape
+    out_t = frames * tr - (1 if remove_head else 0)
+    out = np.zeros((channels, out_t, h * sr, w * sr), np.float32)
+    lib().orc_vae_pixel_shuffle(pk.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), channels,
+                                frames, h, w, frames * h * w, tr, sr, int(bool(remove_head)),
+                                out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
+                                out_t * h * sr * w * sr)
+    return out
+
+
+def vae_upsample3d(post, post_w, post_b, up, up_w, up_b, x, channels, tr, sr, remove_head,
+                   threads=8):
+    """VAEUpsample3D::forward (vae_upsample3d.cpp:258-320) without temporal
+    memory: upscale conv, shuffle, post conv."""
+    code, packed, _ = decomposed_conv3d(up, x, up_w, up_b, threads=threads)
+    assert code > 0
+    sh = vae_pixel_shuffle(packed, channels, tr, sr, remove_head)
+    code, out, _ = decomposed_conv3d(post, sh, post_w, post_b, threads=threads)
+    assert code > 0
+    return out
+
+
+def vae_downsample3d(conv, conv_w, conv_b, x, pad_right, pad_bottom, threads=8):
+    """VAEDownsample3D::forward (vae_downsample3d.cpp:145-172): zero padding
+    on the right and bottom, then the conv."""
+    c, f, h, w = x.shape
+    xp = np.zeros((c, f, h + pad_bottom, w + pad_right), np.float32)
+    xp[:, :, :h, :w] = x
+    code, out, _ = decomposed_conv3d(conv, xp, conv_w, conv_b, threads=threads)
+    assert code > 0
     return out

@@ -802,3 +802,31 @@ void orc_mha(const float* x, int seq, int qdim, int embed, int heads, float scal
     free(k);
     free(v);
 }
+
+/* vae_upsample3d.cpp:270-318 */
+void orc_vae_pixel_shuffle(const float* packed, int channels, int frames, int h, int w,
+                           long packed_cstep, int tr, int sr, int remove_head, float* out,
+                           long out_cstep)
+{
+    const int ow = w * sr, oh = h * sr;
+    const int out_t = frames * tr - (remove_head ? 1 : 0);
+    for (int c = 0; c < channels; c++)
+        for (int f = 0; f < frames; f++)
+            for (int z = 0; z < tr; z++) {
+                const int st = f * tr + z;
+                if (remove_head && st == 1)
+                    continue;
+                const int ot = remove_head && st > 1 ? st - 1 : st;
+                if (ot >= out_t)
+                    continue;
+                for (int yo = 0; yo < sr; yo++)
+                    for (int xo = 0; xo < sr; xo++) {
+                        const int pc = ((yo * sr + xo) * tr + z) * channels + c;
+                        const float* src = packed + pc * packed_cstep + (long)f * h * w;
+                        float* dst = out + c * out_cstep + (long)ot * oh * ow;
+                        for (int y = 0; y < h; y++)
+                            for (int x = 0; x < w; x++)
+                                dst[(long)(y * sr + yo) * ow + x * sr + xo] = src[(long)y * w + x];
+                    }
+            }
+}

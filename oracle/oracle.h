@@ -36,6 +36,8 @@
  *   orc_mha           torch float64 multi_head_attention_forward (self
  *                     attention, default and explicit scale); a subset of
  *                     query rows equals the same rows of the full run.
+ *   orc_vae_pixel_shuffle  torch reshape/permute (depth-to-space over time
+ *                     and space) with the head-frame removal.
  *   orc_decomposed_conv3d  torch float64 conv3d over the temporally padded
  *                     input (frame 0 replicated head_frames times); a run
  *                     split into slices chained through the memory equals
@@ -181,6 +183,17 @@ void orc_mha(const float* x, int seq, int qdim, int embed, int heads, float scal
              const float* wq, const float* bq, const float* wk, const float* bk, const float* wv,
              const float* bv, const float* wo, const float* bo, const int* rows, int count,
              float* out, int num_threads);
+
+/* The depth-to-space shuffle of VAEUpsample3D::forward
+ * (vae_upsample3d.cpp:270-318): packed [channels * tr * sr * sr][frames][h][w]
+ * (channel stride packed_cstep) -> out [channels][out_t][h * sr][w * sr]
+ * (channel stride out_cstep), out_t = frames * tr - remove_head.  Packed
+ * channel ((yo * sr + xo) * tr + z) * channels + c, frame f, pixel (y, x)
+ * lands at channel c, time f * tr + z (minus one after the removed time 1),
+ * pixel (y * sr + yo, x * sr + xo). */
+void orc_vae_pixel_shuffle(const float* packed, int channels, int frames, int h, int w,
+                           long packed_cstep, int tr, int sr, int remove_head, float* out,
+                           long out_cstep);
 
 /* The 16 configuration values of DecomposedConv3D, in the order of its
  * config blob (decomposed_conv3d.cpp:422-441). */

@@ -3,7 +3,8 @@
   seedvr2_ncnn_amd/lib/libseedvr2_hip.so     HIP kernels + the C-ABI (include/seedvr2_hip.h)
   seedvr2_ncnn_amd/lib/libseedvr2_layers.so  ncnn-surface layers (AdaptiveWindowAttention,
                                              SharedLinear, DecomposedConv3D,
-                                             VAEChunkedMHA) over the
+                                             VAEChunkedMHA, VAEDownsample3D,
+                                             VAEUpsample3D) over the
                                              C-ABI, with the ncnn-compatible Mat/Layer
                                              subset
 
@@ -38,7 +39,8 @@ HIP_SOURCES = ["awa_kernels.hip", "linear_kernels.hip", "pipeline_kernels.hip",
                "conv3d_kernels.hip", "mha_kernels.hip", "capi.hip", "awa_plan.cpp"]
 LAYER_SOURCES = ["ncnn/mat.cpp", "ncnn/layer.cpp", "layers/hip_allocator.cpp",
                  "layers/adaptive_window_attention.cpp", "layers/shared_linear.cpp",
-                 "layers/decomposed_conv3d.cpp", "layers/vae_chunked_mha.cpp"]
+                 "layers/decomposed_conv3d.cpp", "layers/vae_chunked_mha.cpp",
+                 "layers/vae_resample3d.cpp"]
 
 HIP_LIB = os.path.join(LIB, "libseedvr2_hip.so")
 LAYER_LIB = os.path.join(LIB, "libseedvr2_layers.so")

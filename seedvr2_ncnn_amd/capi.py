@@ -37,6 +37,7 @@ EXPORTS = (
     "s2_conv3d_output_shape", "s2_conv3d_packed_weight_bytes", "s2_conv3d_pack_weights",
     "s2_conv3d_memory_bytes", "s2_conv3d_workspace_bytes", "s2_conv3d_forward",
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
+    "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle",
 )
 
 
@@ -148,6 +149,9 @@ def lib() -> ctypes.CDLL:
         L.s2_mha_prepare_weights.argtypes = [M3, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
         L.s2_mha_workspace_bytes.argtypes = [M3, ci, P(sz)]
         L.s2_mha_forward.argtypes = [M3, vp, vp, ci, ci, vp, ci, vp, sz, vp]
+        L.s2_conv3d_forward_padded.argtypes = [C3, vp, vp, vp, ci, ci, ci, ci, cl, ci, ci, vp, ci,
+                                               vp, ci, cl, vp, vp, sz, vp]
+        L.s2_vae_pixel_shuffle.argtypes = [vp, ci, ci, ci, ci, ci, cl, ci, ci, ci, vp, cl, vp]
         L.s2_conv3d_forward.argtypes = [C3, vp, vp, vp, ci, ci, ci, ci, cl, vp, ci, vp, ci, cl, vp,
                                         vp, sz, vp]
         _LIB = L

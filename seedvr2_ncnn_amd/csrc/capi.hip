@@ -715,9 +715,24 @@ int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_weights
                       int height, int width, long in_cstep, const void* memory, int memory_frames,
                       void* output, s2_dtype out_dtype, long out_cstep, void* next_memory,
                       void* workspace, size_t workspace_bytes, s2_stream_t stream) {
+    return s2_conv3d_forward_padded(config, packed_weights, bias, input, in_dtype, frames, height,
+                                    width, in_cstep, 0, 0, memory, memory_frames, output,
+                                    out_dtype, out_cstep, next_memory, workspace,
+                                    workspace_bytes, stream);
+}
+
+int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_weights,
+                             const float* bias, const void* input, s2_dtype in_dtype, int frames,
+                             int height, int width, long in_cstep, int pad_right, int pad_bottom,
+                             const void* memory, int memory_frames, void* output,
+                             s2_dtype out_dtype, long out_cstep, void* next_memory,
+                             void* workspace, size_t workspace_bytes, s2_stream_t stream) {
     const int mem = memory ? memory_frames : 0;
     int to, ho, wo;
-    if (!conv3d_out(config, frames, height, width, mem, &to, &ho, &wo))
+    if (pad_right < 0 || pad_bottom < 0) return fail(S2_ERR_INVALID, "negative padding");
+    // the zero padding on the right and bottom only lengthens the output: the
+    // kernel already reads every pixel outside the image as zero
+    if (!conv3d_out(config, frames, height + pad_bottom, width + pad_right, mem, &to, &ho, &wo))
         return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
     if (memory && memory_frames <= 0) return fail(S2_ERR_INVALID, "memory without frames");
     if (!packed_weights || !input || !output || !workspace) return fail(S2_ERR_INVALID, "null pointer");
@@ -892,6 +907,27 @@ int s2_mha_forward(const s2_mha_config* config, const void* prepared, const void
     // out = o Wo^T + bo: [seq][qdim]
     S2_HIP(s2::launch_shared_linear(o, seq, nullptr, 0, kBF, wo, bo, Q, E, S2_ACT_NONE, out,
                                     nullptr, (int)out_dtype, st));
+    return S2_OK;
+}
+
+/* ---- VAEUpsample3D shuffle -------------------------------------------------- */
+
+int s2_vae_pixel_shuffle(const void* packed, s2_dtype dtype, int channels, int frames,
+                         int height, int width, long packed_cstep, int temporal_ratio,
+                         int spatial_ratio, int remove_head, void* output, long out_cstep,
+                         s2_stream_t stream) {
+    if (channels <= 0 || frames <= 0 || height <= 0 || width <= 0 || temporal_ratio <= 0 ||
+        spatial_ratio <= 0 || !dtype_ok(dtype))
+        return fail(S2_ERR_INVALID, "invalid shuffle shape");
+    const int out_t = frames * temporal_ratio - (remove_head ? 1 : 0);
+    if (out_t <= 0) return fail(S2_ERR_INVALID, "no output frames");
+    if (packed_cstep < (long)frames * height * width ||
+        out_cstep < (long)out_t * height * spatial_ratio * width * spatial_ratio)
+        return fail(S2_ERR_INVALID, "channel stride");
+    if (!packed || !output) return fail(S2_ERR_INVALID, "null pointer");
+    S2_HIP(s2::launch_vae_shuffle(packed, (int)dtype, packed_cstep, channels, frames, height,
+                                  width, temporal_ratio, spatial_ratio, remove_head ? 1 : 0,
+                                  output, out_cstep, (hipStream_t)stream));
     return S2_OK;
 }
 

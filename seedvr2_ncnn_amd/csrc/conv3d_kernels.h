@@ -45,4 +45,11 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
                          int t0, int frames_out, const uint16_t* packed, const float* bias,
                          void* out, int out_kind, long out_cstep, hipStream_t stream);
 
+// VAEUpsample3D's shuffle: packed [channels*tr*sr*sr][frames][h][w] (channel
+// stride packed_cstep) -> out [channels][frames*tr - remove_head][h*sr][w*sr]
+// (channel stride out_cstep), elements of type kind (0 fp32; 1, 2 16-bit)
+hipError_t launch_vae_shuffle(const void* packed, int kind, long packed_cstep, int channels,
+                              int frames, int h, int w, int tr, int sr, int remove_head,
+                              void* out, long out_cstep, hipStream_t stream);
+
 }  // namespace s2

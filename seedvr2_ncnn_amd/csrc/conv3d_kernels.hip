@@ -385,7 +385,55 @@ void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
         conv3d_kernel<BN, 0><<<grid, 512, 0, stream>>>(a);
 }
 
+// ---- VAEUpsample3D's depth-to-space shuffle (vae_upsample3d.cpp:270-318) ----
+//
+// One thread per output element (channel blockIdx.y): output time ot is
+// shuffled time st = ot (or ot + 1 past the removed time 1), st = f * tr + z;
+// output pixel (y2, x2) = (y * sr + yo, x * sr + xo) reads packed channel
+// ((yo * sr + xo) * tr + z) * channels + c.  Writes are contiguous; the two
+// (or one) interleaved source planes of a row are each read contiguously.
+template <typename T>
+__global__ __launch_bounds__(256) void vae_shuffle_kernel(const T* __restrict__ packed,
+                                                          long packed_cstep, int channels, int h,
+                                                          int w, int tr, int sr, int remove_head,
+                                                          int out_t, T* __restrict__ out,
+                                                          long out_cstep) {
+    const int c = blockIdx.y;
+    const int ow = w * sr, oh = h * sr;
+    const long plane = (long)oh * ow;
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= plane * out_t) return;
+    const int ot = (int)(i / plane);
+    const long rem = i - (long)ot * plane;
+    const int y2 = (int)(rem / ow), x2 = (int)(rem - (long)y2 * ow);
+    const int st = remove_head && ot >= 1 ? ot + 1 : ot;
+    const int f = st / tr, z = st - f * tr;
+    const int y = y2 / sr, yo = y2 - y * sr;
+    const int x = x2 / sr, xo = x2 - x * sr;
+    const long pc = (long)((yo * sr + xo) * tr + z) * channels + c;
+    out[(long)c * out_cstep + i] = packed[pc * packed_cstep + ((long)f * h + y) * w + x];
+}
+
 }  // namespace
+
+hipError_t launch_vae_shuffle(const void* packed, int kind, long packed_cstep, int channels,
+                              int frames, int h, int w, int tr, int sr, int remove_head,
+                              void* out, long out_cstep, hipStream_t stream) {
+    const int out_t = frames * tr - (remove_head ? 1 : 0);
+    const long n = (long)out_t * h * sr * w * sr;
+    if (n <= 0 || channels <= 0) return hipSuccess;
+    if (channels > 65535) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((n + 255) / 256), (unsigned)channels);
+    if (kind == 0)
+        vae_shuffle_kernel<float><<<grid, 256, 0, stream>>>(
+            (const float*)packed, packed_cstep, channels, h, w, tr, sr, remove_head, out_t,
+            (float*)out, out_cstep);
+    else
+        vae_shuffle_kernel<uint16_t><<<grid, 256, 0, stream>>>(
+            (const uint16_t*)packed, packed_cstep, channels, h, w, tr, sr, remove_head, out_t,
+            (uint16_t*)out, out_cstep);
+    return hipGetLastError();
+}
 
 hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, int cin,
                                long pixels, int cpad, uint16_t* staged, uint16_t* tail,

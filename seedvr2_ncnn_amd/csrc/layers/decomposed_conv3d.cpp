@@ -188,33 +188,41 @@ int DecomposedConv3D::upload_weights_locked() const
     return ret;
 }
 
-// decomposed_conv3d.cpp:605-755
-int DecomposedConv3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
-                              const ncnn::Option& opt) const
+int DecomposedConv3D::output_shape_locked(int frames, int h, int w, size_t elemsize,
+                                          int pad_right, int pad_bottom, int out[3]) const
+{
+    if (weight_data.empty() || pad_right < 0 || pad_bottom < 0)
+        return -1;
+    const bool use_memory = get_vae_memory_state() == MemoryState::ACTIVE && memory_current >= 0;
+    // the memory must hold frames of this input (:617-624)
+    if (use_memory && (memory_w != w || memory_h != h || memory_elemsize != elemsize))
+        return -1;
+    return s2_conv3d_output_shape(&config, frames, h + pad_bottom, w + pad_right,
+                                  use_memory ? memory_frames : 0, out) == S2_OK ? 0 : -1;
+}
+
+int DecomposedConv3D::output_shape(int frames, int h, int w, size_t elemsize, int pad_right,
+                                   int pad_bottom, int out[3]) const
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    return output_shape_locked(frames, h, w, elemsize, pad_right, pad_bottom, out);
+}
+
+// decomposed_conv3d.cpp:605-755 on device memory
+int DecomposedConv3D::forward_device(const void* input, s2_dtype dtype, size_t elemsize,
+                                     int frames, int h, int w, long in_cstep, int pad_right,
+                                     int pad_bottom, void* output, long out_cstep,
+                                     void* stream) const
 {
     std::lock_guard<std::mutex> lock(mutex);
     const MemoryState state = get_vae_memory_state();
     if (state != MemoryState::ACTIVE)
         memory_current = -1;
-    if (weight_data.empty() || bottom_blob.dims != 4 || bottom_blob.c != config.num_input ||
-        bottom_blob.elempack != 1)
-        return -1;
-    HipDeviceAllocator* device = device_allocator_of(bottom_blob);
-    const size_t elemsize = bottom_blob.elemsize;
-    if (!device && elemsize != sizeof(float))
-        return -1;
-    if (device && elemsize != 4 && elemsize != 2)
+    int out[3];
+    if (output_shape_locked(frames, h, w, elemsize, pad_right, pad_bottom, out) != 0)
         return -1;
     const bool use_memory = state == MemoryState::ACTIVE && memory_current >= 0;
-    if (use_memory && (memory_w != bottom_blob.w || memory_h != bottom_blob.h ||
-                       memory_elemsize != elemsize))
-        return -1;
     const int mframes = use_memory ? memory_frames : 0;
-    int out[3];
-    if (s2_conv3d_output_shape(&config, bottom_blob.d, bottom_blob.h, bottom_blob.w, mframes,
-                               out) != S2_OK)
-        return -1;
-
     int devices = 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0)
         return S2_ERR_DEVICE;
@@ -222,8 +230,7 @@ int DecomposedConv3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
     if (ret != 0)
         return ret;
     size_t ws_bytes = 0;
-    ret = s2_conv3d_workspace_bytes(&config, bottom_blob.d, bottom_blob.h, bottom_blob.w, mframes,
-                                    &ws_bytes);
+    ret = s2_conv3d_workspace_bytes(&config, frames, h, w, mframes, &ws_bytes);
     if (ret == 0)
         ret = workspace.reserve(ws_bytes);
     if (ret != 0)
@@ -231,7 +238,7 @@ int DecomposedConv3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
     // the next memory (:727-755): kept unless the memory is disabled
     size_t mem_bytes = 0;
     int cache = 0;
-    ret = s2_conv3d_memory_bytes(&config, bottom_blob.h, bottom_blob.w, &mem_bytes, &cache);
+    ret = s2_conv3d_memory_bytes(&config, h, w, &mem_bytes, &cache);
     if (ret != 0)
         return ret;
     const bool keep = state != MemoryState::DISABLED && cache > 0;
@@ -242,10 +249,46 @@ int DecomposedConv3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
         if (ret != 0)
             return ret;
     }
-    const void* mem_in = use_memory ? memory[memory_current].get() : 0;
-    void* mem_out = keep ? memory[next].get() : 0;
     const float* bias = config.bias_term ? static_cast<const float*>(bias_gpu.get()) : 0;
+    ret = s2_conv3d_forward_padded(&config, packed_gpu.get(), bias, input, dtype, frames, h, w,
+                                   in_cstep, pad_right, pad_bottom,
+                                   use_memory ? memory[memory_current].get() : 0, mframes, output,
+                                   dtype, out_cstep, keep ? memory[next].get() : 0,
+                                   workspace.get(), ws_bytes, stream);
+    if (ret != 0)
+        return ret;
+    if (keep)
+    {
+        memory_current = next;
+        memory_frames = cache;
+        memory_w = w;
+        memory_h = h;
+        memory_elemsize = elemsize;
+    }
+    return 0;
+}
 
+// decomposed_conv3d.cpp:605-755
+int DecomposedConv3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                              const ncnn::Option& opt) const
+{
+    if (bottom_blob.dims != 4 || bottom_blob.c != config.num_input || bottom_blob.elempack != 1)
+        return -1;
+    HipDeviceAllocator* device = device_allocator_of(bottom_blob);
+    const size_t elemsize = bottom_blob.elemsize;
+    if (!device && elemsize != sizeof(float))
+        return -1;
+    if (device && elemsize != 4 && elemsize != 2)
+        return -1;
+    {
+        // a forward outside ACTIVE drops the memory even when it fails
+        std::lock_guard<std::mutex> lock(mutex);
+        if (get_vae_memory_state() != MemoryState::ACTIVE)
+            memory_current = -1;
+    }
+    int out[3];
+    if (output_shape(bottom_blob.d, bottom_blob.h, bottom_blob.w, elemsize, 0, 0, out) != 0)
+        return -1;
     if (device)
     {
         HipDeviceAllocator* out_alloc = dynamic_cast<HipDeviceAllocator*>(opt.blob_allocator);
@@ -254,51 +297,40 @@ int DecomposedConv3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
         top_blob = out_alloc->create_blob(out[2], out[1], out[0], config.num_output, elemsize);
         if (top_blob.empty())
             return -100;
-        const s2_dtype dtype = device_blob_dtype(elemsize, opt);
-        ret = s2_conv3d_forward(&config, packed_gpu.get(), bias, bottom_blob.data, dtype,
-                                bottom_blob.d, bottom_blob.h, bottom_blob.w,
-                                (long)bottom_blob.cstep, mem_in, mframes, top_blob.data, dtype,
-                                (long)top_blob.cstep, mem_out, workspace.get(), ws_bytes,
-                                device->stream());
+        return forward_device(bottom_blob.data, device_blob_dtype(elemsize, opt), elemsize,
+                              bottom_blob.d, bottom_blob.h, bottom_blob.w, (long)bottom_blob.cstep,
+                              0, 0, top_blob.data, (long)top_blob.cstep, device->stream());
     }
-    else
+
+    // Host fp32 blobs: stage, compute, download, synchronise.
+    const size_t in_bytes = bottom_blob.cstep * bottom_blob.c * sizeof(float);
+    const size_t out_cstep = align16((size_t)out[0] * out[1] * out[2] * sizeof(float)) /
+                             sizeof(float);
+    const size_t out_bytes = out_cstep * config.num_output * sizeof(float);
+    int ret;
+    unsigned char* x;
+    unsigned char* y;
     {
-        // Host fp32 blobs: stage, compute, download, synchronise.
-        const size_t in_bytes = bottom_blob.cstep * bottom_blob.c * sizeof(float);
-        const size_t out_cstep = align16((size_t)out[0] * out[1] * out[2] * sizeof(float)) /
-                                 sizeof(float);
-        const size_t out_bytes = out_cstep * config.num_output * sizeof(float);
+        std::lock_guard<std::mutex> lock(mutex);
         ret = staging.reserve(align16(in_bytes) + out_bytes);
-        if (ret != 0)
-            return ret;
-        unsigned char* x = static_cast<unsigned char*>(staging.get());
-        unsigned char* y = x + align16(in_bytes);
-        ret = s2_memcpy_h2d(x, bottom_blob.data, in_bytes, 0);
-        if (ret == 0)
-            ret = s2_conv3d_forward(&config, packed_gpu.get(), bias, x, S2_DTYPE_F32,
-                                    bottom_blob.d, bottom_blob.h, bottom_blob.w,
-                                    (long)bottom_blob.cstep, mem_in, mframes, y, S2_DTYPE_F32,
-                                    (long)out_cstep, mem_out, workspace.get(), ws_bytes, 0);
-        if (ret != 0)
-            return ret;
-        top_blob.create(out[2], out[1], out[0], config.num_output, 4u, opt.blob_allocator);
-        if (top_blob.empty() || top_blob.cstep != out_cstep)
-            return -100;
-        ret = s2_memcpy_d2h(top_blob.data, y, out_bytes, 0);
-        if (ret == 0)
-            ret = s2_stream_synchronize(0);
+        x = static_cast<unsigned char*>(staging.get());
+        y = x + align16(in_bytes);
     }
     if (ret != 0)
         return ret;
-    if (keep)
-    {
-        memory_current = next;
-        memory_frames = cache;
-        memory_w = bottom_blob.w;
-        memory_h = bottom_blob.h;
-        memory_elemsize = elemsize;
-    }
-    return 0;
+    ret = s2_memcpy_h2d(x, bottom_blob.data, in_bytes, 0);
+    if (ret == 0)
+        ret = forward_device(x, S2_DTYPE_F32, 4, bottom_blob.d, bottom_blob.h, bottom_blob.w,
+                             (long)bottom_blob.cstep, 0, 0, y, (long)out_cstep, 0);
+    if (ret != 0)
+        return ret;
+    top_blob.create(out[2], out[1], out[0], config.num_output, 4u, opt.blob_allocator);
+    if (top_blob.empty() || top_blob.cstep != out_cstep)
+        return -100;
+    ret = s2_memcpy_d2h(top_blob.data, y, out_bytes, 0);
+    if (ret == 0)
+        ret = s2_stream_synchronize(0);
+    return ret;
 }
 
 ncnn::Layer* decomposed_conv3d_layer_creator(void* /*userdata*/)

@@ -53,9 +53,26 @@ public:
     void release_completed_temporal_memory() const;
     void reset_temporal_memory() const;
 
+    // For layers built on this one (VAEDownsample3D, VAEUpsample3D): the
+    // output extent {frames, h, w} of a forward under the current memory
+    // state, over input frames padded with pad_right zero columns and
+    // pad_bottom zero rows (-1 where forward would refuse the input) ...
+    int output_shape(int frames, int h, int w, size_t elemsize, int pad_right, int pad_bottom,
+                     int out[3]) const;
+    // ... and forward on device memory: planar input [num_input][in_cstep] and
+    // output [num_output][out_cstep] of element type dtype, on `stream`.
+    int forward_device(const void* input, s2_dtype dtype, size_t elemsize, int frames, int h,
+                       int w, long in_cstep, int pad_right, int pad_bottom, void* output,
+                       long out_cstep, void* stream) const;
+
+    int num_input() const { return config.num_input; }
+    int num_output() const { return config.num_output; }
+
 private:
     int upload_weights_locked() const;
     bool config_ok() const;
+    int output_shape_locked(int frames, int h, int w, size_t elemsize, int pad_right,
+                            int pad_bottom, int out[3]) const;
 
     s2_conv3d_config config;
     ncnn::Mat bias_data;

@@ -19,6 +19,7 @@
 #include "seedvr2_hip.h"
 #include "shared_linear.h"
 #include "vae_chunked_mha.h"
+#include "vae_resample3d.h"
 
 namespace {
 
@@ -62,6 +63,12 @@ int h_layer_create(const char* type, const char* params, const void* model, long
     } else if (strcmp(type, "SeedVR2ChunkedMHA") == 0) {
         h->layer = seedvr2::vae_chunked_mha_layer_creator(0);
         h->destroyer = seedvr2::vae_chunked_mha_layer_destroyer;
+    } else if (strcmp(type, "ExportDownsample3D") == 0) {
+        h->layer = seedvr2::vae_downsample3d_layer_creator(0);
+        h->destroyer = seedvr2::vae_downsample3d_layer_destroyer;
+    } else if (strcmp(type, "ExportUpsample3D") == 0) {
+        h->layer = seedvr2::vae_upsample3d_layer_creator(0);
+        h->destroyer = seedvr2::vae_upsample3d_layer_destroyer;
     } else if (strcmp(type, "DecomposedConv3d") == 0) {
         h->layer = seedvr2::decomposed_conv3d_layer_creator(0);
         h->destroyer = seedvr2::decomposed_conv3d_layer_destroyer;

@@ -83,3 +83,17 @@ def test_rejects_bad_configurations():
     grp = oracle.conv3d_config(num_output=2, num_input=2, kernel_t=3, kernel_h=3, kernel_w=3,
                                head_frames=2, groups=2)
     assert oracle.decomposed_conv3d(grp, x, w)[0] == -1
+
+
+@pytest.mark.parametrize("tr,sr,remove", [(1, 2, False), (2, 2, True), (2, 1, True), (1, 1, False)])
+def test_pixel_shuffle_is_depth_to_space(tr, sr, remove):
+    g = np.random.default_rng(tr * 10 + sr)
+    c, f, h, w = 3, 3, 4, 5
+    packed = g.standard_normal((c * tr * sr * sr, f, h, w)).astype(np.float32)
+    out = oracle.vae_pixel_shuffle(packed, c, tr, sr, remove)
+    # packed channel ((yo*sr + xo)*tr + z)*c + ch -> (yo, xo, z, ch) outermost first
+    t = torch.from_numpy(packed).reshape(sr, sr, tr, c, f, h, w)
+    t = t.permute(3, 4, 2, 5, 0, 6, 1).reshape(c, f * tr, h * sr, w * sr)
+    if remove:
+        t = torch.cat([t[:, :1], t[:, 2:]], dim=1)
+    assert np.array_equal(out, t.numpy())
