@@ -212,6 +212,7 @@ VAE_CONV_LAYERS = [
     ("full_res_128", 128, 128, 4, 720, 1280),
     ("half_res_256", 256, 256, 4, 360, 640),
     ("quarter_res_512", 512, 512, 1, 180, 320),
+    ("rgb_out_128_to_3", 128, 3, 4, 720, 1280),
 ]
 
 

@@ -150,14 +150,15 @@ struct ConvArgs {
     int mtiles, ntiles;
 };
 
-// Eight waves in a (BM/128) x (BN/64) grid of 128x64 wave tiles (4x2 MFMA
-// 32x32x16 accumulators, 128 fp32 per lane), as in the SharedLinear GEMM:
-// BN = 256 gives 256x256 block tiles, BN = 128 (output channels <= 128)
-// gives 512x128 tiles.  Two 64-k LDS stages of (BM + BN) x 128 bytes (64 KB
-// or 80 KB) are filled by DMA one stage ahead of the MFMAs; LDS rows use the
-// GEMM's chunk swizzle.  Wave w loads A rows [w*BM/8, (w+1)*BM/8) and B rows
-// [w*BN/8, (w+1)*BN/8), 8 rows per DMA instruction.  OK is the output type
-// (0 fp32, 1 bf16, 2 fp16).
+// Eight waves in a grid of 128x64 wave tiles (4x2 MFMA 32x32x16
+// accumulators, 128 fp32 per lane), as in the SharedLinear GEMM: BN = 256
+// gives 256x256 block tiles, BN = 128 (output channels <= 128) 512x128
+// tiles.  BN = 32 (output channels <= 32, e.g. a decoder's RGB output) uses
+// 64x32 wave tiles in a 512x32 block, so a 3-channel output pays for 32
+// columns, not 128.  Two 64-k LDS stages of (BM + BN) x 128 bytes are filled
+// by DMA one stage ahead of the MFMAs; LDS rows use the GEMM's chunk swizzle.
+// Wave w loads A rows [w*BM/8, (w+1)*BM/8) and its share of the B rows, 8
+// rows per DMA instruction.  OK is the output type (0 fp32, 1 bf16, 2 fp16).
 //
 // The im2col addressing costs a few VALU operations per row and window
 // position: each A row keeps the byte offset of its window origin
@@ -167,12 +168,17 @@ struct ConvArgs {
 // The k-steps walk (tap, ky, kx, channel chunk) with scalar counters.
 template <int BN, int OK>
 __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
-    constexpr int BM = BN == 128 ? 512 : 256;
+    // wave tile: TM x TN blocks of 32x32 (128x64, or 64x32 for BN = 32)
+    constexpr int TM = BN >= 64 ? 4 : 2, TN = BN >= 64 ? 2 : 1;
+    constexpr int WN = BN / (32 * TN), WM = 8 / WN;
+    constexpr int BM = WM * 32 * TM;
     constexpr int BK = 64, RB = BK * 2;
-    constexpr int WN = BN / 64;
     constexpr int TA = BM * RB, SB = TA + BN * RB;
     constexpr int ARPW = BM / 8, AJ = ARPW / 8;
-    constexpr int BRPW = BN / 8, BJ = BRPW / 8;
+    // B rows: BN / 8 per wave in 8-row DMA instructions; with BN = 32 the
+    // first four waves load 8 rows each
+    constexpr int BRPW = BN >= 64 ? BN / 8 : 8, BJ = BN >= 64 ? BRPW / 8 : 1;
+    constexpr int BWAVES = BN / BRPW;
     constexpr int GROUP = 4;
     __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SB];
 
@@ -232,7 +238,7 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     uint32_t voffb[BJ];
 #pragma unroll
     for (int j = 0; j < BJ; ++j) {
-        const int row = wave * BRPW + j * 8 + (lane >> 3);
+        const int row = (wave % BWAVES) * BRPW + j * 8 + (lane >> 3);
         voffb[j] = (uint32_t)(row * a.kp * 2 + (((lane & 7) ^ lds_swizzle(row)) * 16));
     }
     const i32x4 ra = wave_uniform(buffer_rsrc(a.staged, a.staged_bytes));
@@ -274,26 +280,28 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 #pragma unroll
         for (int j = 0; j < AJ; ++j)
             lds_dma16(memsel[j] ? rm : ra, st + (wave * ARPW + j * 8) * RB, voffa[j], soffa);
+        if (wave < BWAVES) {
 #pragma unroll
-        for (int j = 0; j < BJ; ++j)
-            lds_dma16(rb, st + TA + (wave * BRPW + j * 8) * RB, voffb[j], soffb);
+            for (int j = 0; j < BJ; ++j)
+                lds_dma16(rb, st + TA + (wave * BRPW + j * 8) * RB, voffb[j], soffb);
+        }
     };
 
-    f32x16 acc[4][2];
-    bf16x8 fa[2][4], fb[2][2];
+    f32x16 acc[TM][TN];
+    bf16x8 fa[2][TM], fb[2][TN];
     auto frag = [&](const uint8_t* st, int kk, int slot) {
         const int pc = ((2 * kk + g) ^ sw) * 16;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            fa[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * RB + pc));
+        for (int i = 0; i < TM; ++i)
+            fa[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 32 * TM + 32 * i + l32) * RB + pc));
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-            fb[slot][j] = as_bf16x8(*(const uint4*)(st + TA + (wn * 64 + 32 * j + l32) * RB + pc));
+        for (int j = 0; j < TN; ++j)
+            fb[slot][j] = as_bf16x8(*(const uint4*)(st + TA + (wn * 32 * TN + 32 * j + l32) * RB + pc));
     };
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -329,9 +337,9 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
             if (kk + 1 < BK / 16) frag(st, kk + 1, (kk + 1) & 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j)
+                for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk & 1][i], fb[kk & 1][j],
                                                                          acc[i][j], 0, 0, 0);
         }
@@ -342,16 +350,16 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     // column l32, so each lane holds 4 consecutive output pixels of one
     // output channel: one 16-byte (fp32) or 8-byte store into that plane.
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int col = col0 + wn * 64 + 32 * j + l32;
+    for (int j = 0; j < TN; ++j) {
+        const int col = col0 + wn * 32 * TN + 32 * j + l32;
         if (col >= a.cout) continue;
         const float bv = a.bias ? a.bias[col] : 0.f;
         const long cbase = (long)col * a.out_cstep + a.out_off;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int m = row0 + wm * 128 + 32 * i + 8 * rg + 4 * g;
+                const int m = row0 + wm * 32 * TM + 32 * i + 8 * rg + 4 * g;
                 const float v0 = acc[i][j][4 * rg] + bv, v1 = acc[i][j][4 * rg + 1] + bv;
                 const float v2 = acc[i][j][4 * rg + 2] + bv, v3 = acc[i][j][4 * rg + 3] + bv;
                 if (a.vec_ok && m + 3 < a.M) {
@@ -508,7 +516,11 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.shift = shift;
     a.fbase = frame_base;
     a.t0 = t0;
-    if (s.cout <= 128) {
+    if (s.cout <= 32) {
+        a.mtiles = (int)((m + 511) / 512);
+        a.ntiles = 1;
+        launch_conv3d_kernel<32>(a, stream);
+    } else if (s.cout <= 128) {
         a.mtiles = (int)((m + 511) / 512);
         a.ntiles = (s.cout + 127) / 128;
         launch_conv3d_kernel<128>(a, stream);

@@ -78,6 +78,9 @@ SHAPES = [
     (96, 72, 4, 7, 9, dict(k=(3, 1, 3), p=(0, 1))),    # ragged k window, cin not a multiple of 64
     (256, 256, 1, 8, 8, dict(k=(1, 1, 1), p=(0, 0), head=0)),   # pointwise
     (32, 40, 6, 5, 6, dict(s=(2, 1, 1), d=(2, 1, 2), p=(1, 2), head=4)),
+    (128, 3, 3, 12, 20, {}),                           # RGB output: 512x32 tiles
+    (64, 32, 2, 9, 13, dict(s=(1, 2, 2))),             # 32 output channels, stride 2
+    (16, 16, 4, 8, 10, {}),                            # 16 in and out (latent width)
 ]
 
 
