@@ -284,8 +284,10 @@ typedef struct s2_conv3d_config {
 S2_API int s2_conv3d_output_shape(const s2_conv3d_config* config, int frames, int height,
                                   int width, int memory_frames, int out_shape[3]);
 
-/* Device weights in the kernel's layout: bf16 [num_output][kernel_t]
- * [kernel_h][kernel_w][cpad], cpad = num_input rounded up to 64.  `weights`
+/* Device weights in the kernel's layout: bf16 [num_output][kp], k = window
+ * position ((t * kernel_h + y) * kernel_w + x) * cpad + channel, with cpad 8,
+ * 16 or 32 for at most 32 input channels and num_input rounded up to 64
+ * otherwise, and kp the positions times cpad rounded up to 64.  `weights`
  * is the reference's per-tap ncnn Convolution weights, device fp32
  * [kernel_t][num_output][num_input][kernel_h][kernel_w] (load_model,
  * :457-471). */

@@ -677,7 +677,7 @@ int s2_conv3d_output_shape(const s2_conv3d_config* config, int frames, int heigh
 int s2_conv3d_packed_weight_bytes(const s2_conv3d_config* config, size_t* bytes) {
     if (!bytes || !conv3d_config_ok(config)) return fail(S2_ERR_INVALID, "invalid configuration");
     const s2::Conv3dShape s = conv3d_shape(config);
-    *bytes = (size_t)s.cout * s.kt * s.kh * s.kw * s.cpad * 2;
+    *bytes = (size_t)s.cout * s2::conv3d_kp(s) * 2;
     return S2_OK;
 }
 
@@ -762,7 +762,8 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
     // DMA group stays inside one output frame; otherwise they are copied in
     // front of the staged input.
     const int shift = prefix - mem;
-    const bool direct = mem > 0 && ((long)ho * wo) % 8 == 0 && (long)mem <= max_span;
+    const bool direct = mem > 0 && s.cpad >= 64 && ((long)ho * wo) % 8 == 0 &&
+                        (long)mem <= max_span;
     const int kmem = direct ? mem : 0;
     const int lead = mem - kmem;
     uint16_t* staged = (uint16_t*)workspace;

@@ -2,8 +2,8 @@
 //
 // The convolution runs as an implicit GEMM over a staged copy of its input:
 // the temporally padded frames in channel-last bf16, [frame][y][x][cpad]
-// with cpad = num_input rounded up to 64 (zero channels above num_input).
-// Weights are packed once to bf16 [num_output][kt][kh][kw][cpad], the same k
+// (conv3d_cpad: zero channels above num_input).  Weights are packed once to
+// bf16 [num_output][kp], k = window position * cpad + channel, the same k
 // order, so both MFMA operands are k-contiguous.
 #pragma once
 
@@ -20,7 +20,16 @@ struct Conv3dShape {
     int ph, pw;
 };
 
-inline int conv3d_cpad(int cin) { return (cin + 63) / 64 * 64; }
+// Channels per staged pixel: 8, 16 or 32 for layers of at most 32 input
+// channels (a 64-wide k-step then spans several window positions), else
+// num_input rounded up to 64.
+inline int conv3d_cpad(int cin) {
+    return cin <= 8 ? 8 : cin <= 16 ? 16 : cin <= 32 ? 32 : (cin + 63) / 64 * 64;
+}
+// Packed weight row length: window positions x cpad, rounded up to 64.
+inline long conv3d_kp(const Conv3dShape& s) {
+    return ((long)s.kt * s.kh * s.kw * s.cpad + 63) / 64 * 64;
+}
 
 // planar input [cin][frames*H*W] (channel stride in_cstep; element type
 // in_kind: 0 fp32, 1 bf16, 2 fp16) -> staged [frames*H*W][cpad] bf16.  When
@@ -29,7 +38,7 @@ inline int conv3d_cpad(int cin) { return (cin + 63) / 64 * 64; }
 hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, int cin,
                                long pixels, int cpad, uint16_t* staged, uint16_t* tail,
                                long tail_q0, hipStream_t stream);
-// fp32 [kt][cout][cin][kh][kw] -> bf16 [cout][kt][kh][kw][cpad]
+// fp32 [kt][cout][cin][kh][kw] -> bf16 [cout][kp] (conv3d_kp)
 hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s,
                                       uint16_t* packed, hipStream_t stream);
 // Output frames [t0, t0 + frames_out) of the convolution.  Padded frame p

@@ -55,8 +55,8 @@ __device__ __forceinline__ void load_elem4(const void* p, long i, float (&v)[4])
 
 // One block moves 64 pixels x 64 channels: 64 channel rows of 64 pixels are
 // read as 16-byte runs, transposed in LDS (row pitch 65 floats: conflict-free
-// both ways) and written as 64 pixel rows of 128 bytes.  Channels at or
-// above cin are written as zeros.
+// both ways) and written as 64 pixel rows of 128 bytes (or of cpad channels
+// when cpad is 8, 16 or 32).  Channels at or above cin are written as zeros.
 template <int KIND>
 __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
     const void* __restrict__ in, long cstep, int cin, long pixels, int cpad,
@@ -94,36 +94,40 @@ __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
     uint16_t lo[8], hi[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) lo[i] = h[i], hi[i] = h[8 + i];
+    // a pixel holds cpad channels: with cpad 8 or 16 (at most 16 input
+    // channels) only the first part writes, one or two 16-byte chunks
+    const int nchunk = min(2, (cpad - c0 - part * 16) / 8);
+    if (nchunk <= 0) return;
     const uint4 vlo = pack8_bf16(lo), vhi = pack8_bf16(hi);
     uint4* dst = reinterpret_cast<uint4*>(staged + (q0 + q) * cpad + c0 + part * 16);
     dst[0] = vlo;
-    dst[1] = vhi;
+    if (nchunk > 1) dst[1] = vhi;
     // pixels from tail_q0 on are the next temporal memory as well
     if (tail && q0 + q >= tail_q0) {
         uint4* t2 = reinterpret_cast<uint4*>(tail + (q0 + q - tail_q0) * cpad + c0 + part * 16);
         t2[0] = vlo;
-        t2[1] = vhi;
+        if (nchunk > 1) t2[1] = vhi;
     }
 }
 
-// ---- weights: [kt][cout][cin][kh][kw] fp32 -> [cout][kt][kh][kw][cpad] bf16 --
+// ---- weights: [kt][cout][cin][kh][kw] fp32 -> [cout][kp] bf16 ----------------
 
+// row co of the packed weights: k = p * cpad + ci for window position p =
+// (tap * kh + ky) * kw + kx, zero past the last position and for ci >= cin
 __global__ __launch_bounds__(256) void conv3d_pack_kernel(const float* __restrict__ w,
-                                                          Conv3dShape s, long total,
+                                                          Conv3dShape s, long kp, long total,
                                                           uint16_t* __restrict__ out) {
     const long i = (long)blockIdx.x * 256 + threadIdx.x;
     if (i >= total) return;
-    const int ci = (int)(i % s.cpad);
-    long r = i / s.cpad;
-    const int kx = (int)(r % s.kw);
-    r /= s.kw;
-    const int ky = (int)(r % s.kh);
-    r /= s.kh;
-    const int tap = (int)(r % s.kt);
-    const int co = (int)(r / s.kt);
+    const int co = (int)(i / kp);
+    const long k = i - (long)co * kp;
+    const int p = (int)(k / s.cpad), ci = (int)(k - (long)p * s.cpad);
     float v = 0.f;
-    if (ci < s.cin)
+    if (p < s.kt * s.kh * s.kw && ci < s.cin) {
+        const int kx = p % s.kw, r = p / s.kw;
+        const int ky = r % s.kh, tap = r / s.kh;
         v = w[(((long)tap * s.cout + co) * s.cin + ci) * s.kh * s.kw + ky * s.kw + kx];
+    }
     out[i] = f32_to_bf16(v);
 }
 
@@ -136,7 +140,7 @@ struct ConvArgs {
     uint32_t memory_bytes;
     int mem;
     const uint16_t* packed;
-    int kp;   // packed row length: kt*kh*kw*cpad
+    int kp;   // packed row length (conv3d_kp)
     const float* bias;
     void* out;
     long out_cstep;
@@ -145,7 +149,7 @@ struct ConvArgs {
     int vec_ok;   // 4-pixel vector stores are aligned
     int H, W, Ho, Wo, M;
     int cpad, cout;
-    int kh, kw, st, dt, sh, sw, dh, dw, ph, pw;
+    int kt, kh, kw, st, dt, sh, sw, dh, dw, ph, pw;
     int shift, fbase, t0;
     int mtiles, ntiles;
 };
@@ -166,7 +170,13 @@ struct ConvArgs {
 // (rmask), and the offset of its current temporal tap's frame (rbase,
 // refreshed when the tap changes).  A position then adds one scalar offset.
 // The k-steps walk (tap, ky, kx, channel chunk) with scalar counters.
-template <int BN, int OK>
+//
+// SMALL (at most 32 input channels, cpad = 8, 16 or 32): a 64-wide k-step
+// spans 64 / cpad window positions of cpad channels.  Wave w then loads
+// 16-byte chunk w of every A row (one window position and channel part per
+// wave, decoded with scalar arithmetic), into a chunk-major A tile
+// [8 chunks][BM rows] of 16 bytes; row r of a DMA instruction is lane r.
+template <int BN, int OK, bool SMALL>
 __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     // wave tile: TM x TN blocks of 32x32 (128x64, or 64x32 for BN = 32)
     constexpr int TM = BN >= 64 ? 4 : 2, TN = BN >= 64 ? 2 : 1;
@@ -212,9 +222,9 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     uint32_t rpix[AJ], rmask[AJ];
 #pragma unroll
     for (int j = 0; j < AJ; ++j) {
-        const int row = wave * ARPW + j * 8 + (lane >> 3);
+        const int row = SMALL ? j * 64 + lane : wave * ARPW + j * 8 + (lane >> 3);
         const int m = row0 + row;
-        const uint32_t chk = (uint32_t)(((lane & 7) ^ lds_swizzle(row)) * 16);
+        const uint32_t chk = SMALL ? 0u : (uint32_t)(((lane & 7) ^ lds_swizzle(row)) * 16);
         rpf[j] = INT_MIN / 2;
         rpix[j] = chk;
         rmask[j] = 0;
@@ -271,15 +281,46 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 #pragma unroll
         for (int j = 0; j < AJ; ++j) voffa[j] = (rmask[j] & bit) ? rbase[j] + koff : 0x80000000u;
     };
-    const int cpc = a.cpad / 64;   // k-steps per window position
+    const int cpc = SMALL ? 1 : a.cpad / 64;   // k-steps per window position
     const int nk = a.kp / 64;
+    // SMALL: this wave's 16-byte part of a pixel and window position within
+    // a k-step; the position of k-step ks is ks * (64 / cpad) + its index
+    const int parts = a.cpad / 8;
+    const int my_part = wave % parts, my_pos = wave / parts;
+    const int npos = a.kt * a.kh * a.kw;
+    int cur_tap = -1;
+    auto set_step_small = [&](int ks) {
+        const int p = ks * (8 / parts) + my_pos;
+        if (p >= npos) {
+#pragma unroll
+            for (int j = 0; j < AJ; ++j) voffa[j] = 0x80000000u;
+            return;
+        }
+        const int khw = a.kh * a.kw;
+        const int tap = p / khw, r = p - tap * khw;
+        const int ky = r / a.kw, kx = r - ky * a.kw;
+        if (tap != cur_tap) {
+            set_tap(tap);
+            cur_tap = tap;
+        }
+        const uint32_t koff = (uint32_t)(ky * a.dh * a.W + kx * a.dw) * pix + my_part * 16;
+        const uint32_t bit = 1u << r;
+#pragma unroll
+        for (int j = 0; j < AJ; ++j) voffa[j] = (rmask[j] & bit) ? rbase[j] + koff : 0x80000000u;
+    };
     auto issue = [&](int stage, int ks, int cc) {
         const uint32_t soffa = (uint32_t)(cc * RB);
         const uint32_t soffb = (uint32_t)(ks * RB);
         const uint32_t st = lds_base + stage * SB;
+        if (SMALL) {
 #pragma unroll
-        for (int j = 0; j < AJ; ++j)
-            lds_dma16(memsel[j] ? rm : ra, st + (wave * ARPW + j * 8) * RB, voffa[j], soffa);
+            for (int j = 0; j < AJ; ++j)
+                lds_dma16(ra, st + (wave * BM + j * 64) * 16, voffa[j], 0u);
+        } else {
+#pragma unroll
+            for (int j = 0; j < AJ; ++j)
+                lds_dma16(memsel[j] ? rm : ra, st + (wave * ARPW + j * 8) * RB, voffa[j], soffa);
+        }
         if (wave < BWAVES) {
 #pragma unroll
             for (int j = 0; j < BJ; ++j)
@@ -292,8 +333,11 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     auto frag = [&](const uint8_t* st, int kk, int slot) {
         const int pc = ((2 * kk + g) ^ sw) * 16;
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-            fa[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 32 * TM + 32 * i + l32) * RB + pc));
+        for (int i = 0; i < TM; ++i) {
+            const int row = wm * 32 * TM + 32 * i + l32;
+            fa[slot][i] = as_bf16x8(*(const uint4*)(
+                SMALL ? st + ((2 * kk + g) * BM + row) * 16 : st + row * RB + pc));
+        }
 #pragma unroll
         for (int j = 0; j < TN; ++j)
             fb[slot][j] = as_bf16x8(*(const uint4*)(st + TA + (wn * 32 * TN + 32 * j + l32) * RB + pc));
@@ -307,8 +351,12 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 
     // window position and channel chunk of the next k-step to issue
     int tap = 0, ky = 0, kx = 0, cc = 0;
-    set_tap(0);
-    set_pos(0, 0);
+    if (SMALL) {
+        set_step_small(0);
+    } else {
+        set_tap(0);
+        set_pos(0, 0);
+    }
     issue(0, 0, 0);
 #pragma unroll 1
     for (int ks = 0; ks < nk; ++ks) {
@@ -316,7 +364,9 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();   // stage ks visible to all waves; the other stage no longer read
         if (ks + 1 < nk) {
-            if (++cc == cpc) {
+            if (SMALL) {
+                set_step_small(ks + 1);
+            } else if (++cc == cpc) {
                 cc = 0;
                 if (++kx == a.kw) {
                     kx = 0;
@@ -382,15 +432,23 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     }
 }
 
-template <int BN>
+template <int BN, bool SMALL>
 void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
     const unsigned grid = (unsigned)(a.mtiles * a.ntiles);
     if (a.out_kind == 1)
-        conv3d_kernel<BN, 1><<<grid, 512, 0, stream>>>(a);
+        conv3d_kernel<BN, 1, SMALL><<<grid, 512, 0, stream>>>(a);
     else if (a.out_kind == 2)
-        conv3d_kernel<BN, 2><<<grid, 512, 0, stream>>>(a);
+        conv3d_kernel<BN, 2, SMALL><<<grid, 512, 0, stream>>>(a);
     else
-        conv3d_kernel<BN, 0><<<grid, 512, 0, stream>>>(a);
+        conv3d_kernel<BN, 0, SMALL><<<grid, 512, 0, stream>>>(a);
+}
+
+template <int BN>
+void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
+    if (a.cpad < 64)
+        launch_conv3d_kernel<BN, true>(a, stream);
+    else
+        launch_conv3d_kernel<BN, false>(a, stream);
 }
 
 // ---- VAEUpsample3D's depth-to-space shuffle (vae_upsample3d.cpp:270-318) ----
@@ -447,7 +505,7 @@ hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, in
                                long pixels, int cpad, uint16_t* staged, uint16_t* tail,
                                long tail_q0, hipStream_t stream) {
     if (pixels <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((pixels + 63) / 64), (unsigned)(cpad / 64));
+    const dim3 grid((unsigned)((pixels + 63) / 64), (unsigned)((cpad + 63) / 64));
     if (in_kind == 1)
         conv3d_stage_kernel<1><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
                                                                      cpad, staged, tail, tail_q0);
@@ -462,9 +520,10 @@ hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, in
 
 hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s,
                                       uint16_t* packed, hipStream_t stream) {
-    const long total = (long)s.cout * s.kt * s.kh * s.kw * s.cpad;
+    const long kp = conv3d_kp(s);
+    const long total = (long)s.cout * kp;
     if (total <= 0) return hipSuccess;
-    conv3d_pack_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(weights, s, total,
+    conv3d_pack_kernel<<<(unsigned)((total + 255) / 256), 256, 0, stream>>>(weights, s, kp, total,
                                                                             packed);
     return hipGetLastError();
 }
@@ -476,10 +535,11 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
                          void* out, int out_kind, long out_cstep, hipStream_t stream) {
     if (frames_out <= 0) return hipSuccess;
     const long m = (long)frames_out * ho * wo;
-    const long kp = (long)s.kt * s.kh * s.kw * s.cpad;
+    const long kp = conv3d_kp(s);
+    const bool small = s.cpad < 64;
     if (m > INT_MAX || staged_bytes >= 0x80000000ull || memory_bytes >= 0x80000000ull ||
-        kp * 2 * s.cout >= 0x80000000l || s.cpad % 64 != 0 || s.kh * s.kw > 32 ||
-        (mem > 0 && ((long)ho * wo) % 8 != 0))
+        kp * 2 * s.cout >= 0x80000000l || s.cpad != conv3d_cpad(s.cin) || s.kh * s.kw > 32 ||
+        (mem > 0 && (small || ((long)ho * wo) % 8 != 0)))
         return hipErrorInvalidValue;
     ConvArgs a;
     a.staged = staged;
@@ -503,6 +563,7 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.M = (int)m;
     a.cpad = s.cpad;
     a.cout = s.cout;
+    a.kt = s.kt;
     a.kh = s.kh;
     a.kw = s.kw;
     a.st = s.st;

@@ -81,6 +81,8 @@ SHAPES = [
     (128, 3, 3, 12, 20, {}),                           # RGB output: 512x32 tiles
     (64, 32, 2, 9, 13, dict(s=(1, 2, 2))),             # 32 output channels, stride 2
     (16, 16, 4, 8, 10, {}),                            # 16 in and out (latent width)
+    (24, 64, 3, 7, 9, dict(k=(1, 3, 3))),              # 32-channel pixels, last k-step part empty
+    (8, 130, 2, 11, 6, dict(k=(2, 3, 3), head=1)),     # 8-channel pixels, ragged n
 ]
 
 
@@ -107,13 +109,15 @@ def test_conv3d_16bit_blobs_and_padded_cstep(in_dtype, out_dtype):
 
 
 # 6x10 frames copy the memory in front of the staged input (a DMA group of
-# 8 rows can straddle two frames); 8x10 frames read it in place
+# 8 rows can straddle two frames); 8x10 frames read it in place, except with
+# 16 input channels (16-channel pixels always copy it)
 @pytest.mark.parametrize("split", [1, 2])
 @pytest.mark.parametrize("hw", [(6, 10), (8, 10)])
 @pytest.mark.parametrize("reuse", [False, True])
-def test_conv3d_memory_chains_slices(split, hw, reuse):
-    cfgs = _cfg(64, 128)
-    x, wts, bias = _case(64, 128, 5, hw[0], hw[1], cfgs, 11)
+@pytest.mark.parametrize("cin", [64, 16])
+def test_conv3d_memory_chains_slices(split, hw, reuse, cin):
+    cfgs = _cfg(cin, 128)
+    x, wts, bias = _case(cin, 128, 5, hw[0], hw[1], cfgs, 11)
     conv = _device(cfgs[0], wts, bias)
     a = _run(conv, x[:, :split], keep_memory=True)
     b = _run(conv, x[:, split:], use_memory=True, keep_memory=True, reuse_memory_buffer=reuse)
