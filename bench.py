@@ -542,6 +542,82 @@ def main():
         per_op = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(ops)}
         return total_ms / steps, per_op, wall
 
+    def full_block(steps, warmup):
+        """The whole block around the hot path (regular windows): an fp32
+        residual stream, the norm and AdaSingle modulation before the
+        attention and the MLP (s2_dit_ada_in, bf16 out) and the gate and
+        residual sum after them (s2_dit_ada_out, in place).  Algorithmic
+        bytes: ada_in reads fp32 and writes bf16 rows, 6 B per value;
+        ada_out reads the fp32 residual and the bf16 branch output and
+        writes the residual, 10 B per value."""
+        res_v = torch.randn(lv, HIDDEN, generator=gen, device=dev)
+        res_t = torch.randn(lt, HIDDEN, generator=gen, device=dev)
+        mods = {k: torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1 + (1.0 if k.endswith("scale") else 0.0)
+                for k in ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate")}
+        hin_v = torch.empty(lv, HIDDEN, dtype=bf, device=dev)
+        hin_t = torch.empty(lt, HIDDEN, dtype=bf, device=dev)
+        vr, tr = [lv], [lt]
+        fops = ["attn_norm_modulate", "qkv", "attention", "out", "attn_gate_residual",
+                "mlp_norm_modulate", "mlp_up", "mlp_down", "mlp_gate_residual"]
+
+        def fstep(ev=None):
+            def mark(i):
+                if ev is not None:
+                    ev[i].record()
+            mark(0)
+            capi.ada_in(res_v, res_t, vr, tr, mods["attn_shift"], mods["attn_scale"],
+                        out_video=hin_v, out_text=hin_t)
+            mark(1)
+            capi.shared_linear(hin_v, hin_t, w_qkv, b[3 * HIDDEN], capi.ACT_NONE, y_video=qkv_v,
+                               y_text=qkv_t)
+            mark(2)
+            capi.awa_forward(plans[0], norms, freqs,
+                             qkv_v[:, :HIDDEN], qkv_v[:, HIDDEN:2 * HIDDEN], qkv_v[:, 2 * HIDDEN:],
+                             qkv_t[:, :HIDDEN], qkv_t[:, HIDDEN:2 * HIDDEN], qkv_t[:, 2 * HIDDEN:],
+                             workspace=ws, out_video=a_v, out_text=a_t)
+            mark(3)
+            capi.shared_linear(a_v, a_t, w_o, b[HIDDEN], capi.ACT_NONE, y_video=o_v, y_text=o_t)
+            mark(4)
+            capi.ada_out(res_v, res_t, o_v, o_t, vr, tr, mods["attn_gate"])
+            mark(5)
+            capi.ada_in(res_v, res_t, vr, tr, mods["mlp_shift"], mods["mlp_scale"],
+                        out_video=hin_v, out_text=hin_t)
+            mark(6)
+            capi.shared_linear(hin_v, hin_t, w_up, b[MLP], capi.ACT_GELU, y_video=h_v, y_text=h_t)
+            mark(7)
+            capi.shared_linear(h_v, h_t, w_dn, b[HIDDEN], capi.ACT_NONE, y_video=y_v, y_text=y_t)
+            mark(8)
+            capi.ada_out(res_v, res_t, y_v, y_t, vr, tr, mods["mlp_gate"])
+            mark(9)
+
+        for _ in range(warmup):
+            fstep()
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(10)] for _ in range(steps)]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            fstep(evs[i])
+        end.record()
+        torch.cuda.synchronize()
+        assert bool(torch.isfinite(res_v).all())
+        per = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(fops)}
+        m_rows = lv + lt
+        in_bytes, out_bytes = 6.0 * m_rows * HIDDEN, 10.0 * m_rows * HIDDEN
+        ada_in_ms = (per["attn_norm_modulate"] + per["mlp_norm_modulate"]) / 2
+        ada_out_ms = (per["attn_gate_residual"] + per["mlp_gate_residual"]) / 2
+        return {
+            "ms": round(start.elapsed_time(end) / steps, 4),
+            "ops_ms": {op: round(v, 4) for op, v in per.items()},
+            "norm_modulate": {"ms": round(ada_in_ms, 4), "algorithmic_bytes": int(in_bytes),
+                              "gbs": round(in_bytes / (ada_in_ms * 1e-3) / 1e9, 1),
+                              "frac_hbm_peak": round(in_bytes / (ada_in_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "gate_residual": {"ms": round(ada_out_ms, 4), "algorithmic_bytes": int(out_bytes),
+                              "gbs": round(out_bytes / (ada_out_ms * 1e-3) / 1e9, 1),
+                              "frac_hbm_peak": round(out_bytes / (ada_out_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "note": "fp32 residual stream; per-sample modulation vectors; regular windows",
+        }
+
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -635,6 +711,7 @@ def main():
         },
         "wall_s_timed_region": round(wall, 3),
     }
+    line["full_block"] = full_block(args.steps, args.warmup)
     for p in plans.values():
         p.close()
     del x_v, x_t, w_qkv, w_o, w_up, w_dn, qkv_v, qkv_t, a_v, a_t, o_v, o_t, h_v, h_t, y_v, y_t, ws

@@ -262,6 +262,43 @@ S2_API int s2_denoise_update(const float* positive_patches, const float* negativ
                              float cfg_rescale, float delta, float* latent, long channel_stride,
                              s2_stream_t stream);
 
+/* ---- DiT block: norm and AdaSingle modulation ---------------------------- */
+/* The operations of the DiT block graph between its residual stream, its six
+ * per-sample modulation inputs in4..in9 ([batch][hidden] fp32 each,
+ * src/seedvr2/seedvr2_dit.cpp:441-448, 734-738) and the SharedLinear /
+ * AdaptiveWindowAttention layers.  The exported graph holds them as ncnn
+ * built-ins (its .param is not in the reference); they follow the published
+ * SeedVR2 NaDiT block: a norm without affine (RMSNorm) and h * scale + shift
+ * before the attention and the MLP ("in"), the branch output times gate and
+ * the residual sum after them ("out").  Each of scale, shift and gate is the
+ * per-sample input plus the block's own [hidden] vector for the stream
+ * (video_* / text_*, NULL for none).
+ *
+ * Rows: video_rows[b] / text_rows[b] (host arrays, text_rows may be NULL for
+ * no text) rows of sample b, samples in order, batch 1..64.  hidden is a
+ * multiple of 4, at most 4096; row strides are in elements, at least hidden
+ * and a multiple of 4; fp32 rows 16-byte and 16-bit rows 8-byte aligned;
+ * modulation vectors 16-byte aligned. */
+
+/* out = rmsnorm(x) * (scale[b] + *_scale) + (shift[b] + *_shift), with
+ * rmsnorm(x) = x / sqrt(mean(x^2) + epsilon); fp32 arithmetic. */
+S2_API int s2_dit_ada_in(int hidden, float epsilon, int batch, const int* video_rows,
+                         const int* text_rows, const void* x_video, const void* x_text,
+                         s2_dtype x_dtype, long x_stride, const float* shift, const float* scale,
+                         const float* video_shift, const float* video_scale,
+                         const float* text_shift, const float* text_scale, void* out_video,
+                         void* out_text, s2_dtype out_dtype, long out_stride,
+                         s2_stream_t stream);
+
+/* out = x + y * (gate[b] + *_gate), out of x's element type; out may be x
+ * (in place, same row stride).  Each product and sum is rounded to fp32. */
+S2_API int s2_dit_ada_out(int hidden, int batch, const int* video_rows, const int* text_rows,
+                          const void* x_video, const void* x_text, s2_dtype x_dtype,
+                          long x_stride, const void* y_video, const void* y_text,
+                          s2_dtype y_dtype, long y_stride, const float* gate,
+                          const float* video_gate, const float* text_gate, void* out_video,
+                          void* out_text, long out_stride, s2_stream_t stream);
+
 /* ---- DecomposedConv3D (VAE) ---------------------------------------------- */
 /* The causal 3-D convolution of the VAE (src/seedvr2/decomposed_conv3d.h:33-88,
  * decomposed_conv3d.cpp:605-755) as one implicit GEMM on the matrix cores:

@@ -93,6 +93,8 @@ def lib(fast: bool = False) -> ctypes.CDLL:
         L.orc_apply_cfg.argtypes = [P(cf), P(cf), cl, cf, cf, P(cf)]
         L.orc_euler_step.argtypes = [P(cf), cl, P(cf), cl, cf]
         L.orc_video_tokens.argtypes = [P(cf), P(cf), cl, cl, P(cf)]
+        L.orc_ada_in.argtypes = [P(cf), ci, cf, P(ci), ci, P(cf), P(cf), P(cf), P(cf), P(cf)]
+        L.orc_ada_out.argtypes = [P(cf), P(cf), ci, P(ci), ci, P(cf), P(cf)]
         L.orc_mha.argtypes = [P(cf), ci, ci, ci, ci, cf, P(cf), P(cf), P(cf), P(cf), P(cf), P(cf),
                               P(cf), P(cf), P(ci), ci, P(cf), ci]
         L.orc_vae_pixel_shuffle.argtypes = [P(cf), ci, ci, ci, ci, cl, ci, ci, ci, P(cf), cl]
@@ -322,6 +324,48 @@ def video_tokens(latent, condition, tokens):
     lib().orc_video_tokens(pl, pc, lat.shape[1], tokens,
                            out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
     return out
+
+
+def _opt_vec(v, dim):
+    """None -> (None, NULL); else a float32 [dim] vector and its pointer."""
+    if v is None:
+        return None, ctypes.POINTER(ctypes.c_float)()
+    a, p = _f32(np.ravel(v))
+    assert a.shape == (dim,)
+    return a, p
+
+
+def ada_in(x, sample_rows, shift_a, scale_a, shift_b=None, scale_b=None, eps=1e-5):
+    """Norm + AdaSingle "in" of the DiT block (seedvr2_dit.cpp:441-448): x
+    [rows][dim] with rows = sum(sample_rows); shift_a/scale_a [batch][dim]."""
+    xs, px = _f32(x)
+    rows, dim = xs.shape
+    counts = np.ascontiguousarray(sample_rows, dtype=np.int32)
+    assert int(counts.sum()) == rows
+    sa, psa = _f32(np.reshape(shift_a, (len(counts), dim)))
+    ca, pca = _f32(np.reshape(scale_a, (len(counts), dim)))
+    sb, psb = _opt_vec(shift_b, dim)
+    cb, pcb = _opt_vec(scale_b, dim)
+    out = np.zeros_like(xs)
+    lib().orc_ada_in(px, dim, float(eps), counts.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                     len(counts), psa, pca, psb, pcb,
+                     out.ctypes.data_as(ctypes.POINTER(ctypes.c_float)))
+    return out
+
+
+def ada_out(x, y, sample_rows, gate_a, gate_b=None):
+    """AdaSingle "out" and the residual sum: returns x + y * (gate_a[b] + gate_b)."""
+    xs = np.array(x, dtype=np.float32, copy=True, order="C")
+    ys, py = _f32(y)
+    rows, dim = xs.shape
+    assert ys.shape == xs.shape
+    counts = np.ascontiguousarray(sample_rows, dtype=np.int32)
+    assert int(counts.sum()) == rows
+    ga, pga = _f32(np.reshape(gate_a, (len(counts), dim)))
+    gb, pgb = _opt_vec(gate_b, dim)
+    lib().orc_ada_out(xs.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), py, dim,
+                      counts.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), len(counts), pga, pgb)
+    return xs
 
 
 def _planar(a, pad):

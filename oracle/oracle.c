@@ -830,3 +830,47 @@ void orc_vae_pixel_shuffle(const float* packed, int channels, int frames, int h,
                     }
             }
 }
+
+/* ---- DiT block norm and AdaSingle modulation (seedvr2_dit.cpp:441-448) --- */
+
+void orc_ada_in(const float* x, int dim, float eps, const int* sample_rows, int batch,
+                const float* shift_a, const float* scale_a, const float* shift_b,
+                const float* scale_b, float* out) {
+    long row = 0;
+    for (int b = 0; b < batch; ++b) {
+        const float* sa = shift_a + (long)b * dim;
+        const float* ca = scale_a + (long)b * dim;
+        for (int i = 0; i < sample_rows[b]; ++i, ++row) {
+            const float* xr = x + row * dim;
+            float* yr = out + row * dim;
+            double ss = 0.0;
+            for (int c = 0; c < dim; ++c) ss += (double)xr[c] * xr[c];
+            const float ms = (float)(ss / dim);
+            const float rs = 1.0f / sqrtf(ms + eps);
+            for (int c = 0; c < dim; ++c) {
+                const float sc = ca[c] + (scale_b ? scale_b[c] : 0.0f);
+                const float sh = sa[c] + (shift_b ? shift_b[c] : 0.0f);
+                const float n = xr[c] * rs;
+                const float m = n * sc;
+                yr[c] = m + sh;
+            }
+        }
+    }
+}
+
+void orc_ada_out(float* x, const float* y, int dim, const int* sample_rows, int batch,
+                 const float* gate_a, const float* gate_b) {
+    long row = 0;
+    for (int b = 0; b < batch; ++b) {
+        const float* ga = gate_a + (long)b * dim;
+        for (int i = 0; i < sample_rows[b]; ++i, ++row) {
+            float* xr = x + row * dim;
+            const float* yr = y + row * dim;
+            for (int c = 0; c < dim; ++c) {
+                const float g = ga[c] + (gate_b ? gate_b[c] : 0.0f);
+                const float p = yr[c] * g;
+                xr[c] = xr[c] + p;
+            }
+        }
+    }
+}

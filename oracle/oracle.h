@@ -38,6 +38,12 @@
  *                     query rows equals the same rows of the full run.
  *   orc_vae_pixel_shuffle  torch reshape/permute (depth-to-space over time
  *                     and space) with the head-frame removal.
+ *   orc_ada_in        torch float64 rms_norm; unit-RMS rows at scale 1 and
+ *                     shift 0; invariance under scaling of a row (eps 0);
+ *                     per-sample constants identify each row's sample.
+ *   orc_ada_out       gate 0 leaves the stream bit-exact; gate 1 adds y
+ *                     bit-exact; per-sample constants identify each row's
+ *                     sample.
  *   orc_decomposed_conv3d  torch float64 conv3d over the temporally padded
  *                     input (frame 0 replicated head_frames times); a run
  *                     split into slices chained through the memory equals
@@ -164,6 +170,30 @@ void orc_apply_cfg(const float* positive, const float* negative, long count, flo
  * += delta * prediction[t][c], c < 16, as a product then a sum. */
 void orc_euler_step(float* latent, long channel_stride, const float* prediction, long tokens,
                     float delta);
+
+/* The norm and AdaSingle modulation around the DiT block's attention and MLP.
+ * The block graph takes six modulation inputs of [batch][hidden] floats
+ * (in4..in9, seedvr2_dit.cpp:441-448, 734-738); the operations between them
+ * and the hot path are ncnn built-ins of the exported .param, which is not in
+ * the reference.  They are restated from the published SeedVR2 NaDiT block:
+ * a norm without affine (RMSNorm), the modulation "in"
+ * h * (scale_a + scale_b) + (shift_a + shift_b) before the attention and the
+ * MLP, the modulation "out" h * (gate_a + gate_b), and the residual sum.
+ * The *_a vectors are the per-sample modulation inputs [batch][dim], the *_b
+ * vectors the block's own [dim] parameters (NULL: zero).
+ *
+ * orc_ada_in: row r of sample b (sample_rows[b] rows per sample, in order):
+ * out = (x * rs) * (scale_a[b] + scale_b) + (shift_a[b] + shift_b),
+ * rs = 1 / sqrt(mean(x^2) + eps), the mean of squares summed in double and
+ * rounded to float; every other operation fp32, in this order. */
+void orc_ada_in(const float* x, int dim, float eps, const int* sample_rows, int batch,
+                const float* shift_a, const float* scale_a, const float* shift_b,
+                const float* scale_b, float* out);
+
+/* orc_ada_out: x += y * (gate_a[b] + gate_b) per row of sample b, the
+ * gate sum, the product and the residual sum each rounded to fp32. */
+void orc_ada_out(float* x, const float* y, int dim, const int* sample_rows, int batch,
+                 const float* gate_a, const float* gate_b);
 
 /* The video tokens of SeedVR2Pipeline::predict (seedvr2_pipeline.cpp:296-317):
  * row t of destination [tokens][33] is latent channel 0..15 at t, condition

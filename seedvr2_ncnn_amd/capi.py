@@ -37,7 +37,7 @@ EXPORTS = (
     "s2_conv3d_output_shape", "s2_conv3d_packed_weight_bytes", "s2_conv3d_pack_weights",
     "s2_conv3d_memory_bytes", "s2_conv3d_workspace_bytes", "s2_conv3d_forward",
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
-    "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle",
+    "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
 )
 
 
@@ -154,6 +154,10 @@ def lib() -> ctypes.CDLL:
         L.s2_vae_pixel_shuffle.argtypes = [vp, ci, ci, ci, ci, ci, cl, ci, ci, ci, vp, cl, vp]
         L.s2_conv3d_forward.argtypes = [C3, vp, vp, vp, ci, ci, ci, ci, cl, vp, ci, vp, ci, cl, vp,
                                         vp, sz, vp]
+        L.s2_dit_ada_in.argtypes = [ci, cf, ci, P(ci), P(ci), vp, vp, ci, cl, vp, vp, vp, vp, vp,
+                                    vp, vp, vp, ci, cl, vp]
+        L.s2_dit_ada_out.argtypes = [ci, ci, P(ci), P(ci), vp, vp, ci, cl, vp, vp, ci, cl, vp, vp,
+                                     vp, vp, vp, cl, vp]
         _LIB = L
     return _LIB
 
@@ -367,6 +371,71 @@ def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, 
                                          _dtype_code(y_video), _stream(stream)),
           "s2_shared_linear_forward")
     return y_video, y_text
+
+
+# ---- DiT block: norm and AdaSingle modulation -------------------------------
+
+def _row_stride(*ts):
+    strides = {t.stride(0) for t in ts if t is not None and t.shape[0] > 0}
+    assert len(strides) <= 1, "the two streams must share one row stride"
+    for t in ts:
+        assert t is None or (t.dim() == 2 and t.stride(1) == 1)
+    return strides.pop() if strides else 0
+
+
+def ada_in(x_video, x_text, video_rows, text_rows, shift, scale, video_shift=None,
+           video_scale=None, text_shift=None, text_scale=None, eps=1e-5, out_dtype=None,
+           out_video=None, out_text=None, stream=None):
+    """s2_dit_ada_in: rmsnorm(x) * (scale[b] + *_scale) + (shift[b] + *_shift)
+    for both streams.  x_*: [rows, hidden] row views; shift/scale [batch, hidden]
+    fp32; video_rows/text_rows: rows per sample.  Returns (out_video, out_text)."""
+    import torch
+    hidden = x_video.shape[1]
+    batch = len(video_rows)
+    assert text_rows is None or len(text_rows) == batch
+    nt = 0 if text_rows is None else sum(int(r) for r in text_rows)
+    odt = out_dtype or x_video.dtype
+    if out_video is None:
+        out_video = torch.empty((x_video.shape[0], hidden), dtype=odt, device=x_video.device)
+    if out_text is None and nt:
+        out_text = torch.empty((nt, hidden), dtype=odt, device=x_video.device)
+    xs = _row_stride(x_video, x_text if nt else None)
+    os_ = _row_stride(out_video, out_text if nt else None)
+    check(lib().s2_dit_ada_in(hidden, float(eps), batch, _ints(video_rows),
+                              _ints(text_rows) if text_rows is not None else None,
+                              _ptr(x_video), _ptr(x_text) if nt else None,
+                              _dtype_code(x_video), xs or hidden, _ptr(shift), _ptr(scale),
+                              _ptr(video_shift), _ptr(video_scale), _ptr(text_shift),
+                              _ptr(text_scale), _ptr(out_video), _ptr(out_text) if nt else None,
+                              _dtype_code(out_video), os_ or hidden, _stream(stream)),
+          "s2_dit_ada_in")
+    return out_video, out_text
+
+
+def ada_out(x_video, x_text, y_video, y_text, video_rows, text_rows, gate, video_gate=None,
+            text_gate=None, out_video=None, out_text=None, stream=None):
+    """s2_dit_ada_out: x + y * (gate[b] + *_gate) for both streams; by
+    default in place (out = x).  Returns (out_video, out_text)."""
+    hidden = x_video.shape[1]
+    batch = len(video_rows)
+    nt = 0 if text_rows is None else sum(int(r) for r in text_rows)
+    if out_video is None:
+        out_video = x_video
+    if out_text is None and nt:
+        out_text = x_text
+    assert out_video.dtype == x_video.dtype
+    xs = _row_stride(x_video, x_text if nt else None)
+    ys = _row_stride(y_video, y_text if nt else None)
+    os_ = _row_stride(out_video, out_text if nt else None)
+    check(lib().s2_dit_ada_out(hidden, batch, _ints(video_rows),
+                               _ints(text_rows) if text_rows is not None else None,
+                               _ptr(x_video), _ptr(x_text) if nt else None,
+                               _dtype_code(x_video), xs or hidden, _ptr(y_video),
+                               _ptr(y_text) if nt else None, _dtype_code(y_video), ys or hidden,
+                               _ptr(gate), _ptr(video_gate), _ptr(text_gate), _ptr(out_video),
+                               _ptr(out_text) if nt else None, os_ or hidden, _stream(stream)),
+          "s2_dit_ada_out")
+    return out_video, out_text
 
 
 # ---- DiT frontend and tail, sampler step -------------------------------------

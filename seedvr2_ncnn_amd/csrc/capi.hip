@@ -1,4 +1,5 @@
 // extern "C" boundary of the window-attention hot path (include/seedvr2_hip.h).
+#include <limits.h>
 #include <string.h>
 
 #include <algorithm>
@@ -8,6 +9,7 @@
 
 #include "awa_kernels.h"
 #include "awa_plan.h"
+#include "block_kernels.h"
 #include "conv3d_kernels.h"
 #include "mha_kernels.h"
 #include "pipeline_kernels.h"
@@ -658,6 +660,128 @@ int s2_denoise_update(const float* positive_patches, const float* negative_patch
     S2_HIP(s2::launch_denoise_update(positive_patches, negative_patches, frames, height, width,
                                      cfg_scale, cfg_rescale, delta, latent, channel_stride,
                                      (hipStream_t)stream));
+    return S2_OK;
+}
+
+/* ---- DiT block: norm and AdaSingle modulation ---------------------------- */
+
+namespace {
+
+// The two streams' per-sample row counts as kernel row tables; the stream
+// pointers and strides are checked against the rows they must cover.
+int ada_rows(int hidden, int batch, const int* video_rows, const int* text_rows,
+             s2::AdaRows* rows) {
+    if (hidden <= 0 || hidden % 4 != 0 || hidden > s2::kAdaMaxDim)
+        return fail(S2_ERR_INVALID, "hidden size must be a positive multiple of 4, at most 4096");
+    if (batch <= 0 || batch > s2::kAdaMaxBatch)
+        return fail(S2_ERR_INVALID, "batch must be 1..64");
+    if (!video_rows) return fail(S2_ERR_INVALID, "null row counts");
+    memset(rows, 0, sizeof(*rows));
+    rows->batch = batch;
+    long v = 0, t = 0;
+    for (int b = 0; b < batch; ++b) {
+        const int tr = text_rows ? text_rows[b] : 0;
+        if (video_rows[b] < 0 || tr < 0) return fail(S2_ERR_INVALID, "negative row count");
+        v += video_rows[b];
+        t += tr;
+        if (v + t > INT_MAX) return fail(S2_ERR_INVALID, "too many rows");
+        rows->end[b] = (int)v;
+        rows->end[s2::kAdaMaxBatch + b] = (int)t;
+    }
+    rows->video_rows = (int)v;
+    rows->text_rows = (int)t;
+    return S2_OK;
+}
+
+// a stream of `n` rows: pointer, row stride (elements) and alignment
+bool ada_stream_ok(const void* p, int n, long stride, int hidden, s2_dtype dt) {
+    if (n == 0) return true;
+    return p && stride >= hidden && stride % 4 == 0 && aligned(p, dt == S2_DTYPE_F32 ? 16 : 8);
+}
+
+bool ada_vec_ok(const float* p) { return !p || aligned(p, 16); }
+
+}  // namespace
+
+int s2_dit_ada_in(int hidden, float epsilon, int batch, const int* video_rows,
+                  const int* text_rows, const void* x_video, const void* x_text, s2_dtype x_dtype,
+                  long x_stride, const float* shift, const float* scale, const float* video_shift,
+                  const float* video_scale, const float* text_shift, const float* text_scale,
+                  void* out_video, void* out_text, s2_dtype out_dtype, long out_stride,
+                  s2_stream_t stream) {
+    s2::AdaInArgs a;
+    const int rc = ada_rows(hidden, batch, video_rows, text_rows, &a.rows);
+    if (rc != S2_OK) return rc;
+    if (!dtype_ok(x_dtype) || !dtype_ok(out_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (!(epsilon >= 0.f)) return fail(S2_ERR_INVALID, "epsilon must be >= 0");
+    const int nv = a.rows.video_rows, nt = a.rows.text_rows;
+    if (!ada_stream_ok(x_video, nv, x_stride, hidden, x_dtype) ||
+        !ada_stream_ok(x_text, nt, x_stride, hidden, x_dtype) ||
+        !ada_stream_ok(out_video, nv, out_stride, hidden, out_dtype) ||
+        !ada_stream_ok(out_text, nt, out_stride, hidden, out_dtype))
+        return fail(S2_ERR_INVALID, "stream pointer, row stride (>= hidden, multiple of 4) or alignment");
+    if (!shift || !scale || !aligned(shift, 16) || !aligned(scale, 16) || !ada_vec_ok(video_shift) ||
+        !ada_vec_ok(video_scale) || !ada_vec_ok(text_shift) || !ada_vec_ok(text_scale))
+        return fail(S2_ERR_INVALID, "modulation vectors must be non-null (shift, scale) and 16-byte aligned");
+    a.x[0] = x_video;
+    a.x[1] = x_text;
+    a.x_stride = x_stride;
+    a.x_kind = (int)x_dtype;
+    a.out[0] = out_video;
+    a.out[1] = out_text;
+    a.out_stride = out_stride;
+    a.out_kind = (int)out_dtype;
+    a.dim = hidden;
+    a.eps = epsilon;
+    a.shift_a = shift;
+    a.scale_a = scale;
+    a.shift_b[0] = video_shift;
+    a.shift_b[1] = text_shift;
+    a.scale_b[0] = video_scale;
+    a.scale_b[1] = text_scale;
+    S2_HIP(s2::launch_ada_in(a, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_dit_ada_out(int hidden, int batch, const int* video_rows, const int* text_rows,
+                   const void* x_video, const void* x_text, s2_dtype x_dtype, long x_stride,
+                   const void* y_video, const void* y_text, s2_dtype y_dtype, long y_stride,
+                   const float* gate, const float* video_gate, const float* text_gate,
+                   void* out_video, void* out_text, long out_stride, s2_stream_t stream) {
+    s2::AdaOutArgs a;
+    const int rc = ada_rows(hidden, batch, video_rows, text_rows, &a.rows);
+    if (rc != S2_OK) return rc;
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    const int nv = a.rows.video_rows, nt = a.rows.text_rows;
+    if (!ada_stream_ok(x_video, nv, x_stride, hidden, x_dtype) ||
+        !ada_stream_ok(x_text, nt, x_stride, hidden, x_dtype) ||
+        !ada_stream_ok(y_video, nv, y_stride, hidden, y_dtype) ||
+        !ada_stream_ok(y_text, nt, y_stride, hidden, y_dtype) ||
+        !ada_stream_ok(out_video, nv, out_stride, hidden, x_dtype) ||
+        !ada_stream_ok(out_text, nt, out_stride, hidden, x_dtype))
+        return fail(S2_ERR_INVALID, "stream pointer, row stride (>= hidden, multiple of 4) or alignment");
+    // in place needs the output rows to be the input rows
+    if ((out_video == x_video && nv > 0 && out_stride != x_stride) ||
+        (out_text == x_text && nt > 0 && out_stride != x_stride))
+        return fail(S2_ERR_INVALID, "in-place output must keep the residual's row stride");
+    if (!gate || !aligned(gate, 16) || !ada_vec_ok(video_gate) || !ada_vec_ok(text_gate))
+        return fail(S2_ERR_INVALID, "gate vectors must be non-null (gate) and 16-byte aligned");
+    a.x[0] = x_video;
+    a.x[1] = x_text;
+    a.x_stride = x_stride;
+    a.x_kind = (int)x_dtype;
+    a.y[0] = y_video;
+    a.y[1] = y_text;
+    a.y_stride = y_stride;
+    a.y_kind = (int)y_dtype;
+    a.out[0] = out_video;
+    a.out[1] = out_text;
+    a.out_stride = out_stride;
+    a.dim = hidden;
+    a.gate_a = gate;
+    a.gate_b[0] = video_gate;
+    a.gate_b[1] = text_gate;
+    S2_HIP(s2::launch_ada_out(a, (hipStream_t)stream));
     return S2_OK;
 }
 

@@ -55,3 +55,32 @@ def test_latent_patches_and_steps_reject_bad_arguments(L):
     assert L.s2_denoise_update(FAKE, None, 2, 3, 4, 1.0, 0.0, 0.1, FAKE, 32, None) == INVALID
     assert L.s2_denoise_update(FAKE, ctypes.c_void_p(0x10004), 2, 4, 4, 1.0, 0.0, 0.1, FAKE, 32,
                                None) == INVALID
+
+
+def test_block_modulation_rejects_bad_arguments(L):
+    rows = _shapes((4,))
+    F32, BF16 = capi.DTYPE_F32, capi.DTYPE_BF16
+
+    def ada_in(hidden=64, batch=1, vr=rows, x=FAKE, xs=64, shift=FAKE, out=FAKE, os_=64, eps=1e-5):
+        return L.s2_dit_ada_in(hidden, eps, batch, vr, None, x, None, F32, xs, shift, FAKE, None,
+                               None, None, None, out, None, BF16, os_, None)
+
+    assert ada_in(hidden=62, xs=62, os_=62) == INVALID      # hidden not a multiple of 4
+    assert ada_in(hidden=4100, xs=4100, os_=4100) == INVALID   # wider than 4096
+    assert ada_in(batch=0) == INVALID
+    assert ada_in(batch=65, vr=_shapes(tuple([1] * 65))) == INVALID
+    assert ada_in(vr=_shapes((-1,))) == INVALID
+    assert ada_in(xs=60) == INVALID                         # stride below hidden
+    assert ada_in(x=ctypes.c_void_p(0x10008)) == INVALID    # fp32 rows need 16 bytes
+    assert ada_in(shift=None) == INVALID
+    assert ada_in(eps=-1.0) == INVALID
+    assert ada_in(vr=_shapes((0,))) == capi.S2_OK           # no rows: nothing to do
+
+    def ada_out(x=FAKE, xs=64, out=FAKE, os_=64, gate=FAKE, y=FAKE):
+        return L.s2_dit_ada_out(64, 1, rows, None, x, None, F32, xs, y, None, BF16, 64, gate,
+                                None, None, out, None, os_, None)
+
+    assert ada_out(gate=None) == INVALID
+    assert ada_out(y=None) == INVALID
+    assert ada_out(out=FAKE, xs=64, os_=128) == INVALID     # in place with another stride
+    assert ada_out(gate=ctypes.c_void_p(0x10004)) == INVALID
