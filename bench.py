@@ -545,11 +545,12 @@ def main():
     def full_block(steps, warmup):
         """The whole block around the hot path (regular windows): an fp32
         residual stream, the norm and AdaSingle modulation before the
-        attention and the MLP (s2_dit_ada_in, bf16 out) and the gate and
-        residual sum after them (s2_dit_ada_out, in place).  Algorithmic
-        bytes: ada_in reads fp32 and writes bf16 rows, 6 B per value;
-        ada_out reads the fp32 residual and the bf16 branch output and
-        writes the residual, 10 B per value."""
+        attention (s2_dit_ada_in, bf16 out), the attention's gate and
+        residual sum fused with the MLP's norm and modulation
+        (s2_dit_ada_out_in) and the MLP's gate and residual sum
+        (s2_dit_ada_out, in place).  Algorithmic bytes per value: 6 (fp32
+        in, bf16 out), 12 (fp32 residual and bf16 branch in, fp32 residual
+        and bf16 out) and 10 (fp32 residual and bf16 branch in, fp32 out)."""
         res_v = torch.randn(lv, HIDDEN, generator=gen, device=dev)
         res_t = torch.randn(lt, HIDDEN, generator=gen, device=dev)
         mods = {k: torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1 + (1.0 if k.endswith("scale") else 0.0)
@@ -557,8 +558,9 @@ def main():
         hin_v = torch.empty(lv, HIDDEN, dtype=bf, device=dev)
         hin_t = torch.empty(lt, HIDDEN, dtype=bf, device=dev)
         vr, tr = [lv], [lt]
-        fops = ["attn_norm_modulate", "qkv", "attention", "out", "attn_gate_residual",
-                "mlp_norm_modulate", "mlp_up", "mlp_down", "mlp_gate_residual"]
+        fops = ["attn_norm_modulate", "qkv", "attention", "out",
+                "attn_gate_residual_mlp_norm_modulate", "mlp_up", "mlp_down",
+                "mlp_gate_residual"]
 
         def fstep(ev=None):
             def mark(i):
@@ -578,22 +580,22 @@ def main():
             mark(3)
             capi.shared_linear(a_v, a_t, w_o, b[HIDDEN], capi.ACT_NONE, y_video=o_v, y_text=o_t)
             mark(4)
-            capi.ada_out(res_v, res_t, o_v, o_t, vr, tr, mods["attn_gate"])
+            # the attention's gate and residual sum with the MLP's norm and
+            # modulation, one pass over the residual stream
+            capi.ada_out_in(res_v, res_t, o_v, o_t, vr, tr, mods["attn_gate"], mods["mlp_shift"],
+                            mods["mlp_scale"], h_video=hin_v, h_text=hin_t)
             mark(5)
-            capi.ada_in(res_v, res_t, vr, tr, mods["mlp_shift"], mods["mlp_scale"],
-                        out_video=hin_v, out_text=hin_t)
-            mark(6)
             capi.shared_linear(hin_v, hin_t, w_up, b[MLP], capi.ACT_GELU, y_video=h_v, y_text=h_t)
-            mark(7)
+            mark(6)
             capi.shared_linear(h_v, h_t, w_dn, b[HIDDEN], capi.ACT_NONE, y_video=y_v, y_text=y_t)
-            mark(8)
+            mark(7)
             capi.ada_out(res_v, res_t, y_v, y_t, vr, tr, mods["mlp_gate"])
-            mark(9)
+            mark(8)
 
         for _ in range(warmup):
             fstep()
         torch.cuda.synchronize()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(10)] for _ in range(steps)]
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(9)] for _ in range(steps)]
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for i in range(steps):
@@ -603,18 +605,18 @@ def main():
         assert bool(torch.isfinite(res_v).all())
         per = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(fops)}
         m_rows = lv + lt
-        in_bytes, out_bytes = 6.0 * m_rows * HIDDEN, 10.0 * m_rows * HIDDEN
-        ada_in_ms = (per["attn_norm_modulate"] + per["mlp_norm_modulate"]) / 2
-        ada_out_ms = (per["attn_gate_residual"] + per["mlp_gate_residual"]) / 2
+
+        def hbm(op, bytes_per_value):
+            nbytes = bytes_per_value * m_rows * HIDDEN
+            return {"ms": round(per[op], 4), "algorithmic_bytes": int(nbytes),
+                    "gbs": round(nbytes / (per[op] * 1e-3) / 1e9, 1),
+                    "frac_hbm_peak": round(nbytes / (per[op] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
         return {
             "ms": round(start.elapsed_time(end) / steps, 4),
             "ops_ms": {op: round(v, 4) for op, v in per.items()},
-            "norm_modulate": {"ms": round(ada_in_ms, 4), "algorithmic_bytes": int(in_bytes),
-                              "gbs": round(in_bytes / (ada_in_ms * 1e-3) / 1e9, 1),
-                              "frac_hbm_peak": round(in_bytes / (ada_in_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
-            "gate_residual": {"ms": round(ada_out_ms, 4), "algorithmic_bytes": int(out_bytes),
-                              "gbs": round(out_bytes / (ada_out_ms * 1e-3) / 1e9, 1),
-                              "frac_hbm_peak": round(out_bytes / (ada_out_ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)},
+            "norm_modulate": hbm("attn_norm_modulate", 6.0),
+            "gate_residual_norm_modulate": hbm("attn_gate_residual_mlp_norm_modulate", 12.0),
+            "gate_residual": hbm("mlp_gate_residual", 10.0),
             "note": "fp32 residual stream; per-sample modulation vectors; regular windows",
         }
 

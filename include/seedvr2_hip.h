@@ -299,6 +299,23 @@ S2_API int s2_dit_ada_out(int hidden, int batch, const int* video_rows, const in
                           const float* video_gate, const float* text_gate, void* out_video,
                           void* out_text, long out_stride, s2_stream_t stream);
 
+/* s2_dit_ada_out and then s2_dit_ada_in on its output in one pass over the
+ * residual stream: out = x + y * (gate[b] + *_gate), and h = rmsnorm(out) *
+ * (scale[b] + *_scale) + (shift[b] + *_shift), the norm taken over out as
+ * stored.  The attention branch's gate and residual sum with the MLP's norm
+ * and modulation (or the MLP's with the next block's).  h must not overlap
+ * x, y or out. */
+S2_API int s2_dit_ada_out_in(int hidden, int batch, const int* video_rows, const int* text_rows,
+                             const void* x_video, const void* x_text, s2_dtype x_dtype,
+                             long x_stride, const void* y_video, const void* y_text,
+                             s2_dtype y_dtype, long y_stride, const float* gate,
+                             const float* video_gate, const float* text_gate, void* out_video,
+                             void* out_text, long out_stride, float epsilon, const float* shift,
+                             const float* scale, const float* video_shift,
+                             const float* video_scale, const float* text_shift,
+                             const float* text_scale, void* h_video, void* h_text,
+                             s2_dtype h_dtype, long h_stride, s2_stream_t stream);
+
 /* ---- DecomposedConv3D (VAE) ---------------------------------------------- */
 /* The causal 3-D convolution of the VAE (src/seedvr2/decomposed_conv3d.h:33-88,
  * decomposed_conv3d.cpp:605-755) as one implicit GEMM on the matrix cores:

@@ -38,6 +38,7 @@ EXPORTS = (
     "s2_conv3d_memory_bytes", "s2_conv3d_workspace_bytes", "s2_conv3d_forward",
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
+    "s2_dit_ada_out_in",
 )
 
 
@@ -158,6 +159,9 @@ def lib() -> ctypes.CDLL:
                                     vp, vp, vp, ci, cl, vp]
         L.s2_dit_ada_out.argtypes = [ci, ci, P(ci), P(ci), vp, vp, ci, cl, vp, vp, ci, cl, vp, vp,
                                      vp, vp, vp, cl, vp]
+        L.s2_dit_ada_out_in.argtypes = [ci, ci, P(ci), P(ci), vp, vp, ci, cl, vp, vp, ci, cl, vp,
+                                        vp, vp, vp, vp, cl, cf, vp, vp, vp, vp, vp, vp, vp, vp,
+                                        ci, cl, vp]
         _LIB = L
     return _LIB
 
@@ -436,6 +440,44 @@ def ada_out(x_video, x_text, y_video, y_text, video_rows, text_rows, gate, video
                                _ptr(out_text) if nt else None, os_ or hidden, _stream(stream)),
           "s2_dit_ada_out")
     return out_video, out_text
+
+
+def ada_out_in(x_video, x_text, y_video, y_text, video_rows, text_rows, gate, shift, scale,
+               video_gate=None, text_gate=None, video_shift=None, video_scale=None,
+               text_shift=None, text_scale=None, eps=1e-5, h_dtype=None, h_video=None,
+               h_text=None, out_video=None, out_text=None, stream=None):
+    """s2_dit_ada_out_in: x += y * gate (in place by default), then
+    h = rmsnorm(x) * scale + shift.  Returns (out_video, out_text, h_video, h_text)."""
+    import torch
+    hidden = x_video.shape[1]
+    batch = len(video_rows)
+    nt = 0 if text_rows is None else sum(int(r) for r in text_rows)
+    hdt = h_dtype or torch.bfloat16
+    if out_video is None:
+        out_video = x_video
+    if out_text is None and nt:
+        out_text = x_text
+    if h_video is None:
+        h_video = torch.empty((x_video.shape[0], hidden), dtype=hdt, device=x_video.device)
+    if h_text is None and nt:
+        h_text = torch.empty((nt, hidden), dtype=hdt, device=x_video.device)
+    xs = _row_stride(x_video, x_text if nt else None)
+    ys = _row_stride(y_video, y_text if nt else None)
+    os_ = _row_stride(out_video, out_text if nt else None)
+    hs = _row_stride(h_video, h_text if nt else None)
+    check(lib().s2_dit_ada_out_in(hidden, batch, _ints(video_rows),
+                                  _ints(text_rows) if text_rows is not None else None,
+                                  _ptr(x_video), _ptr(x_text) if nt else None,
+                                  _dtype_code(x_video), xs or hidden, _ptr(y_video),
+                                  _ptr(y_text) if nt else None, _dtype_code(y_video),
+                                  ys or hidden, _ptr(gate), _ptr(video_gate), _ptr(text_gate),
+                                  _ptr(out_video), _ptr(out_text) if nt else None, os_ or hidden,
+                                  float(eps), _ptr(shift), _ptr(scale), _ptr(video_shift),
+                                  _ptr(video_scale), _ptr(text_shift), _ptr(text_scale),
+                                  _ptr(h_video), _ptr(h_text) if nt else None,
+                                  _dtype_code(h_video), hs or hidden, _stream(stream)),
+          "s2_dit_ada_out_in")
+    return out_video, out_text, h_video, h_text
 
 
 # ---- DiT frontend and tail, sampler step -------------------------------------

@@ -53,11 +53,23 @@ struct AdaOutArgs {
     const float* gate_a;      // [batch][dim]
     const float* gate_b[2];   // [dim] per stream, or null
     AdaRows rows;
+    // norm != 0: also h = norm(out) * (scale_a[b] + scale_b) + (shift_a[b] +
+    // shift_b) of the stored out rows, into h (element type h_kind)
+    int norm;
+    void* h[2];
+    long h_stride;
+    int h_kind;
+    float eps;
+    const float* shift_a;
+    const float* scale_a;
+    const float* shift_b[2];
+    const float* scale_b[2];
 };
 
 // out = norm(x) * (scale_a[b] + scale_b) + (shift_a[b] + shift_b)
 hipError_t launch_ada_in(const AdaInArgs& a, hipStream_t stream);
-// out = x + y * (gate_a[b] + gate_b)
+// out = x + y * (gate_a[b] + gate_b), and with a.norm the modulated norm of
+// out (the next ada_in) in the same pass
 hipError_t launch_ada_out(const AdaOutArgs& a, hipStream_t stream);
 
 }  // namespace s2

@@ -4,14 +4,21 @@
 // block graph receives the per-sample modulation vectors as its inputs
 // in4..in9 (src/seedvr2/seedvr2_dit.cpp:441-448, 734-738).
 //
-// Both kernels are HBM-bound streams over [rows][dim].  A workgroup of four
-// waves owns 16 consecutive rows; a wave holds one row at a time in
-// registers (NG float4 per lane), so each row is read from HBM once.  The
-// workgroup sums the modulation vectors of its first row's sample once into
-// LDS; a row of another sample (at most one boundary per few workgroups)
-// sums them from global memory.
+// Both kernels are HBM-bound streams over [rows][dim].  The grid is
+// persistent (as many workgroups as fit on the device at once); workgroup i
+// takes the groups of four consecutive rows i, i + grid, ..., one row per
+// wave, held in registers (NG float4 per lane), so each row is read from HBM
+// once.  The workgroup keeps the summed modulation vectors of the sample of
+// its current group's first row in LDS and refills them only when that
+// sample changes (never, for one sample); a row of another sample than its
+// group's first sums them from global memory.
 
 #include <math.h>
+
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <utility>
 
 #include "block_kernels.h"
 #include "s2_device.h"
@@ -21,8 +28,7 @@
 namespace s2 {
 namespace {
 
-constexpr int kRows = 4;   // rows per wave
-constexpr int kBlockRows = 4 * kRows;
+constexpr int kBlockRows = 4;   // rows per workgroup and group, one per wave
 
 template <int K>
 __device__ __forceinline__ void load4(const void* base, long idx, float (&v)[4]) {
@@ -60,28 +66,82 @@ __device__ __forceinline__ void locate(const AdaRows& rows, int r, int& stream, 
     sample = b;
 }
 
-// shared memory of a workgroup: up to two summed vectors of kAdaMaxDim
+// shared memory of a workgroup: up to three summed vectors of kAdaMaxDim
 extern __shared__ float4 ada_lds[];
+
+// Writes norm(v) * sc + sh of the row held in v (NG float4 per lane) to row
+// `oo` of o (element type ok).  sc / sh come from LDS when `home`, else are
+// summed from the sample's vectors.
+template <int NG>
+__device__ __forceinline__ void norm_modulate(const float (&v)[NG][4], int lane, int dim, float eps,
+                                              bool home, const float4* lsc, const float4* lsh,
+                                              const float* sca, const float* scb, const float* sha,
+                                              const float* shb, void* o, long oo, int ok) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ss += v[i][e] * v[i][e];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    const float rs = 1.0f / sqrtf(ss / (float)dim + eps);
+#pragma unroll
+    for (int i = 0; i < NG; ++i) {
+        const int c = (i * 64 + lane) * 4;
+        if (c >= dim) break;
+        float4 sc4, sh4;
+        if (home) {
+            sc4 = lsc[c / 4];
+            sh4 = lsh[c / 4];
+        } else {
+            sc4 = sum4(sca, scb, c);
+            sh4 = sum4(sha, shb, c);
+        }
+        const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
+        const float sh[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
+        float r[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float n = v[i][e] * rs;
+            const float m = n * sc[e];
+            r[e] = m + sh[e];
+        }
+        store4(o, oo + c, r[0], r[1], r[2], r[3], ok);
+    }
+}
+
+// the value an element of type K stores for x
+template <int K>
+__device__ __forceinline__ float stored(float x) {
+    if (K == 1) return bf16_to_f32(f32_to_bf16(x));
+    if (K == 2) return (float)(_Float16)x;
+    return x;
+}
 
 template <int NG, int XK, int OK>
 __global__ __launch_bounds__(256) void ada_in_kernel(AdaInArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int total = a.rows.video_rows + a.rows.text_rows;
-    const int rb = blockIdx.x * kBlockRows;
+    const int groups = (total + kBlockRows - 1) / kBlockRows;
     const int g4 = a.dim / 4;
     float4* lsc = ada_lds;
     float4* lsh = ada_lds + g4;
-    int hs, hl, hb;
-    locate(a.rows, rb, hs, hl, hb);
-    for (int i = threadIdx.x; i < g4; i += 256) {
-        lsc[i] = sum4(a.scale_a + (long)hb * a.dim, a.scale_b[hs], 4 * i);
-        lsh[i] = sum4(a.shift_a + (long)hb * a.dim, a.shift_b[hs], 4 * i);
-    }
-    __syncthreads();
-    for (int k = 0; k < kRows; ++k) {
-        const int r = rb + wave * kRows + k;
-        if (r >= total) break;
+    int cur = -1;   // (stream, sample) of the vectors in LDS
+    for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+        int hs, hl, hb;
+        locate(a.rows, grp * kBlockRows, hs, hl, hb);
+        if (hs * kAdaMaxBatch + hb != cur) {   // uniform over the workgroup
+            cur = hs * kAdaMaxBatch + hb;
+            __syncthreads();   // the old vectors are no longer read
+            for (int i = threadIdx.x; i < g4; i += 256) {
+                lsc[i] = sum4(a.scale_a + (long)hb * a.dim, a.scale_b[hs], 4 * i);
+                lsh[i] = sum4(a.shift_a + (long)hb * a.dim, a.shift_b[hs], 4 * i);
+            }
+            __syncthreads();
+        }
+        const int r = grp * kBlockRows + wave;
+        if (r >= total) continue;
         int stream, local, b;
         locate(a.rows, r, stream, local, b);
         const bool home = stream == hs && b == hb;
@@ -97,58 +157,40 @@ __global__ __launch_bounds__(256) void ada_in_kernel(AdaInArgs a) {
                 v[i][0] = v[i][1] = v[i][2] = v[i][3] = 0.f;
             }
         }
-        float ss = 0.f;
-#pragma unroll
-        for (int i = 0; i < NG; ++i)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) ss += v[i][e] * v[i][e];
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-        const float rs = 1.0f / sqrtf(ss / (float)a.dim + a.eps);
-        void* orow = stream ? a.out[1] : a.out[0];
-        const long oo = (long)local * a.out_stride;
-#pragma unroll
-        for (int i = 0; i < NG; ++i) {
-            const int c = (i * 64 + lane) * 4;
-            if (c >= a.dim) break;
-            float4 sc4, sh4;
-            if (home) {
-                sc4 = lsc[c / 4];
-                sh4 = lsh[c / 4];
-            } else {
-                sc4 = sum4(a.scale_a + (long)b * a.dim, a.scale_b[stream], c);
-                sh4 = sum4(a.shift_a + (long)b * a.dim, a.shift_b[stream], c);
-            }
-            const float sc[4] = {sc4.x, sc4.y, sc4.z, sc4.w};
-            const float sh[4] = {sh4.x, sh4.y, sh4.z, sh4.w};
-            float o[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float n = v[i][e] * rs;
-                const float m = n * sc[e];
-                o[e] = m + sh[e];
-            }
-            store4(orow, oo + c, o[0], o[1], o[2], o[3], OK);
-        }
+        norm_modulate<NG>(v, lane, a.dim, a.eps, home, lsc, lsh, a.scale_a + (long)b * a.dim,
+                          a.scale_b[stream], a.shift_a + (long)b * a.dim, a.shift_b[stream],
+                          stream ? a.out[1] : a.out[0], (long)local * a.out_stride, OK);
     }
 }
 
-template <int NG, int XK, int YK>
+template <int NG, int XK, int YK, bool NORM>
 __global__ __launch_bounds__(256) void ada_out_kernel(AdaOutArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
     const int total = a.rows.video_rows + a.rows.text_rows;
-    const int rb = blockIdx.x * kBlockRows;
+    const int groups = (total + kBlockRows - 1) / kBlockRows;
     const int g4 = a.dim / 4;
     float4* lgt = ada_lds;
-    int hs, hl, hb;
-    locate(a.rows, rb, hs, hl, hb);
-    for (int i = threadIdx.x; i < g4; i += 256)
-        lgt[i] = sum4(a.gate_a + (long)hb * a.dim, a.gate_b[hs], 4 * i);
-    __syncthreads();
-    for (int k = 0; k < kRows; ++k) {
-        const int r = rb + wave * kRows + k;
-        if (r >= total) break;
+    float4* lsc = ada_lds + g4;
+    float4* lsh = ada_lds + 2 * g4;
+    int cur = -1;
+    for (int grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+        int hs, hl, hb;
+        locate(a.rows, grp * kBlockRows, hs, hl, hb);
+        if (hs * kAdaMaxBatch + hb != cur) {   // uniform over the workgroup
+            cur = hs * kAdaMaxBatch + hb;
+            __syncthreads();
+            for (int i = threadIdx.x; i < g4; i += 256) {
+                lgt[i] = sum4(a.gate_a + (long)hb * a.dim, a.gate_b[hs], 4 * i);
+                if (NORM) {
+                    lsc[i] = sum4(a.scale_a + (long)hb * a.dim, a.scale_b[hs], 4 * i);
+                    lsh[i] = sum4(a.shift_a + (long)hb * a.dim, a.shift_b[hs], 4 * i);
+                }
+            }
+            __syncthreads();
+        }
+        const int r = grp * kBlockRows + wave;
+        if (r >= total) continue;
         int stream, local, b;
         locate(a.rows, r, stream, local, b);
         const bool home = stream == hs && b == hb;
@@ -161,9 +203,13 @@ __global__ __launch_bounds__(256) void ada_out_kernel(AdaOutArgs a) {
 #pragma unroll
         for (int i = 0; i < NG; ++i) {
             const int c = (i * 64 + lane) * 4;
-            if (c >= a.dim) break;
-            load4<XK>(xr, xo + c, xv[i]);
-            load4<YK>(yr, yo + c, yv[i]);
+            if (c < a.dim) {
+                load4<XK>(xr, xo + c, xv[i]);
+                load4<YK>(yr, yo + c, yv[i]);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[i][e] = yv[i][e] = 0.f;
+            }
         }
 #pragma unroll
         for (int i = 0; i < NG; ++i) {
@@ -172,19 +218,53 @@ __global__ __launch_bounds__(256) void ada_out_kernel(AdaOutArgs a) {
             const float4 g4v = home ? lgt[c / 4]
                                     : sum4(a.gate_a + (long)b * a.dim, a.gate_b[stream], c);
             const float g[4] = {g4v.x, g4v.y, g4v.z, g4v.w};
-            float o[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const float p = yv[i][e] * g[e];
-                o[e] = xv[i][e] + p;
+                xv[i][e] = xv[i][e] + p;
             }
-            store4(orow, oo + c, o[0], o[1], o[2], o[3], XK);
+            store4(orow, oo + c, xv[i][0], xv[i][1], xv[i][2], xv[i][3], XK);
+            if (NORM) {
+                // the norm reads the residual as stored
+#pragma unroll
+                for (int e = 0; e < 4; ++e) xv[i][e] = stored<XK>(xv[i][e]);
+            }
         }
+        if (NORM)
+            norm_modulate<NG>(xv, lane, a.dim, a.eps, home, lsc, lsh, a.scale_a + (long)b * a.dim,
+                              a.scale_b[stream], a.shift_a + (long)b * a.dim, a.shift_b[stream],
+                              stream ? a.h[1] : a.h[0], (long)local * a.h_stride, a.h_kind);
     }
 }
 
-unsigned ada_blocks(const AdaRows& r) {
-    return (unsigned)(((long)r.video_rows + r.text_rows + kBlockRows - 1) / kBlockRows);
+// Workgroups of a persistent launch of `func`: as many as fit on the device
+// at once (the occupancy of that kernel at `lds` bytes, per device), at most
+// one per group of rows.
+unsigned persistent_grid(const void* func, size_t lds, const AdaRows& r) {
+    static std::mutex mu;
+    static std::map<std::pair<int, std::pair<const void*, size_t>>, int> cache;
+    const long groups = ((long)r.video_rows + r.text_rows + kBlockRows - 1) / kBlockRows;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return (unsigned)groups;
+    int slots = 0;
+    {
+        std::lock_guard<std::mutex> lock(mu);
+        const auto key = std::make_pair(dev, std::make_pair(func, lds));
+        auto it = cache.find(key);
+        if (it != cache.end()) {
+            slots = it->second;
+        } else {
+            int per_cu = 0, cus = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, func, 256, lds) !=
+                    hipSuccess ||
+                hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                    hipSuccess)
+                return (unsigned)groups;
+            slots = std::max(1, per_cu) * std::max(1, cus);
+            cache[key] = slots;
+        }
+    }
+    return (unsigned)std::min<long>(groups, slots);
 }
 
 // float4 groups per lane for a row of `dim` values
@@ -193,16 +273,21 @@ int ada_groups(int dim) {
     return g <= 4 ? 4 : g <= 8 ? 8 : g <= 10 ? 10 : g <= 12 ? 12 : 16;
 }
 
+template <int NG, int XK, int OK>
+void ada_in_launch(const AdaInArgs& a, hipStream_t stream) {
+    const size_t lds = 2 * (size_t)a.dim * sizeof(float);
+    const void* f = reinterpret_cast<const void*>(&ada_in_kernel<NG, XK, OK>);
+    ada_in_kernel<NG, XK, OK><<<persistent_grid(f, lds, a.rows), 256, lds, stream>>>(a);
+}
+
 template <int NG, int XK>
 void ada_in_launch(const AdaInArgs& a, hipStream_t stream) {
-    const unsigned grid = ada_blocks(a.rows);
-    const size_t lds = 2 * (size_t)a.dim * sizeof(float);
     if (a.out_kind == 1)
-        ada_in_kernel<NG, XK, 1><<<grid, 256, lds, stream>>>(a);
+        ada_in_launch<NG, XK, 1>(a, stream);
     else if (a.out_kind == 2)
-        ada_in_kernel<NG, XK, 2><<<grid, 256, lds, stream>>>(a);
+        ada_in_launch<NG, XK, 2>(a, stream);
     else
-        ada_in_kernel<NG, XK, 0><<<grid, 256, lds, stream>>>(a);
+        ada_in_launch<NG, XK, 0>(a, stream);
 }
 
 template <int NG>
@@ -215,16 +300,29 @@ void ada_in_x_kind(const AdaInArgs& a, hipStream_t stream) {
         ada_in_launch<NG, 0>(a, stream);
 }
 
+template <int NG, int XK, int YK, bool NORM>
+void ada_out_launch(const AdaOutArgs& a, hipStream_t stream) {
+    const size_t lds = (NORM ? 3 : 1) * (size_t)a.dim * sizeof(float);
+    const void* f = reinterpret_cast<const void*>(&ada_out_kernel<NG, XK, YK, NORM>);
+    ada_out_kernel<NG, XK, YK, NORM><<<persistent_grid(f, lds, a.rows), 256, lds, stream>>>(a);
+}
+
+template <int NG, int XK, bool NORM>
+void ada_out_launch(const AdaOutArgs& a, hipStream_t stream) {
+    if (a.y_kind == 1)
+        ada_out_launch<NG, XK, 1, NORM>(a, stream);
+    else if (a.y_kind == 2)
+        ada_out_launch<NG, XK, 2, NORM>(a, stream);
+    else
+        ada_out_launch<NG, XK, 0, NORM>(a, stream);
+}
+
 template <int NG, int XK>
 void ada_out_launch(const AdaOutArgs& a, hipStream_t stream) {
-    const unsigned grid = ada_blocks(a.rows);
-    const size_t lds = (size_t)a.dim * sizeof(float);
-    if (a.y_kind == 1)
-        ada_out_kernel<NG, XK, 1><<<grid, 256, lds, stream>>>(a);
-    else if (a.y_kind == 2)
-        ada_out_kernel<NG, XK, 2><<<grid, 256, lds, stream>>>(a);
+    if (a.norm)
+        ada_out_launch<NG, XK, true>(a, stream);
     else
-        ada_out_kernel<NG, XK, 0><<<grid, 256, lds, stream>>>(a);
+        ada_out_launch<NG, XK, false>(a, stream);
 }
 
 template <int NG>

@@ -709,7 +709,7 @@ int s2_dit_ada_in(int hidden, float epsilon, int batch, const int* video_rows,
                   const float* video_scale, const float* text_shift, const float* text_scale,
                   void* out_video, void* out_text, s2_dtype out_dtype, long out_stride,
                   s2_stream_t stream) {
-    s2::AdaInArgs a;
+    s2::AdaInArgs a = {};
     const int rc = ada_rows(hidden, batch, video_rows, text_rows, &a.rows);
     if (rc != S2_OK) return rc;
     if (!dtype_ok(x_dtype) || !dtype_ok(out_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
@@ -748,7 +748,7 @@ int s2_dit_ada_out(int hidden, int batch, const int* video_rows, const int* text
                    const void* y_video, const void* y_text, s2_dtype y_dtype, long y_stride,
                    const float* gate, const float* video_gate, const float* text_gate,
                    void* out_video, void* out_text, long out_stride, s2_stream_t stream) {
-    s2::AdaOutArgs a;
+    s2::AdaOutArgs a = {};
     const int rc = ada_rows(hidden, batch, video_rows, text_rows, &a.rows);
     if (rc != S2_OK) return rc;
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
@@ -781,6 +781,69 @@ int s2_dit_ada_out(int hidden, int batch, const int* video_rows, const int* text
     a.gate_a = gate;
     a.gate_b[0] = video_gate;
     a.gate_b[1] = text_gate;
+    S2_HIP(s2::launch_ada_out(a, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_dit_ada_out_in(int hidden, int batch, const int* video_rows, const int* text_rows,
+                      const void* x_video, const void* x_text, s2_dtype x_dtype, long x_stride,
+                      const void* y_video, const void* y_text, s2_dtype y_dtype, long y_stride,
+                      const float* gate, const float* video_gate, const float* text_gate,
+                      void* out_video, void* out_text, long out_stride, float epsilon,
+                      const float* shift, const float* scale, const float* video_shift,
+                      const float* video_scale, const float* text_shift, const float* text_scale,
+                      void* h_video, void* h_text, s2_dtype h_dtype, long h_stride,
+                      s2_stream_t stream) {
+    s2::AdaOutArgs a = {};
+    const int rc = ada_rows(hidden, batch, video_rows, text_rows, &a.rows);
+    if (rc != S2_OK) return rc;
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype) || !dtype_ok(h_dtype))
+        return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (!(epsilon >= 0.f)) return fail(S2_ERR_INVALID, "epsilon must be >= 0");
+    const int nv = a.rows.video_rows, nt = a.rows.text_rows;
+    if (!ada_stream_ok(x_video, nv, x_stride, hidden, x_dtype) ||
+        !ada_stream_ok(x_text, nt, x_stride, hidden, x_dtype) ||
+        !ada_stream_ok(y_video, nv, y_stride, hidden, y_dtype) ||
+        !ada_stream_ok(y_text, nt, y_stride, hidden, y_dtype) ||
+        !ada_stream_ok(out_video, nv, out_stride, hidden, x_dtype) ||
+        !ada_stream_ok(out_text, nt, out_stride, hidden, x_dtype) ||
+        !ada_stream_ok(h_video, nv, h_stride, hidden, h_dtype) ||
+        !ada_stream_ok(h_text, nt, h_stride, hidden, h_dtype))
+        return fail(S2_ERR_INVALID, "stream pointer, row stride (>= hidden, multiple of 4) or alignment");
+    if ((out_video == x_video && nv > 0 && out_stride != x_stride) ||
+        (out_text == x_text && nt > 0 && out_stride != x_stride))
+        return fail(S2_ERR_INVALID, "in-place output must keep the residual's row stride");
+    if (!gate || !aligned(gate, 16) || !ada_vec_ok(video_gate) || !ada_vec_ok(text_gate) ||
+        !shift || !scale || !aligned(shift, 16) || !aligned(scale, 16) || !ada_vec_ok(video_shift) ||
+        !ada_vec_ok(video_scale) || !ada_vec_ok(text_shift) || !ada_vec_ok(text_scale))
+        return fail(S2_ERR_INVALID, "modulation vectors must be non-null (gate, shift, scale) and 16-byte aligned");
+    a.x[0] = x_video;
+    a.x[1] = x_text;
+    a.x_stride = x_stride;
+    a.x_kind = (int)x_dtype;
+    a.y[0] = y_video;
+    a.y[1] = y_text;
+    a.y_stride = y_stride;
+    a.y_kind = (int)y_dtype;
+    a.out[0] = out_video;
+    a.out[1] = out_text;
+    a.out_stride = out_stride;
+    a.dim = hidden;
+    a.gate_a = gate;
+    a.gate_b[0] = video_gate;
+    a.gate_b[1] = text_gate;
+    a.norm = 1;
+    a.h[0] = h_video;
+    a.h[1] = h_text;
+    a.h_stride = h_stride;
+    a.h_kind = (int)h_dtype;
+    a.eps = epsilon;
+    a.shift_a = shift;
+    a.scale_a = scale;
+    a.shift_b[0] = video_shift;
+    a.shift_b[1] = text_shift;
+    a.scale_b[0] = video_scale;
+    a.scale_b[1] = text_scale;
     S2_HIP(s2::launch_ada_out(a, (hipStream_t)stream));
     return S2_OK;
 }

@@ -136,3 +136,49 @@ def test_ada_in_strided_rows_and_separate_output():
         assert np.all(o[:, :hidden] == 0) and np.all(o[:, 2 * hidden:] == 0)
         ref = oracle.ada_in(x, rows, mod["shift"], mod["scale"])
         assert np.all(np.abs(o[:, hidden:2 * hidden] - ref) <= 2.0 ** -8 * np.abs(ref) + 1e-6)
+
+
+@pytest.mark.parametrize("hidden,vr,tr", CASES)
+@pytest.mark.parametrize("x_dt,y_dt,h_dt", [("f32", "bf16", "bf16"), ("bf16", "bf16", "f32"),
+                                            ("f16", "f32", "f16")])
+def test_fused_out_in_equals_the_two_passes(hidden, vr, tr, x_dt, y_dt, h_dt):
+    """s2_dit_ada_out_in gives bit for bit what s2_dit_ada_out followed by
+    s2_dit_ada_in gives, and h matches the oracle composite"""
+    torch = _torch()
+    from seedvr2_ncnn_amd import capi
+    dts = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}
+    xv, xt, mod, own = _data(hidden, vr, tr, 3 * hidden + len(vr))
+    g = np.random.default_rng(hidden + 1)
+    yv = _stored(g.standard_normal(xv.shape).astype(np.float32), dts[y_dt])
+    yt = _stored(g.standard_normal(xt.shape).astype(np.float32), dts[y_dt])
+    xv, xt = _stored(xv, dts[x_dt]), _stored(xt, dts[x_dt])
+    nt = sum(tr or [])
+    y_d = (_dev(yv, dts[y_dt]), _dev(yt, dts[y_dt]) if nt else None)
+    vecs = {k: _dev(v) for k, v in own.items()}
+    m = {k: _dev(v) for k, v in mod.items()}
+
+    # two passes
+    x2 = (_dev(xv, dts[x_dt]), _dev(xt, dts[x_dt]) if nt else None)
+    capi.ada_out(*x2, *y_d, vr, tr, m["gate"], vecs["video_gate"], vecs["text_gate"])
+    h2 = capi.ada_in(*x2, vr, tr, m["shift"], m["scale"], vecs["video_shift"], vecs["video_scale"],
+                     vecs["text_shift"], vecs["text_scale"], out_dtype=dts[h_dt])
+    # one pass
+    x1 = (_dev(xv, dts[x_dt]), _dev(xt, dts[x_dt]) if nt else None)
+    _, _, hv1, ht1 = capi.ada_out_in(*x1, *y_d, vr, tr, m["gate"], m["shift"], m["scale"],
+                                     vecs["video_gate"], vecs["text_gate"], vecs["video_shift"],
+                                     vecs["video_scale"], vecs["text_shift"], vecs["text_scale"],
+                                     h_dtype=dts[h_dt])
+    torch.cuda.synchronize()
+    assert torch.equal(x1[0], x2[0]) and torch.equal(hv1, h2[0])
+    if nt:
+        assert torch.equal(x1[1], x2[1]) and torch.equal(ht1, h2[1])
+    for stream, x, y, rows, h in (("video", xv, yv, vr, hv1), ("text", xt, yt, tr, ht1)):
+        if not rows or sum(rows) == 0:
+            continue
+        res = _stored(oracle.ada_out(x, y, rows, mod["gate"], own[f"{stream}_gate"]), dts[x_dt])
+        ref = oracle.ada_in(res, rows, mod["shift"], mod["scale"], own[f"{stream}_shift"],
+                            own[f"{stream}_scale"])
+        got = h.float().cpu().numpy()
+        tol = {"f32": 2e-6 * max(1.0, float(np.abs(ref).max())), "bf16": 2.0 ** -8 * np.abs(ref) + 1e-6,
+               "f16": 2.0 ** -11 * np.abs(ref) + 1e-6}[h_dt]
+        assert np.all(np.abs(got - ref) <= tol)

@@ -84,3 +84,20 @@ def test_block_modulation_rejects_bad_arguments(L):
     assert ada_out(y=None) == INVALID
     assert ada_out(out=FAKE, xs=64, os_=128) == INVALID     # in place with another stride
     assert ada_out(gate=ctypes.c_void_p(0x10004)) == INVALID
+
+
+def test_fused_block_modulation_rejects_bad_arguments(L):
+    rows = _shapes((4,))
+    F32, BF16 = capi.DTYPE_F32, capi.DTYPE_BF16
+
+    def call(gate=FAKE, shift=FAKE, h=FAKE, hs=64, eps=1e-5, hidden=64):
+        return L.s2_dit_ada_out_in(hidden, 1, rows, None, FAKE, None, F32, 64, FAKE, None, BF16,
+                                   64, gate, None, None, FAKE, None, 64, eps, shift, FAKE, None,
+                                   None, None, None, h, None, BF16, hs, None)
+
+    assert call(gate=None) == INVALID
+    assert call(shift=None) == INVALID
+    assert call(h=None) == INVALID
+    assert call(hs=60) == INVALID
+    assert call(eps=float("nan")) == INVALID
+    assert call(hidden=66) == INVALID
