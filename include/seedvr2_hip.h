@@ -281,7 +281,8 @@ S2_API int s2_denoise_update(const float* positive_patches, const float* negativ
  * modulation vectors 16-byte aligned. */
 
 /* out = rmsnorm(x) * (scale[b] + *_scale) + (shift[b] + *_shift), with
- * rmsnorm(x) = x / sqrt(mean(x^2) + epsilon); fp32 arithmetic. */
+ * rmsnorm(x) = x / sqrt(mean(x^2) + epsilon); fp32 arithmetic.  out must not
+ * overlap x. */
 S2_API int s2_dit_ada_in(int hidden, float epsilon, int batch, const int* video_rows,
                          const int* text_rows, const void* x_video, const void* x_text,
                          s2_dtype x_dtype, long x_stride, const float* shift, const float* scale,
@@ -290,8 +291,9 @@ S2_API int s2_dit_ada_in(int hidden, float epsilon, int batch, const int* video_
                          void* out_text, s2_dtype out_dtype, long out_stride,
                          s2_stream_t stream);
 
-/* out = x + y * (gate[b] + *_gate), out of x's element type; out may be x
- * (in place, same row stride).  Each product and sum is rounded to fp32. */
+/* out = x + y * (gate[b] + *_gate), out of x's element type; out is either x
+ * (in place, same row stride) or does not overlap x or y.  Each product and
+ * sum is rounded to fp32. */
 S2_API int s2_dit_ada_out(int hidden, int batch, const int* video_rows, const int* text_rows,
                           const void* x_video, const void* x_text, s2_dtype x_dtype,
                           long x_stride, const void* y_video, const void* y_text,
