@@ -949,8 +949,8 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
     // DMA group stays inside one output frame; otherwise they are copied in
     // front of the staged input.
     const int shift = prefix - mem;
-    const bool direct = mem > 0 && s.cpad >= 64 && ((long)ho * wo) % 8 == 0 &&
-                        (long)mem <= max_span;
+    const bool direct = mem > 0 && (long)mem <= max_span &&
+                        (s2::conv3d_halo_ok(s, wo) || (s.cpad >= 64 && ((long)ho * wo) % 8 == 0));
     const int kmem = direct ? mem : 0;
     const int lead = mem - kmem;
     uint16_t* staged = (uint16_t*)workspace;

@@ -152,6 +152,7 @@ struct ConvArgs {
     int kt, kh, kw, st, dt, sh, sw, dh, dw, ph, pw;
     int shift, fbase, t0;
     int mtiles, ntiles;
+    int ytiles, xtiles;   // halo kernel: output tiles per frame
 };
 
 // Eight waves in a grid of 128x64 wave tiles (4x2 MFMA 32x32x16
@@ -432,6 +433,218 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     }
 }
 
+// ---- 3x3 spatial windows, stride 1: the halo kernel --------------------------
+//
+// For a 3x3 spatial window with unit stride and dilation, the nine window
+// positions of one output tile read nine shifted copies of the same input
+// pixels.  This kernel tiles the output frame in 2-D blocks of TH x 128
+// pixels (TH = 4, 512 GEMM rows) and loads, per k-chunk of 16 input
+// channels and temporal tap, the (TH + 2) x 130 input halo once into LDS
+// (32 bytes per pixel) together with the chunk's weights for all nine
+// positions; the nine positions are then nine 16-k MFMA slices that read the
+// halo at shifted pixel offsets.  Against one 64-channel A tile per window
+// position, this cuts the LDS writes per MFMA by 3x and the A traffic from L2
+// by about 6x, and takes one barrier per 144 k instead of per 64 k.
+//
+// LDS stage: halo [780 pixels][2 chunks of 16 bytes], then weights
+// [9 positions][BN rows][2 chunks]; chunk c of pixel (or row) p is stored at
+// position c ^ ((p >> 3) & 1), which puts the 16 lanes of each ds_read_b128
+// phase (16 consecutive pixels or rows) on distinct banks for any shift.
+// Two stages: the next chunk's DMA overlaps this chunk's MFMAs.  Each tile
+// lies in one output frame, so a tap's input frame, memory or staged, is
+// the same for the whole tile.
+constexpr int kHaloTW = 128;             // output tile width
+constexpr int kHaloW = kHaloTW + 2;      // halo width
+constexpr int kHaloRows = 6;             // halo rows (TH + 2)
+constexpr int kHaloPix = kHaloRows * kHaloW;
+constexpr int kHaloBytes = kHaloPix * 32;
+
+template <int BN, int OK>
+__global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
+    constexpr int TM = BN >= 64 ? 4 : 2, TN = BN >= 64 ? 2 : 1;
+    constexpr int WN = BN / (32 * TN), WM = 8 / WN;
+    constexpr int BM = WM * 32 * TM;
+    static_assert(BM == 512, "the halo tile is 4 x 128 output pixels");
+    constexpr int TH = BM / kHaloTW;
+    constexpr int BBYTES = 9 * BN * 32;
+    constexpr int SB = kHaloBytes + BBYTES;
+    constexpr int HSLOTS = kHaloPix * 2, HINS = (HSLOTS + 511) / 512;
+    constexpr int BSLOTS = 9 * BN * 2, BINS = (BSLOTS + 511) / 512;
+    constexpr uint32_t OOB = 0x80000000u;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SB];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int wm = wave / WN;
+    const int wn = wave % WN;
+    const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+
+    // tile: output frame to, rows [y0, y0 + TH), columns [x0, x0 + 128)
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int xt = lid % a.xtiles;
+    const int yt = (lid / a.xtiles) % a.ytiles;
+    const int to = lid / (a.xtiles * a.ytiles);
+    const int y0 = yt * TH, x0 = xt * kHaloTW;
+    // this wave's GEMM rows: output row ty, columns tx0 + [0, 32 TM)
+    const int ty = (wm * 32 * TM) / kHaloTW;
+    const int tx0 = (wm * 32 * TM) % kHaloTW;
+
+    const uint32_t pix = (uint32_t)(a.cpad * 2);
+    const uint32_t frame_bytes = (uint32_t)(a.H * a.W) * pix;
+    // Slot sl of a DMA instruction set: halo (pixel sl / 2, stored chunk
+    // sl % 2) at the frame offset of that pixel and chunk; weights (position
+    // q, row, stored chunk) at the row's k offset of q; the tap and channel
+    // chunk go in soffset.  Recomputed per issue: a few VALU operations a
+    // slot, against 72 MFMAs a chunk.
+    auto halo_off = [&](int sl) -> uint32_t {
+        const int p = sl >> 1;
+        const int c = (sl & 1) ^ ((p >> 3) & 1);
+        const int hy = p / kHaloW;
+        const int yy = y0 - a.ph + hy;
+        const int xx = x0 - a.pw + (p - hy * kHaloW);
+        const bool in = (unsigned)yy < (unsigned)a.H && (unsigned)xx < (unsigned)a.W;
+        return in ? (uint32_t)(yy * a.W + xx) * pix + c * 16 : OOB;
+    };
+    auto weight_off = [&](int sl) -> uint32_t {
+        const int q = sl / (BN * 2);
+        const int row = (sl >> 1) - q * BN;
+        const int c = (sl & 1) ^ ((row >> 3) & 1);
+        return (uint32_t)(row * a.kp + q * a.cpad) * 2 + c * 16;
+    };
+    const i32x4 ra = wave_uniform(buffer_rsrc(a.staged, a.staged_bytes));
+    const i32x4 rm = wave_uniform(buffer_rsrc(a.memory, a.memory_bytes));
+    const i32x4 rb = wave_uniform(
+        buffer_rsrc(a.packed, (uint32_t)(min(a.cout, BN) * a.kp * 2)));
+
+    const int cpc = a.cpad / 16;   // 16-channel chunks per pixel
+    const int nchunks = a.kt * cpc;
+    const int tbase = (a.t0 + to) * a.st - a.shift;
+    auto issue = [&](int stage, int cs) {
+        const int tap = cs / cpc, cc = cs - tap * cpc;
+        const int v = max(tbase + tap * a.dt, 0);
+        const bool fm = v < a.mem;
+        const uint32_t fo = (uint32_t)(fm ? v : v - a.mem - a.fbase) * frame_bytes + cc * 32;
+        const uint32_t st = lds_base + stage * SB;
+#pragma unroll
+        for (int j = 0; j < HINS; ++j) {
+            const int sl0 = (j * 8 + wave) * 64;   // wave-uniform
+            if (sl0 >= HSLOTS) break;
+            if (sl0 + lane < HSLOTS)
+                lds_dma16(fm ? rm : ra, st + sl0 * 16, halo_off(sl0 + lane),
+                          __builtin_amdgcn_readfirstlane(fo));
+        }
+        const uint32_t kb = (uint32_t)(tap * 9 * a.cpad + cc * 16) * 2;
+#pragma unroll
+        for (int j = 0; j < BINS; ++j) {
+            const int sl0 = (j * 8 + wave) * 64;
+            if (sl0 >= BSLOTS) break;
+            if (sl0 + lane < BSLOTS)
+                lds_dma16(rb, st + kHaloBytes + sl0 * 16, weight_off(sl0 + lane),
+                          __builtin_amdgcn_readfirstlane(kb));
+        }
+    };
+
+    f32x16 acc[TM][TN];
+    bf16x8 fa[2][TM], fb[2][TN];
+    // fragments of window position q (ky = q / 3, kx = q % 3).  Fragment i
+    // is 32 pixels (rows) after fragment 0, which keeps the swizzle bit
+    // ((p >> 3) & 1): its address is fragment 0's plus 1 KB.
+    const int pa = ty * kHaloW + tx0 + l32;
+    const int rowb = wn * 32 * TN + l32;
+    const int boffl = (rowb * 2 + (g ^ ((rowb >> 3) & 1))) * 16;
+    auto frag = [&](const uint8_t* st, int q, int slot) {
+        const int ky = q / 3, kx = q - 3 * ky;
+        const int p = pa + ky * kHaloW + kx;
+        const uint8_t* ab = st + (p * 2 + (g ^ ((p >> 3) & 1))) * 16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i) fa[slot][i] = as_bf16x8(*(const uint4*)(ab + 1024 * i));
+        const uint8_t* bb = st + kHaloBytes + q * BN * 32 + boffl;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) fb[slot][j] = as_bf16x8(*(const uint4*)(bb + 1024 * j));
+    };
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    issue(0, 0);
+#pragma unroll 1
+    for (int cs = 0; cs < nchunks; ++cs) {
+        const int stage = cs & 1;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();   // chunk cs visible to all waves; the other stage no longer read
+        if (cs + 1 < nchunks) issue(stage ^ 1, cs + 1);
+        const uint8_t* st = lds + stage * SB;
+        frag(st, 0, 0);
+#pragma unroll
+        for (int q = 0; q < 9; ++q) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (q + 1 < 9) frag(st, q + 1, (q + 1) & 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[q & 1][i], fb[q & 1][j],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Epilogue: register r of a 32x32 accumulator is GEMM row 8(r/4) + 4g +
+    // r%4 of its block, i.e. 4 consecutive output pixels of one row.
+    const int y = y0 + ty;
+    if (y >= a.Ho) return;
+    const long mrow = ((long)to * a.Ho + y) * a.Wo;
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = wn * 32 * TN + 32 * j + l32;
+        if (col >= a.cout) continue;
+        const float bv = a.bias ? a.bias[col] : 0.f;
+        const long cbase = (long)col * a.out_cstep + a.out_off + mrow;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int x = x0 + tx0 + 32 * i + 8 * rg + 4 * g;
+                if (x >= a.Wo) continue;
+                const float v[4] = {acc[i][j][4 * rg] + bv, acc[i][j][4 * rg + 1] + bv,
+                                    acc[i][j][4 * rg + 2] + bv, acc[i][j][4 * rg + 3] + bv};
+                if (a.vec_ok && x + 3 < a.Wo) {
+                    store4(a.out, cbase + x, v[0], v[1], v[2], v[3], OK);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (x + e >= a.Wo) continue;
+                        const long idx = cbase + x + e;
+                        if (OK == 1)
+                            ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
+                        else if (OK == 2)
+                            ((_Float16*)a.out)[idx] = (_Float16)v[e];
+                        else
+                            ((float*)a.out)[idx] = v[e];
+                    }
+                }
+            }
+    }
+}
+
+template <int BN>
+void launch_conv3d_halo(const ConvArgs& a, hipStream_t stream) {
+    const unsigned grid = (unsigned)a.mtiles;
+    if (a.out_kind == 1)
+        conv3d_halo_kernel<BN, 1><<<grid, 512, 0, stream>>>(a);
+    else if (a.out_kind == 2)
+        conv3d_halo_kernel<BN, 2><<<grid, 512, 0, stream>>>(a);
+    else
+        conv3d_halo_kernel<BN, 0><<<grid, 512, 0, stream>>>(a);
+}
+
 template <int BN, bool SMALL>
 void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
     const unsigned grid = (unsigned)(a.mtiles * a.ntiles);
@@ -537,9 +750,13 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     const long m = (long)frames_out * ho * wo;
     const long kp = conv3d_kp(s);
     const bool small = s.cpad < 64;
+    const bool halo = conv3d_halo_ok(s, wo);
+    // the implicit-GEMM kernel reads memory frames in place only when each
+    // 8-row DMA group lies in one output frame; the halo kernel's tiles
+    // always do
     if (m > INT_MAX || staged_bytes >= 0x80000000ull || memory_bytes >= 0x80000000ull ||
         kp * 2 * s.cout >= 0x80000000l || s.cpad != conv3d_cpad(s.cin) || s.kh * s.kw > 32 ||
-        (mem > 0 && (small || ((long)ho * wo) % 8 != 0)))
+        (mem > 0 && !halo && (small || ((long)ho * wo) % 8 != 0)))
         return hipErrorInvalidValue;
     ConvArgs a;
     a.staged = staged;
@@ -577,6 +794,21 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.shift = shift;
     a.fbase = frame_base;
     a.t0 = t0;
+    a.ytiles = a.xtiles = 0;
+    if (halo) {
+        a.ytiles = (ho + 3) / 4;
+        a.xtiles = (wo + kHaloTW - 1) / kHaloTW;
+        const long tiles = (long)frames_out * a.ytiles * a.xtiles;
+        if (tiles > INT_MAX) return hipErrorInvalidValue;
+        a.mtiles = (int)tiles;
+        a.ntiles = 1;
+        a.vec_ok = a.vec_ok && wo % 4 == 0;
+        if (s.cout <= 32)
+            launch_conv3d_halo<32>(a, stream);
+        else
+            launch_conv3d_halo<128>(a, stream);
+        return hipGetLastError();
+    }
     if (s.cout <= 32) {
         a.mtiles = (int)((m + 511) / 512);
         a.ntiles = 1;

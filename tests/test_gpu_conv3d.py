@@ -83,6 +83,13 @@ SHAPES = [
     (16, 16, 4, 8, 10, {}),                            # 16 in and out (latent width)
     (24, 64, 3, 7, 9, dict(k=(1, 3, 3))),              # 32-channel pixels, last k-step part empty
     (8, 130, 2, 11, 6, dict(k=(2, 3, 3), head=1)),     # 8-channel pixels, ragged n
+    # 3x3 stride-1 layers with at most 128 outputs on frames at least ~100
+    # wide take the halo kernel (4 x 128 output tiles)
+    (128, 128, 3, 6, 120, {}),                         # ragged tile rows and columns
+    (64, 3, 2, 9, 250, {}),                            # RGB output, two tile columns
+    (16, 64, 2, 5, 110, dict(head=1)),                 # 16-channel pixels
+    (32, 96, 3, 4, 128, dict(p=(0, 1))),               # no row padding
+    (96, 128, 3, 7, 210, dict(k=(2, 3, 3), s=(2, 1, 1))),   # temporal stride 2
 ]
 
 
@@ -110,9 +117,10 @@ def test_conv3d_16bit_blobs_and_padded_cstep(in_dtype, out_dtype):
 
 # 6x10 frames copy the memory in front of the staged input (a DMA group of
 # 8 rows can straddle two frames); 8x10 frames read it in place, except with
-# 16 input channels (16-channel pixels always copy it)
+# 16 input channels (16-channel pixels always copy it); the halo kernel's
+# 5x120 frames always read it in place
 @pytest.mark.parametrize("split", [1, 2])
-@pytest.mark.parametrize("hw", [(6, 10), (8, 10)])
+@pytest.mark.parametrize("hw", [(6, 10), (8, 10), (5, 120)])   # (5, 120): the halo kernel
 @pytest.mark.parametrize("reuse", [False, True])
 @pytest.mark.parametrize("cin", [64, 16])
 def test_conv3d_memory_chains_slices(split, hw, reuse, cin):
