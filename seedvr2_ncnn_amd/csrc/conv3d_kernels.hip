@@ -36,77 +36,76 @@ __device__ __forceinline__ float load_elem(const void* p, long i) {
     return ((const float*)p)[i];
 }
 
-template <int KIND>
-__device__ __forceinline__ void load_elem4(const void* p, long i, float (&v)[4]) {
-    if (KIND == 0) {
-        const float4 f = *reinterpret_cast<const float4*>((const float*)p + i);
-        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
-    } else {
-        const uint2 u = *reinterpret_cast<const uint2*>((const uint16_t*)p + i);
-        const uint32_t w[2] = {u.x, u.y};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
-            v[e] = KIND == 1 ? __builtin_bit_cast(float, (uint32_t)h << 16)
-                             : (float)__builtin_bit_cast(_Float16, h);
-        }
-    }
-}
-
-// One block moves 64 pixels x 64 channels: 64 channel rows of 64 pixels are
-// read as 16-byte runs, transposed in LDS (row pitch 65 floats: conflict-free
-// both ways) and written as 64 pixel rows of 128 bytes (or of cpad channels
-// when cpad is 8, 16 or 32).  Channels at or above cin are written as zeros.
+// One block moves 128 pixels x 64 channels: 64 channel rows of 128 pixels
+// are read as 16-byte runs (8 elements of a 16-bit blob, 4 of an fp32 one;
+// single elements when the rows are not 16-byte aligned, `vec` false),
+// transposed in LDS (row pitch 129 floats) and written as 128 pixel rows of
+// 128 bytes (or of cpad channels when cpad is 8, 16 or 32), 16 bytes a
+// thread.  Channels at or above cin are written as zeros.
 template <int KIND>
 __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
-    const void* __restrict__ in, long cstep, int cin, long pixels, int cpad,
+    const void* __restrict__ in, long cstep, int cin, long pixels, int cpad, int vec,
     uint16_t* __restrict__ staged, uint16_t* __restrict__ tail, long tail_q0) {
-    __shared__ float tile[64 * 65];
-    const long q0 = (long)blockIdx.x * 64;
+    constexpr int P = 128;              // pixels per block
+    constexpr int PITCH = P + 1;
+    constexpr int EL = KIND == 0 ? 4 : 8;   // elements per 16-byte load
+    constexpr int RUNS = P / EL;            // runs per channel row
+    __shared__ float tile[64 * PITCH];
+    const long q0 = (long)blockIdx.x * P;
     const int c0 = blockIdx.y * 64;
     const int t = threadIdx.x;
-    const int q4 = (t & 15) * 4;
-    const bool full = q0 + 64 <= pixels;
+    const bool full = vec && q0 + P <= pixels;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int cl = (t >> 4) + 16 * i;
+    for (int i = 0; i < 64 * RUNS / kStageThreads; ++i) {
+        const int idx = i * kStageThreads + t;
+        const int cl = idx / RUNS;
+        const int qe = (idx % RUNS) * EL;
         const int c = c0 + cl;
-        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        float v[EL];
+#pragma unroll
+        for (int e = 0; e < EL; ++e) v[e] = 0.f;
         if (c < cin) {
-            const long base = (long)c * cstep + q0 + q4;
+            const long base = (long)c * cstep + q0 + qe;
             if (full) {
-                load_elem4<KIND>(in, base, v);
+                if (KIND == 0) {
+                    const float4 f = *reinterpret_cast<const float4*>((const float*)in + base);
+                    v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+                } else {
+                    const uint4 u = *reinterpret_cast<const uint4*>((const uint16_t*)in + base);
+                    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int e = 0; e < EL; ++e) {
+                        const uint16_t h = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+                        v[e] = KIND == 1 ? __uint_as_float((uint32_t)h << 16)
+                                         : (float)__builtin_bit_cast(_Float16, h);
+                    }
+                }
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (q0 + q4 + e < pixels) v[e] = load_elem<KIND>(in, base + e);
+                for (int e = 0; e < EL; ++e)
+                    if (q0 + qe + e < pixels) v[e] = load_elem<KIND>(in, base + e);
             }
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) tile[cl * 65 + q4 + e] = v[e];
+        for (int e = 0; e < EL; ++e) tile[cl * PITCH + qe + e] = v[e];
     }
     __syncthreads();
-    const int q = t >> 2, part = t & 3;
-    if (q0 + q >= pixels) return;
-    uint16_t h[16];
+    // a pixel holds cpad channels: with cpad 8, 16 or 32 only the first
+    // cpad / 8 parts of 8 channels are written
+    const int parts = min(8, (cpad - c0) / 8);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) h[i] = f32_to_bf16(tile[(part * 16 + i) * 65 + q]);
-    uint16_t lo[8], hi[8];
+    for (int i = 0; i < P * 8 / kStageThreads; ++i) {
+        const int idx = i * kStageThreads + t;
+        const int q = idx >> 3, part = idx & 7;
+        if (part >= parts || q0 + q >= pixels) continue;
+        uint16_t h[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) lo[i] = h[i], hi[i] = h[8 + i];
-    // a pixel holds cpad channels: with cpad 8 or 16 (at most 16 input
-    // channels) only the first part writes, one or two 16-byte chunks
-    const int nchunk = min(2, (cpad - c0 - part * 16) / 8);
-    if (nchunk <= 0) return;
-    const uint4 vlo = pack8_bf16(lo), vhi = pack8_bf16(hi);
-    uint4* dst = reinterpret_cast<uint4*>(staged + (q0 + q) * cpad + c0 + part * 16);
-    dst[0] = vlo;
-    if (nchunk > 1) dst[1] = vhi;
-    // pixels from tail_q0 on are the next temporal memory as well
-    if (tail && q0 + q >= tail_q0) {
-        uint4* t2 = reinterpret_cast<uint4*>(tail + (q0 + q - tail_q0) * cpad + c0 + part * 16);
-        t2[0] = vlo;
-        if (nchunk > 1) t2[1] = vhi;
+        for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(tile[(part * 8 + e) * PITCH + q]);
+        const uint4 val = pack8_bf16(h);
+        *reinterpret_cast<uint4*>(staged + (q0 + q) * cpad + c0 + part * 8) = val;
+        // pixels from tail_q0 on are the next temporal memory as well
+        if (tail && q0 + q >= tail_q0)
+            *reinterpret_cast<uint4*>(tail + (q0 + q - tail_q0) * cpad + c0 + part * 8) = val;
     }
 }
 
@@ -718,16 +717,19 @@ hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, in
                                long pixels, int cpad, uint16_t* staged, uint16_t* tail,
                                long tail_q0, hipStream_t stream) {
     if (pixels <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((pixels + 63) / 64), (unsigned)((cpad + 63) / 64));
+    const dim3 grid((unsigned)((pixels + 127) / 128), (unsigned)((cpad + 63) / 64));
+    // 16-byte runs need 16-byte aligned channel rows
+    const int esz = in_kind == 0 ? 4 : 2;
+    const int vec = ((uintptr_t)input % 16) == 0 && (in_cstep * esz) % 16 == 0;
     if (in_kind == 1)
-        conv3d_stage_kernel<1><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
-                                                                     cpad, staged, tail, tail_q0);
+        conv3d_stage_kernel<1><<<grid, kStageThreads, 0, stream>>>(
+            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
     else if (in_kind == 2)
-        conv3d_stage_kernel<2><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
-                                                                     cpad, staged, tail, tail_q0);
+        conv3d_stage_kernel<2><<<grid, kStageThreads, 0, stream>>>(
+            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
     else
-        conv3d_stage_kernel<0><<<grid, kStageThreads, 0, stream>>>(input, in_cstep, cin, pixels,
-                                                                     cpad, staged, tail, tail_q0);
+        conv3d_stage_kernel<0><<<grid, kStageThreads, 0, stream>>>(
+            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
     return hipGetLastError();
 }
 
