@@ -437,7 +437,8 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 // For a 3x3 spatial window with unit stride and dilation, the nine window
 // positions of one output tile read nine shifted copies of the same input
 // pixels.  This kernel tiles the output frame in 2-D blocks of TH x 128
-// pixels (TH = 4, 512 GEMM rows) and loads, per k-chunk of 16 input
+// pixels (TH = 4, 512 GEMM rows; times BN-channel tiles of the outputs)
+// and loads, per k-chunk of 16 input
 // channels and temporal tap, the (TH + 2) x 130 input halo once into LDS
 // (32 bytes per pixel) together with the chunk's weights for all nine
 // positions; the nine positions are then nine 16-k MFMA slices that read the
@@ -481,12 +482,17 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
     const int wn = wave % WN;
     const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
 
-    // tile: output frame to, rows [y0, y0 + TH), columns [x0, x0 + 128)
+    // tile: output channels [col0, col0 + BN) of output frame to, rows
+    // [y0, y0 + TH), columns [x0, x0 + 128); the channel tiles of one block
+    // of pixels are neighbours, so they share its halo in L2
     const int lid = xcd_remap(blockIdx.x, gridDim.x);
-    const int xt = lid % a.xtiles;
-    const int yt = (lid / a.xtiles) % a.ytiles;
-    const int to = lid / (a.xtiles * a.ytiles);
+    const int nt = lid % a.ntiles;
+    const int sp = lid / a.ntiles;
+    const int xt = sp % a.xtiles;
+    const int yt = (sp / a.xtiles) % a.ytiles;
+    const int to = sp / (a.xtiles * a.ytiles);
     const int y0 = yt * TH, x0 = xt * kHaloTW;
+    const int col0 = nt * BN;
     // this wave's GEMM rows: output row ty, columns tx0 + [0, 32 TM)
     const int ty = (wm * 32 * TM) / kHaloTW;
     const int tx0 = (wm * 32 * TM) % kHaloTW;
@@ -515,8 +521,8 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
     };
     const i32x4 ra = wave_uniform(buffer_rsrc(a.staged, a.staged_bytes));
     const i32x4 rm = wave_uniform(buffer_rsrc(a.memory, a.memory_bytes));
-    const i32x4 rb = wave_uniform(
-        buffer_rsrc(a.packed, (uint32_t)(min(a.cout, BN) * a.kp * 2)));
+    const i32x4 rb = wave_uniform(buffer_rsrc(a.packed + (long)col0 * a.kp,
+                                              (uint32_t)(min(a.cout - col0, BN) * a.kp * 2)));
 
     const int cpc = a.cpad / 16;   // 16-channel chunks per pixel
     const int nchunks = a.kt * cpc;
@@ -602,7 +608,7 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
     const long mrow = ((long)to * a.Ho + y) * a.Wo;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
-        const int col = wn * 32 * TN + 32 * j + l32;
+        const int col = col0 + wn * 32 * TN + 32 * j + l32;
         if (col >= a.cout) continue;
         const float bv = a.bias ? a.bias[col] : 0.f;
         const long cbase = (long)col * a.out_cstep + a.out_off + mrow;
@@ -800,10 +806,10 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     if (halo) {
         a.ytiles = (ho + 3) / 4;
         a.xtiles = (wo + kHaloTW - 1) / kHaloTW;
-        const long tiles = (long)frames_out * a.ytiles * a.xtiles;
+        a.ntiles = s.cout <= 32 ? 1 : (s.cout + 127) / 128;
+        const long tiles = (long)frames_out * a.ytiles * a.xtiles * a.ntiles;
         if (tiles > INT_MAX) return hipErrorInvalidValue;
         a.mtiles = (int)tiles;
-        a.ntiles = 1;
         a.vec_ok = a.vec_ok && wo % 4 == 0;
         if (s.cout <= 32)
             launch_conv3d_halo<32>(a, stream);

@@ -83,13 +83,15 @@ SHAPES = [
     (16, 16, 4, 8, 10, {}),                            # 16 in and out (latent width)
     (24, 64, 3, 7, 9, dict(k=(1, 3, 3))),              # 32-channel pixels, last k-step part empty
     (8, 130, 2, 11, 6, dict(k=(2, 3, 3), head=1)),     # 8-channel pixels, ragged n
-    # 3x3 stride-1 layers with at most 128 outputs on frames at least ~100
-    # wide take the halo kernel (4 x 128 output tiles)
+    # 3x3 stride-1 layers on frames that fill 128-column tiles to 93% take the
+    # halo kernel (4 x 128 output tiles, 128 or 32 output channels a tile)
     (128, 128, 3, 6, 120, {}),                         # ragged tile rows and columns
     (64, 3, 2, 9, 250, {}),                            # RGB output, two tile columns
-    (16, 64, 2, 5, 110, dict(head=1)),                 # 16-channel pixels
+    (16, 64, 2, 5, 124, dict(head=1)),                 # 16-channel pixels
     (32, 96, 3, 4, 128, dict(p=(0, 1))),               # no row padding
-    (96, 128, 3, 7, 210, dict(k=(2, 3, 3), s=(2, 1, 1))),   # temporal stride 2
+    (96, 128, 3, 7, 240, dict(k=(2, 3, 3), s=(2, 1, 1))),   # temporal stride 2
+    (64, 200, 2, 5, 120, {}),                          # two channel tiles, the second ragged
+    (256, 256, 2, 4, 128, {}),                         # 256 channels in and out
 ]
 
 
