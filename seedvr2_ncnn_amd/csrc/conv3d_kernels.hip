@@ -527,7 +527,7 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
     const int cpc = a.cpad / 16;   // 16-channel chunks per pixel
     const int nchunks = a.kt * cpc;
     const int tbase = (a.t0 + to) * a.st - a.shift;
-    auto issue = [&](int stage, int cs) {
+    auto issue_halo = [&](int stage, int cs) {
         const int tap = cs / cpc, cc = cs - tap * cpc;
         const int v = max(tbase + tap * a.dt, 0);
         const bool fm = v < a.mem;
@@ -541,6 +541,10 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
                 lds_dma16(fm ? rm : ra, st + sl0 * 16, halo_off(sl0 + lane),
                           __builtin_amdgcn_readfirstlane(fo));
         }
+    };
+    auto issue_weights = [&](int stage, int cs) {
+        const int tap = cs / cpc, cc = cs - tap * cpc;
+        const uint32_t st = lds_base + stage * SB;
         const uint32_t kb = (uint32_t)(tap * 9 * a.cpad + cc * 16) * 2;
 #pragma unroll
         for (int j = 0; j < BINS; ++j) {
@@ -577,15 +581,19 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-    issue(0, 0);
+    issue_halo(0, 0);
+    issue_weights(0, 0);
 #pragma unroll 1
     for (int cs = 0; cs < nchunks; ++cs) {
         const int stage = cs & 1;
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();   // chunk cs visible to all waves; the other stage no longer read
-        if (cs + 1 < nchunks) issue(stage ^ 1, cs + 1);
         const uint8_t* st = lds + stage * SB;
         frag(st, 0, 0);
+        // The next chunk's DMA into the other stage is issued behind the
+        // first two positions' MFMAs, so that its address arithmetic runs
+        // while they execute and the first fragment reads are not queued
+        // behind it.
 #pragma unroll
         for (int q = 0; q < 9; ++q) {
             __builtin_amdgcn_sched_barrier(0);
@@ -597,6 +605,9 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
                 for (int j = 0; j < TN; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[q & 1][i], fb[q & 1][j],
                                                                          acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            if (q == 0 && cs + 1 < nchunks) issue_halo(stage ^ 1, cs + 1);
+            if (q == 1 && cs + 1 < nchunks) issue_weights(stage ^ 1, cs + 1);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
