@@ -437,8 +437,8 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 // For a 3x3 spatial window with unit stride and dilation, the nine window
 // positions of one output tile read nine shifted copies of the same input
 // pixels.  This kernel tiles the output frame in 2-D blocks of TH x 128
-// pixels (TH = 4, 512 GEMM rows; times BN-channel tiles of the outputs)
-// and loads, per k-chunk of 16 input
+// pixels (TH = 4 at BN 128, 8 at BN 32; one output row per wave; times
+// BN-channel tiles of the outputs) and loads, per k-chunk of 16 input
 // channels and temporal tap, the (TH + 2) x 130 input halo once into LDS
 // (32 bytes per pixel) together with the chunk's weights for all nine
 // positions; the nine positions are then nine 16-k MFMA slices that read the
@@ -446,7 +446,7 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 // position, this cuts the LDS writes per MFMA by 3x and the A traffic from L2
 // by about 6x, and takes one barrier per 144 k instead of per 64 k.
 //
-// LDS stage: halo [780 pixels][2 chunks of 16 bytes], then weights
+// LDS stage: halo [(TH + 2) * 130 pixels][2 chunks of 16 bytes], then weights
 // [9 positions][BN rows][2 chunks]; chunk c of pixel (or row) p is stored at
 // position c ^ ((p >> 3) & 1), which puts the 16 lanes of each ds_read_b128
 // phase (16 consecutive pixels or rows) on distinct banks for any shift.
@@ -455,17 +455,19 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 // the same for the whole tile.
 constexpr int kHaloTW = 128;             // output tile width
 constexpr int kHaloW = kHaloTW + 2;      // halo width
-constexpr int kHaloRows = 6;             // halo rows (TH + 2)
-constexpr int kHaloPix = kHaloRows * kHaloW;
-constexpr int kHaloBytes = kHaloPix * 32;
+// output tile rows: one per wave (128 x 64 wave tiles) at BN 128, and
+// 128 x 32 wave tiles over 8 rows at BN 32
+constexpr int halo_tile_rows(int bn) { return bn >= 64 ? 4 : 8; }
 
 template <int BN, int OK>
 __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
-    constexpr int TM = BN >= 64 ? 4 : 2, TN = BN >= 64 ? 2 : 1;
+    constexpr int TM = 4, TN = BN >= 64 ? 2 : 1;
     constexpr int WN = BN / (32 * TN), WM = 8 / WN;
     constexpr int BM = WM * 32 * TM;
-    static_assert(BM == 512, "the halo tile is 4 x 128 output pixels");
     constexpr int TH = BM / kHaloTW;
+    static_assert(TH == halo_tile_rows(BN), "tile rows");
+    constexpr int kHaloPix = (TH + 2) * kHaloW;
+    constexpr int kHaloBytes = kHaloPix * 32;
     constexpr int BBYTES = 9 * BN * 32;
     constexpr int SB = kHaloBytes + BBYTES;
     constexpr int HSLOTS = kHaloPix * 2, HINS = (HSLOTS + 511) / 512;
@@ -815,7 +817,8 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.t0 = t0;
     a.ytiles = a.xtiles = 0;
     if (halo) {
-        a.ytiles = (ho + 3) / 4;
+        const int th = halo_tile_rows(s.cout <= 32 ? 32 : 128);
+        a.ytiles = (ho + th - 1) / th;
         a.xtiles = (wo + kHaloTW - 1) / kHaloTW;
         a.ntiles = s.cout <= 32 ? 1 : (s.cout + 127) / 128;
         const long tiles = (long)frames_out * a.ytiles * a.xtiles * a.ntiles;
