@@ -27,13 +27,19 @@ inline int conv3d_cpad(int cin) {
     return cin <= 8 ? 8 : cin <= 16 ? 16 : cin <= 32 ? 32 : (cin + 63) / 64 * 64;
 }
 // The halo kernel takes layers with a 3x3 spatial window of unit stride and
-// dilation, at least 16 input channels, and output frames whose width fills
-// its 128-pixel tiles to at least 93% (at 320 columns, 17% of the MFMA work
-// would fall past the frame, and the implicit-GEMM kernel is faster).
-inline bool conv3d_halo_ok(const Conv3dShape& s, int wo) {
-    return s.kh == 3 && s.kw == 3 && s.sh == 1 && s.sw == 1 && s.dh == 1 && s.dw == 1 &&
-           s.cpad % 16 == 0 && wo > 0 && (long)(wo + 127) / 128 * 128 * 100 <= (long)wo * 107;
+// dilation and at least 16 input channels, in tiles 128 or 64 output columns
+// wide, whichever the output width fills to at least 93% (128 first): below
+// that, enough MFMA work falls past the frame that the implicit-GEMM kernel
+// is faster.  Returns the tile width, or 0 for the implicit-GEMM kernel.
+inline int conv3d_halo_width(const Conv3dShape& s, int wo) {
+    if (s.kh != 3 || s.kw != 3 || s.sh != 1 || s.sw != 1 || s.dh != 1 || s.dw != 1 ||
+        s.cpad % 16 != 0 || wo <= 0)
+        return 0;
+    for (int tw = 128; tw >= 64; tw /= 2)
+        if ((long)(wo + tw - 1) / tw * tw * 100 <= (long)wo * 107) return tw;
+    return 0;
 }
+inline bool conv3d_halo_ok(const Conv3dShape& s, int wo) { return conv3d_halo_width(s, wo) > 0; }
 // Packed weight row length: window positions x cpad, rounded up to 64.
 inline long conv3d_kp(const Conv3dShape& s) {
     return ((long)s.kt * s.kh * s.kw * s.cpad + 63) / 64 * 64;

@@ -436,36 +436,38 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
 //
 // For a 3x3 spatial window with unit stride and dilation, the nine window
 // positions of one output tile read nine shifted copies of the same input
-// pixels.  This kernel tiles the output frame in 2-D blocks of TH x 128
-// pixels (TH = 4 at BN 128, 8 at BN 32; one output row per wave; times
-// BN-channel tiles of the outputs) and loads, per k-chunk of 16 input
-// channels and temporal tap, the (TH + 2) x 130 input halo once into LDS
+// pixels.  This kernel tiles the output frame in 2-D blocks of TH x TW
+// pixels (TW = 128, or 64 for frames whose width 128-pixel tiles fit
+// badly; TH x TW = 512 GEMM rows at BN 128, 1024 at BN 32; a wave owns 128
+// of them, i.e. 128 / TW output rows; times BN-channel tiles of the
+// outputs) and loads, per k-chunk of 16 input
+// channels and temporal tap, the (TH + 2) x (TW + 2) input halo once into LDS
 // (32 bytes per pixel) together with the chunk's weights for all nine
 // positions; the nine positions are then nine 16-k MFMA slices that read the
 // halo at shifted pixel offsets.  Against one 64-channel A tile per window
 // position, this cuts the LDS writes per MFMA by 3x and the A traffic from L2
 // by about 6x, and takes one barrier per 144 k instead of per 64 k.
 //
-// LDS stage: halo [(TH + 2) * 130 pixels][2 chunks of 16 bytes], then weights
+// LDS stage: halo [(TH + 2) * (TW + 2) pixels][2 chunks of 16 bytes], then weights
 // [9 positions][BN rows][2 chunks]; chunk c of pixel (or row) p is stored at
 // position c ^ ((p >> 3) & 1), which puts the 16 lanes of each ds_read_b128
 // phase (16 consecutive pixels or rows) on distinct banks for any shift.
 // Two stages: the next chunk's DMA overlaps this chunk's MFMAs.  Each tile
 // lies in one output frame, so a tap's input frame, memory or staged, is
 // the same for the whole tile.
-constexpr int kHaloTW = 128;             // output tile width
-constexpr int kHaloW = kHaloTW + 2;      // halo width
-// output tile rows: one per wave (128 x 64 wave tiles) at BN 128, and
-// 128 x 32 wave tiles over 8 rows at BN 32
-constexpr int halo_tile_rows(int bn) { return bn >= 64 ? 4 : 8; }
+// Output tile rows at tile width tw: 512 GEMM rows (128 x 64 wave tiles) at
+// BN 128, 1024 (128 x 32 wave tiles) at BN 32.
+constexpr int halo_tile_rows(int bn, int tw) { return (bn >= 64 ? 512 : 1024) / tw; }
 
-template <int BN, int OK>
+template <int BN, int TW, int OK>
 __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
     constexpr int TM = 4, TN = BN >= 64 ? 2 : 1;
     constexpr int WN = BN / (32 * TN), WM = 8 / WN;
     constexpr int BM = WM * 32 * TM;
-    constexpr int TH = BM / kHaloTW;
-    static_assert(TH == halo_tile_rows(BN), "tile rows");
+    constexpr int TH = BM / TW;
+    static_assert(TH == halo_tile_rows(BN, TW) && (TW == 128 || TW == 64), "tile shape");
+    constexpr int kHaloW = TW + 2;              // halo width
+    constexpr int FPR = TW / 32;                // fragments per image row
     constexpr int kHaloPix = (TH + 2) * kHaloW;
     constexpr int kHaloBytes = kHaloPix * 32;
     constexpr int BBYTES = 9 * BN * 32;
@@ -493,11 +495,11 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
     const int xt = sp % a.xtiles;
     const int yt = (sp / a.xtiles) % a.ytiles;
     const int to = sp / (a.xtiles * a.ytiles);
-    const int y0 = yt * TH, x0 = xt * kHaloTW;
+    const int y0 = yt * TH, x0 = xt * TW;
     const int col0 = nt * BN;
-    // this wave's GEMM rows: output row ty, columns tx0 + [0, 32 TM)
-    const int ty = (wm * 32 * TM) / kHaloTW;
-    const int tx0 = (wm * 32 * TM) % kHaloTW;
+    // this wave's 128 GEMM rows: output rows ty .. ty + 128 / TW - 1 of the
+    // tile, fragment i at row ty + i / FPR, columns 32 (i % FPR) + [0, 32)
+    const int ty = (wm * 32 * TM) / TW;
 
     const uint32_t pix = (uint32_t)(a.cpad * 2);
     const uint32_t frame_bytes = (uint32_t)(a.H * a.W) * pix;
@@ -560,18 +562,22 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
 
     f32x16 acc[TM][TN];
     bf16x8 fa[2][TM], fb[2][TN];
-    // fragments of window position q (ky = q / 3, kx = q % 3).  Fragment i
-    // is 32 pixels (rows) after fragment 0, which keeps the swizzle bit
-    // ((p >> 3) & 1): its address is fragment 0's plus 1 KB.
-    const int pa = ty * kHaloW + tx0 + l32;
+    // fragments of window position q (ky = q / 3, kx = q % 3).  Within an
+    // image row, fragment i is 32 pixels after the row's first, which keeps
+    // the swizzle bit ((p >> 3) & 1): its address is that one's plus 1 KB.
+    const int pa = ty * kHaloW + l32;
     const int rowb = wn * 32 * TN + l32;
     const int boffl = (rowb * 2 + (g ^ ((rowb >> 3) & 1))) * 16;
     auto frag = [&](const uint8_t* st, int q, int slot) {
         const int ky = q / 3, kx = q - 3 * ky;
-        const int p = pa + ky * kHaloW + kx;
-        const uint8_t* ab = st + (p * 2 + (g ^ ((p >> 3) & 1))) * 16;
 #pragma unroll
-        for (int i = 0; i < TM; ++i) fa[slot][i] = as_bf16x8(*(const uint4*)(ab + 1024 * i));
+        for (int r = 0; r < TM / FPR; ++r) {
+            const int p = pa + (r + ky) * kHaloW + kx;
+            const uint8_t* ab = st + (p * 2 + (g ^ ((p >> 3) & 1))) * 16;
+#pragma unroll
+            for (int i = 0; i < FPR; ++i)
+                fa[slot][r * FPR + i] = as_bf16x8(*(const uint4*)(ab + 1024 * i));
+        }
         const uint8_t* bb = st + kHaloBytes + q * BN * 32 + boffl;
 #pragma unroll
         for (int j = 0; j < TN; ++j) fb[slot][j] = as_bf16x8(*(const uint4*)(bb + 1024 * j));
@@ -616,30 +622,29 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
 
     // Epilogue: register r of a 32x32 accumulator is GEMM row 8(r/4) + 4g +
     // r%4 of its block, i.e. 4 consecutive output pixels of one row.
-    const int y = y0 + ty;
-    if (y >= a.Ho) return;
-    const long mrow = ((long)to * a.Ho + y) * a.Wo;
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int col = col0 + wn * 32 * TN + 32 * j + l32;
         if (col >= a.cout) continue;
         const float bv = a.bias ? a.bias[col] : 0.f;
-        const long cbase = (long)col * a.out_cstep + a.out_off + mrow;
+        const long cbase = (long)col * a.out_cstep + a.out_off;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int rg = 0; rg < 4; ++rg) {
-                const int x = x0 + tx0 + 32 * i + 8 * rg + 4 * g;
-                if (x >= a.Wo) continue;
+                const int y = y0 + ty + i / FPR;
+                const int x = x0 + 32 * (i % FPR) + 8 * rg + 4 * g;
+                if (y >= a.Ho || x >= a.Wo) continue;
+                const long xrow = ((long)to * a.Ho + y) * a.Wo + x;
                 const float v[4] = {acc[i][j][4 * rg] + bv, acc[i][j][4 * rg + 1] + bv,
                                     acc[i][j][4 * rg + 2] + bv, acc[i][j][4 * rg + 3] + bv};
                 if (a.vec_ok && x + 3 < a.Wo) {
-                    store4(a.out, cbase + x, v[0], v[1], v[2], v[3], OK);
+                    store4(a.out, cbase + xrow, v[0], v[1], v[2], v[3], OK);
                 } else {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         if (x + e >= a.Wo) continue;
-                        const long idx = cbase + x + e;
+                        const long idx = cbase + xrow + e;
                         if (OK == 1)
                             ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
                         else if (OK == 2)
@@ -652,15 +657,15 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
     }
 }
 
-template <int BN>
+template <int BN, int TW>
 void launch_conv3d_halo(const ConvArgs& a, hipStream_t stream) {
     const unsigned grid = (unsigned)a.mtiles;
     if (a.out_kind == 1)
-        conv3d_halo_kernel<BN, 1><<<grid, 512, 0, stream>>>(a);
+        conv3d_halo_kernel<BN, TW, 1><<<grid, 512, 0, stream>>>(a);
     else if (a.out_kind == 2)
-        conv3d_halo_kernel<BN, 2><<<grid, 512, 0, stream>>>(a);
+        conv3d_halo_kernel<BN, TW, 2><<<grid, 512, 0, stream>>>(a);
     else
-        conv3d_halo_kernel<BN, 0><<<grid, 512, 0, stream>>>(a);
+        conv3d_halo_kernel<BN, TW, 0><<<grid, 512, 0, stream>>>(a);
 }
 
 template <int BN, bool SMALL>
@@ -771,7 +776,8 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     const long m = (long)frames_out * ho * wo;
     const long kp = conv3d_kp(s);
     const bool small = s.cpad < 64;
-    const bool halo = conv3d_halo_ok(s, wo);
+    const int tw = conv3d_halo_width(s, wo);
+    const bool halo = tw > 0;
     // the implicit-GEMM kernel reads memory frames in place only when each
     // 8-row DMA group lies in one output frame; the halo kernel's tiles
     // always do
@@ -817,18 +823,18 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.t0 = t0;
     a.ytiles = a.xtiles = 0;
     if (halo) {
-        const int th = halo_tile_rows(s.cout <= 32 ? 32 : 128);
+        const int th = halo_tile_rows(s.cout <= 32 ? 32 : 128, tw);
         a.ytiles = (ho + th - 1) / th;
-        a.xtiles = (wo + kHaloTW - 1) / kHaloTW;
+        a.xtiles = (wo + tw - 1) / tw;
         a.ntiles = s.cout <= 32 ? 1 : (s.cout + 127) / 128;
         const long tiles = (long)frames_out * a.ytiles * a.xtiles * a.ntiles;
         if (tiles > INT_MAX) return hipErrorInvalidValue;
         a.mtiles = (int)tiles;
         a.vec_ok = a.vec_ok && wo % 4 == 0;
         if (s.cout <= 32)
-            launch_conv3d_halo<32>(a, stream);
+            tw == 128 ? launch_conv3d_halo<32, 128>(a, stream) : launch_conv3d_halo<32, 64>(a, stream);
         else
-            launch_conv3d_halo<128>(a, stream);
+            tw == 128 ? launch_conv3d_halo<128, 128>(a, stream) : launch_conv3d_halo<128, 64>(a, stream);
         return hipGetLastError();
     }
     if (s.cout <= 32) {

@@ -92,6 +92,8 @@ SHAPES = [
     (96, 128, 3, 7, 240, dict(k=(2, 3, 3), s=(2, 1, 1))),   # temporal stride 2
     (64, 200, 2, 5, 120, {}),                          # two channel tiles, the second ragged
     (256, 256, 2, 4, 128, {}),                         # 256 channels in and out
+    (64, 160, 2, 10, 192, {}),                         # 64-column tiles (192 = 3 x 64)
+    (128, 3, 2, 9, 320, {}),                           # RGB output in 64-column tiles
 ]
 
 
