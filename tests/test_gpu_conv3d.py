@@ -105,15 +105,20 @@ def test_conv3d_matches_oracle(cin, cout, frames, h, w, kw):
     _check(got, x, wts, bias, cfgs[1])
 
 
+# (10, 12): the implicit-GEMM kernel; (6, 120): the halo kernel.  A channel
+# stride padded by 4 elements leaves 16-bit channel rows without 16-byte
+# alignment, which the staging pass reads element by element.
 @pytest.mark.parametrize("in_dtype,out_dtype", [("bf16", "bf16"), ("f16", "f32"), ("f32", "f16")])
-def test_conv3d_16bit_blobs_and_padded_cstep(in_dtype, out_dtype):
+@pytest.mark.parametrize("hw", [(10, 12), (6, 120)])
+@pytest.mark.parametrize("cstep_pad", [8, 4])
+def test_conv3d_16bit_blobs_and_padded_cstep(in_dtype, out_dtype, hw, cstep_pad):
     import torch
     dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
     cfgs = _cfg(64, 128)
-    x, wts, bias = _case(64, 128, 2, 10, 12, cfgs, 7)
+    x, wts, bias = _case(64, 128, 2, hw[0], hw[1], cfgs, 7)
     if in_dtype != "f32":
         x = torch.from_numpy(x).to(dt[in_dtype]).float().numpy()    # the stored values
-    got = _run(_device(cfgs[0], wts, bias), x, cstep_pad=8, dtype=dt[in_dtype],
+    got = _run(_device(cfgs[0], wts, bias), x, cstep_pad=cstep_pad, dtype=dt[in_dtype],
                out_dtype=dt[out_dtype])
     _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)
     assert_close(got, ref)
