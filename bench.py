@@ -207,14 +207,16 @@ def sampler_tail(reps=50):
 
 
 # VAE decoder DecomposedConv3D layers (3x3x3, pad 1, causal 2-frame memory)
-# at 720p: one temporal slice of 4 output frames at each resolution level,
-# and the encoder's RGB input layer over 4 full-resolution frames
+# at 720p: one temporal slice of 4 output frames at each resolution level
+# (one frame at the two lowest), and the encoder's RGB input layer over 4
+# full-resolution frames
 VAE_CONV_LAYERS = [
     ("full_res_128", 128, 128, 4, 720, 1280),
     ("half_res_256", 256, 256, 4, 360, 640),
     ("quarter_res_512", 512, 512, 1, 180, 320),
     ("rgb_out_128_to_3", 128, 3, 4, 720, 1280),
     ("rgb_in_3_to_128", 3, 128, 4, 720, 1280),
+    ("latent_res_512", 512, 512, 1, 90, 160),
 ]
 
 
