@@ -36,17 +36,18 @@ __device__ __forceinline__ float load_elem(const void* p, long i) {
     return ((const float*)p)[i];
 }
 
-// One block moves 128 pixels x 64 channels: 64 channel rows of 128 pixels
-// are read as 16-byte runs (8 elements of a 16-bit blob, 4 of an fp32 one;
+// One block moves P pixels x 64 channels (P = 128; 64 for layers of at most
+// 32 input channels, whose blocks have few channel rows to read): 64 channel
+// rows of P pixels are read as 16-byte runs (8 elements of a 16-bit blob, 4 of an fp32 one;
 // single elements when the rows are not 16-byte aligned, `vec` false),
-// transposed in LDS (row pitch 129 floats) and written as 128 pixel rows of
+// transposed in LDS (row pitch P + 1 floats) and written as P pixel rows of
 // 128 bytes (or of cpad channels when cpad is 8, 16 or 32), 16 bytes a
 // thread.  Channels at or above cin are written as zeros.
-template <int KIND>
+template <int KIND, int P>
 __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
     const void* __restrict__ in, long cstep, int cin, long pixels, int cpad, int vec,
     uint16_t* __restrict__ staged, uint16_t* __restrict__ tail, long tail_q0) {
-    constexpr int P = 128;              // pixels per block
+    static_assert(P == 128 || P == 64, "pixels per block");
     constexpr int PITCH = P + 1;
     constexpr int EL = KIND == 0 ? 4 : 8;   // elements per 16-byte load
     constexpr int RUNS = P / EL;            // runs per channel row
@@ -737,23 +738,35 @@ hipError_t launch_vae_shuffle(const void* packed, int kind, long packed_cstep, i
     return hipGetLastError();
 }
 
+template <int P>
+static void stage_launch(const void* input, int in_kind, long in_cstep, int cin, long pixels,
+                         int cpad, int vec, uint16_t* staged, uint16_t* tail, long tail_q0,
+                         hipStream_t stream) {
+    const dim3 grid((unsigned)((pixels + P - 1) / P), (unsigned)((cpad + 63) / 64));
+    if (in_kind == 1)
+        conv3d_stage_kernel<1, P><<<grid, kStageThreads, 0, stream>>>(
+            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
+    else if (in_kind == 2)
+        conv3d_stage_kernel<2, P><<<grid, kStageThreads, 0, stream>>>(
+            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
+    else
+        conv3d_stage_kernel<0, P><<<grid, kStageThreads, 0, stream>>>(
+            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
+}
+
 hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, int cin,
                                long pixels, int cpad, uint16_t* staged, uint16_t* tail,
                                long tail_q0, hipStream_t stream) {
     if (pixels <= 0) return hipSuccess;
-    const dim3 grid((unsigned)((pixels + 127) / 128), (unsigned)((cpad + 63) / 64));
     // 16-byte runs need 16-byte aligned channel rows
     const int esz = in_kind == 0 ? 4 : 2;
     const int vec = ((uintptr_t)input % 16) == 0 && (in_cstep * esz) % 16 == 0;
-    if (in_kind == 1)
-        conv3d_stage_kernel<1><<<grid, kStageThreads, 0, stream>>>(
-            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
-    else if (in_kind == 2)
-        conv3d_stage_kernel<2><<<grid, kStageThreads, 0, stream>>>(
-            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
+    if (cpad < 64)
+        stage_launch<64>(input, in_kind, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0,
+                         stream);
     else
-        conv3d_stage_kernel<0><<<grid, kStageThreads, 0, stream>>>(
-            input, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0);
+        stage_launch<128>(input, in_kind, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0,
+                          stream);
     return hipGetLastError();
 }
 
