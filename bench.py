@@ -358,7 +358,8 @@ def stack_7b(steps, warmup):
     grid: per block QKV -> window attention (regular windows in even blocks,
     shifted in odd ones) -> out -> MLP up GELU -> down, each block's output
     feeding the next; the 64 text tokens are projected 5120 -> 3072 once per
-    stack.  Every block has its own random-init bf16 weights (7.2 GB)."""
+    stack.  Every block has its own random-init bf16 weights (7.2 GB).  Also
+    timed: the same stack with every block's norm and AdaSingle modulation."""
     import torch
     from seedvr2_ncnn_amd import capi
     dev = torch.device("cuda:0")
@@ -407,17 +408,61 @@ def stack_7b(steps, warmup):
             capi.shared_linear(o_v, o_t, blk["up"], blk["bup"], capi.ACT_GELU, y_video=h_v, y_text=h_t)
             capi.shared_linear(h_v, h_t, blk["dn"], blk["bdn"], capi.ACT_NONE, y_video=x_v, y_text=x_t)
 
-    for _ in range(warmup):
-        forward()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(steps):
-        forward()
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / steps
+    # The whole stack with each block's norm and AdaSingle modulation on an
+    # fp32 residual stream: block i's MLP gate and residual sum share one
+    # s2_dit_ada_out_in pass with block i + 1's attention norm and modulation.
+    res_v = torch.empty(lv, D, device=dev)
+    res_t = torch.empty(lt, D, device=dev)
+    hin_v, hin_t = torch.empty_like(x_v), torch.empty_like(x_t)
+    mods = [{k: torch.randn(1, D, generator=gen, device=dev) * 0.1 + (1.0 if k.endswith("scale") else 0.0)
+             for k in ("a_shift", "a_scale", "a_gate", "m_shift", "m_scale", "m_gate")}
+            for _ in range(STACK_BLOCKS)]
+    vr, tr = [lv], [lt]
+
+    def forward_full():
+        res_v.copy_(x_v0)
+        capi.shared_linear(text_in, None, w_text, b_text, capi.ACT_NONE, y_video=x_t)
+        res_t.copy_(x_t)
+        capi.ada_in(res_v, res_t, vr, tr, mods[0]["a_shift"], mods[0]["a_scale"],
+                    out_video=hin_v, out_text=hin_t)
+        for i, blk in enumerate(blocks):
+            md = mods[i]
+            capi.shared_linear(hin_v, hin_t, blk["qkv"], blk["bqkv"], capi.ACT_NONE, y_video=qkv_v,
+                               y_text=qkv_t)
+            capi.awa_forward(plans[i % 2], blk["norms"], freqs,
+                             qkv_v[:, :D], qkv_v[:, D:2 * D], qkv_v[:, 2 * D:],
+                             qkv_t[:, :D], qkv_t[:, D:2 * D], qkv_t[:, 2 * D:],
+                             workspace=ws, out_video=a_v, out_text=a_t)
+            capi.shared_linear(a_v, a_t, blk["o"], blk["bo"], capi.ACT_NONE, y_video=o_v, y_text=o_t)
+            capi.ada_out_in(res_v, res_t, o_v, o_t, vr, tr, md["a_gate"], md["m_shift"],
+                            md["m_scale"], h_video=hin_v, h_text=hin_t)
+            capi.shared_linear(hin_v, hin_t, blk["up"], blk["bup"], capi.ACT_GELU, y_video=h_v,
+                               y_text=h_t)
+            capi.shared_linear(h_v, h_t, blk["dn"], blk["bdn"], capi.ACT_NONE, y_video=o_v,
+                               y_text=o_t)
+            if i + 1 < len(blocks):
+                nx = mods[i + 1]
+                capi.ada_out_in(res_v, res_t, o_v, o_t, vr, tr, md["m_gate"], nx["a_shift"],
+                                nx["a_scale"], h_video=hin_v, h_text=hin_t)
+            else:
+                capi.ada_out(res_v, res_t, o_v, o_t, vr, tr, md["m_gate"])
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            fn()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+    ms = timed(forward)
     finite = bool(torch.isfinite(x_v.float()).all().item())
+    ms_full = timed(forward_full)
+    finite = finite and bool(torch.isfinite(res_v).all().item())
 
     m = lv + lt
     gemm = 2 * m * D * (3 * D + D + 2 * F)
@@ -436,6 +481,10 @@ def stack_7b(steps, warmup):
             "steps": steps, "warmup": warmup, "ms_per_stack": round(ms, 3),
             "ms_per_block": round(ms / STACK_BLOCKS, 4), "stack_tflop": round(flops / 1e12, 3),
             "tflops": round(tf, 1), "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2),
+            "ms_per_stack_with_modulation": round(ms_full, 3),
+            "modulation_note": "fp32 residual stream; each block's norm + AdaSingle modulation "
+                               "and gated residual sums (s2_dit_ada_in once, s2_dit_ada_out_in "
+                               "twice per block, s2_dit_ada_out after the last)",
             "output_finite": finite}
 
 
