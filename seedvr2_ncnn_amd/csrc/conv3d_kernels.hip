@@ -37,30 +37,32 @@ __device__ __forceinline__ float load_elem(const void* p, long i) {
 }
 
 // One block moves P pixels x 64 channels (P = 128; 64 for layers of at most
-// 32 input channels, whose blocks have few channel rows to read): 64 channel
-// rows of P pixels are read as 16-byte runs (8 elements of a 16-bit blob, 4 of an fp32 one;
-// single elements when the rows are not 16-byte aligned, `vec` false),
-// transposed in LDS (row pitch P + 1 floats) and written as P pixel rows of
-// 128 bytes (or of cpad channels when cpad is 8, 16 or 32), 16 bytes a
-// thread.  Channels at or above cin are written as zeros.
+// 32 input channels, whose blocks have few channel rows to read).  Lane l of
+// a load reads 16 bytes (8 elements of a 16-bit blob, 4 of an fp32 one;
+// single elements when the rows are not 16-byte aligned, `vec` false) of
+// channel l at one run of pixels, and writes them to an LDS tile stored
+// pixel-major ([pixel][68 floats]: consecutive lanes, consecutive words);
+// a pixel's 8-channel parts then come out as two 16-byte LDS reads and leave
+// as one 16-byte store, 8 consecutive threads covering a 128-byte channel run
+// (cpad channels when cpad is 8, 16 or 32).  Channels at or above cin are
+// written as zeros.
 template <int KIND, int P>
 __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
     const void* __restrict__ in, long cstep, int cin, long pixels, int cpad, int vec,
     uint16_t* __restrict__ staged, uint16_t* __restrict__ tail, long tail_q0) {
     static_assert(P == 128 || P == 64, "pixels per block");
-    constexpr int PITCH = P + 1;
-    constexpr int EL = KIND == 0 ? 4 : 8;   // elements per 16-byte load
-    constexpr int RUNS = P / EL;            // runs per channel row
-    __shared__ float tile[64 * PITCH];
+    constexpr int PITCH = 68;                 // floats per pixel row (16-byte multiple)
+    constexpr int EL = KIND == 0 ? 4 : 8;     // elements per 16-byte load
+    __shared__ __attribute__((aligned(16))) float tile[P * PITCH];
     const long q0 = (long)blockIdx.x * P;
     const int c0 = blockIdx.y * 64;
     const int t = threadIdx.x;
     const bool full = vec && q0 + P <= pixels;
 #pragma unroll
-    for (int i = 0; i < 64 * RUNS / kStageThreads; ++i) {
-        const int idx = i * kStageThreads + t;
-        const int cl = idx / RUNS;
-        const int qe = (idx % RUNS) * EL;
+    for (int i = 0; i < 64 * (P / EL) / kStageThreads; ++i) {
+        const int item = i * kStageThreads + t;
+        const int cl = item & 63;
+        const int qe = (item >> 6) * EL;
         const int c = c0 + cl;
         float v[EL];
 #pragma unroll
@@ -88,7 +90,7 @@ __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
             }
         }
 #pragma unroll
-        for (int e = 0; e < EL; ++e) tile[cl * PITCH + qe + e] = v[e];
+        for (int e = 0; e < EL; ++e) tile[(qe + e) * PITCH + cl] = v[e];
     }
     __syncthreads();
     // a pixel holds cpad channels: with cpad 8, 16 or 32 only the first
@@ -99,10 +101,10 @@ __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
         const int idx = i * kStageThreads + t;
         const int q = idx >> 3, part = idx & 7;
         if (part >= parts || q0 + q >= pixels) continue;
-        uint16_t h[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = f32_to_bf16(tile[(part * 8 + e) * PITCH + q]);
-        const uint4 val = pack8_bf16(h);
+        const float4 lo = *reinterpret_cast<const float4*>(&tile[q * PITCH + part * 8]);
+        const float4 hi = *reinterpret_cast<const float4*>(&tile[q * PITCH + part * 8 + 4]);
+        const uint4 val = make_uint4(pack2_bf16_rne(lo.x, lo.y), pack2_bf16_rne(lo.z, lo.w),
+                                     pack2_bf16_rne(hi.x, hi.y), pack2_bf16_rne(hi.z, hi.w));
         *reinterpret_cast<uint4*>(staged + (q0 + q) * cpad + c0 + part * 8) = val;
         // pixels from tail_q0 on are the next temporal memory as well
         if (tail && q0 + q >= tail_q0)
