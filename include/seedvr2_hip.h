@@ -357,6 +357,11 @@ S2_API int s2_conv3d_pack_weights(const s2_conv3d_config* config, const float* w
  * (0: the layer keeps no memory). */
 S2_API int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, int width,
                                   size_t* bytes, int* frames);
+/* Workspace of a forward: the staged input frames (and copied memory
+ * frames), plus, for layers whose output tiles would leave most of the chip
+ * idle, fp32 partial tiles of a k loop split over the temporal taps.  A
+ * smaller workspace that still holds the staged frames is accepted; the
+ * forward then runs the k loop unsplit. */
 S2_API int s2_conv3d_workspace_bytes(const s2_conv3d_config* config, int frames, int height,
                                      int width, int memory_frames, size_t* bytes);
 

@@ -894,6 +894,11 @@ int s2_conv3d_workspace_bytes(const s2_conv3d_config* config, int frames, int he
         return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
     *bytes = align256((size_t)(frames + memory_frames) * height * width *
                       s2::conv3d_cpad(config->num_input) * 2);
+    // fp32 partial tiles when the k loop is split over the temporal taps
+    const s2::Conv3dShape s = conv3d_shape(config);
+    const long mo = (long)to * ho * wo;
+    const int splits = s2::conv3d_tap_split(s, mo, wo);
+    if (splits > 1) *bytes += align256((size_t)splits * s.cout * mo * 4);
     return S2_OK;
 }
 
@@ -968,6 +973,17 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
                                    s.cpad, staged + (size_t)lead * frame_elems,
                                    tail_in_stage ? (uint16_t*)next_memory : nullptr,
                                    (long)(frames - cache) * plane_in, st));
+    // fp32 partial tiles of a k loop split over the taps, after the staged
+    // frames, when the workspace holds them (s2_conv3d_workspace_bytes counts
+    // them; a smaller workspace runs the whole k loop per tile instead)
+    float* part = nullptr;
+    {
+        const size_t need = align256((size_t)(mem + frames) * frame_bytes);
+        const long mo = (long)to * ho * wo;
+        const int splits = s2::conv3d_tap_split(s, mo, wo);
+        if (splits > 1 && workspace_bytes >= need + (size_t)splits * s.cout * mo * 4)
+            part = (float*)((uint8_t*)workspace + need);
+    }
     auto vframe = [&](long p) { return (int)std::max(p - shift, 0L); };
     const long reach = (long)(config->kernel_t - 1) * config->dilation_t;
     for (int t0 = 0; t0 < to;) {
@@ -982,7 +998,7 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
         S2_HIP(s2::launch_conv3d(s, (const uint16_t*)memory, kmem, (size_t)kmem * frame_bytes,
                                  staged + (size_t)lo * frame_elems, span, lo, shift, height, width,
                                  ho, wo, t0, n, (const uint16_t*)packed_weights, bias, output,
-                                 (int)out_dtype, out_cstep, st));
+                                 (int)out_dtype, out_cstep, part, st));
         t0 += n;
     }
     if (want_memory && !tail_in_stage) {

@@ -40,6 +40,19 @@ inline int conv3d_halo_width(const Conv3dShape& s, int wo) {
     return 0;
 }
 inline bool conv3d_halo_ok(const Conv3dShape& s, int wo) { return conv3d_halo_width(s, wo) > 0; }
+// Output tiles of the implicit-GEMM kernel for m output pixels.
+inline long conv3d_gemm_tiles(const Conv3dShape& s, long m) {
+    if (s.cout <= 128) return (m + 511) / 512 * ((s.cout + 127) / 128);
+    return (m + 255) / 256 * ((s.cout + 255) / 256);
+}
+// Temporal taps the implicit-GEMM kernel splits its k loop over (one
+// workgroup per tap and tile, partial tiles summed by a second pass) when its
+// tiles would leave most of the chip idle: layers of at least 64 input
+// channels with fewer tiles than 256 (the CU count).  1: no split.
+inline int conv3d_tap_split(const Conv3dShape& s, long m, int wo) {
+    if (s.cpad < 64 || s.kt < 2 || conv3d_halo_width(s, wo) > 0) return 1;
+    return conv3d_gemm_tiles(s, m) < 256 ? s.kt : 1;
+}
 // Packed weight row length: window positions x cpad, rounded up to 64.
 inline long conv3d_kp(const Conv3dShape& s) {
     return ((long)s.kt * s.kh * s.kw * s.cpad + 63) / 64 * 64;
@@ -62,11 +75,14 @@ hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s
 // hold every input frame these outputs read).  Both buffers < 2 GiB; mem > 0
 // needs ho*wo % 8 == 0.  out: planar [cout][...], element (co, t, y, x) at
 // co*out_cstep + (t*Ho + y)*Wo + x, type out_kind; bias fp32 [cout] or null.
+// part: fp32 scratch of conv3d_tap_split(s, frames_out*ho*wo, wo) x cout x
+// frames_out*ho*wo floats for the split k loop, or null (no split).
 hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
                          size_t memory_bytes, const uint16_t* staged, size_t staged_bytes,
                          int frame_base, int shift, int height, int width, int ho, int wo,
                          int t0, int frames_out, const uint16_t* packed, const float* bias,
-                         void* out, int out_kind, long out_cstep, hipStream_t stream);
+                         void* out, int out_kind, long out_cstep, float* part,
+                         hipStream_t stream);
 
 // VAEUpsample3D's shuffle: packed [channels*tr*sr*sr][frames][h][w] (channel
 // stride packed_cstep) -> out [channels][frames*tr - remove_head][h*sr][w*sr]

@@ -155,6 +155,11 @@ struct ConvArgs {
     int shift, fbase, t0;
     int mtiles, ntiles;
     int ytiles, xtiles;   // halo kernel: output tiles per frame
+    // k loop split over the temporal taps: workgroup row blockIdx.y takes
+    // tap blockIdx.y and stores its raw fp32 tile to part + blockIdx.y *
+    // part_split (planar [cout][M]); null: the whole loop, normal epilogue
+    float* part;
+    long part_split;
 };
 
 // Eight waves in a grid of 128x64 wave tiles (4x2 MFMA 32x32x16
@@ -285,7 +290,10 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
         for (int j = 0; j < AJ; ++j) voffa[j] = (rmask[j] & bit) ? rbase[j] + koff : 0x80000000u;
     };
     const int cpc = SMALL ? 1 : a.cpad / 64;   // k-steps per window position
-    const int nk = a.kp / 64;
+    // taps [tap0, tap0 + ntaps) of the k loop (all of them unless split)
+    const int tap0 = (!SMALL && a.part) ? (int)blockIdx.y : 0;
+    const int kbase = tap0 * a.kh * a.kw * cpc;
+    const int nk = (!SMALL && a.part) ? a.kh * a.kw * cpc : a.kp / 64;
     // SMALL: this wave's 16-byte part of a pixel and window position within
     // a k-step; the position of k-step ks is ks * (64 / cpad) + its index
     const int parts = a.cpad / 8;
@@ -313,7 +321,7 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     };
     auto issue = [&](int stage, int ks, int cc) {
         const uint32_t soffa = (uint32_t)(cc * RB);
-        const uint32_t soffb = (uint32_t)(ks * RB);
+        const uint32_t soffb = (uint32_t)((ks + kbase) * RB);
         const uint32_t st = lds_base + stage * SB;
         if (SMALL) {
 #pragma unroll
@@ -353,11 +361,11 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // window position and channel chunk of the next k-step to issue
-    int tap = 0, ky = 0, kx = 0, cc = 0;
+    int tap = tap0, ky = 0, kx = 0, cc = 0;
     if (SMALL) {
         set_step_small(0);
     } else {
-        set_tap(0);
+        set_tap(tap0);
         set_pos(0, 0);
     }
     issue(0, 0, 0);
@@ -402,6 +410,33 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
     // Epilogue: register r of a 32x32 accumulator is row 8(r/4) + 4g + r%4,
     // column l32, so each lane holds 4 consecutive output pixels of one
     // output channel: one 16-byte (fp32) or 8-byte store into that plane.
+    if (!SMALL && a.part) {
+        // raw partial tile of this tap, fp32 [cout][M]
+        float* pp = a.part + (long)blockIdx.y * a.part_split;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = col0 + wn * 32 * TN + 32 * j + l32;
+            if (col >= a.cout) continue;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int rg = 0; rg < 4; ++rg) {
+                    const int m = row0 + wm * 32 * TM + 32 * i + 8 * rg + 4 * g;
+                    const long idx = (long)col * a.M + m;
+                    if ((a.M & 3) == 0 && m + 3 < a.M) {
+                        // m and M multiples of 4: a 16-byte aligned run
+                        *reinterpret_cast<float4*>(pp + idx) =
+                            make_float4(acc[i][j][4 * rg], acc[i][j][4 * rg + 1],
+                                        acc[i][j][4 * rg + 2], acc[i][j][4 * rg + 3]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (m + e < a.M) pp[idx + e] = acc[i][j][4 * rg + e];
+                    }
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < TN; ++j) {
         const int col = col0 + wn * 32 * TN + 32 * j + l32;
@@ -671,9 +706,32 @@ void launch_conv3d_halo(const ConvArgs& a, hipStream_t stream) {
         conv3d_halo_kernel<BN, TW, 0><<<grid, 512, 0, stream>>>(a);
 }
 
+// sum of the taps' partial tiles in tap order, plus the bias, stored as
+// out_kind at out[col * out_cstep + out_off + m]
+__global__ __launch_bounds__(256) void conv3d_reduce_kernel(const float* __restrict__ part,
+                                                            int splits, long part_split, int cout,
+                                                            int M, const float* __restrict__ bias,
+                                                            void* __restrict__ out, int out_kind,
+                                                            long out_cstep, long out_off) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)cout * M) return;
+    const int col = (int)(i / M);
+    const long m = i - (long)col * M;
+    float v = part[i];
+    for (int sp = 1; sp < splits; ++sp) v += part[sp * part_split + i];
+    if (bias) v += bias[col];
+    const long idx = (long)col * out_cstep + out_off + m;
+    if (out_kind == 1)
+        ((uint16_t*)out)[idx] = f32_to_bf16(v);
+    else if (out_kind == 2)
+        ((_Float16*)out)[idx] = (_Float16)v;
+    else
+        ((float*)out)[idx] = v;
+}
+
 template <int BN, bool SMALL>
 void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
-    const unsigned grid = (unsigned)(a.mtiles * a.ntiles);
+    const dim3 grid((unsigned)(a.mtiles * a.ntiles), a.part ? (unsigned)a.kt : 1u);
     if (a.out_kind == 1)
         conv3d_kernel<BN, 1, SMALL><<<grid, 512, 0, stream>>>(a);
     else if (a.out_kind == 2)
@@ -786,7 +844,8 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
                          size_t memory_bytes, const uint16_t* staged, size_t staged_bytes,
                          int frame_base, int shift, int height, int width, int ho, int wo,
                          int t0, int frames_out, const uint16_t* packed, const float* bias,
-                         void* out, int out_kind, long out_cstep, hipStream_t stream) {
+                         void* out, int out_kind, long out_cstep, float* part,
+                         hipStream_t stream) {
     if (frames_out <= 0) return hipSuccess;
     const long m = (long)frames_out * ho * wo;
     const long kp = conv3d_kp(s);
@@ -837,6 +896,13 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.fbase = frame_base;
     a.t0 = t0;
     a.ytiles = a.xtiles = 0;
+    a.part = nullptr;
+    a.part_split = 0;
+    const int splits = part ? conv3d_tap_split(s, m, wo) : 1;
+    if (splits > 1) {
+        a.part = part;
+        a.part_split = (long)s.cout * m;
+    }
     if (halo) {
         const int th = halo_tile_rows(s.cout <= 32 ? 32 : 128, tw);
         a.ytiles = (ho + th - 1) / th;
@@ -864,6 +930,12 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
         a.mtiles = (int)((m + 255) / 256);
         a.ntiles = (s.cout + 255) / 256;
         launch_conv3d_kernel<256>(a, stream);
+    }
+    if (a.part) {
+        const long n = (long)s.cout * m;
+        conv3d_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
+            a.part, splits, a.part_split, s.cout, (int)m, bias, out, out_kind, out_cstep,
+            a.out_off);
     }
     return hipGetLastError();
 }

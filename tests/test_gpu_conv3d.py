@@ -94,6 +94,11 @@ SHAPES = [
     (256, 256, 2, 4, 128, {}),                         # 256 channels in and out
     (64, 160, 2, 10, 192, {}),                         # 64-column tiles (192 = 3 x 64)
     (128, 3, 2, 9, 320, {}),                           # RGB output in 64-column tiles
+    # layers of at least 64 input channels with fewer than 256 implicit-GEMM
+    # tiles split the k loop over the temporal taps (most small cases above
+    # do too); these two are a latent-width frame and two temporal taps
+    (512, 512, 1, 9, 16, {}),                          # 512 channels, 3 taps
+    (64, 96, 3, 6, 10, dict(k=(2, 3, 3))),             # 2 taps
 ]
 
 
