@@ -181,15 +181,18 @@ S2_API int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2
  * operands: fp32 and fp16 activations are rounded to bf16 (nearest even) as
  * they are staged.  Either stream may have m == 0 (its pointers are then
  * ignored).  k must be a multiple of 8; x, y and weight 16-byte aligned.
- * The first call on a device allocates that device's split-k scratch (about
- * 128 MB of partial-tile slots and their counters), kept until the process
- * ends; calls whose kernels overlap in time on one device (different streams)
- * share it and must not run concurrently. */
+ * When the last wave of output tiles would leave the chip mostly idle, its
+ * tiles are split along k over several workgroups, which meet in a scratch
+ * of partial tiles: the first such call on a (device, stream) pair allocates
+ * that pair's scratch (one 256 KB slot per compute unit, 64 MB on MI355X,
+ * plus counters), kept until the process ends.  Calls on different streams
+ * therefore never share scratch and may run concurrently. */
 S2_API int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
                              s2_dtype x_dtype, const uint16_t* weight, const float* bias,
                              int n, int k, int activation,
                              void* y_video, void* y_text, s2_dtype y_dtype,
                              s2_stream_t stream);
+
 
 /* ---- DiT frontend and tail, sampler step -------------------------------- */
 /* The steps either side of the block stack, on device fp32 buffers.  A video
@@ -364,6 +367,14 @@ S2_API int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, in
  * forward then runs the k loop unsplit. */
 S2_API int s2_conv3d_workspace_bytes(const s2_conv3d_config* config, int frames, int height,
                                      int width, int memory_frames, size_t* bytes);
+/* The workspace of s2_conv3d_forward_padded: the staged frames are those of
+ * the unpadded input, the output extent (and with it the partial tiles of a
+ * split k loop) that of the frames padded with pad_right columns and
+ * pad_bottom rows, as in VAEDownsample3D (vae_downsample3d.cpp:145-172).
+ * Valid for inputs that only the padding makes large enough. */
+S2_API int s2_conv3d_workspace_bytes_padded(const s2_conv3d_config* config, int frames,
+                                            int height, int width, int pad_right, int pad_bottom,
+                                            int memory_frames, size_t* bytes);
 
 /* DecomposedConv3D::forward (decomposed_conv3d.cpp:605-755).  input: device
  * planar [num_input][frames][height][width] in in_dtype, channel stride
@@ -385,8 +396,8 @@ S2_API int s2_conv3d_forward(const s2_conv3d_config* config, const void* packed_
 /* s2_conv3d_forward over the input padded with pad_right zero columns and
  * pad_bottom zero rows: VAEDownsample3D's padding (vae_downsample3d.cpp:145-172)
  * without materialising it.  The output extent is s2_conv3d_output_shape of
- * (height + pad_bottom, width + pad_right); the memory and the workspace are
- * those of the unpadded frames. */
+ * (height + pad_bottom, width + pad_right); the memory is that of the
+ * unpadded frames; the workspace is s2_conv3d_workspace_bytes_padded. */
 S2_API int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_weights,
                                     const float* bias, const void* input, s2_dtype in_dtype,
                                     int frames, int height, int width, long in_cstep,

@@ -38,7 +38,7 @@ EXPORTS = (
     "s2_conv3d_memory_bytes", "s2_conv3d_workspace_bytes", "s2_conv3d_forward",
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
-    "s2_dit_ada_out_in",
+    "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded",
 )
 
 
@@ -145,6 +145,7 @@ def lib() -> ctypes.CDLL:
         L.s2_conv3d_pack_weights.argtypes = [C3, vp, vp, vp]
         L.s2_conv3d_memory_bytes.argtypes = [C3, ci, ci, P(sz), P(ci)]
         L.s2_conv3d_workspace_bytes.argtypes = [C3, ci, ci, ci, ci, P(sz)]
+        L.s2_conv3d_workspace_bytes_padded.argtypes = [C3, ci, ci, ci, ci, ci, ci, P(sz)]
         M3 = P(MhaConfig)
         L.s2_mha_weight_bytes.argtypes = [M3, P(sz)]
         L.s2_mha_prepare_weights.argtypes = [M3, vp, vp, vp, vp, vp, vp, vp, vp, vp, vp]
@@ -369,11 +370,11 @@ def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, 
         y_video = torch.empty((m0, n), dtype=odt, device=dev)
     if y_text is None and m1:
         y_text = torch.empty((m1, n), dtype=odt, device=dev)
-    check(lib().s2_shared_linear_forward(_ptr(x_video), m0, _ptr(x_text) if m1 else None, m1, xd,
-                                         _ptr(weight_bf16), _ptr(bias), n, k, activation,
-                                         _ptr(y_video), _ptr(y_text) if m1 else None,
-                                         _dtype_code(y_video), _stream(stream)),
-          "s2_shared_linear_forward")
+    name = "s2_shared_linear_forward"
+    check(getattr(lib(), name)(_ptr(x_video), m0, _ptr(x_text) if m1 else None, m1, xd,
+                               _ptr(weight_bf16), _ptr(bias), n, k, activation, _ptr(y_video),
+                               _ptr(y_text) if m1 else None, _dtype_code(y_video),
+                               _stream(stream)), name)
     return y_video, y_text
 
 
@@ -591,10 +592,13 @@ class Conv3d:
         return tuple(out)
 
     def forward(self, x, frames, height, width, cstep=None, use_memory=False, keep_memory=False,
-                out_dtype=None, out_cstep=None, reuse_memory_buffer=False, stream=None):
+                out_dtype=None, out_cstep=None, reuse_memory_buffer=False, stream=None,
+                staged_only_workspace=False):
         """x: device [num_input, cstep] planar (cstep >= frames*height*width).
         Returns the output as [num_output, out_cstep].  reuse_memory_buffer
-        writes the new memory over the one this call reads."""
+        writes the new memory over the one this call reads.
+        staged_only_workspace passes a workspace that holds only the staged
+        frames (no partial tiles), which runs the k loop unsplit."""
         import torch
         cfg = self.config
         mem = self.memory if use_memory and self.memory is not None else None
@@ -606,6 +610,11 @@ class Conv3d:
         ws_n = ctypes.c_size_t()
         check(lib().s2_conv3d_workspace_bytes(ctypes.byref(cfg), frames, height, width, mframes,
                                               ctypes.byref(ws_n)), "s2_conv3d_workspace_bytes")
+        if staged_only_workspace:
+            cin = cfg.num_input
+            cpad = 8 if cin <= 8 else 16 if cin <= 16 else 32 if cin <= 32 else (cin + 63) // 64 * 64
+            staged = (frames + mframes) * height * width * cpad * 2
+            ws_n.value = min(ws_n.value, (staged + 255) // 256 * 256)
         ws = torch.empty(ws_n.value, dtype=torch.uint8, device=x.device)
         nxt = None
         if keep_memory:

@@ -466,6 +466,9 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
     if (!plan || !norm_weights || !video_q || !video_k || !video_v || !text_q || !text_k ||
         !text_v || !out_video || !out_text || !workspace)
         return fail(S2_ERR_INVALID, "null argument");
+    // rows are read as 16-byte chunks
+    if ((video_row_stride % 8) != 0 || (text_row_stride % 8) != 0)
+        return fail(S2_ERR_INVALID, "row strides must be multiples of 8 elements");
     if ((plan->config.rope_pairs_per_axis > 0 && !rope_freqs))
         return fail(S2_ERR_INVALID, "missing rope frequencies");
     if (workspace_bytes < plan->workspace_bytes) return fail(S2_ERR_INVALID, "workspace too small");
@@ -542,10 +545,11 @@ int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream
     return S2_OK;
 }
 
-int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
-                             s2_dtype x_dtype, const uint16_t* weight, const float* bias, int n,
-                             int k, int activation, void* y_video, void* y_text, s2_dtype y_dtype,
-                             s2_stream_t stream) {
+// Argument checks of the SharedLinear entry points (shared_linear.cpp:87-90
+// for the widths; the alignment and k rules are this build's).
+static int linear_args_ok(const void* x_video, int m_video, const void* x_text, int m_text,
+                          s2_dtype x_dtype, const uint16_t* weight, int n, int k, int activation,
+                          void* y_video, void* y_text, s2_dtype y_dtype) {
     if (n <= 0 || k <= 0 || m_video < 0 || m_text < 0 || !weight)
         return fail(S2_ERR_INVALID, "invalid linear shape");
     if ((m_video > 0 && (!x_video || !y_video)) || (m_text > 0 && (!x_text || !y_text)))
@@ -558,6 +562,16 @@ int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_tex
     if (((uintptr_t)x_video) % (8 * xe) || ((uintptr_t)x_text) % (8 * xe) ||
         ((uintptr_t)weight) % 16 || ((uintptr_t)y_video) % 16 || ((uintptr_t)y_text) % 16)
         return fail(S2_ERR_INVALID, "operands must be 16-byte aligned");
+    return S2_OK;
+}
+
+int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
+                             s2_dtype x_dtype, const uint16_t* weight, const float* bias, int n,
+                             int k, int activation, void* y_video, void* y_text, s2_dtype y_dtype,
+                             s2_stream_t stream) {
+    const int ret = linear_args_ok(x_video, m_video, x_text, m_text, x_dtype, weight, n, k,
+                                   activation, y_video, y_text, y_dtype);
+    if (ret != S2_OK) return ret;
     S2_HIP(s2::launch_shared_linear(x_video, m_video, x_text, m_text, (int)x_dtype, weight, bias,
                                     n, k, activation, y_video, y_text, (int)y_dtype,
                                     (hipStream_t)stream));
@@ -889,8 +903,19 @@ int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, int width
 
 int s2_conv3d_workspace_bytes(const s2_conv3d_config* config, int frames, int height, int width,
                               int memory_frames, size_t* bytes) {
+    return s2_conv3d_workspace_bytes_padded(config, frames, height, width, 0, 0, memory_frames,
+                                            bytes);
+}
+
+int s2_conv3d_workspace_bytes_padded(const s2_conv3d_config* config, int frames, int height,
+                                     int width, int pad_right, int pad_bottom, int memory_frames,
+                                     size_t* bytes) {
     int to, ho, wo;
-    if (!bytes || !conv3d_out(config, frames, height, width, memory_frames, &to, &ho, &wo))
+    if (pad_right < 0 || pad_bottom < 0) return fail(S2_ERR_INVALID, "negative padding");
+    // the output extent (and the partial tiles) follow the padded frames,
+    // the staged frames the unpadded input
+    if (!bytes || !conv3d_out(config, frames, height + pad_bottom, width + pad_right,
+                              memory_frames, &to, &ho, &wo))
         return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
     *bytes = align256((size_t)(frames + memory_frames) * height * width *
                       s2::conv3d_cpad(config->num_input) * 2);

@@ -226,6 +226,11 @@ void AdaptiveWindowAttention::set_runtime_shapes(
 
 int AdaptiveWindowAttention::create_pipeline(const ncnn::Option& /*opt*/)
 {
+    return layer_status(create_pipeline_impl());
+}
+
+int AdaptiveWindowAttention::create_pipeline_impl()
+{
     std::lock_guard<std::mutex> lock(mutex);
     int devices = 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0)
@@ -313,6 +318,13 @@ int AdaptiveWindowAttention::plan_for_locked(const std::vector<int>& shapes,
 }
 
 int AdaptiveWindowAttention::forward(const std::vector<ncnn::Mat>& bottom_blobs,
+                                     std::vector<ncnn::Mat>& top_blobs,
+                                     const ncnn::Option& opt) const
+{
+    return layer_status(forward_impl(bottom_blobs, top_blobs, opt));
+}
+
+int AdaptiveWindowAttention::forward_impl(const std::vector<ncnn::Mat>& bottom_blobs,
                                      std::vector<ncnn::Mat>& top_blobs,
                                      const ncnn::Option& opt) const
 {

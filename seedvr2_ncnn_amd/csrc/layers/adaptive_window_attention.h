@@ -98,6 +98,11 @@ public:
                             const std::vector<int>& text_lengths);
 
 private:
+    // forward and create_pipeline without the mapping of C-ABI codes to the
+    // reference's (layer_status)
+    int forward_impl(const std::vector<ncnn::Mat>& bottom_blobs, std::vector<ncnn::Mat>& top_blobs,
+                     const ncnn::Option& opt) const;
+    int create_pipeline_impl();
     int upload_weights_locked() const;
     int plan_for_locked(const std::vector<int>& shapes, const std::vector<int>& text_lengths) const;
     void release_device_locked() const;

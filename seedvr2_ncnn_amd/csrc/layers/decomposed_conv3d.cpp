@@ -117,6 +117,11 @@ int DecomposedConv3D::load_model(const ncnn::ModelBin& mb)
 
 int DecomposedConv3D::create_pipeline(const ncnn::Option& /*opt*/)
 {
+    return layer_status(create_pipeline_impl());
+}
+
+int DecomposedConv3D::create_pipeline_impl()
+{
     std::lock_guard<std::mutex> lock(mutex);
     int devices = 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0 || weight_data.empty() ||
@@ -230,7 +235,8 @@ int DecomposedConv3D::forward_device(const void* input, s2_dtype dtype, size_t e
     if (ret != 0)
         return ret;
     size_t ws_bytes = 0;
-    ret = s2_conv3d_workspace_bytes(&config, frames, h, w, mframes, &ws_bytes);
+    ret = s2_conv3d_workspace_bytes_padded(&config, frames, h, w, pad_right, pad_bottom, mframes,
+                                           &ws_bytes);
     if (ret == 0)
         ret = workspace.reserve(ws_bytes);
     if (ret != 0)
@@ -270,6 +276,12 @@ int DecomposedConv3D::forward_device(const void* input, s2_dtype dtype, size_t e
 
 // decomposed_conv3d.cpp:605-755
 int DecomposedConv3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                              const ncnn::Option& opt) const
+{
+    return layer_status(forward_impl(bottom_blob, top_blob, opt));
+}
+
+int DecomposedConv3D::forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
                               const ncnn::Option& opt) const
 {
     if (bottom_blob.dims != 4 || bottom_blob.c != config.num_input || bottom_blob.elempack != 1)

@@ -69,6 +69,11 @@ public:
     int num_output() const { return config.num_output; }
 
 private:
+    // forward and create_pipeline without the mapping of C-ABI codes to the
+    // reference's (layer_status)
+    int forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                     const ncnn::Option& opt) const;
+    int create_pipeline_impl();
     int upload_weights_locked() const;
     bool config_ok() const;
     int output_shape_locked(int frames, int h, int w, size_t elemsize, int pad_right,

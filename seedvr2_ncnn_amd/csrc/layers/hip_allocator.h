@@ -67,6 +67,16 @@ inline s2_dtype device_blob_dtype(size_t elemsize, const ncnn::Option& opt)
     return opt.use_fp16_storage && !opt.use_bf16_storage ? S2_DTYPE_F16 : S2_DTYPE_BF16;
 }
 
+// Return code of a layer entry point.  The reference layers return 0, -1
+// (invalid configuration, shape or arity), -2 (plan inconsistency) or -100
+// (allocation or weight-load failure); ncnn callers handle only those.  A
+// HIP runtime failure or a missing gfx950 device (S2_ERR_DEVICE at the
+// C-ABI) is therefore reported as -100, and s2_last_error() keeps the detail.
+inline int layer_status(int ret)
+{
+    return (ret == S2_OK || ret == S2_ERR_INVALID || ret == S2_ERR_PLAN) ? ret : S2_ERR_ALLOC;
+}
+
 // Device buffer that only grows; used for layer workspaces and staging.
 class DeviceBuffer {
 public:

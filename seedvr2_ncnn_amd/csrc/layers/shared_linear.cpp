@@ -65,6 +65,11 @@ int SharedLinear::load_model(const ncnn::ModelBin& mb)
 
 int SharedLinear::create_pipeline(const ncnn::Option& /*opt*/)
 {
+    return layer_status(create_pipeline_impl());
+}
+
+int SharedLinear::create_pipeline_impl()
+{
     std::lock_guard<std::mutex> lock(mutex);
     int devices = 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0 || weight_data.empty())
@@ -111,6 +116,13 @@ int SharedLinear::upload_weights_locked() const
 }
 
 int SharedLinear::forward(const std::vector<ncnn::Mat>& bottom_blobs,
+                          std::vector<ncnn::Mat>& top_blobs,
+                          const ncnn::Option& opt) const
+{
+    return layer_status(forward_impl(bottom_blobs, top_blobs, opt));
+}
+
+int SharedLinear::forward_impl(const std::vector<ncnn::Mat>& bottom_blobs,
                           std::vector<ncnn::Mat>& top_blobs,
                           const ncnn::Option& opt) const
 {

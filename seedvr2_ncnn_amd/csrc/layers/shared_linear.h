@@ -37,6 +37,11 @@ public:
                         const ncnn::Option& opt) const;
 
 private:
+    // forward and create_pipeline without the mapping of C-ABI codes to the
+    // reference's (layer_status)
+    int forward_impl(const std::vector<ncnn::Mat>& bottom_blobs, std::vector<ncnn::Mat>& top_blobs,
+                     const ncnn::Option& opt) const;
+    int create_pipeline_impl();
     int upload_weights_locked() const;
 
     int num_output;

@@ -67,6 +67,11 @@ int VAEChunkedMHA::load_model(const ncnn::ModelBin& mb)
 
 int VAEChunkedMHA::create_pipeline(const ncnn::Option& /*opt*/)
 {
+    return layer_status(create_pipeline_impl());
+}
+
+int VAEChunkedMHA::create_pipeline_impl()
+{
     std::lock_guard<std::mutex> lock(mutex);
     int devices = 0;
     const int qdim = embed_dim > 0 ? weight_data_size / embed_dim : 0;
@@ -124,6 +129,12 @@ int VAEChunkedMHA::upload_weights_locked() const
 
 // vae_chunked_mha.cpp:223-235
 int VAEChunkedMHA::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                           const ncnn::Option& opt) const
+{
+    return layer_status(forward_impl(bottom_blob, top_blob, opt));
+}
+
+int VAEChunkedMHA::forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
                            const ncnn::Option& opt) const
 {
     std::lock_guard<std::mutex> lock(mutex);

@@ -36,6 +36,11 @@ public:
                         const ncnn::Option& opt) const;
 
 private:
+    // forward and create_pipeline without the mapping of C-ABI codes to the
+    // reference's (layer_status)
+    int forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                     const ncnn::Option& opt) const;
+    int create_pipeline_impl();
     int upload_weights_locked() const;
 
     int embed_dim;

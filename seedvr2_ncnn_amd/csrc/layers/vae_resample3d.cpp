@@ -87,6 +87,12 @@ void VAEDownsample3D::reset_temporal_memory() const
 int VAEDownsample3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
                              const ncnn::Option& opt) const
 {
+    return layer_status(forward_impl(bottom_blob, top_blob, opt));
+}
+
+int VAEDownsample3D::forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                             const ncnn::Option& opt) const
+{
     std::lock_guard<std::mutex> lock(mutex);
     size_t elemsize = 0;
     HipDeviceAllocator* device = 0;
@@ -260,6 +266,12 @@ int VAEUpsample3D::run(const void* input, s2_dtype dtype, size_t elemsize, int f
 
 // vae_upsample3d.cpp:258-321
 int VAEUpsample3D::forward(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                           const ncnn::Option& opt) const
+{
+    return layer_status(forward_impl(bottom_blob, top_blob, opt));
+}
+
+int VAEUpsample3D::forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
                            const ncnn::Option& opt) const
 {
     std::lock_guard<std::mutex> lock(mutex);

@@ -47,6 +47,10 @@ public:
     void reset_temporal_memory() const;
 
 private:
+    // forward without the mapping of C-ABI codes to the reference's
+    int forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                     const ncnn::Option& opt) const;
+
     int channels;
     int pad_right;
     int pad_bottom;
@@ -72,6 +76,9 @@ public:
     void reset_temporal_memory() const;
 
 private:
+    // forward without the mapping of C-ABI codes to the reference's
+    int forward_impl(const ncnn::Mat& bottom_blob, ncnn::Mat& top_blob,
+                     const ncnn::Option& opt) const;
     int run(const void* input, s2_dtype dtype, size_t elemsize, int frames, int h, int w,
             long in_cstep, void* output, long out_cstep, void* stream) const;
     int output_shape(int frames, int h, int w, size_t elemsize, int out[3], int packed[3],

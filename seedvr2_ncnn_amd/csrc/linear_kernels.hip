@@ -13,6 +13,7 @@
 
 #include "awa_kernels.h"
 #include "s2_device.h"
+#include "stream_scratch.h"
 
 namespace s2 {
 
@@ -255,8 +256,9 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 struct SkTail {
     int dp_tiles;      // tiles [0, dp_tiles): one workgroup each
     int sk_tiles;      // tiles [dp_tiles, dp_tiles + sk_tiles): shared out along k
-    int sk_groups;     // workgroups sharing them, <= sk_tiles * (k / 64)
-    float* slots;      // [sk_groups][2][kSlotFloats] partial accumulators
+    int sk_groups;     // workgroups sharing them: a multiple of sk_tiles, so that
+                       // each workgroup's k range lies inside one tile
+    float* slots;      // [sk_groups][kSlotFloats] partial accumulators
     int* counters;     // [sk_tiles] arrivals; zero between launches
 };
 
@@ -522,8 +524,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             // slot layout: float4 c (4 accumulator registers) of thread tid
             // at byte (c * 512 + tid) * 16; the chunk index goes in soffset
             const __amdgpu_buffer_rsrc_t mine = __builtin_amdgcn_make_buffer_rsrc(
-                sk.slots + ((long)s * 2 + (first ? 0 : 1)) * kSlotFloats, (short)0,
-                kSlotFloats * 4, 0x00020000);
+                sk.slots + (long)s * kSlotFloats, (short)0, kSlotFloats * 4, 0x00020000);
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
@@ -536,12 +537,16 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                             __builtin_bit_cast(u32x4, v), mine, tid * 16,
                             ((ii * 2 + j) * 4 + c) * 512 * 16, kCoherent);
                     }
-            // the slot stores write through to memory; wait for all of them
-            // before the arrival is counted
+            // The slot stores write through to memory; every wave waits for
+            // its own before the workgroup barrier.  The arrival is an
+            // agent-scope acquire-release read-modify-write: it releases this
+            // part's slot (ordered after the barrier) and, for the last part,
+            // acquires every earlier part's, which the second barrier passes
+            // on to the other waves of the workgroup.
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
             if (tid == 0)
-                arrival = __hip_atomic_fetch_add(&sk.counters[t], 1, __ATOMIC_RELAXED,
+                arrival = __hip_atomic_fetch_add(&sk.counters[t], 1, __ATOMIC_ACQ_REL,
                                                  __HIP_MEMORY_SCOPE_AGENT);
             __syncthreads();
             const int lo = owner((long)t * nk);
@@ -557,11 +562,8 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                         for (int r = 0; r < 16; ++r) acc[ii][j][r] = 0.f;
 #pragma unroll 1
                 for (int q = lo; q <= hi; ++q) {
-                    // q's segment of tile t is its first one iff its range starts in t
-                    const int qslot = (bound(q) / nk == t) ? 0 : 1;
                     const __amdgpu_buffer_rsrc_t other = __builtin_amdgcn_make_buffer_rsrc(
-                        sk.slots + ((long)q * 2 + qslot) * kSlotFloats, (short)0, kSlotFloats * 4,
-                        0x00020000);
+                        sk.slots + (long)q * kSlotFloats, (short)0, kSlotFloats * 4, 0x00020000);
                     // sixteen 16-byte loads in flight per batch (four
                     // accumulators; the fragment registers are free here)
 #pragma unroll
@@ -632,48 +634,33 @@ hipError_t launch_cast_bf16_f32(const uint16_t* src, float* dst, size_t n, hipSt
     return hipGetLastError();
 }
 
-// Per-device scratch of the stream-K tail: partial-accumulator slots and
-// arrival counters, allocated on first use and kept for the process.
+// Scratch of the split-k tail: one partial-accumulator slot per workgroup
+// that shares a tile (at most one per CU), then one arrival counter per
+// shared tile (fewer than the CUs).
 namespace {
 
-struct SkScratch {
-    int groups = 0;
-    float* slots = nullptr;
-    int* counters = nullptr;
-};
-
 constexpr int kMaxDevices = 64;
-SkScratch g_sk[kMaxDevices];
-std::mutex g_sk_mutex;
 
-hipError_t sk_scratch(SkScratch** out) {
+// Compute units of the current device (the workgroups of one wave of tiles).
+hipError_t device_cus(int* cus) {
+    static int g_cus[kMaxDevices];
+    static std::once_flag g_once[kMaxDevices];
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lock(g_sk_mutex);
-    SkScratch& sc = g_sk[dev];
-    if (!sc.slots) {
-        int cus = 0;
-        e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return e;
-        const int groups = cus > 0 ? cus : 256;
-        float* slots = nullptr;
-        int* counters = nullptr;
-        e = hipMalloc((void**)&slots, sizeof(float) * (size_t)groups * 2 * kSlotFloats);
-        if (e != hipSuccess) return e;
-        // the shared-out tiles number fewer than two waves of workgroups
-        e = hipMalloc((void**)&counters, sizeof(int) * (size_t)groups * 2);
-        if (e != hipSuccess) { (void)hipFree(slots); return e; }
-        e = hipMemset(counters, 0, sizeof(int) * (size_t)groups * 2);
-        if (e == hipSuccess) e = hipDeviceSynchronize();
-        if (e != hipSuccess) { (void)hipFree(slots); (void)hipFree(counters); return e; }
-        sc.groups = groups;
-        sc.slots = slots;
-        sc.counters = counters;
-    }
-    *out = &sc;
+    std::call_once(g_once[dev], [dev] {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+            n = 0;
+        g_cus[dev] = n > 0 ? n : 256;
+    });
+    *cus = g_cus[dev];
     return hipSuccess;
+}
+
+size_t sk_scratch_bytes(int groups) {
+    return (size_t)groups * kSlotFloats * sizeof(float) + (size_t)groups * sizeof(int);
 }
 
 }  // namespace
@@ -691,12 +678,11 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
         const int mtiles = (mv + m1 + 255) / 256;
         const long tiles = (long)mtiles * ntiles;
         if (tiles == 0) return hipSuccess;
-        SkScratch* sc = nullptr;
-        hipError_t e = sk_scratch(&sc);
+        int G = 0;
+        hipError_t e = device_cus(&G);
         if (e != hipSuccess) return e;
-        const int G = sc->groups;
         const int nk = k / 64;
-        SkTail sk{(int)tiles, 0, 0, sc->slots, sc->counters};
+        SkTail sk{(int)tiles, 0, 0, nullptr, nullptr};
         // When the last wave of tiles would leave more than 3% of the
         // workgroup slots idle, each tile of that wave is split along k into
         // P equal parts on P workgroups (P <= 4, at least 8 k-iterations a
@@ -711,6 +697,13 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
                 sk.sk_tiles = (int)rem;
                 sk.sk_groups = (int)(rem * parts);
             }
+        }
+        if (sk.sk_groups > 0) {
+            void* base = nullptr;
+            e = stream_scratch(kScratchSplitK, stream, sk_scratch_bytes(G), &base);
+            if (e != hipSuccess) return e;
+            sk.slots = (float*)base;
+            sk.counters = (int*)((char*)base + (size_t)G * kSlotFloats * 4);
         }
         const long blocks = (long)sk.dp_tiles + sk.sk_groups;
         shared_linear_256_kernel<YK, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
@@ -742,19 +735,27 @@ template <typename TX>
 static hipError_t linear_out(int y_kind, int act, const void* x0, int m0, const void* x1, int m1,
                              const uint16_t* w, const float* bias, int n, int k, void* y0,
                              void* y1, hipStream_t stream) {
-    if (y_kind == 1) return linear_act<TX, 1>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
-    if (y_kind == 2) return linear_act<TX, 2>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+    if (y_kind == 1)
+        return linear_act<TX, 1>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+    if (y_kind == 2)
+        return linear_act<TX, 2>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
     return linear_act<TX, 0>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
 }
 
-hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, int x_kind,
-                                const uint16_t* w, const float* bias, int n, int k, int act,
-                                void* y0, void* y1, int y_kind, hipStream_t stream) {
+static hipError_t linear_dispatch(const void* x0, int m0, const void* x1, int m1, int x_kind,
+                                  const uint16_t* w, const float* bias, int n, int k, int act,
+                                  void* y0, void* y1, int y_kind, hipStream_t stream) {
     if (x_kind == 1)
         return linear_out<uint16_t>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
     if (x_kind == 2)
         return linear_out<_Float16>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
     return linear_out<float>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+}
+
+hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, int x_kind,
+                                const uint16_t* w, const float* bias, int n, int k, int act,
+                                void* y0, void* y1, int y_kind, hipStream_t stream) {
+    return linear_dispatch(x0, m0, x1, m1, x_kind, w, bias, n, k, act, y0, y1, y_kind, stream);
 }
 
 }  // namespace s2

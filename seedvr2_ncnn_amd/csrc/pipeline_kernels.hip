@@ -11,9 +11,9 @@
 // guidance rescale statistics are accumulated in fp64 like the reference's.
 #include <math.h>
 
-#include <mutex>
 
 #include "pipeline_kernels.h"
+#include "stream_scratch.h"
 
 namespace s2 {
 namespace {
@@ -397,32 +397,12 @@ __global__ void __launch_bounds__(kThreads) denoise_update_kernel(
     }
 }
 
-// ---- per-device scratch of the guidance statistics ---------------------------
+// ---- scratch of the guidance statistics ------------------------------------
+// One CfgScratch per (device, stream): rescaling calls on different streams
+// never share it.
 
-constexpr int kMaxDevices = 64;
-CfgScratch* g_cfg[kMaxDevices];
-std::mutex g_cfg_mutex;
-
-hipError_t cfg_scratch(CfgScratch** out) {
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return e;
-    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-    std::lock_guard<std::mutex> lock(g_cfg_mutex);
-    if (!g_cfg[dev]) {
-        CfgScratch* sc = nullptr;
-        e = hipMalloc((void**)&sc, sizeof(CfgScratch));
-        if (e != hipSuccess) return e;
-        e = hipMemset(sc, 0, sizeof(CfgScratch));
-        if (e == hipSuccess) e = hipDeviceSynchronize();
-        if (e != hipSuccess) {
-            (void)hipFree(sc);
-            return e;
-        }
-        g_cfg[dev] = sc;
-    }
-    *out = g_cfg[dev];
-    return hipSuccess;
+hipError_t cfg_scratch(hipStream_t stream, CfgScratch** out) {
+    return stream_scratch(kScratchCfg, stream, sizeof(CfgScratch), (void**)out);
 }
 
 hipError_t launch_stats(const float* pos, const float* neg, long count, float scale, float rescale,
@@ -497,7 +477,7 @@ hipError_t launch_cfg(const float* pos, const float* neg, long count, float scal
         return hipGetLastError();
     }
     CfgScratch* sc = nullptr;
-    hipError_t e = cfg_scratch(&sc);
+    hipError_t e = cfg_scratch(stream, &sc);
     if (e != hipSuccess) return e;
     e = launch_stats(pos, neg, count, scale, rescale, out, sc, stream);
     if (e != hipSuccess) return e;
@@ -525,7 +505,7 @@ hipError_t launch_denoise_update(const float* pos_patches, const float* neg_patc
     const long count = prows * pw * 64;
     if (neg_patches && rescale != 0.f && count >= 2) {
         CfgScratch* sc = nullptr;
-        hipError_t e = cfg_scratch(&sc);
+        hipError_t e = cfg_scratch(stream, &sc);
         if (e != hipSuccess) return e;
         e = launch_stats(pos_patches, neg_patches, count, scale, rescale, nullptr, sc, stream);
         if (e != hipSuccess) return e;

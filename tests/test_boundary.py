@@ -172,8 +172,27 @@ def test_awa_split_form_checks_each_part():
 
 @pytest.mark.skipif("not _no_device()")
 def test_awa_forward_without_device_fails_loudly():
+    # no device: the reference's -100, never the C-ABI's S2_ERR_DEVICE
     layer = _awa()
-    assert layer.forward(_blobs(), OUTS)[0] == capi.S2_ERR_DEVICE
+    assert layer.forward(_blobs(), OUTS)[0] == -100
+
+
+def test_awa_rejects_head_dims_the_kernels_lack():
+    """Stated deviation: the attention kernels exist for head_dim 64 and 128
+    only (the SeedVR2 DiTs use 128).  The reference accepts any head_dim with
+    6 * rope_pairs <= head_dim (adaptive_window_attention.cpp:770); here other
+    widths return -1 before any device work."""
+    heads, d, pairs = 2, 96, 16
+    params = awa_param_string(heads, d, (1, 2, 2), 0, 1e-5, pairs)
+    g = np.random.default_rng(1)
+    w = [g.standard_normal(d).astype(np.float32) for _ in range(4)] + [np.ones(pairs, np.float32)]
+    layer = Layer("AdaptiveWindowAttention", params, w)
+    assert layer.create_code == 0
+    inner = heads * d
+    blobs = [np.zeros((16, 3 * inner), np.float32), np.zeros((3, 3 * inner), np.float32),
+             np.asarray([1, 4, 4], np.float32), np.asarray([3], np.float32)]
+    outs = [((16, inner), np.float32), ((3, inner), np.float32)]
+    assert layer.forward(blobs, outs)[0] == -1
 
 
 # ---- SharedLinear layer surface ------------------------------------------------------
@@ -196,7 +215,33 @@ def test_shared_linear_forward_codes():
     assert layer.forward([np.zeros((4, 8), np.float32), np.zeros(8, np.float32)], outs)[0] == -1
     if _no_device():
         assert layer.forward([np.zeros((4, 8), np.float32), np.zeros((2, 8), np.float32)],
-                             outs)[0] == capi.S2_ERR_DEVICE
+                             outs)[0] == -100
+
+
+def test_shared_linear_rejects_input_widths_not_a_multiple_of_8():
+    """Stated deviation: operand rows are read as 16-byte chunks, so
+    num_input must be a multiple of 8 (the SeedVR2 widths 2560, 3072, 5120,
+    10240 and 3456 are).  The reference computes any width
+    (shared_linear.cpp:83-96); here the forward returns -1."""
+    w = np.zeros(16 * 12, np.float32)
+    layer = Layer("SharedLinear", "0=16 1=12 2=0", [w])
+    assert layer.create_code == 0
+    outs = [((4, 16), np.float32), ((2, 16), np.float32)]
+    assert layer.forward([np.zeros((4, 12), np.float32), np.zeros((2, 12), np.float32)],
+                         outs)[0] == -1
+
+
+def test_awa_c_abi_rejects_row_strides_not_a_multiple_of_8():
+    """Stated deviation of the C-ABI (the layers always pass strides of
+    heads * head_dim or 3 * heads * head_dim, multiples of 8): q/k/v rows are
+    read as 16-byte chunks, so a row stride that is not a multiple of 8
+    elements returns S2_ERR_INVALID before any device work."""
+    L = capi.lib()
+    dummy = ctypes.c_void_p(256)
+    for vstride, tstride in ((3 * 128 * 2 + 4, 3 * 128 * 2), (3 * 128 * 2, 3 * 128 * 2 + 2)):
+        assert L.s2_awa_forward(dummy, dummy, dummy, dummy, dummy, dummy, vstride, dummy, dummy,
+                                dummy, tstride, 1, dummy, dummy, 1, dummy, 1 << 20,
+                                None) == capi.S2_ERR_INVALID
 
 
 def test_param_text_parser_accepts_ncnn_fields():
@@ -220,4 +265,4 @@ def test_awa_one_dim_text_length_blob_reads_column_zero_for_every_sample():
     one_dim = layer.forward([video, text, shapes, np.asarray([3, 2], np.float32)], outs)[0]
     assert one_dim == -1          # lengths read as (3, 3): 6 text rows expected, 5 given
     two_dim = layer.forward([video, text, shapes, np.asarray([[3], [2]], np.float32)], outs)[0]
-    assert two_dim in (0, capi.S2_ERR_DEVICE)
+    assert two_dim in (0, -100)

@@ -267,6 +267,47 @@ def test_official_bf16_attention(official):
         assert np.array_equal(ov.view(np.uint32) & 0xFFFF, np.zeros_like(ov.view(np.uint32)))
 
 
+def test_official_bf16_non_finite_values():
+    """round_bf16 (adaptive_window_attention.cpp:499-508) skips the rounding
+    increment for Inf and NaN and then clears the low 16 bits, so a NaN whose
+    payload lies only in those bits becomes an infinity (the GLSL copy at
+    :50-57 keeps it a NaN); the device follows the CPU forward.  fp32 inputs
+    (the only storage that holds such a NaN) with +-Inf, quiet and negative
+    NaNs and low-payload NaNs in v: the non-finite pattern of both outputs
+    (NaN, +Inf, -Inf per element) equals the oracle's, the finite elements
+    meet the path's bar."""
+    import torch
+    shapes, tl = [(2, 10, 14)], [9]
+    heads, d, pairs = 2, 128, 21
+    inner = heads * d
+    case = make_awa_inputs(808, shapes, tl, heads, d, pairs)
+    video, text = case["video"].copy(), case["text"].copy()
+    vbits, tbits = video.view(np.uint32), text.view(np.uint32)
+    v0 = 2 * inner   # first v column of the fused rows
+    specials = [  # (token, head, channel, bits)
+        (5, 0, 3, 0x7F800001),      # low-payload NaN -> +Inf
+        (37, 1, 10, 0x7F800000),    # +Inf
+        (80, 0, 20, 0xFF800000),    # -Inf
+        (100, 1, 40, 0x7FC00000),   # quiet NaN
+        (120, 0, 50, 0xFFC12345),   # negative NaN with a high payload
+        (150, 1, 70, 0xFF800003),   # negative low-payload NaN -> -Inf
+    ]
+    for tok, h, c, bits in specials:
+        vbits[tok, v0 + h * d + c] = bits
+    tbits[2, v0 + 1 * d + 60] = 0x7F800002   # a text key's low-payload NaN -> +Inf everywhere
+    case["video"], case["text"] = video, text
+    ov, ot = _run_capi(case, heads, d, (4, 3, 3), 0, pairs, shapes, tl, False, torch.float32,
+                       official=True)
+    rv, rt = oracle_awa(case, heads, d, (4, 3, 3), 0, 1e-5, pairs, shapes, tl, official_bf16=True)
+    for got, ref, what in ((ov, rv, "video"), (ot, rt, "text")):
+        assert np.isposinf(ref).any() and np.isneginf(ref).any() and np.isnan(ref).any(), what
+        np.testing.assert_array_equal(np.isnan(got), np.isnan(ref), what + " NaN pattern")
+        np.testing.assert_array_equal(np.isposinf(got), np.isposinf(ref), what + " +Inf pattern")
+        np.testing.assert_array_equal(np.isneginf(got), np.isneginf(ref), what + " -Inf pattern")
+        fin = np.isfinite(ref)
+        assert_close(got[fin], ref[fin], what + " finite elements")
+
+
 def test_literal_weights_and_fp32_inputs_split():
     import torch
     shapes, tl = [(4, 20, 33)], [64]

@@ -110,6 +110,37 @@ def test_conv3d_matches_oracle(cin, cout, frames, h, w, kw):
     _check(got, x, wts, bias, cfgs[1])
 
 
+# The unsplit implicit-GEMM k loop of layers with several temporal taps: one
+# workgroup advances from tap to tap and runs the bias epilogue on the whole
+# sum.  Small layers of at least 64 input channels split their k loop over
+# the taps when the workspace holds the partial tiles; a workspace with only
+# the staged frames (which the forward accepts) runs them unsplit.
+@pytest.mark.parametrize("cin,cout,frames,h,w,kw", [
+    (64, 128, 3, 10, 12, {}),                    # 512 x 128 tiles, 3 taps
+    (64, 256, 2, 9, 13, dict(k=(2, 3, 3))),      # 256 x 256 tiles, 2 taps
+    (128, 96, 3, 6, 10, dict(s=(1, 2, 2))),      # stride 2, ragged n
+])
+def test_conv3d_unsplit_taps_with_staged_only_workspace(cin, cout, frames, h, w, kw):
+    cfgs = _cfg(cin, cout, **kw)
+    x, wts, bias = _case(cin, cout, frames, h, w, cfgs, 3 * cin + cout)
+    conv = _device(cfgs[0], wts, bias)
+    got = _run(conv, x, staged_only_workspace=True)
+    _check(got, x, wts, bias, cfgs[1])
+    split = _run(conv, x)
+    assert_close(split, got)
+
+
+def test_conv3d_unsplit_taps_at_256_tiles():
+    """A layer that fills 256 implicit-GEMM tiles never splits its k loop:
+    64 -> 256 channels, 2 taps, stride (1, 2, 2) (not the halo kernel), two
+    output frames of 128 x 256 pixels = 256 tiles of 256 x 256."""
+    cfgs = _cfg(64, 256, k=(2, 3, 3), s=(1, 2, 2), head=1)
+    x, wts, bias = _case(64, 256, 2, 256, 512, cfgs, 11)
+    got = _run(_device(cfgs[0], wts, bias), x)
+    assert got.shape == (256, 2, 128, 256)
+    _check(got, x, wts, bias, cfgs[1])
+
+
 # (10, 12): the implicit-GEMM kernel; (6, 120): the halo kernel.  A channel
 # stride padded by 4 elements leaves 16-bit channel rows without 16-byte
 # alignment, which the staging pass reads element by element.

@@ -221,3 +221,47 @@ def test_fp32_activations_medium_shape():
     assert_close(yt, oracle.linear(xt, w, b, 1, threads=THREADS), "text")
     assert _tight(yv[rows], bf16_round(xv), bf16_round(w), b, 1, rows=rows) < 2e-4
 
+
+
+def test_concurrent_streams_keep_their_own_split_scratch():
+    """Two SharedLinear calls whose kernels overlap on two streams, both with
+    a split-k tail (the 720p out projection: 860 tiles, the last 82 split in
+    three): each stream has its own partial-tile scratch, so both results
+    equal the same calls made one at a time (bit for bit) and meet the bar
+    against the oracle."""
+    import torch
+    g = np.random.default_rng(2024)
+    mv, mt, k, n = 21600, 64, 2560, 2560
+    xs = [bf16_round(g.standard_normal((mv + mt, k), dtype=np.float32)) for _ in range(2)]
+    ws = [(0.02 * g.standard_normal((n, k), dtype=np.float32)) for _ in range(2)]
+    bs = [(0.02 * g.standard_normal(n)).astype(np.float32) for _ in range(2)]
+    dx = [torch.from_numpy(x).cuda().to(torch.bfloat16) for x in xs]
+    dw = [capi.cast_f32_to_bf16(torch.from_numpy(w).cuda()) for w in ws]
+    db = [torch.from_numpy(b).cuda() for b in bs]
+    torch.cuda.synchronize()
+
+    def call(i, stream=None):
+        return capi.shared_linear(dx[i][:mv], dx[i][mv:], dw[i], db[i], capi.ACT_NONE,
+                                  out_dtype=torch.float32, stream=stream)
+
+    alone = [call(i) for i in range(2)]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = [[], []]
+    for _ in range(4):   # interleaved: the tails of calls on the two streams overlap
+        for i in range(2):
+            with torch.cuda.stream(streams[i]):
+                outs[i].append(call(i, stream=streams[i]))
+    torch.cuda.synchronize()
+    rows = np.concatenate([np.arange(0, 2), g.integers(0, mv, 24), np.arange(mv - 2, mv)]).astype(np.int32)
+    for i in range(2):
+        ref_v, ref_t = (t.cpu().numpy() for t in alone[i])
+        for yv, yt in outs[i]:
+            np.testing.assert_array_equal(yv.cpu().numpy(), ref_v)
+            np.testing.assert_array_equal(yt.cpu().numpy(), ref_t)
+        assert_close(ref_v[rows], oracle.linear(xs[i][:mv], ws[i], bs[i], rows=rows,
+                                                threads=THREADS), f"stream {i} video rows")
+        assert_close(ref_t, oracle.linear(xs[i][mv:], ws[i], bs[i], threads=THREADS),
+                     f"stream {i} text")

@@ -65,6 +65,32 @@ def test_downsample(device, pr, pb):
 
 
 @pytest.mark.parametrize("device", [False, True])
+@pytest.mark.parametrize("h,w", [(2, 9), (5, 2)])
+def test_downsample_input_valid_only_after_padding(device, h, w):
+    """A frame two rows (or columns) wide is narrower than a 3 x 3 window
+    without padding until the bottom (right) zero padding lengthens it to 3;
+    the workspace and the output follow the padded extent
+    (vae_downsample3d.cpp:145-172).  64 -> 128 channels over 3 taps: the few
+    output tiles split the k loop over the taps."""
+    import torch
+    g = np.random.default_rng(40 + h)
+    c, f = 64, 3
+    cfg, wt, b = _conv(g, c, 128, s=(1, 1, 1), p=(0, 0))
+    layer = Layer("ExportDownsample3D", "", weights=[np.asarray([c, 1, 1], np.float32)] +
+                  _conv_blobs(cfg, wt, b))
+    assert layer.create_code == 0 and layer.create_pipeline() == 0
+    x = g.standard_normal((c, f, h, w)).astype(np.float32)
+    if device:
+        x = torch.from_numpy(x).to(torch.bfloat16).float().numpy()
+    set_vae_memory_state(0)
+    ref = oracle.vae_downsample3d(cfg, wt, b, x, 1, 1)
+    code, got = layer.forward_planar(x, (w, h, f, c), tuple(reversed(ref.shape[1:])) + (128,),
+                                     device=device, dtype=torch.bfloat16 if device else None)
+    assert code == 0
+    assert_close(got, ref)
+
+
+@pytest.mark.parametrize("device", [False, True])
 @pytest.mark.parametrize("tr,sr", [(2, 2), (1, 2), (2, 1)])
 def test_upsample(device, tr, sr):
     import torch
