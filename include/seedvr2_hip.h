@@ -193,6 +193,21 @@ S2_API int s2_shared_linear_forward(const void* x_video, int m_video, const void
                              void* y_video, void* y_text, s2_dtype y_dtype,
                              s2_stream_t stream);
 
+/* s2_shared_linear_forward without any device allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate (HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Same arguments,
+ * kernels and results (bit-identical); the split-k scratch is a static
+ * device array of about 64 MB (256 partial-tile slots of 256 KB and their
+ * counters) that each GPU the library runs on holds until the process ends.
+ * A split needing more than 256 sharing workgroups returns S2_ERR_INVALID
+ * (it cannot happen on a device of at most 256 compute units).  Every call
+ * on one GPU shares that array: calls whose kernels overlap in time on one
+ * GPU (different streams) race and must not be made. */
+S2_API int s2_shared_linear_forward_noalloc(const void* x_video, int m_video, const void* x_text,
+                                            int m_text, s2_dtype x_dtype, const uint16_t* weight,
+                                            const float* bias, int n, int k, int activation,
+                                            void* y_video, void* y_text, s2_dtype y_dtype,
+                                            s2_stream_t stream);
 
 /* ---- DiT frontend and tail, sampler step -------------------------------- */
 /* The steps either side of the block stack, on device fp32 buffers.  A video

@@ -38,7 +38,7 @@ EXPORTS = (
     "s2_conv3d_memory_bytes", "s2_conv3d_workspace_bytes", "s2_conv3d_forward",
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
-    "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded",
+    "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded", "s2_shared_linear_forward_noalloc",
 )
 
 
@@ -130,6 +130,7 @@ def lib() -> ctypes.CDLL:
         L.s2_cast_f32_to_bf16.argtypes = [vp, vp, sz, vp]
         L.s2_cast_bf16_to_f32.argtypes = [vp, vp, sz, vp]
         L.s2_shared_linear_forward.argtypes = [vp, ci, vp, ci, ci, vp, vp, ci, ci, ci, vp, vp, ci, vp]
+        L.s2_shared_linear_forward_noalloc.argtypes = L.s2_shared_linear_forward.argtypes
         L.s2_awa_stage_timing.argtypes = [ci]
         L.s2_awa_stage_times.argtypes = [P(ctypes.c_float)]
         L.s2_patchify_video.argtypes = [vp, cl, P(ci), ci, vp, vp]
@@ -355,8 +356,9 @@ def cast_f32_to_bf16(src, dst=None, stream=None):
 
 
 def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, out_dtype=None,
-                  y_video=None, y_text=None, stream=None):
-    """s2_shared_linear_forward: y = act(x W^T + b) for both streams."""
+                  y_video=None, y_text=None, stream=None, noalloc=False):
+    """s2_shared_linear_forward: y = act(x W^T + b) for both streams
+    (s2_shared_linear_forward_noalloc with noalloc=True)."""
     import torch
     n, k = weight_bf16.shape
     assert weight_bf16.dtype == torch.bfloat16 and weight_bf16.is_contiguous()
@@ -370,7 +372,7 @@ def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, 
         y_video = torch.empty((m0, n), dtype=odt, device=dev)
     if y_text is None and m1:
         y_text = torch.empty((m1, n), dtype=odt, device=dev)
-    name = "s2_shared_linear_forward"
+    name = "s2_shared_linear_forward_noalloc" if noalloc else "s2_shared_linear_forward"
     check(getattr(lib(), name)(_ptr(x_video), m0, _ptr(x_text) if m1 else None, m1, xd,
                                _ptr(weight_bf16), _ptr(bias), n, k, activation, _ptr(y_video),
                                _ptr(y_text) if m1 else None, _dtype_code(y_video),

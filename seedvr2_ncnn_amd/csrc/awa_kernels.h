@@ -30,5 +30,10 @@ hipError_t launch_cast_bf16_f32(const uint16_t* src, float* dst, size_t n, hipSt
 hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, int x_kind,
                                 const uint16_t* w, const float* bias, int n, int k, int act,
                                 void* y0, void* y1, int y_kind, hipStream_t stream);
+// The same with the split-k scratch in a static device array: no allocation.
+hipError_t launch_shared_linear_noalloc(const void* x0, int m0, const void* x1, int m1,
+                                        int x_kind, const uint16_t* w, const float* bias, int n,
+                                        int k, int act, void* y0, void* y1, int y_kind,
+                                        hipStream_t stream);
 
 }  // namespace s2

@@ -578,6 +578,24 @@ int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_tex
     return S2_OK;
 }
 
+int s2_shared_linear_forward_noalloc(const void* x_video, int m_video, const void* x_text,
+                                     int m_text, s2_dtype x_dtype, const uint16_t* weight,
+                                     const float* bias, int n, int k, int activation,
+                                     void* y_video, void* y_text, s2_dtype y_dtype,
+                                     s2_stream_t stream) {
+    const int ret = linear_args_ok(x_video, m_video, x_text, m_text, x_dtype, weight, n, k,
+                                   activation, y_video, y_text, y_dtype);
+    if (ret != S2_OK) return ret;
+    const hipError_t e = s2::launch_shared_linear_noalloc(
+        x_video, m_video, x_text, m_text, (int)x_dtype, weight, bias, n, k, activation, y_video,
+        y_text, (int)y_dtype, (hipStream_t)stream);
+    if (e == hipErrorNotSupported)
+        return fail(S2_ERR_INVALID,
+                    "split-k tail needs more workgroups than the static scratch holds (256)");
+    S2_HIP(e);
+    return S2_OK;
+}
+
 /* ---- DiT frontend and tail, sampler step ---------------------------------- */
 
 int s2_patchify_video(const float* video, long tokens, const int* video_shapes, int batch,

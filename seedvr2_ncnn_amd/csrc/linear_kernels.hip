@@ -15,6 +15,7 @@
 #include "s2_device.h"
 #include "stream_scratch.h"
 
+
 namespace s2 {
 
 namespace {
@@ -663,12 +664,50 @@ size_t sk_scratch_bytes(int groups) {
     return (size_t)groups * kSlotFloats * sizeof(float) + (size_t)groups * sizeof(int);
 }
 
+// The no-allocation entry point's scratch: slots and counters for up to
+// kNoallocGroups sharing workgroups (the split of a 256-CU device), about
+// 64 MB that every GPU the library runs on holds until the process ends.
+constexpr int kNoallocGroups = 256;
+constexpr size_t kNoallocBytes = (size_t)kNoallocGroups * kSlotFloats * sizeof(float) +
+                                 (size_t)kNoallocGroups * sizeof(int);
+static __device__ __align__(256) unsigned char scratch[kNoallocBytes];
+
+// Device address of `scratch` on the current device.  The host-side name is
+// only a stand-in for the symbol: kernels get this address instead.
+hipError_t noalloc_scratch(void** out) {
+    static void* g_ptr[kMaxDevices];
+    static hipError_t g_err[kMaxDevices];
+    static std::once_flag g_once[kMaxDevices];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::call_once(g_once[dev], [dev] {
+        void* p = nullptr;
+        g_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_ptr[dev] = p;
+    });
+    if (g_err[dev] != hipSuccess) return g_err[dev];
+    *out = g_ptr[dev];
+    return hipSuccess;
+}
+
+__global__ void zero_counters_kernel(int* counters, int n) {
+    for (int i = threadIdx.x; i < n; i += blockDim.x) counters[i] = 0;
+}
+
 }  // namespace
+
+// Where the split-k tail keeps its partial tiles: the calling stream's own
+// allocation (stream_scratch), or, for the no-allocation entry point, the
+// static `scratch` array (whose counters are cleared before every launch
+// that uses them, since a call keeps whatever the last one left).
+enum class SkSource { kStream, kStatic };
 
 template <typename TX, int YK, int ACT>
 static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, const uint16_t* w,
                               const float* bias, int n, int k, void* y0, void* y1,
-                              hipStream_t stream) {
+                              hipStream_t stream, SkSource source) {
     // bf16 activations (the operand type of the MFMAs) go straight to LDS;
     // fp32 and fp16 ones are rounded to bf16 while staged by the 128 kernel
     if (std::is_same<TX, uint16_t>::value && k % 64 == 0 &&
@@ -700,10 +739,23 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
         }
         if (sk.sk_groups > 0) {
             void* base = nullptr;
-            e = stream_scratch(kScratchSplitK, stream, sk_scratch_bytes(G), &base);
-            if (e != hipSuccess) return e;
-            sk.slots = (float*)base;
-            sk.counters = (int*)((char*)base + (size_t)G * kSlotFloats * 4);
+            if (source == SkSource::kStatic) {
+                // (hipErrorNotSupported: the caller reports a size beyond the
+                // static scratch)
+                if (sk.sk_groups > kNoallocGroups) return hipErrorNotSupported;
+                e = noalloc_scratch(&base);
+                if (e != hipSuccess) return e;
+                sk.slots = (float*)base;
+                sk.counters = (int*)((char*)base + (size_t)kNoallocGroups * kSlotFloats * 4);
+                zero_counters_kernel<<<1, 256, 0, stream>>>(sk.counters, sk.sk_tiles);
+                e = hipGetLastError();
+                if (e != hipSuccess) return e;
+            } else {
+                e = stream_scratch(kScratchSplitK, stream, sk_scratch_bytes(G), &base);
+                if (e != hipSuccess) return e;
+                sk.slots = (float*)base;
+                sk.counters = (int*)((char*)base + (size_t)G * kSlotFloats * 4);
+            }
         }
         const long blocks = (long)sk.dp_tiles + sk.sk_groups;
         shared_linear_256_kernel<YK, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
@@ -725,37 +777,47 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
 template <typename TX, int YK>
 static hipError_t linear_act(int act, const void* x0, int m0, const void* x1, int m1,
                              const uint16_t* w, const float* bias, int n, int k, void* y0,
-                             void* y1, hipStream_t stream) {
+                             void* y1, hipStream_t stream, SkSource src) {
     if (act == S2_ACT_GELU)
-        return linear_impl<TX, YK, S2_ACT_GELU>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
-    return linear_impl<TX, YK, S2_ACT_NONE>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+        return linear_impl<TX, YK, S2_ACT_GELU>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
+    return linear_impl<TX, YK, S2_ACT_NONE>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
 }
 
 template <typename TX>
 static hipError_t linear_out(int y_kind, int act, const void* x0, int m0, const void* x1, int m1,
                              const uint16_t* w, const float* bias, int n, int k, void* y0,
-                             void* y1, hipStream_t stream) {
+                             void* y1, hipStream_t stream, SkSource src) {
     if (y_kind == 1)
-        return linear_act<TX, 1>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+        return linear_act<TX, 1>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
     if (y_kind == 2)
-        return linear_act<TX, 2>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
-    return linear_act<TX, 0>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+        return linear_act<TX, 2>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
+    return linear_act<TX, 0>(act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
 }
 
 static hipError_t linear_dispatch(const void* x0, int m0, const void* x1, int m1, int x_kind,
                                   const uint16_t* w, const float* bias, int n, int k, int act,
-                                  void* y0, void* y1, int y_kind, hipStream_t stream) {
+                                  void* y0, void* y1, int y_kind, hipStream_t stream,
+                                  SkSource src) {
     if (x_kind == 1)
-        return linear_out<uint16_t>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+        return linear_out<uint16_t>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
     if (x_kind == 2)
-        return linear_out<_Float16>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
-    return linear_out<float>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream);
+        return linear_out<_Float16>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
+    return linear_out<float>(y_kind, act, x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
 }
 
 hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, int x_kind,
                                 const uint16_t* w, const float* bias, int n, int k, int act,
                                 void* y0, void* y1, int y_kind, hipStream_t stream) {
-    return linear_dispatch(x0, m0, x1, m1, x_kind, w, bias, n, k, act, y0, y1, y_kind, stream);
+    return linear_dispatch(x0, m0, x1, m1, x_kind, w, bias, n, k, act, y0, y1, y_kind, stream,
+                           SkSource::kStream);
+}
+
+hipError_t launch_shared_linear_noalloc(const void* x0, int m0, const void* x1, int m1,
+                                        int x_kind, const uint16_t* w, const float* bias, int n,
+                                        int k, int act, void* y0, void* y1, int y_kind,
+                                        hipStream_t stream) {
+    return linear_dispatch(x0, m0, x1, m1, x_kind, w, bias, n, k, act, y0, y1, y_kind, stream,
+                           SkSource::kStatic);
 }
 
 }  // namespace s2
