@@ -215,12 +215,12 @@ __global__ __launch_bounds__(256, 2) void shared_linear_kernel(
 // Large-tile path for bf16 activations with k % 64 == 0.
 //
 // Block tile 256x256 with eight waves, two per SIMD, in a 2 (m) x 4 (n) grid
-// of 128x64 wave tiles (4x2 MFMA 32x32x16 accumulators = 128 fp32 per lane):
-// while one wave of a SIMD waits on LDS or the stage barrier the other keeps
-// the matrix core busy.  Per 16-k step a wave issues 6 LDS reads for 8 MFMAs.
-// The operands stream through two 64-k LDS stages (64 KB each) filled by
-// buffer_load_dwordx4 ... lds (global -> LDS, no VGPR staging) one stage
-// ahead of the MFMAs.  The buffer descriptors bound each tile to its valid
+// of 128x64 wave tiles (4x2 MFMA 32x32x16 accumulators = 128 fp32 per lane).
+// The two waves of a SIMD ping-pong: one issues a whole 64-k step of MFMAs
+// from fragment registers while the other reads its next step's fragments
+// from LDS (the main loop below).  The operands stream through two 64-k LDS
+// stages (64 KB each) filled by buffer_load_dwordx4 ... lds (global -> LDS,
+// no VGPR staging).  The buffer descriptors bound each tile to its valid
 // rows, so ragged m and n read zeros.  LDS rows are 128 bytes; 16-byte chunk
 // c of row r is stored at position c ^ (((r >> 1) ^ ((r & 1) << 2)) & 7), so
 // the rows one ds_read_b128 phase touches land on distinct banks.  The bf16
@@ -280,7 +280,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform
     const int l32 = lane & 31;
     const int g = lane >> 5;
     const int wm = wave >> 2;
@@ -313,48 +313,73 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     };
 
     f32x16 acc[4][2];
-    bf16x8 a[2][4], b[2][2];
 
-    // acc = sum over 64-k iterations [kb, ke) of the current tile
+    // acc = sum over 64-k iterations [kb, ke) of the current tile.
+    //
+    // Ping-pong main loop.  The two waves of each SIMD (wave w and w + 4:
+    // group 0 owns tile rows 0-127, group 1 rows 128-255) take turns: one
+    // issues the 32 MFMAs of a whole 64-k step from fragment registers while
+    // the other reads its fragments of the next step from LDS, so the matrix
+    // core never waits on an LDS read.  Every phase ends at a workgroup
+    // barrier; group 1 runs one phase behind group 0.  The DMA of a step is
+    // split between the groups: group 1 loads the B rows into the stage it
+    // has just finished reading (it is that stage's last reader), group 0 the
+    // A rows one phase later; each waits for its DMA two phases after issuing
+    // it, before the barrier that opens the stage to its first reader.
+    //
+    //   phase     2s                        2s + 1
+    //   group 0   DMA A of step s + 1,      MFMAs of step s,
+    //             read step s               wait for its DMA
+    //   group 1   MFMAs of step s - 1       read step s, wait for its DMA of
+    //                                       step s + 1, DMA B of step s + 2
     auto mainloop = [&](int kb, int ke) {
-        // the tile is the same for every lane: keep the descriptors in SGPRs.
-        // Both A descriptors address tile row r at byte r * k * 2; each only
-        // covers its own stream's rows (the text one starts at row mv).
+        const int grp = wave >> 2;
+        const int wq = wave & 3;
         const i32x4 rav = wave_uniform(
             buffer_rsrc(x0 + (long)row0 * k, (uint32_t)(max(min(m0 - row0, BM), 0) * k * 2)));
         const i32x4 rat = wave_uniform(
             buffer_rsrc(x1 + (long)(row0 - mv) * k,
                         (uint32_t)(row0 + BM > mv ? min(mv + m1 - row0, BM) * k * 2 : 0)));
-        const int wrow = __builtin_amdgcn_readfirstlane(row0 + wave * 32);
+        const int wrow = __builtin_amdgcn_readfirstlane(row0 + wq * 64);
         const i32x4 rb =
             wave_uniform(buffer_rsrc(wgt + (long)col0 * k, (uint32_t)(min(n - col0, BN) * k * 2)));
-        // Wave w fills LDS rows 32w .. 32w+31 of each operand with 4 DMA
-        // instructions of 8 rows: lane i takes row +i/8 and the logical
-        // chunk stored at position i%8.
-        uint32_t voff[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = wave * 32 + j * 8 + (lane >> 3);
-            voff[j] = (uint32_t)(row * k * 2 + (((lane & 7) ^ lds_swizzle(row)) * 16));
-        }
-        auto issue = [&](int stage, int kt) {
+        // Wave wq of a group fills LDS rows 64 wq .. 64 wq + 63 of its operand
+        // (group 0: A, group 1: B) with 8 DMA instructions of 8 rows.  Row
+        // r + 8j has the swizzle of row r with bit 2 flipped for odd j, so two
+        // offsets serve all eight.
+        const int row_a = wq * 64 + (lane >> 3);
+        const uint32_t vrow = (uint32_t)(row_a * k * 2);
+        const uint32_t voff_even = vrow + (((lane & 7) ^ lds_swizzle(row_a)) * 16);
+        const uint32_t voff_odd = vrow + (((lane & 7) ^ lds_swizzle(row_a) ^ 4) * 16);
+        auto issue = [&](int stage, int kt, int operand) {
             const uint32_t soff = __builtin_amdgcn_readfirstlane((uint32_t)(kt * BK * 2));
-            const uint32_t st = lds_base + stage * SB + wave * 4 * 1024;
+            const uint32_t st = lds_base + stage * SB + operand * TB + wq * 8 * 1024;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                lds_dma16(wrow + j * 8 < mv ? rav : rat,
-                          __builtin_amdgcn_readfirstlane(st + j * 1024), voff[j], soff);
-                lds_dma16(rb, __builtin_amdgcn_readfirstlane(st + TB + j * 1024), voff[j], soff);
+            for (int j = 0; j < 8; ++j) {
+                const uint32_t vo = ((j & 1) ? voff_odd : voff_even) + (uint32_t)(j * 8 * k * 2);
+                lds_dma16(operand ? rb : (wrow + j * 8 < mv ? rav : rat),
+                          __builtin_amdgcn_readfirstlane(st + j * 1024), vo, soff);
             }
         };
-        auto frag = [&](const uint8_t* st, int kk, int slot) {
-            const int pc = ((2 * kk + g) ^ sw) * 16;
+        bf16x8 fa[4][4], fb[4][2];
+        auto read_step = [&](int stage) {
+            const uint8_t* st = lds + stage * SB;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                a[slot][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * RB + pc));
+            for (int kk = 0; kk < BK / 16; ++kk) {
+                const int pc = ((2 * kk + g) ^ sw) * 16;
 #pragma unroll
-            for (int j = 0; j < 2; ++j)
-                b[slot][j] = as_bf16x8(*(const uint4*)(st + TB + (wn * 64 + 32 * j + l32) * RB + pc));
+                for (int i = 0; i < 4; ++i)
+                    fa[kk][i] = as_bf16x8(*(const uint4*)(st + (wm * 128 + 32 * i + l32) * RB + pc));
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    fb[kk][j] =
+                        as_bf16x8(*(const uint4*)(st + TB + (wn * 64 + 32 * j + l32) * RB + pc));
+            }
+        };
+        auto barrier = [] {
+            __builtin_amdgcn_sched_barrier(0);
+            asm volatile("s_barrier" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
         };
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -362,32 +387,39 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             for (int j = 0; j < 2; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
-        issue(0, kb);
+        const int steps = ke - kb;
+        // steps 0 and 1: group 0 loads A, group 1 B
+        issue(0, kb, grp);
+        if (steps > 1) issue(1, kb + 1, grp);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        barrier();
+        if (grp == 1) barrier();
 #pragma unroll 1
-        for (int kt = kb; kt < ke; ++kt) {
-            const int stage = (kt - kb) & 1;
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();   // stage kt visible to all waves; the other stage no longer read
-            if (kt + 1 < ke) issue(stage ^ 1, kt + 1);
-            const uint8_t* st = lds + stage * SB;
-            frag(st, 0, 0);
-            // The scheduling barriers keep the next slice's LDS reads ahead
-            // of this slice's MFMAs (two fragment buffers), instead of the
-            // compiler sinking each read next to its first use.
+        for (int s = 0; s < steps; ++s) {
+            // memory phase
+            if (grp == 0 && s >= 1 && s + 1 < steps) issue((s + 1) & 1, kb + s + 1, 0);
+            read_step(s & 1);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            if (grp == 1) {
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // B of step s + 1
+                if (s + 2 < steps) issue(s & 1, kb + s + 2, 1);
+            }
+            barrier();
+            // MFMA phase
+            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int kk = 0; kk < BK / 16; ++kk) {
-                __builtin_amdgcn_sched_barrier(0);
-                if (kk + 1 < BK / 16) frag(st, kk + 1, (kk + 1) & 1);
-                __builtin_amdgcn_sched_barrier(0);
+            for (int kk = 0; kk < BK / 16; ++kk)
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int j = 0; j < 2; ++j)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                            a[kk & 1][i], b[kk & 1][j], acc[i][j], 0, 0, 0);
-            }
-            __builtin_amdgcn_sched_barrier(0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][i], fb[kk][j],
+                                                                            acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+            if (grp == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // A of step s + 1
+            barrier();
         }
+        if (grp == 0) barrier();
     };
 
     // y tile = act(acc + bias)
