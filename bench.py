@@ -78,52 +78,237 @@ def measured_traffic():
     return None
 
 
-def cpu_baseline(threads, gemm_rows=2048):
-    """The oracle's optimised build (oracle/liboracle_fast.so, the reference's
-    CPU forward restated in C) timed on a bounded sample of the same block:
-    the whole attention layer (all 27 windows) and the first `gemm_rows` rows
-    of each of the four GEMMs, whose time is scaled to all 21,664 rows.
-    About 10-20 s of CPU work."""
+def host_cpu():
+    """CPU model, logical CPUs of the host and CPUs this process may run on."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    logical = os.cpu_count() or 1
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = logical
+    return model, logical, allowed
+
+
+def job_cpu_threads():
+    """Threads of the multi-threaded CPU legs: the CPUs this process may run
+    on, at most 16, which is one GPU's share of the host's cores on a shared
+    8-GPU machine."""
+    return max(1, min(16, host_cpu()[2]))
+
+
+def _torch_gemm_seconds(rows, k, n, act, threads, g):
+    """fp32 torch.matmul on the CPU (oneDNN/MKL-backed) of `rows` x k by
+    k x n plus bias and, for act == 1, erf-GELU: the optimised-library
+    stand-in for ncnn's Gemm."""
+    import torch
+    torch.set_num_threads(threads)
+    x = torch.from_numpy(g.standard_normal((rows, k), dtype="float32"))
+    w = torch.from_numpy(0.02 * g.standard_normal((n, k), dtype="float32"))
+    b = torch.from_numpy(0.02 * g.standard_normal(n, dtype="float32"))
+    y = torch.addmm(b, x, w.t())   # warm-up (page-in, thread pool)
+    best = float("inf")
+    for _ in range(2):
+        t0 = time.perf_counter()
+        y = torch.addmm(b, x, w.t())
+        if act == 1:
+            y = torch.nn.functional.gelu(y)
+        best = min(best, time.perf_counter() - t0)
+    return best
+
+
+def cpu_baseline(threads):
+    """The reference's CPU path restated and timed on this host's cores.
+
+    Attention: the oracle's optimised build (oracle/liboracle_fast.so, the
+    reference CPU forward of adaptive_window_attention.cpp:764-978 restated in
+    C: serial window loop, fp32 SDPA per head) over all 27 windows with
+    `threads` OpenMP threads, and over windows 0 and 1 on one thread (the
+    reference build's NCNN_OPENMP OFF), scaled by FLOPs to all 27.
+    GEMMs: fp32 torch.matmul (addmm) as the optimised-library stand-in for
+    ncnn's Gemm, on the first rows of each of the four GEMMs (2048 rows with
+    `threads` threads, 256 rows on one), scaled to all 21,664 rows.
+    About 15-30 s of CPU work."""
     import numpy as np
-    import oracle
+    import torch
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from common import make_awa_inputs, oracle_awa
+    from seedvr2_ncnn_amd import capi
 
     t_start = time.time()
     shapes, tl = [VIDEO_SHAPE], [TEXT_TOKENS]
     case = make_awa_inputs(7, shapes, tl, HEADS, HEAD_DIM, PAIRS, bf16=True)
+    wins, _, _ = capi.plan_windows([VIDEO_SHAPE], TARGET, 0)
+    win_flops = [4 * HEADS * HEAD_DIM * (w[8] + TEXT_TOKENS) ** 2 for w in wins]
     t0 = time.perf_counter()
     oracle_awa(case, HEADS, HEAD_DIM, TARGET, 0, 1e-5, PAIRS, shapes, tl, threads=threads, fast=True)
-    attn_time = time.perf_counter() - t0
+    attn_mt = time.perf_counter() - t0
+    subset = [0, 1]
+    t0 = time.perf_counter()
+    oracle_awa(case, HEADS, HEAD_DIM, TARGET, 0, 1e-5, PAIRS, shapes, tl, threads=1, fast=True,
+               window_subset=subset)
+    attn_1 = (time.perf_counter() - t0) * sum(win_flops) / sum(win_flops[i] for i in subset)
     del case
-    g = np.random.default_rng(3)
-    rows = np.arange(gemm_rows, dtype=np.int32)
-    gemm_time = 0.0
     m = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2] + TEXT_TOKENS
-    sample_gemm = 0
-    for k, n, act in ((HIDDEN, 3 * HIDDEN, 0), (HIDDEN, HIDDEN, 0), (HIDDEN, MLP, 1), (MLP, HIDDEN, 0)):
-        x = g.standard_normal((gemm_rows, k), dtype=np.float32)
-        w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
-        t0 = time.perf_counter()
-        oracle.linear(x, w, None, act, rows=rows, threads=threads, fast=True)
-        dt = time.perf_counter() - t0
-        sample_gemm += 2 * gemm_rows * k * n
-        gemm_time += dt * m / gemm_rows
-    block_time = attn_time + gemm_time
-    total = attention_flops(0) + 2 * m * (HIDDEN * 3 * HIDDEN + HIDDEN * HIDDEN + 2 * HIDDEN * MLP)
+    shapes_g = ((HIDDEN, 3 * HIDDEN, 0), (HIDDEN, HIDDEN, 0), (HIDDEN, MLP, 1), (MLP, HIDDEN, 0))
+    g = np.random.default_rng(3)
+    prev = torch.get_num_threads()
+    gemm_mt = sum(_torch_gemm_seconds(2048, k, n, a, threads, g) * m / 2048 for k, n, a in shapes_g)
+    gemm_1 = sum(_torch_gemm_seconds(256, k, n, a, 1, g) * m / 256 for k, n, a in shapes_g)
+    torch.set_num_threads(prev)
+    total = sum(win_flops) + 2 * m * (HIDDEN * 3 * HIDDEN + HIDDEN * HIDDEN + 2 * HIDDEN * MLP)
+    block_mt, block_1 = attn_mt + gemm_mt, attn_1 + gemm_1
+    model, logical, allowed = host_cpu()
     return {
-        "value": round(total / block_time / 1e12, 6),
+        "value": round(total / block_mt / 1e12, 6),
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": (f"oracle/liboracle_fast.so (reference CPU forward restated in C, fp32, "
-                   f"OpenMP over heads/rows): the whole regular-window attention layer "
-                   f"({attention_flops(0) / 1e9:.1f} GFLOP, {attn_time:.1f} s) and the first "
-                   f"{gemm_rows} of 21664 rows of each of the 4 GEMMs ({sample_gemm / 1e9:.1f} GFLOP), "
-                   f"GEMM time scaled to all rows: {block_time:.1f} s per block; "
-                   f"sampled in {time.time() - t_start:.1f} s"),
-        "ms_per_block": round(block_time * 1e3, 1),
+        "sample": (f"attention: oracle/liboracle_fast.so (the reference CPU forward restated in C, "
+                   f"fp32, OpenMP over heads) on all 27 windows ({sum(win_flops) / 1e9:.1f} GFLOP, "
+                   f"{attn_mt:.2f} s on {threads} threads); GEMMs: fp32 torch.addmm on the CPU as "
+                   f"the optimised-library stand-in for ncnn Gemm, first 2048 of 21664 rows of "
+                   f"QKV/out/MLP-up+GELU/MLP-down scaled to all rows ({gemm_mt:.2f} s): "
+                   f"{block_mt:.1f} s per block; sampled in {time.time() - t_start:.1f} s"),
+        "ms_per_block": round(block_mt * 1e3, 1),
+        "one_thread": {
+            "value": round(total / block_1 / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
+            "ms_per_block": round(block_1 * 1e3, 1),
+            "sample": (f"attention windows 0-1 of 27 on one thread scaled by FLOPs "
+                       f"({attn_1:.1f} s per layer); GEMMs on the first 256 rows scaled "
+                       f"({gemm_1:.1f} s per block); the reference build runs ncnn with "
+                       f"NCNN_OPENMP OFF"),
+        },
+        "cpu_model": model,
+        "host_logical_cpus": logical,
+        "cpus_allowed": allowed,
+        "threads_note": "multi-threaded legs use the CPUs this process may run on, at most 16 "
+                        "(one GPU's share of a shared 8-GPU host)",
     }
+
+
+def awa_configs(threads, reps=20):
+    """The single-layer attention configurations, each on the GPU (kernel
+    time of one s2_awa_forward, HIP events on the launching stream, inputs
+    resident) and on the CPU (the oracle's optimised build on one thread and
+    on `threads` threads), with the parity of the GPU output against the
+    oracle's test build on the same inputs, computed outside the timed
+    region:
+      cfg1  grid 1x32x32, 8 heads x 64, target (1,8,8), unshifted, fp32 in/out
+      cfg2  grid 1x64x64, 20 heads x 128, target (4,3,3), regular and shifted, bf16 in
+      cfg3  grid 6x45x80, 20 heads x 128, target (4,3,3), regular and shifted, bf16 in
+            (parity only: its time is the headline's attention)."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from common import MAX_ABS_TOL, COSINE_TOL, make_awa_inputs, metrics, oracle_awa
+    from seedvr2_ncnn_amd import capi
+    dev = torch.device("cuda:0")
+    cases = [("cfg1", (1, 32, 32), 8, 64, 10, (1, 8, 8), 0, False),
+             ("cfg2_regular", (1, 64, 64), 20, 128, 21, (4, 3, 3), 0, True),
+             ("cfg2_shifted", (1, 64, 64), 20, 128, 21, (4, 3, 3), 1, True),
+             ("cfg3_regular", VIDEO_SHAPE, 20, 128, 21, (4, 3, 3), 0, True),
+             ("cfg3_shifted", VIDEO_SHAPE, 20, 128, 21, (4, 3, 3), 1, True)]
+    out = {}
+    for name, grid, heads, d, pairs, target, shifted, bf16 in cases:
+        shapes, tl = [grid], [TEXT_TOKENS]
+        inner = heads * d
+        case = make_awa_inputs(101, shapes, tl, heads, d, pairs, bf16=bf16)
+        dt = torch.bfloat16 if bf16 else torch.float32
+        v = torch.from_numpy(case["video"]).to(dev).to(dt)
+        t = torch.from_numpy(case["text"]).to(dev).to(dt)
+        norms = torch.from_numpy(case["norms"]).to(dev)
+        freqs = torch.from_numpy(case["freqs"]).to(dev)
+        cfg = capi.awa_config(heads, d, target, shifted, 1e-5, pairs)
+        rec = {"grid": list(grid), "heads": heads, "head_dim": d, "target": list(target),
+               "shifted": shifted, "dtype": "bf16" if bf16 else "fp32", "text_tokens": TEXT_TOKENS}
+        with capi.AwaPlan(cfg, shapes, tl) as plan:
+            ws = torch.empty(plan.info.workspace_bytes, dtype=torch.uint8, device=dev)
+            ov = torch.empty(plan.info.video_tokens, inner, dtype=torch.float32, device=dev)
+            ot = torch.empty(plan.info.text_tokens, inner, dtype=torch.float32, device=dev)
+
+            def fwd():
+                capi.awa_forward(plan, norms, freqs, v[:, :inner], v[:, inner:2 * inner],
+                                 v[:, 2 * inner:], t[:, :inner], t[:, inner:2 * inner],
+                                 t[:, 2 * inner:], workspace=ws, out_video=ov, out_text=ot)
+            fwd()
+            torch.cuda.synchronize()
+            got_v, got_t = ov.cpu().numpy(), ot.cpu().numpy()
+            if not name.startswith("cfg3"):
+                for _ in range(3):
+                    fwd()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                start.record()
+                for _ in range(reps):
+                    fwd()
+                end.record()
+                torch.cuda.synchronize()
+                gpu_ms = start.elapsed_time(end) / reps
+                wins, _ = plan.windows()
+                flops = sum(4 * heads * d * (w[8] + TEXT_TOKENS) ** 2 for w in wins)
+                rec.update(gpu_ms=round(gpu_ms, 4), gflop=round(flops / 1e9, 3),
+                           gpu_tflops=round(flops / (gpu_ms * 1e-3) / 1e12, 1))
+        ref_v, ref_t = oracle_awa(case, heads, d, target, shifted, 1e-5, pairs, shapes, tl,
+                                  threads=threads)
+        ma_v, cs_v = metrics(got_v, ref_v)
+        ma_t, cs_t = metrics(got_t, ref_t)
+        rec["parity"] = {"video_max_abs": ma_v, "video_cosine": cs_v, "text_max_abs": ma_t,
+                         "text_cosine": cs_t, "tol_max_abs": MAX_ABS_TOL, "tol_cosine": COSINE_TOL,
+                         "pass": bool(max(ma_v, ma_t) <= MAX_ABS_TOL and min(cs_v, cs_t) >= COSINE_TOL)}
+        if not name.startswith("cfg3"):
+            cpu = {}
+            for th in (1, threads):
+                t0 = time.perf_counter()
+                oracle_awa(case, heads, d, target, shifted, 1e-5, pairs, shapes, tl, threads=th,
+                           fast=True)
+                cpu[th] = (time.perf_counter() - t0) * 1e3
+            rec["cpu_ms_one_thread"] = round(cpu[1], 2)
+            rec[f"cpu_ms_{threads}_threads"] = round(cpu[threads], 2)
+        out[name] = rec
+        del v, t
+    return out
+
+
+def gemm_parity(x_v, x_t, weights, rows=256):
+    """Parity of the four block GEMMs (cfg4 shapes) on the first `rows`
+    video rows and all text rows: the GPU's fp32-output SharedLinear on the
+    same bf16 inputs against the oracle's fp32 X W^T + b, outside the timed
+    region."""
+    import numpy as np
+    import torch
+    import oracle
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from common import MAX_ABS_TOL, COSINE_TOL, metrics
+    from seedvr2_ncnn_amd import capi
+    out = {}
+    threads = job_cpu_threads()
+    for name, (w, bias, act) in weights.items():
+        k = w.shape[1]
+        xv = x_v[:, :k] if x_v.shape[1] >= k else None
+        if xv is None:
+            g = torch.Generator(device=x_v.device).manual_seed(5)
+            xv = torch.randn(x_v.shape[0], k, generator=g, device=x_v.device).to(torch.bfloat16)
+            xt = torch.randn(x_t.shape[0], k, generator=g, device=x_v.device).to(torch.bfloat16)
+        else:
+            xt = x_t[:, :k]
+        xv, xt = xv.contiguous(), xt.contiguous()
+        yv, yt = capi.shared_linear(xv, xt, w, bias, act, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        xs = torch.cat([xv[:rows], xt]).float().cpu().numpy()
+        ref = oracle.linear(xs, w.float().cpu().numpy(), bias.cpu().numpy(), act, threads=threads)
+        got = torch.cat([yv[:rows], yt]).cpu().numpy()
+        ma, cs = metrics(got, ref)
+        out[name] = {"rows_checked": int(xs.shape[0]), "max_abs": ma, "cosine": cs,
+                     "tol_max_abs": MAX_ABS_TOL, "tol_cosine": COSINE_TOL,
+                     "pass": bool(ma <= MAX_ABS_TOL and cs >= COSINE_TOL)}
+    return out
 
 
 LATENT_SHAPE = (6, 90, 160)    # 720p latent: 21 frames -> 6, 720/8, 1280/8
@@ -494,6 +679,12 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-parity", action="store_true",
+                    help="skip the single-layer configurations (cfg1-cfg3 timings and parity) "
+                         "and the GEMM parity records")
+    ap.add_argument("--block-only", action="store_true",
+                    help="time only the DiT block (no stack, sampler tail, VAE, parity or CPU "
+                         "baseline): the run that rocprofv3 counter passes profile")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-stack", action="store_true", help="skip the 32-block 7B-shaped stack")
     ap.add_argument("--stack-steps", type=int, default=3)
@@ -508,6 +699,8 @@ def main():
                     help="also run one 1 GiB device copy (a plain copy kernel of known size) so "
                          "that PMC byte counters can be calibrated in the same profiler run")
     args = ap.parse_args()
+    if args.block_only:
+        args.no_stack = args.no_tail = args.no_vae = args.no_parity = args.no_cpu_baseline = True
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the multi-GPU sharding is a design, not a measured path)", file=sys.stderr)
@@ -520,7 +713,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.vae_only:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or job_cpu_threads()
         print(json.dumps({"vae_conv3d": vae_conv3d(cpu_threads=threads,
                                                    cpu=not args.no_cpu_baseline),
                           "vae_mha": vae_mha(cpu_threads=threads, cpu=not args.no_cpu_baseline)}),
@@ -761,24 +954,33 @@ def main():
             "unit": "TFLOP/s",
             "frac": round(up_tf / PEAK_BF16_TFLOPS, 4),
             "traffic": measured_traffic(),
+            "traffic_source": "profiles/shared_linear_mlp_up_720p_video_traffic.md (two rocprofv3 "
+                              "--pmc passes, FETCH_SIZE and WRITE_SIZE, copy-calibrated); read "
+                              "from that file, not measured in this run",
         },
         "wall_s_timed_region": round(wall, 3),
     }
     line["full_block"] = full_block(args.steps, args.warmup)
+    if not args.no_parity:
+        line["parity_gemm_cfg4"] = gemm_parity(
+            x_v, x_t, {"qkv": (w_qkv, b[3 * HIDDEN], capi.ACT_NONE), "out": (w_o, b[HIDDEN], capi.ACT_NONE),
+                       "mlp_up": (w_up, b[MLP], capi.ACT_GELU), "mlp_down": (w_dn, b[HIDDEN], capi.ACT_NONE)})
     for p in plans.values():
         p.close()
     del x_v, x_t, w_qkv, w_o, w_up, w_dn, qkv_v, qkv_t, a_v, a_t, o_v, o_t, h_v, h_t, y_v, y_t, ws
     torch.cuda.empty_cache()
+    if not args.no_parity:
+        line["attention_configs"] = awa_configs(args.cpu_threads or job_cpu_threads())
     if not args.no_stack:
         line["stack_7b"] = stack_7b(args.stack_steps, 1)
     if not args.no_tail:
         line["sampler_tail"] = sampler_tail()
     if not args.no_vae:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or job_cpu_threads()
         line["vae_conv3d"] = vae_conv3d(cpu_threads=threads, cpu=not args.no_cpu_baseline)
         line["vae_mha"] = vae_mha(cpu_threads=threads, cpu=not args.no_cpu_baseline)
     if not args.no_cpu_baseline:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or job_cpu_threads()
         line["cpu_baseline"] = cpu_baseline(threads)
     print(json.dumps(line), flush=True)
 
