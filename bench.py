@@ -4,8 +4,10 @@ Workload (one step = one DiT block's hot path at the SeedVR2-3B 720p video
 shape, 21 frames at 1280x720 -> 6x45x80 = 21,600 video tokens + 64 text
 tokens, hidden 2560, 20 heads x 128, bf16 with fp32 accumulation):
 
-  SharedLinear QKV   2560 -> 7680        (both streams, one grouped launch)
-  AdaptiveWindowAttention, regular 3-D windows (27 windows of 780/810 tokens)
+  SharedLinear QKV   2560 -> 7680        (both streams, one grouped launch) and
+  AdaptiveWindowAttention, regular 3-D windows (27 windows of 780/810 tokens),
+                     in one call (s2_awa_qkv_forward: the window gather, RMSNorm
+                     and RoPE run in the projection's epilogue)
   SharedLinear out   2560 -> 2560
   SharedLinear MLP   2560 -> 10240, GELU
   SharedLinear MLP   10240 -> 2560
@@ -14,7 +16,9 @@ Algorithmic work per step: 4*H*d*sum_w (n_w+64)^2 attention FLOPs (206.45 G)
 plus 2*M*K*N per GEMM with M = 21,664 (3,407.45 G): 3.614 TFLOP.  Inputs and
 weights are resident in HBM before the timed region (seeded N(0,1)
 activations, N(0,0.02) weights).  The shifted-window block (64 ragged
-windows) is timed too and reported beside the headline, and so is the
+windows) is timed too and reported beside the headline, as is the same block
+with the projection and the attention as two calls (s2_shared_linear_forward
+writing the QKV blob, then s2_awa_forward), and so is the
 SeedVR2-7B-shaped stack of 32 blocks (hidden 3072, 24 heads x 128, MLP
 3072 -> 12288 -> 3072, regular windows in even and shifted windows in odd
 blocks, 64 text tokens projected 5120 -> 3072 once) under "stack_7b".  The
@@ -569,8 +573,6 @@ def stack_7b(steps, warmup):
     freqs = (10000.0 ** (-torch.arange(PAIRS, device=dev, dtype=torch.float64) / PAIRS)).float()
     x_v0, text_in = randn(lv, D), randn(lt, STACK_TEXT_WIDTH)
     x_v, x_t = torch.empty(lv, D, dtype=bf, device=dev), torch.empty(lt, D, dtype=bf, device=dev)
-    qkv_v = torch.empty(lv, 3 * D, dtype=bf, device=dev)
-    qkv_t = torch.empty(lt, 3 * D, dtype=bf, device=dev)
     a_v, a_t = torch.empty_like(x_v), torch.empty_like(x_t)
     o_v, o_t = torch.empty_like(x_v), torch.empty_like(x_t)
     h_v = torch.empty(lv, F, dtype=bf, device=dev)
@@ -583,12 +585,8 @@ def stack_7b(steps, warmup):
         x_v.copy_(x_v0)
         capi.shared_linear(text_in, None, w_text, b_text, capi.ACT_NONE, y_video=x_t)
         for i, blk in enumerate(blocks):
-            capi.shared_linear(x_v, x_t, blk["qkv"], blk["bqkv"], capi.ACT_NONE, y_video=qkv_v,
-                               y_text=qkv_t)
-            capi.awa_forward(plans[i % 2], blk["norms"], freqs,
-                             qkv_v[:, :D], qkv_v[:, D:2 * D], qkv_v[:, 2 * D:],
-                             qkv_t[:, :D], qkv_t[:, D:2 * D], qkv_t[:, 2 * D:],
-                             workspace=ws, out_video=a_v, out_text=a_t)
+            capi.awa_qkv_forward(plans[i % 2], x_v, x_t, blk["qkv"], blk["bqkv"], blk["norms"],
+                                 freqs, workspace=ws, out_video=a_v, out_text=a_t)
             capi.shared_linear(a_v, a_t, blk["o"], blk["bo"], capi.ACT_NONE, y_video=o_v, y_text=o_t)
             capi.shared_linear(o_v, o_t, blk["up"], blk["bup"], capi.ACT_GELU, y_video=h_v, y_text=h_t)
             capi.shared_linear(h_v, h_t, blk["dn"], blk["bdn"], capi.ACT_NONE, y_video=x_v, y_text=x_t)
@@ -612,12 +610,8 @@ def stack_7b(steps, warmup):
                     out_video=hin_v, out_text=hin_t)
         for i, blk in enumerate(blocks):
             md = mods[i]
-            capi.shared_linear(hin_v, hin_t, blk["qkv"], blk["bqkv"], capi.ACT_NONE, y_video=qkv_v,
-                               y_text=qkv_t)
-            capi.awa_forward(plans[i % 2], blk["norms"], freqs,
-                             qkv_v[:, :D], qkv_v[:, D:2 * D], qkv_v[:, 2 * D:],
-                             qkv_t[:, :D], qkv_t[:, D:2 * D], qkv_t[:, 2 * D:],
-                             workspace=ws, out_video=a_v, out_text=a_t)
+            capi.awa_qkv_forward(plans[i % 2], hin_v, hin_t, blk["qkv"], blk["bqkv"],
+                                 blk["norms"], freqs, workspace=ws, out_video=a_v, out_text=a_t)
             capi.shared_linear(a_v, a_t, blk["o"], blk["bo"], capi.ACT_NONE, y_video=o_v, y_text=o_t)
             capi.ada_out_in(res_v, res_t, o_v, o_t, vr, tr, md["a_gate"], md["m_shift"],
                             md["m_scale"], h_video=hin_v, h_text=hin_t)
@@ -748,42 +742,53 @@ def main():
     ws = torch.empty(max(p.info.workspace_bytes for p in plans.values()), dtype=torch.uint8, device=dev)
 
     ops = ["qkv", "attention", "out", "mlp_up", "mlp_down"]
+    fused_ops = ["qkv_attention", "out", "mlp_up", "mlp_down"]
 
-    def step(shifted, ev=None):
+    def step(shifted, ev=None, fused=True):
         def mark(i):
             if ev is not None:
                 ev[i].record()
         mark(0)
-        capi.shared_linear(x_v, x_t, w_qkv, b[3 * HIDDEN], capi.ACT_NONE, y_video=qkv_v, y_text=qkv_t)
-        mark(1)
-        capi.awa_forward(plans[shifted], norms, freqs,
-                         qkv_v[:, :HIDDEN], qkv_v[:, HIDDEN:2 * HIDDEN], qkv_v[:, 2 * HIDDEN:],
-                         qkv_t[:, :HIDDEN], qkv_t[:, HIDDEN:2 * HIDDEN], qkv_t[:, 2 * HIDDEN:],
-                         workspace=ws, out_video=a_v, out_text=a_t)
-        mark(2)
+        if fused:
+            # QKV projection with the attention prologue in its epilogue,
+            # then the attention (s2_awa_qkv_forward)
+            capi.awa_qkv_forward(plans[shifted], x_v, x_t, w_qkv, b[3 * HIDDEN], norms, freqs,
+                                 workspace=ws, out_video=a_v, out_text=a_t)
+        else:
+            capi.shared_linear(x_v, x_t, w_qkv, b[3 * HIDDEN], capi.ACT_NONE, y_video=qkv_v,
+                               y_text=qkv_t)
+            mark(1)
+            capi.awa_forward(plans[shifted], norms, freqs,
+                             qkv_v[:, :HIDDEN], qkv_v[:, HIDDEN:2 * HIDDEN], qkv_v[:, 2 * HIDDEN:],
+                             qkv_t[:, :HIDDEN], qkv_t[:, HIDDEN:2 * HIDDEN], qkv_t[:, 2 * HIDDEN:],
+                             workspace=ws, out_video=a_v, out_text=a_t)
+        o = 1 if fused else 2
+        mark(o)
         capi.shared_linear(a_v, a_t, w_o, b[HIDDEN], capi.ACT_NONE, y_video=o_v, y_text=o_t)
-        mark(3)
+        mark(o + 1)
         capi.shared_linear(o_v, o_t, w_up, b[MLP], capi.ACT_GELU, y_video=h_v, y_text=h_t)
-        mark(4)
+        mark(o + 2)
         capi.shared_linear(h_v, h_t, w_dn, b[HIDDEN], capi.ACT_NONE, y_video=y_v, y_text=y_t)
-        mark(5)
+        mark(o + 3)
 
-    def run(shifted, steps, warmup):
+    def run(shifted, steps, warmup, fused=True):
+        names = fused_ops if fused else ops
         for _ in range(warmup):
-            step(shifted)
+            step(shifted, fused=fused)
         torch.cuda.synchronize()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(steps)]
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+               for _ in range(steps)]
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         start.record()
         for i in range(steps):
-            step(shifted, evs[i])
+            step(shifted, evs[i], fused=fused)
         end.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         total_ms = start.elapsed_time(end)
-        per_op = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(ops)}
+        per_op = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(names)}
         return total_ms / steps, per_op, wall
 
     def full_block(steps, warmup):
@@ -802,7 +807,7 @@ def main():
         hin_v = torch.empty(lv, HIDDEN, dtype=bf, device=dev)
         hin_t = torch.empty(lt, HIDDEN, dtype=bf, device=dev)
         vr, tr = [lv], [lt]
-        fops = ["attn_norm_modulate", "qkv", "attention", "out",
+        fops = ["attn_norm_modulate", "qkv_attention", "out",
                 "attn_gate_residual_mlp_norm_modulate", "mlp_up", "mlp_down",
                 "mlp_gate_residual"]
 
@@ -814,32 +819,27 @@ def main():
             capi.ada_in(res_v, res_t, vr, tr, mods["attn_shift"], mods["attn_scale"],
                         out_video=hin_v, out_text=hin_t)
             mark(1)
-            capi.shared_linear(hin_v, hin_t, w_qkv, b[3 * HIDDEN], capi.ACT_NONE, y_video=qkv_v,
-                               y_text=qkv_t)
+            capi.awa_qkv_forward(plans[0], hin_v, hin_t, w_qkv, b[3 * HIDDEN], norms, freqs,
+                                 workspace=ws, out_video=a_v, out_text=a_t)
             mark(2)
-            capi.awa_forward(plans[0], norms, freqs,
-                             qkv_v[:, :HIDDEN], qkv_v[:, HIDDEN:2 * HIDDEN], qkv_v[:, 2 * HIDDEN:],
-                             qkv_t[:, :HIDDEN], qkv_t[:, HIDDEN:2 * HIDDEN], qkv_t[:, 2 * HIDDEN:],
-                             workspace=ws, out_video=a_v, out_text=a_t)
-            mark(3)
             capi.shared_linear(a_v, a_t, w_o, b[HIDDEN], capi.ACT_NONE, y_video=o_v, y_text=o_t)
-            mark(4)
+            mark(3)
             # the attention's gate and residual sum with the MLP's norm and
             # modulation, one pass over the residual stream
             capi.ada_out_in(res_v, res_t, o_v, o_t, vr, tr, mods["attn_gate"], mods["mlp_shift"],
                             mods["mlp_scale"], h_video=hin_v, h_text=hin_t)
-            mark(5)
+            mark(4)
             capi.shared_linear(hin_v, hin_t, w_up, b[MLP], capi.ACT_GELU, y_video=h_v, y_text=h_t)
-            mark(6)
+            mark(5)
             capi.shared_linear(h_v, h_t, w_dn, b[HIDDEN], capi.ACT_NONE, y_video=y_v, y_text=y_t)
-            mark(7)
+            mark(6)
             capi.ada_out(res_v, res_t, y_v, y_t, vr, tr, mods["mlp_gate"])
-            mark(8)
+            mark(7)
 
         for _ in range(warmup):
             fstep()
         torch.cuda.synchronize()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(9)] for _ in range(steps)]
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fops) + 1)] for _ in range(steps)]
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record()
         for i in range(steps):
@@ -874,28 +874,36 @@ def main():
     m = lv + lt
     gemm = {"qkv": 2 * m * HIDDEN * 3 * HIDDEN, "out": 2 * m * HIDDEN * HIDDEN,
             "mlp_up": 2 * m * HIDDEN * MLP, "mlp_down": 2 * m * MLP * HIDDEN}
-    results = {}
+    results, separate = {}, {}
     for shifted in (0, 1):
+        attn = attention_flops(shifted)
         ms, per_op, wall = run(shifted, args.steps, args.warmup)
-        flops = dict(gemm, attention=attention_flops(shifted))
+        flops = dict(gemm, attention=attn)
         results[shifted] = (ms, per_op, flops, wall)
+        ms_u, per_op_u, _ = run(shifted, args.steps, args.warmup, fused=False)
+        separate[shifted] = (ms_u, per_op_u, flops)
 
     # per-kernel times of the attention forward from events the library
-    # records around its four kernels (separate runs: the timed loop above
-    # records none)
-    stages = {}
-    for shifted in (0, 1):
+    # records around its four stages (separate runs: the timed loops above
+    # record none)
+    def stage_times(shifted, fused):
         capi.awa_stage_timing(True)
         acc = {}
         reps = max(3, args.steps // 2)
         for _ in range(reps):
-            step(shifted)
+            step(shifted, fused=fused)
             for key, v in capi.awa_stage_times().items():
                 acc[key] = acc.get(key, 0.0) + v / reps
         capi.awa_stage_timing(False)
-        pb = prologue_bytes(shifted)
+        return acc
+
+    stages = {}
+    for shifted in (0, 1):
+        mode = "shifted" if shifted else "regular"
         af = attention_flops(shifted)
-        stages["shifted" if shifted else "regular"] = {
+        acc = stage_times(shifted, False)
+        pb = prologue_bytes(shifted)
+        stages[mode] = {
             "rope_table_ms": round(acc["rope_table"], 4),
             "prologue_ms": round(acc["prologue"], 4),
             "prologue_algorithmic_bytes": pb,
@@ -906,14 +914,33 @@ def main():
             "attention_kernel_frac_bf16_peak": round(af / (acc["attention"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
             "text_pool_ms": round(acc["text_pool"], 4),
         }
+        accf = stage_times(shifted, True)
+        qf = gemm["qkv"]
+        stages[mode + "_fused"] = {
+            "rope_table_ms": round(accf["rope_table"], 4),
+            "qkv_prologue_broadcast_ms": round(accf["prologue"], 4),
+            "qkv_prologue_tflops": round(qf / (accf["prologue"] * 1e-3) / 1e12, 1),
+            "attention_kernel_ms": round(accf["attention"], 4),
+            "text_pool_ms": round(accf["text_pool"], 4),
+        }
 
     ms, per_op, flops, wall = results[0]
     block_flops = sum(flops.values())
     value = block_flops / (ms * 1e-3) / 1e12
-    kernels = {op: {"ms": round(per_op[op], 4), "gflop": round(flops[op] / 1e9, 3),
-                    "tflops": round(flops[op] / (per_op[op] * 1e-3) / 1e12, 1),
-                    "frac_bf16_peak": round(flops[op] / (per_op[op] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
-               for op in ops}
+
+    def op_record(t_ms, gf):
+        return {"ms": round(t_ms, 4), "gflop": round(gf / 1e9, 3),
+                "tflops": round(gf / (t_ms * 1e-3) / 1e12, 1),
+                "frac_bf16_peak": round(gf / (t_ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+    kernels = {"qkv_attention": op_record(per_op["qkv_attention"], flops["qkv"] + flops["attention"])}
+    kernels.update({op: op_record(per_op[op], flops[op]) for op in ("out", "mlp_up", "mlp_down")})
+    ms_u, per_op_u, flops_u = separate[0]
+    separate_rec = {"ms_per_block": round(ms_u, 4),
+                    "ms_per_block_shifted": round(separate[1][0], 4),
+                    "kernels": {op: op_record(per_op_u[op], flops_u[op]) for op in ops},
+                    "note": "the QKV GEMM writing a bf16 QKV blob, then s2_awa_forward (window "
+                            "gather prologue, attention, text pool); the headline runs "
+                            "s2_awa_qkv_forward, whose outputs are bit-identical"}
     up_ms = per_op["mlp_up"]
     up_tf = flops["mlp_up"] / (up_ms * 1e-3) / 1e12
     ms_s, per_op_s, flops_s, _ = results[1]
@@ -933,7 +960,8 @@ def main():
         "config": {
             "workload": "SeedVR2-3B DiT block hot path at 720p video: 21 frames 1280x720 -> "
                         "6x45x80 = 21600 video + 64 text tokens, hidden 2560, 20x128 heads, "
-                        "regular 3-D windows (target 4,3,3); QKV 2560->7680, window attention, "
+                        "regular 3-D windows (target 4,3,3); QKV 2560->7680 with the window "
+                        "gather, RMSNorm and RoPE in its epilogue, window attention, "
                         "out 2560->2560, MLP 2560->10240 GELU ->2560",
             "video_tokens": lv, "text_tokens": lt, "hidden": HIDDEN, "heads": HEADS,
             "head_dim": HEAD_DIM, "block_tflop": round(block_flops / 1e12, 4),
@@ -942,9 +970,10 @@ def main():
         "ms_per_block": round(ms, 4),
         "ms_per_block_shifted": round(ms_s, 4),
         "tflops_shifted": round(sum(flops_s.values()) / (ms_s * 1e-3) / 1e12, 2),
-        "attention_shifted": {"ms": round(per_op_s["attention"], 4),
-                              "tflops": round(flops_s["attention"] / (per_op_s["attention"] * 1e-3) / 1e12, 1)},
+        "qkv_attention_shifted": op_record(per_op_s["qkv_attention"],
+                                           flops_s["qkv"] + flops_s["attention"]),
         "kernels": kernels,
+        "separate_qkv_and_attention": separate_rec,
         "attention_stages": stages,
         "roofline": {
             "kernel": "s2::shared_linear_256_kernel<true, 1> (MLP up 2560->10240 + GELU, M=21664)",

@@ -156,10 +156,38 @@ S2_API int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights,
                    void* out_video, void* out_text, s2_dtype out_dtype,
                    void* workspace, size_t workspace_bytes, s2_stream_t stream);
 
+/* The QKV projection and the attention layer in one call: SharedLinear::forward
+ * with the fused QKV weight (shared_linear.cpp:83-96) feeding
+ * AdaptiveWindowAttention::forward in its 4-input form
+ * (adaptive_window_attention.cpp:764-978), as the fused seedvr2_blocks graph
+ * chains them.  The projection's epilogue writes the attention's window-ordered
+ * Q, K and V^T directly (RMSNorm and RoPE applied), so the [L][3*inner]
+ * QKV blob never reaches memory and the gather pass of s2_awa_forward is not
+ * needed.  Numerically the norm reads the fp32 projection (+ bias) instead of
+ * a rounded QKV blob; everything else is as s2_awa_forward.
+ *
+ * x_video [video_tokens][hidden], x_text [text_tokens][hidden]: device bf16
+ *   rows, contiguous, 16-byte aligned.
+ * qkv_weight: device bf16 [3*inner][hidden] (columns [q|k|v] of the output,
+ *   head h at h*head_dim, :890-892); qkv_bias: device fp32 [3*inner] or NULL.
+ * norm_weights, rope_freqs, out_*, workspace, stream: as s2_awa_forward
+ *   (the same workspace size, info.workspace_bytes).
+ * Requires heads*head_dim a multiple of 256, head_dim 64 or 128 and hidden a
+ * multiple of 64; otherwise S2_ERR_INVALID (use s2_shared_linear_forward and
+ * s2_awa_forward).  The projection shares the split-k scratch of
+ * s2_shared_linear_forward (per device and stream). */
+S2_API int s2_awa_qkv_forward(const s2_awa_plan* plan, const void* x_video, const void* x_text,
+                       int hidden, const uint16_t* qkv_weight, const float* qkv_bias,
+                       const float* norm_weights, const float* rope_freqs,
+                       void* out_video, void* out_text, s2_dtype out_dtype,
+                       void* workspace, size_t workspace_bytes, s2_stream_t stream);
+
 /* Stage timing of s2_awa_forward, a diagnostic with no counterpart in the
  * reference.  While enabled on the calling thread, every s2_awa_forward
  * records HIP events on its stream around its four kernels: RoPE table,
- * prologue (window gather, RMSNorm, RoPE), attention, text pool.
+ * prologue (window gather, RMSNorm, RoPE), attention, text pool
+ * (s2_awa_qkv_forward: RoPE table, QKV projection with the fused prologue
+ * and the text broadcast, attention, text pool).
  * s2_awa_stage_times waits for the last such forward and returns the four
  * durations in milliseconds. */
 S2_API int s2_awa_stage_timing(int enable);

@@ -39,6 +39,7 @@ EXPORTS = (
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
     "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded", "s2_shared_linear_forward_noalloc",
+    "s2_awa_qkv_forward",
 )
 
 
@@ -127,6 +128,7 @@ def lib() -> ctypes.CDLL:
         L.s2_awa_plan_tables.argtypes = [vp, vp, vp, vp, vp]
         L.s2_awa_forward.argtypes = [vp, vp, vp, vp, vp, vp, cl, vp, vp, vp, cl, ci, vp, vp, ci,
                                      vp, sz, vp]
+        L.s2_awa_qkv_forward.argtypes = [vp, vp, vp, ci, vp, vp, vp, vp, vp, vp, ci, vp, sz, vp]
         L.s2_cast_f32_to_bf16.argtypes = [vp, vp, sz, vp]
         L.s2_cast_bf16_to_f32.argtypes = [vp, vp, sz, vp]
         L.s2_shared_linear_forward.argtypes = [vp, ci, vp, ci, ci, vp, vp, ci, ci, ci, vp, vp, ci, vp]
@@ -326,6 +328,35 @@ def awa_forward(plan: AwaPlan, norm_weights, rope_freqs, video_q, video_k, video
                                _ptr(out_video), _ptr(out_text), _dtype_code(out_video),
                                _ptr(workspace), workspace.numel(), _stream(stream)),
           "s2_awa_forward")
+    return out_video, out_text
+
+
+def awa_qkv_forward(plan: AwaPlan, x_video, x_text, qkv_weight_bf16, qkv_bias, norm_weights,
+                    rope_freqs, out_dtype=None, workspace=None, out_video=None, out_text=None,
+                    stream=None):
+    """s2_awa_qkv_forward: the QKV projection (bf16 activations x_* [L][hidden],
+    weight [3*inner][hidden]) and the attention layer in one call.  Returns
+    (out_video, out_text)."""
+    import torch
+    inner = plan.config.heads * plan.config.head_dim
+    assert x_video.dtype == torch.bfloat16 and x_text.dtype == torch.bfloat16
+    assert x_video.is_contiguous() and x_text.is_contiguous()
+    hidden = x_video.shape[1]
+    assert x_text.shape[1] == hidden and qkv_weight_bf16.shape == (3 * inner, hidden)
+    assert qkv_weight_bf16.dtype == torch.bfloat16 and qkv_weight_bf16.is_contiguous()
+    odt = out_dtype or torch.bfloat16
+    dev = x_video.device
+    if out_video is None:
+        out_video = torch.empty((plan.info.video_tokens, inner), dtype=odt, device=dev)
+    if out_text is None:
+        out_text = torch.empty((plan.info.text_tokens, inner), dtype=odt, device=dev)
+    if workspace is None:
+        workspace = torch.empty(plan.info.workspace_bytes, dtype=torch.uint8, device=dev)
+    check(lib().s2_awa_qkv_forward(plan.handle, _ptr(x_video), _ptr(x_text), hidden,
+                                   _ptr(qkv_weight_bf16), _ptr(qkv_bias), _ptr(norm_weights),
+                                   _ptr(rope_freqs), _ptr(out_video), _ptr(out_text),
+                                   _dtype_code(out_video), _ptr(workspace), workspace.numel(),
+                                   _stream(stream)), "s2_awa_qkv_forward")
     return out_video, out_text
 
 

@@ -24,6 +24,17 @@ hipError_t launch_awa_text_pool(const s2_awa_plan& plan, const float* partial, v
 hipError_t launch_awa_plan_tables(const s2_awa_plan& plan, int* indices, int* inverse,
                                   int* positions, hipStream_t stream);
 
+// The fused QKV projection + attention prologue (x [L][k] bf16, W [3 inner][k]):
+// writes the plan's Q, K and V^T workspace, text tokens to their staging rows.
+hipError_t launch_awa_qkv(const s2_awa_plan& plan, const uint16_t* x_video, const uint16_t* x_text,
+                          int k, const uint16_t* w, const float* bias, const float* norm,
+                          const float2* rope, uint16_t* q, uint16_t* kk, uint16_t* vt,
+                          hipStream_t stream);
+// Copies the staged text Q/K/V^T into every window segment of its sample and
+// zeroes the V^T padding keys of every segment.
+hipError_t launch_awa_text_broadcast(const s2_awa_plan& plan, uint16_t* q, uint16_t* k,
+                                     uint16_t* vt, hipStream_t stream);
+
 hipError_t launch_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream);
 hipError_t launch_cast_bf16_f32(const uint16_t* src, float* dst, size_t n, hipStream_t stream);
 // Grouped y_s = act(x_s W^T + b) over the video and text streams.

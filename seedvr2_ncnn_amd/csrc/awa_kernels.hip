@@ -19,39 +19,11 @@
 
 #include <type_traits>
 
+#include "awa_index.h"
 #include "awa_kernels.h"
 #include "s2_device.h"
 
 namespace s2 {
-
-// ---------------------------------------------------------------------------
-// Index math shared by the kernels (append_slice order, :462-471).
-struct TokenCoord {
-    int lt, lh, lw;
-    long src;
-};
-
-// a / b for 0 <= a < 2^22, b > 0: the fp32 quotient is within one of the
-// true one, and one correction step makes it exact (cheaper than the
-// integer division sequence)
-__device__ __forceinline__ int div_small(int a, int b) {
-    int q = (int)((float)a * __builtin_amdgcn_rcpf((float)b));
-    const int r = a - q * b;
-    q += (r >= b) - (r < 0);
-    return q;
-}
-
-__device__ __forceinline__ TokenCoord window_token(const WinMeta& w, int r) {
-    TokenCoord c;
-    const int plane = w.eh * w.ew;
-    c.lt = div_small(r, plane);
-    const int rem = r - c.lt * plane;
-    c.lh = div_small(rem, w.ew);
-    c.lw = rem - c.lh * w.ew;
-    c.src = (long)w.tok_off +
-            ((long)(w.t0 + c.lt) * w.grid_h + (w.h0 + c.lh)) * w.grid_w + (w.w0 + c.lw);
-    return c;
-}
 
 // ---------------------------------------------------------------------------
 // cos/sin table: table[pos * pairs + p] = (cos(pos*f[p]), sin(pos*f[p])), the
@@ -210,9 +182,10 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
                 sq2 += __shfl_xor(sq2, off);
                 sk2 += __shfl_xor(sk2, off);
             }
-            // rms_norm (:510-519): x * (1 / sqrt(sum/size + eps)) * w
-            const float inv_q = 1.f / sqrtf(sq2 / (float)D + eps);
-            const float inv_k = 1.f / sqrtf(sk2 / (float)D + eps);
+            // rms_norm (:510-519): x * (1 / sqrt(sum/size + eps)) * w, the
+            // reciprocal square root by v_rsq_f32 (within 1 ulp)
+            const float inv_q = __builtin_amdgcn_rsqf(sq2 / (float)D + eps);
+            const float inv_k = __builtin_amdgcn_rsqf(sk2 / (float)D + eps);
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 q[i] = q[i] * inv_q * (video ? nw[0][i] : nw[2][i]);
@@ -598,6 +571,77 @@ __global__ void awa_text_pool_kernel(const SampleMeta* __restrict__ samples,
 }
 
 // ---------------------------------------------------------------------------
+// Text broadcast of the fused QKV path: one workgroup per (window, head)
+// copies the sample's text Q and K rows and V^T keys from the staging rows
+// (where the fused projection wrote each text token once) to the rows after
+// the window's video tokens, which is where the window sequence
+// [video tokens] ++ [text tokens] (:886-927) expects them, and zeroes the
+// V^T keys of the segment's padding (zero values keep p * v finite for the
+// masked keys).
+constexpr int kBroadcastSplit = 4;   // workgroups per (window, head)
+
+template <int D>
+__global__ __launch_bounds__(256) void awa_text_broadcast_kernel(const WinMeta* __restrict__ wins,
+                                                                 long seg_total, long seg_text,
+                                                                 uint16_t* __restrict__ q,
+                                                                 uint16_t* __restrict__ k,
+                                                                 uint16_t* __restrict__ vt) {
+    constexpr int CPR = D / 8;                    // 16-byte chunks per row
+    constexpr int DC = D / kBroadcastSplit;       // V^T channels of this workgroup
+    constexpr int U = DC / 4;                     // channels per thread and pass
+    const WinMeta w = wins[blockIdx.x];
+    const int head = blockIdx.y;
+    const int part = blockIdx.z;
+    const int tid = threadIdx.x;
+    const long hq = (long)head * seg_total;
+    // Q and K: this workgroup's share of the text rows' 16-byte chunks,
+    // every load issued before any store
+    const int nq = w.text_len * CPR;
+    const int q0 = nq * part / kBroadcastSplit, q1 = nq * (part + 1) / kBroadcastSplit;
+    for (int base = q0; base < q1; base += 256 * 2) {
+        uint4 vq[2], vk[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int idx = base + u * 256 + tid;
+            if (idx < q1) {
+                const int t = idx / CPR;
+                const long src = (hq + seg_text + w.text_off + t) * D + (idx - t * CPR) * 8;
+                vq[u] = *reinterpret_cast<const uint4*>(q + src);
+                vk[u] = *reinterpret_cast<const uint4*>(k + src);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int idx = base + u * 256 + tid;
+            if (idx < q1) {
+                const int t = idx / CPR;
+                const long dst = (hq + w.seg_off + w.n_video + t) * D + (idx - t * CPR) * 8;
+                *reinterpret_cast<uint4*>(q + dst) = vq[u];
+                *reinterpret_cast<uint4*>(k + dst) = vk[u];
+            }
+        }
+    }
+    // V^T keys [n_video, padded) of this workgroup's channels: the text
+    // keys, then zeros; lanes along the keys, U channels per thread in flight
+    const int nk = (w.seq + kSegAlign - 1) / kSegAlign * kSegAlign - w.n_video;
+    const int dbase = part * DC + (tid >> 6);
+    for (int j0 = 0; j0 < nk; j0 += 64) {
+        const int j = j0 + (tid & 63);
+        uint16_t v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint16_t* row = vt + ((long)head * D + dbase + 4 * u) * seg_total;
+            v[u] = (j < w.text_len) ? row[seg_text + w.text_off + j] : (uint16_t)0;
+        }
+        if (j < nk) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                vt[((long)head * D + dbase + 4 * u) * seg_total + w.seg_off + w.n_video + j] = v[u];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Plan tables (AdaptiveWindowPlan's per-token arrays) from the same index math.
 __global__ void awa_plan_tables_kernel(const WinMeta* __restrict__ wins, int* __restrict__ indices,
                                        int* __restrict__ inverse, int* __restrict__ positions) {
@@ -694,6 +738,21 @@ hipError_t launch_awa_text_pool(const s2_awa_plan& plan, const float* partial, v
     awa_text_pool_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
         plan.d_samples, plan.d_text_sample, plan.d_wins, partial, plan.text_tokens, inner,
         out_text, out_kind);
+    return hipGetLastError();
+}
+
+hipError_t launch_awa_text_broadcast(const s2_awa_plan& plan, uint16_t* q, uint16_t* k,
+                                     uint16_t* vt, hipStream_t stream) {
+    if (plan.num_windows == 0) return hipSuccess;
+    dim3 grid(plan.num_windows, plan.config.heads, kBroadcastSplit);
+    if (plan.config.head_dim == 128)
+        awa_text_broadcast_kernel<128><<<grid, 256, 0, stream>>>(plan.d_wins, plan.seg_total,
+                                                                 plan.seg_text, q, k, vt);
+    else if (plan.config.head_dim == 64)
+        awa_text_broadcast_kernel<64><<<grid, 256, 0, stream>>>(plan.d_wins, plan.seg_total,
+                                                                plan.seg_text, q, k, vt);
+    else
+        return hipErrorInvalidValue;
     return hipGetLastError();
 }
 

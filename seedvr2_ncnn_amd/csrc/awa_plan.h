@@ -30,7 +30,8 @@ struct WinMeta {
     int grid_h, grid_w;   // sample token grid h, w
     int tok_off;          // first video row of the sample
     int tpart_off;        // first row of this window's text partials
-    int pad_;
+    int grow_off;         // first row of this window's video tokens in the row space of
+                          // the fused QKV projection (even; see s2_awa_plan::qkv_text_row)
 };
 static_assert(sizeof(WinMeta) == 72, "WinMeta layout");
 
@@ -56,6 +57,18 @@ constexpr int kSegAlign = 64;
 
 // MI355X has 8 XCDs; workgroups are dealt to them round-robin.
 constexpr int kNumXcd = 8;
+
+// One row of the fused QKV projection's row space: its source row (video or
+// text token; -1 for a gap or padding row), its workspace row, its RoPE
+// position and its kind (0 none, 1 video, 2 text).  A row of a window's run
+// past the window's tokens (a gap) keeps the workspace row that follows the
+// window's video rows, so that V^T key pairs stay contiguous.
+struct QkvRow {
+    int src;
+    int dest;
+    int pos01;   // position axis 0 | axis 1 << 16
+    int pos2;    // position axis 2 | kind << 16
+};
 
 // One prologue work item: 64 rows of one window's sequence.
 struct ChunkRef {
@@ -94,7 +107,17 @@ struct s2_awa_plan {
     int slots_per_xcd = 0;
     int max_window_tokens = 0;
     int rope_positions = 0;                 // rows of the cos/sin table
-    long seg_total = 0;                     // padded rows over all windows
+    long seg_total = 0;                     // row pitch of the Q/K/V^T workspace: the padded
+                                            // window segments, then text staging rows
+    long seg_text = 0;                      // first text staging row (the fused QKV path
+                                            // writes each text token's Q/K/V^T there once)
+    // Row space of the fused QKV projection (s2_awa_qkv_forward): the video
+    // tokens in window order, each window's run starting at an even row
+    // (WinMeta::grow_off), then the text tokens from qkv_text_row (a multiple
+    // of 8) to qkv_rows.
+    int qkv_text_row = 0;
+    int qkv_rows = 0;
+    s2::QkvRow* d_qkv_rows = nullptr;       // [qkv_rows rounded up to 256]
     int text_partial_rows = 0;
     // workspace layout (byte offsets)
     size_t off_q = 0, off_k = 0, off_vt = 0, off_rope = 0, off_tpart = 0;

@@ -301,7 +301,7 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
     // Window records, padded segments, text partial rows, prologue chunks.
     std::vector<s2::ChunkRef> chunks;
     long seg = 0;
-    int tpart = 0, rope_pos = 1;
+    int tpart = 0, rope_pos = 1, grow = 0;
     plan->win_meta.resize(plan->num_windows);
     for (int i = 0; i < plan->num_windows; ++i) {
         const s2_window_slice& s = plan->windows[i];
@@ -320,7 +320,8 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
         m.grid_w = video_shapes[3 * b + 2];
         m.tok_off = tok_off[b];
         m.tpart_off = tpart;
-        m.pad_ = 0;
+        m.grow_off = grow;
+        grow += (s.token_count + 1) / 2 * 2;
         const int padded = (m.seq + s2::kSegAlign - 1) / s2::kSegAlign * s2::kSegAlign;
         for (int r = 0; r < padded; r += s2::kSegAlign) chunks.push_back(s2::ChunkRef{i, r});
         seg += padded;
@@ -330,7 +331,11 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
         rope_pos = std::max(rope_pos, m.text_len);
         plan->max_window_tokens = std::max(plan->max_window_tokens, m.n_video);
     }
-    plan->seg_total = seg;
+    // text staging rows of the fused QKV path after the window segments
+    plan->seg_text = seg;
+    plan->seg_total = seg + (plan->text_tokens + s2::kSegAlign - 1) / s2::kSegAlign * s2::kSegAlign;
+    plan->qkv_text_row = (grow + 7) / 8 * 8;
+    plan->qkv_rows = plan->qkv_text_row + plan->text_tokens;
     plan->text_partial_rows = tpart;
     plan->rope_positions = rope_pos;
     plan->num_chunks = (int)chunks.size();
@@ -370,13 +375,51 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
     for (int b = 0; b < batch; ++b)
         for (int t = 0; t < text_lengths[b]; ++t) text_sample[text_off[b] + t] = b;
 
+    // Row table of the fused QKV projection: window runs in plan order, each
+    // starting at its grow_off, then the text tokens from qkv_text_row.  A
+    // video row holds its source token (append_slice's t,h,w walk,
+    // adaptive_window_attention.cpp:462-471) and its window-local position
+    // with the temporal axis offset by the text length (:901-902); a text row
+    // its token and the position (i, i, i) within its sample (:915).
+    const int qkv_tiles = (plan->qkv_rows + 255) / 256;
+    std::vector<s2::QkvRow> qrows((size_t)qkv_tiles * 256, s2::QkvRow{-1, 0, 0, 0});
+    for (int i = 0; i < plan->num_windows; ++i) {
+        const s2::WinMeta& m = plan->win_meta[i];
+        const int run_end = i + 1 < plan->num_windows ? plan->win_meta[i + 1].grow_off
+                                                      : plan->qkv_text_row;
+        for (int R = m.grow_off; R < run_end; ++R) {
+            const int r = R - m.grow_off;
+            s2::QkvRow& q = qrows[R];
+            q.dest = m.seg_off + r;
+            if (r < m.n_video) {
+                const int plane = m.eh * m.ew;
+                const int lt = r / plane, lh = (r - lt * plane) / m.ew, lw = r - lt * plane - lh * m.ew;
+                q.src = m.tok_off + ((m.t0 + lt) * m.grid_h + (m.h0 + lh)) * m.grid_w + (m.w0 + lw);
+                q.pos01 = (lt + m.text_len) | (lh << 16);
+                q.pos2 = lw | (1 << 16);
+            }
+        }
+    }
+    for (int R = plan->qkv_text_row; R < qkv_tiles * 256; ++R) {
+        const int t = R - plan->qkv_text_row;
+        s2::QkvRow& q = qrows[R];
+        q.dest = (int)plan->seg_text + t;
+        if (t < plan->text_tokens) {
+            const int tt = t - text_off[text_sample[t]];
+            q.src = t;
+            q.pos01 = tt | (tt << 16);
+            q.pos2 = tt | (2 << 16);
+        }
+    }
+
     // One device allocation for all metadata.
     const size_t sz_w = align256(sizeof(s2::WinMeta) * plan->num_windows);
     const size_t sz_s = align256(sizeof(s2::SampleMeta) * batch);
     const size_t sz_t = align256(sizeof(int) * plan->text_tokens);
     const size_t sz_c = align256(sizeof(s2::ChunkRef) * chunks.size());
     const size_t sz_i = align256(sizeof(s2::AttnItem) * items.size());
-    std::vector<unsigned char> host(sz_w + sz_s + sz_t + sz_c + sz_i, 0);
+    const size_t sz_q = align256(sizeof(s2::QkvRow) * qrows.size());
+    std::vector<unsigned char> host(sz_w + sz_s + sz_t + sz_c + sz_i + sz_q, 0);
     size_t o = 0;
     memcpy(host.data() + o, plan->win_meta.data(), sizeof(s2::WinMeta) * plan->num_windows);
     o += sz_w;
@@ -387,6 +430,8 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
     memcpy(host.data() + o, chunks.data(), sizeof(s2::ChunkRef) * chunks.size());
     o += sz_c;
     memcpy(host.data() + o, items.data(), sizeof(s2::AttnItem) * items.size());
+    o += sz_i;
+    memcpy(host.data() + o, qrows.data(), sizeof(s2::QkvRow) * qrows.size());
 
     hipError_t e = hipGetDevice(&plan->device);
     if (e == hipSuccess) e = hipMalloc(&plan->d_meta, host.size());
@@ -402,10 +447,11 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
     plan->d_text_sample = (int*)(base + sz_w + sz_s);
     plan->d_chunks = (s2::ChunkRef*)(base + sz_w + sz_s + sz_t);
     plan->d_items = (s2::AttnItem*)(base + sz_w + sz_s + sz_t + sz_c);
+    plan->d_qkv_rows = (s2::QkvRow*)(base + sz_w + sz_s + sz_t + sz_c + sz_i);
 
     // Workspace layout: Q and K [heads][seg_total][d], V^T [heads][d][seg_total]
     // (bf16), the cos/sin table, and fp32 text partials [rows][inner].
-    const size_t qkv = align256((size_t)heads * seg * d * 2);
+    const size_t qkv = align256((size_t)heads * plan->seg_total * d * 2);
     plan->off_q = 0;
     plan->off_k = qkv;
     plan->off_vt = 2 * qkv;
@@ -502,6 +548,59 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
     S2_HIP(s2::launch_awa_prologue(*plan, video_q, video_k, video_v, video_row_stride, text_q,
                                    text_k, text_v, text_row_stride, (int)in_dtype, norm_weights, rope, q,
                                    k, vt, s));
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[2], s));
+    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart, s));
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[3], s));
+    S2_HIP(s2::launch_awa_text_pool(*plan, tpart, out_text, (int)out_dtype, s));
+    if (tm.on) {
+        S2_HIP(hipEventRecord(tm.ev[4], s));
+        tm.recorded = true;
+    }
+    return S2_OK;
+}
+
+int s2_awa_qkv_forward(const s2_awa_plan* plan, const void* x_video, const void* x_text, int hidden,
+                       const uint16_t* qkv_weight, const float* qkv_bias,
+                       const float* norm_weights, const float* rope_freqs, void* out_video,
+                       void* out_text, s2_dtype out_dtype, void* workspace,
+                       size_t workspace_bytes, s2_stream_t stream) {
+    if (!plan || !x_video || !x_text || !qkv_weight || !norm_weights || !out_video || !out_text ||
+        !workspace)
+        return fail(S2_ERR_INVALID, "null argument");
+    const int d = plan->config.head_dim;
+    const int inner = plan->config.heads * d;
+    if ((d != 64 && d != 128) || inner % 256 != 0)
+        return fail(S2_ERR_INVALID, "fused QKV path needs head_dim 64 or 128 and heads*head_dim % 256 == 0");
+    if (hidden <= 0 || hidden % 64 != 0) return fail(S2_ERR_INVALID, "hidden must be a multiple of 64");
+    if ((long)(plan->video_tokens + 1) * hidden * 2 > 0x7fffffffL ||
+        (long)(plan->text_tokens + 1) * hidden * 2 > 0x7fffffffL)
+        return fail(S2_ERR_INVALID, "activations beyond the 32-bit buffer offsets");
+    if (plan->config.rope_pairs_per_axis > 0 && !rope_freqs)
+        return fail(S2_ERR_INVALID, "missing rope frequencies");
+    if (workspace_bytes < plan->workspace_bytes) return fail(S2_ERR_INVALID, "workspace too small");
+    if (!dtype_ok(out_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (((uintptr_t)x_video) % 16 != 0 || ((uintptr_t)x_text) % 16 != 0 ||
+        ((uintptr_t)qkv_weight) % 16 != 0 || ((uintptr_t)out_video) % 16 != 0 ||
+        ((uintptr_t)out_text) % 16 != 0)
+        return fail(S2_ERR_INVALID, "inputs and outputs must be 16-byte aligned");
+    if (((uintptr_t)workspace) % 256 != 0) return fail(S2_ERR_INVALID, "workspace alignment");
+
+    hipStream_t s = (hipStream_t)stream;
+    unsigned char* ws = (unsigned char*)workspace;
+    uint16_t* q = (uint16_t*)(ws + plan->off_q);
+    uint16_t* k = (uint16_t*)(ws + plan->off_k);
+    uint16_t* vt = (uint16_t*)(ws + plan->off_vt);
+    float2* rope = (float2*)(ws + plan->off_rope);
+    float* tpart = (float*)(ws + plan->off_tpart);
+    StageTimer& tm = stage_timer();
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[0], s));
+    if (plan->config.rope_pairs_per_axis > 0)
+        S2_HIP(s2::launch_rope_table(rope_freqs, plan->config.rope_pairs_per_axis,
+                                     plan->rope_positions, rope, s));
+    if (tm.on) S2_HIP(hipEventRecord(tm.ev[1], s));
+    S2_HIP(s2::launch_awa_qkv(*plan, (const uint16_t*)x_video, (const uint16_t*)x_text, hidden,
+                              qkv_weight, qkv_bias, norm_weights, rope, q, k, vt, s));
+    S2_HIP(s2::launch_awa_text_broadcast(*plan, q, k, vt, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[2], s));
     S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[3], s));

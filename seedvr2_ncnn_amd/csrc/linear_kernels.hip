@@ -11,6 +11,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "awa_index.h"
 #include "awa_kernels.h"
 #include "s2_device.h"
 #include "stream_scratch.h"
@@ -242,6 +243,22 @@ namespace {
 
 __device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
 
+// Sum over aligned groups of N lanes (N = 8 or 16) by DPP lane moves: quad
+// permutations [1,0,3,2] and [2,3,0,1], then the half-row and row mirrors.
+// Each step adds the value of a lane of the other half of the group, which
+// after the previous steps holds the same partial sum as lane ^ (N/2), so
+// the result equals the shuffle-xor reduction over masks 1, 2, 4, 8 bit for
+// bit (and needs no LDS round trip).
+template <int N>
+__device__ __forceinline__ float row_sum(float x) {
+    static_assert(N == 8 || N == 16, "row_sum over 8 or 16 lanes");
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0xB1, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x4E, 0xF, 0xF, false));
+    x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x141, 0xF, 0xF, false));
+    if (N == 16) x += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(x), 0x140, 0xF, 0xF, false));
+    return x;
+}
+
 constexpr int kSlotFloats = 128 * 512;   // one workgroup's accumulators
 
 // Cache policy of the slot stores and loads: sc0 sc1, coherent across the
@@ -263,11 +280,33 @@ struct SkTail {
     int* counters;     // [sk_tiles] arrivals; zero between launches
 };
 
-template <int YK, int ACT>
+// The fused QKV projection of the attention layer (AWA = head dim): the
+// tile rows are the plan's QKV row space (video tokens in window order, then
+// the text tokens), gathered from the source-ordered activations, and the
+// epilogue writes the attention workspace directly: RMS-normalised and
+// rotated Q and K rows [head][seg_total][D] and V transposed [head][D][seg_total]
+// (adaptive_window_attention.cpp:886-927), text tokens to their staging rows.
+struct AwaQkvArgs {
+    const QkvRow* row_table;  // the plan's rows, [mtiles * 256]
+    int inner;                // heads * head_dim
+    long seg_total;           // row pitch of Q, K and V^T
+    long seg_text;            // first text staging row
+    const float* norm;        // [4][D]: video q, video k, text q, text k
+    const float2* rope;       // (cos, sin) [position][pairs]
+    int pairs;
+    float eps;
+    int official_bf16;
+    uint16_t* q;
+    uint16_t* k;
+    uint16_t* vt;
+};
+
+template <int YK, int ACT, int AWA = 0>
 __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const uint16_t* __restrict__ x0, int m0, const uint16_t* __restrict__ x1, int m1,
     const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
-    void* __restrict__ y0, void* __restrict__ y1, int mv, int mtiles, int ntiles, SkTail sk) {
+    void* __restrict__ y0, void* __restrict__ y1, int mv, int mtiles, int ntiles, SkTail sk,
+    AwaQkvArgs awa) {
     constexpr int BM = 256, BN = 256, BK = 64;
     constexpr int TB = BM * BK * 2;   // 32 KB per operand per stage
     constexpr int SB = 2 * TB;        // 64 KB per stage
@@ -277,6 +316,11 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     constexpr int GROUP = 4;   // row-tiles per raster group (4 measured 1-3% faster than 8 or 16)
     __shared__ __attribute__((aligned(1024))) uint8_t lds[LDS_BYTES];
     __shared__ int arrival;
+    __shared__ QkvRow qrows[AWA ? BM : 1];
+    // fused QKV: byte offsets of the gathered A rows of every lane of the
+    // four A-loading waves, eight per lane (read back at each DMA issue:
+    // the main loop has no registers to spare for them)
+    __shared__ uint4 goff_lds[AWA ? 4 * 64 * 2 : 1];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -312,6 +356,14 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         return nullptr;
     };
 
+    // Fused QKV projection: the current tile's rows of the plan's row table
+    // (one row per thread of the first four waves).
+    auto build_rows = [&]() {
+        if constexpr (AWA != 0) {
+            if (tid < BM) qrows[tid] = awa.row_table[row0 + tid];
+        }
+    };
+
     f32x16 acc[4][2];
 
     // acc = sum over 64-k iterations [kb, ke) of the current tile.
@@ -335,11 +387,15 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     auto mainloop = [&](int kb, int ke) {
         const int grp = wave >> 2;
         const int wq = wave & 3;
-        const i32x4 rav = wave_uniform(
-            buffer_rsrc(x0 + (long)row0 * k, (uint32_t)(max(min(m0 - row0, BM), 0) * k * 2)));
-        const i32x4 rat = wave_uniform(
-            buffer_rsrc(x1 + (long)(row0 - mv) * k,
-                        (uint32_t)(row0 + BM > mv ? min(mv + m1 - row0, BM) * k * 2 : 0)));
+        // plain: the tile's rows of each stream; fused QKV: whole streams,
+        // each DMA lane addressing its gathered row
+        const i32x4 rav = AWA ? wave_uniform(buffer_rsrc(x0, (uint32_t)((long)m0 * k * 2)))
+                              : wave_uniform(buffer_rsrc(
+                                    x0 + (long)row0 * k, (uint32_t)(max(min(m0 - row0, BM), 0) * k * 2)));
+        const i32x4 rat =
+            AWA ? wave_uniform(buffer_rsrc(x1, (uint32_t)((long)m1 * k * 2)))
+                : wave_uniform(buffer_rsrc(x1 + (long)(row0 - mv) * k,
+                                           (uint32_t)(row0 + BM > mv ? min(mv + m1 - row0, BM) * k * 2 : 0)));
         const int wrow = __builtin_amdgcn_readfirstlane(row0 + wq * 64);
         const i32x4 rb =
             wave_uniform(buffer_rsrc(wgt + (long)col0 * k, (uint32_t)(min(n - col0, BN) * k * 2)));
@@ -351,12 +407,39 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         const uint32_t vrow = (uint32_t)(row_a * k * 2);
         const uint32_t voff_even = vrow + (((lane & 7) ^ lds_swizzle(row_a)) * 16);
         const uint32_t voff_odd = vrow + (((lane & 7) ^ lds_swizzle(row_a) ^ 4) * 16);
+        // fused QKV: byte offsets of this lane's eight gathered A rows (a gap
+        // or padding row points one row past its stream: the DMA reads zeros)
+        if constexpr (AWA != 0) {
+            if (grp == 0) {
+                uint32_t go[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int src = qrows[row_a + 8 * j].src;
+                    const int rr = src >= 0 ? src : (wrow + j * 8 < mv ? m0 : m1);
+                    go[j] = (uint32_t)rr * (uint32_t)(k * 2) +
+                            (uint32_t)((((lane & 7) ^ lds_swizzle(row_a) ^ ((j & 1) << 2))) * 16);
+                }
+                goff_lds[(wq * 64 + lane) * 2] = make_uint4(go[0], go[1], go[2], go[3]);
+                goff_lds[(wq * 64 + lane) * 2 + 1] = make_uint4(go[4], go[5], go[6], go[7]);
+            }
+        }
         auto issue = [&](int stage, int kt, int operand) {
             const uint32_t soff = __builtin_amdgcn_readfirstlane((uint32_t)(kt * BK * 2));
             const uint32_t st = lds_base + stage * SB + operand * TB + wq * 8 * 1024;
+            uint32_t go[8];
+            if constexpr (AWA != 0) {
+                if (!operand) {
+                    const uint4 g0 = goff_lds[(wq * 64 + lane) * 2];
+                    const uint4 g1 = goff_lds[(wq * 64 + lane) * 2 + 1];
+                    go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w;
+                    go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
-                const uint32_t vo = ((j & 1) ? voff_odd : voff_even) + (uint32_t)(j * 8 * k * 2);
+                uint32_t vo = ((j & 1) ? voff_odd : voff_even) + (uint32_t)(j * 8 * k * 2);
+                if constexpr (AWA != 0)
+                    if (!operand) vo = go[j];
                 lds_dma16(operand ? rb : (wrow + j * 8 < mv ? rav : rat),
                           __builtin_amdgcn_readfirstlane(st + j * 1024), vo, soff);
             }
@@ -422,8 +505,190 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         if (grp == 0) barrier();
     };
 
+    // Fused QKV epilogue.  The tile's 256 columns lie in one of q, k, v
+    // (inner is a multiple of 256) and cover 256 / D heads from hbase.  The
+    // tile is first rounded to bf16 (acc + bias, nearest even: the values a
+    // bf16 QKV blob would hold) and staged in LDS, so that every value the
+    // attention then reads is bit-identical to what the separate projection
+    // and the attention prologue (awa_prologue_kernel) produce.
+    //   q, k: row-major staging; D/8 threads per (row, head) hold 8
+    //     channels each, reduce the sum of squares with DPP lane moves, apply
+    //     rms_norm (:510-519) with the video or text weights, then
+    //     apply_mm_rope (:521-543) at the row's position, in the prologue's
+    //     fp32 operation order, and store 16 bytes of the head's row.
+    //   v: transposed staging (channel rows of the 256 tile rows); every
+    //     thread then stores 4-byte key pairs of V^T.  Window runs and the
+    //     text rows start at even rows of the row space and segments at
+    //     even workspace rows, so each pair of tile rows is one aligned pair
+    //     of workspace keys.
+    auto awa_epilogue = [&]() {
+        if constexpr (AWA != 0) {
+#pragma clang fp contract(off)
+            constexpr int D = AWA;
+            constexpr int SP = BN * 2 + 16;   // bytes per staged row
+            // an opaque copy of the thread index: nothing the epilogue derives
+            // from it is hoisted above the main loop, where every register is
+            // taken
+            int etid = tid;
+            asm volatile("" : "+v"(etid));
+            const int part = col0 / awa.inner;   // 0 q, 1 k, 2 v
+            const int hbase = (col0 - part * awa.inner) / D;
+            __syncthreads();   // every wave is done reading the last stage
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int cl = wn * 64 + 32 * j + l32;
+                const float bv = bias ? bias[col0 + cl] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; ++q4) {
+                        // registers 4 q4 .. 4 q4 + 3: rows rl .. rl + 3 of column cl
+                        const int rl = wm * 128 + 32 * i + 8 * q4 + 4 * g;
+                        uint16_t hv[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            hv[e] = __builtin_bit_cast(uint16_t, (__bf16)(acc[i][j][4 * q4 + e] + bv));
+                        if (part < 2) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) *(uint16_t*)(lds + (rl + e) * SP + cl * 2) = hv[e];
+                        } else {
+                            *(uint2*)(lds + cl * SP + rl * 2) =
+                                make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+                        }
+                    }
+            }
+            __syncthreads();
+            if (part < 2) {
+                constexpr int TPR = D / 8;        // threads per (row, head)
+                uint16_t* dst = part == 0 ? awa.q : awa.k;
+                const int ch = etid & 31;          // 8-channel chunk of the 256 columns
+                const int hl = ch * 8 / D;
+                const int d0 = ch * 8 - hl * D;
+                float wv[8], wt[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    wv[i] = awa.norm[part * D + d0 + i];
+                    wt[i] = awa.norm[(2 + part) * D + d0 + i];
+                }
+                // RoPE slots of this thread's four channel pairs: pair
+                // (2p, 2p+1) of axis a lies in [a*2P, (a+1)*2P); 6P <= D.
+                // A row's position on axis a is bits [sh, sh+16) of one of
+                // its two position words.
+                const int P = awa.pairs;
+                int pair[4], sh[4], rmask[4];
+                bool rot[4], word2[4];
+#pragma unroll
+                for (int pp = 0; pp < 4; ++pp) {
+                    const int d = d0 + 2 * pp;
+                    rot[pp] = d < 6 * P;
+                    const int axis = rot[pp] ? d / (2 * P) : 0;
+                    pair[pp] = rot[pp] ? (d - axis * 2 * P) >> 1 : 0;
+                    word2[pp] = axis == 2;
+                    sh[pp] = axis == 1 ? 16 : 0;
+                    rmask[pp] = rot[pp] ? -1 : 0;
+                }
+                // (cos, sin) of the four pairs at a row's position, without
+                // branches (so that the wait for these loads is exact): rows
+                // and pairs without rotation read entry 0 of the table, which
+                // is always inside the workspace, and do not use it.  The
+                // loads of pass p + 1 are issued before pass p computes.
+                auto rope_load = [&](const QkvRow& ri, float2 (&cs)[4]) {
+                    const int live = (ri.pos2 >> 16) != 0 ? -1 : 0;
+#pragma unroll
+                    for (int pp = 0; pp < 4; ++pp) {
+                        const int wv2 = word2[pp] ? ri.pos2 : ri.pos01;
+                        const int pos = (wv2 >> sh[pp]) & 0xffff;
+                        const int idx = (pos * P + pair[pp]) & rmask[pp] & live;
+                        cs[pp] = awa.rope[idx];
+                    }
+                };
+                // The results of all passes stay in registers (the
+                // accumulators are dead by now) and are stored after the
+                // loop, so the loop holds loads only and each pass waits for
+                // its own loads, not for earlier stores.
+                constexpr int PASSES = BM / 16;
+                QkvRow ri_next = qrows[etid >> 5];
+                float2 cs_next[4];
+                rope_load(ri_next, cs_next);
+                uint4 res[PASSES];
+#pragma unroll
+                for (int pass = 0; pass < PASSES; ++pass) {
+                    const int rl = pass * 16 + (etid >> 5);
+                    const QkvRow ri = ri_next;
+                    float2 cs[4];
+#pragma unroll
+                    for (int pp = 0; pp < 4; ++pp) cs[pp] = cs_next[pp];
+                    if (pass + 1 < PASSES) {
+                        ri_next = qrows[rl + 16];
+                        rope_load(ri_next, cs_next);
+                    }
+                    const int kind = ri.pos2 >> 16;
+                    const uint4 raw = *(const uint4*)(lds + rl * SP + ch * 16);
+                    const uint32_t wd[4] = {raw.x, raw.y, raw.z, raw.w};
+                    float x[8];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        x[2 * i] = __uint_as_float(wd[i] << 16);
+                        x[2 * i + 1] = __uint_as_float(wd[i] & 0xffff0000u);
+                    }
+                    float ss = 0.f;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+                    ss = row_sum<TPR>(ss);
+                    const float inv = __builtin_amdgcn_rsqf(ss / (float)D + awa.eps);
+                    const bool video = kind == 1;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) x[i] = x[i] * inv * (video ? wv[i] : wt[i]);
+#pragma unroll
+                    for (int pp = 0; pp < 4; ++pp) {
+                        if (rot[pp]) {
+                            const float a0 = x[2 * pp], a1 = x[2 * pp + 1];
+                            x[2 * pp] = a0 * cs[pp].x - a1 * cs[pp].y;
+                            x[2 * pp + 1] = a0 * cs[pp].y + a1 * cs[pp].x;
+                        }
+                    }
+                    uint16_t hb[8];
+                    if (awa.official_bf16) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) hb[i] = round_bf16_ref_bits(x[i]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) hb[i] = __builtin_bit_cast(uint16_t, (__bf16)x[i]);
+                    }
+                    res[pass] = pack8_bf16(hb);
+                }
+#pragma unroll
+                for (int pass = 0; pass < PASSES; ++pass) {
+                    const QkvRow ri = qrows[pass * 16 + (etid >> 5)];
+                    if (ri.pos2 >> 16)
+                        __builtin_nontemporal_store(
+                            __builtin_bit_cast(u32x4, res[pass]),
+                            (u32x4*)(dst + ((long)(hbase + hl) * awa.seg_total + ri.dest) * D + d0));
+                }
+            } else {
+                // thread t stores key pair t % 128 (tile rows 2q, 2q + 1) of
+                // channels t / 128 + 4c
+                const int qp = etid & 127;
+                const QkvRow ri = qrows[2 * qp];
+                if (ri.pos2 >> 16) {
+                    uint16_t* base = awa.vt + (long)hbase * D * awa.seg_total + ri.dest;
+#pragma unroll 8
+                    for (int c = 0; c < 64; ++c) {
+                        const int cl = (etid >> 7) + 4 * c;
+                        const uint32_t v = *(const uint32_t*)(lds + cl * SP + qp * 4);
+                        __builtin_nontemporal_store(v, (uint32_t*)(base + (long)cl * awa.seg_total));
+                    }
+                }
+            }
+        }
+    };
+
     // y tile = act(acc + bias)
     auto epilogue = [&]() {
+        if constexpr (AWA != 0) {
+            awa_epilogue();
+            return;
+        }
         if (YK && (n & 7) == 0) {
             __syncthreads();   // every wave is done reading the last stage
 #pragma unroll
@@ -551,6 +816,10 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             set_tile(xcd_remap(blockIdx.x, sk.dp_tiles));
         }
         if (!first) __syncthreads();   // the previous segment's LDS is no longer read
+        if constexpr (AWA != 0) {
+            build_rows();
+            __syncthreads();
+        }
         mainloop(kb, ke);
         bool finish = kb == 0 && ke == nk;
         if (!finish) {
@@ -736,6 +1005,50 @@ __global__ void zero_counters_kernel(int* counters, int n) {
 // that uses them, since a call keeps whatever the last one left).
 enum class SkSource { kStream, kStatic };
 
+// Split-k tail of a launch of `tiles` 256x256 tiles with nk 64-k steps:
+// when the last wave of tiles would leave more than 3% of the workgroup
+// slots idle, each tile of that wave is split along k into P equal parts on
+// P workgroups (P <= 4, at least 8 k-iterations a part): the wave then takes
+// about 1/P of a tile's time plus the reduction of P partial tiles.
+static hipError_t plan_sk_tail(long tiles, int nk, SkSource source, hipStream_t stream, SkTail* out) {
+    int G = 0;
+    hipError_t e = device_cus(&G);
+    if (e != hipSuccess) return e;
+    SkTail sk{(int)tiles, 0, 0, nullptr, nullptr};
+    const long waves = (tiles + G - 1) / G;
+    const long rem = tiles % G == 0 ? G : tiles % G;
+    if ((double)tiles / (double)(waves * G) < 0.97) {
+        const long parts = std::min<long>(4, std::min<long>(G / rem, nk / 8));
+        if (parts >= 2) {
+            sk.dp_tiles = (int)(tiles - rem);
+            sk.sk_tiles = (int)rem;
+            sk.sk_groups = (int)(rem * parts);
+        }
+    }
+    if (sk.sk_groups > 0) {
+        void* base = nullptr;
+        if (source == SkSource::kStatic) {
+            // (hipErrorNotSupported: the caller reports a size beyond the
+            // static scratch)
+            if (sk.sk_groups > kNoallocGroups) return hipErrorNotSupported;
+            e = noalloc_scratch(&base);
+            if (e != hipSuccess) return e;
+            sk.slots = (float*)base;
+            sk.counters = (int*)((char*)base + (size_t)kNoallocGroups * kSlotFloats * 4);
+            zero_counters_kernel<<<1, 256, 0, stream>>>(sk.counters, sk.sk_tiles);
+            e = hipGetLastError();
+            if (e != hipSuccess) return e;
+        } else {
+            e = stream_scratch(kScratchSplitK, stream, sk_scratch_bytes(G), &base);
+            if (e != hipSuccess) return e;
+            sk.slots = (float*)base;
+            sk.counters = (int*)((char*)base + (size_t)G * kSlotFloats * 4);
+        }
+    }
+    *out = sk;
+    return hipSuccess;
+}
+
 template <typename TX, int YK, int ACT>
 static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, const uint16_t* w,
                               const float* bias, int n, int k, void* y0, void* y1,
@@ -749,50 +1062,13 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
         const int mtiles = (mv + m1 + 255) / 256;
         const long tiles = (long)mtiles * ntiles;
         if (tiles == 0) return hipSuccess;
-        int G = 0;
-        hipError_t e = device_cus(&G);
+        SkTail sk;
+        hipError_t e = plan_sk_tail(tiles, k / 64, source, stream, &sk);
         if (e != hipSuccess) return e;
-        const int nk = k / 64;
-        SkTail sk{(int)tiles, 0, 0, nullptr, nullptr};
-        // When the last wave of tiles would leave more than 3% of the
-        // workgroup slots idle, each tile of that wave is split along k into
-        // P equal parts on P workgroups (P <= 4, at least 8 k-iterations a
-        // part): the wave then takes about 1/P of a tile's time plus the
-        // reduction of P partial tiles.
-        const long waves = (tiles + G - 1) / G;
-        const long rem = tiles % G == 0 ? G : tiles % G;
-        if ((double)tiles / (double)(waves * G) < 0.97) {
-            const long parts = std::min<long>(4, std::min<long>(G / rem, nk / 8));
-            if (parts >= 2) {
-                sk.dp_tiles = (int)(tiles - rem);
-                sk.sk_tiles = (int)rem;
-                sk.sk_groups = (int)(rem * parts);
-            }
-        }
-        if (sk.sk_groups > 0) {
-            void* base = nullptr;
-            if (source == SkSource::kStatic) {
-                // (hipErrorNotSupported: the caller reports a size beyond the
-                // static scratch)
-                if (sk.sk_groups > kNoallocGroups) return hipErrorNotSupported;
-                e = noalloc_scratch(&base);
-                if (e != hipSuccess) return e;
-                sk.slots = (float*)base;
-                sk.counters = (int*)((char*)base + (size_t)kNoallocGroups * kSlotFloats * 4);
-                zero_counters_kernel<<<1, 256, 0, stream>>>(sk.counters, sk.sk_tiles);
-                e = hipGetLastError();
-                if (e != hipSuccess) return e;
-            } else {
-                e = stream_scratch(kScratchSplitK, stream, sk_scratch_bytes(G), &base);
-                if (e != hipSuccess) return e;
-                sk.slots = (float*)base;
-                sk.counters = (int*)((char*)base + (size_t)G * kSlotFloats * 4);
-            }
-        }
         const long blocks = (long)sk.dp_tiles + sk.sk_groups;
         shared_linear_256_kernel<YK, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
             (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mv, mtiles,
-            ntiles, sk);
+            ntiles, sk, AwaQkvArgs{});
         return hipGetLastError();
     }
     const int mt0 = (m0 + 127) / 128;
@@ -850,6 +1126,49 @@ hipError_t launch_shared_linear_noalloc(const void* x0, int m0, const void* x1, 
                                         hipStream_t stream) {
     return linear_dispatch(x0, m0, x1, m1, x_kind, w, bias, n, k, act, y0, y1, y_kind, stream,
                            SkSource::kStatic);
+}
+
+hipError_t launch_awa_qkv(const s2_awa_plan& plan, const uint16_t* x_video, const uint16_t* x_text,
+                          int k, const uint16_t* w, const float* bias, const float* norm,
+                          const float2* rope, uint16_t* q, uint16_t* kk, uint16_t* vt,
+                          hipStream_t stream) {
+    const int d = plan.config.head_dim;
+    const int inner = plan.config.heads * d;
+    if ((d != 64 && d != 128) || inner % 256 != 0 || k % 64 != 0 ||
+        (long)(plan.video_tokens + 1) * k * 2 > 0x7fffffffL ||
+        (long)(plan.text_tokens + 1) * k * 2 > 0x7fffffffL)
+        return hipErrorInvalidValue;
+    const int n = 3 * inner;
+    const int ntiles = n / 256;
+    const int mtiles = (plan.qkv_rows + 255) / 256;
+    const long tiles = (long)mtiles * ntiles;
+    if (tiles == 0) return hipSuccess;
+    SkTail sk;
+    hipError_t e = plan_sk_tail(tiles, k / 64, SkSource::kStream, stream, &sk);
+    if (e != hipSuccess) return e;
+    AwaQkvArgs a;
+    a.row_table = plan.d_qkv_rows;
+    a.inner = inner;
+    a.seg_total = plan.seg_total;
+    a.seg_text = plan.seg_text;
+    a.norm = norm;
+    a.rope = rope;
+    a.pairs = plan.config.rope_pairs_per_axis;
+    a.eps = plan.config.epsilon;
+    a.official_bf16 = plan.config.official_bf16_attention;
+    a.q = q;
+    a.k = kk;
+    a.vt = vt;
+    const long blocks = (long)sk.dp_tiles + sk.sk_groups;
+    if (d == 128)
+        shared_linear_256_kernel<1, S2_ACT_NONE, 128><<<(unsigned)blocks, 512, 0, stream>>>(
+            x_video, plan.video_tokens, x_text, plan.text_tokens, w, bias, n, k, nullptr, nullptr,
+            plan.qkv_text_row, mtiles, ntiles, sk, a);
+    else
+        shared_linear_256_kernel<1, S2_ACT_NONE, 64><<<(unsigned)blocks, 512, 0, stream>>>(
+            x_video, plan.video_tokens, x_text, plan.text_tokens, w, bias, n, k, nullptr, nullptr,
+            plan.qkv_text_row, mtiles, ntiles, sk, a);
+    return hipGetLastError();
 }
 
 }  // namespace s2
