@@ -200,6 +200,12 @@ S2_API int s2_awa_stage_times(float stage_ms[4]);
 S2_API int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream_t stream);
 S2_API int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream_t stream);
 
+/* Elementwise erf-GELU, y = x * Phi(x), over count values of dtype (fp32
+ * arithmetic; y may equal x).  The device path of the ncnn GELU layer
+ * (param 0 fast_gelu = 0) when a block graph keeps its MLP activation as a
+ * layer of its own instead of SharedLinear's fused epilogue (param 3). */
+S2_API int s2_gelu(const void* x, void* y, size_t count, s2_dtype dtype, s2_stream_t stream);
+
 /* SharedLinear::forward (shared_linear.cpp:83-96): one projection applied to
  * two token streams in ONE grouped launch sharing the weight:
  *   y_video = act(x_video W^T + b),  y_text = act(x_text W^T + b).

@@ -4,9 +4,10 @@
   seedvr2_ncnn_amd/lib/libseedvr2_layers.so  ncnn-surface layers (AdaptiveWindowAttention,
                                              SharedLinear, DecomposedConv3D,
                                              VAEChunkedMHA, VAEDownsample3D,
-                                             VAEUpsample3D) over the
-                                             C-ABI, with the ncnn-compatible Mat/Layer
-                                             subset
+                                             VAEUpsample3D, the DiT block's norm /
+                                             modulation layers) over the C-ABI, the
+                                             ncnn-compatible Mat/Layer/Net subset and
+                                             the DiT block-graph runner
 
 Every HIP file is compiled for gfx950 only, with packed-fp32 instruction
 selection disabled.  Usage: python -m seedvr2_ncnn_amd.build [--force]
@@ -38,10 +39,11 @@ CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I" + INCLUDE,
 HIP_SOURCES = ["awa_kernels.hip", "linear_kernels.hip", "pipeline_kernels.hip", "block_kernels.hip",
                "conv3d_kernels.hip", "mha_kernels.hip", "capi.hip", "awa_plan.cpp",
                "stream_scratch.cpp"]
-LAYER_SOURCES = ["ncnn/mat.cpp", "ncnn/layer.cpp", "layers/hip_allocator.cpp",
+LAYER_SOURCES = ["ncnn/mat.cpp", "ncnn/layer.cpp", "ncnn/net.cpp", "layers/hip_allocator.cpp",
                  "layers/adaptive_window_attention.cpp", "layers/shared_linear.cpp",
                  "layers/decomposed_conv3d.cpp", "layers/vae_chunked_mha.cpp",
-                 "layers/vae_resample3d.cpp"]
+                 "layers/vae_resample3d.cpp", "layers/dit_block_ops.cpp",
+                 "layers/dit_block_graph.cpp"]
 
 HIP_LIB = os.path.join(LIB, "libseedvr2_hip.so")
 LAYER_LIB = os.path.join(LIB, "libseedvr2_layers.so")

@@ -39,7 +39,7 @@ EXPORTS = (
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
     "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded", "s2_shared_linear_forward_noalloc",
-    "s2_awa_qkv_forward",
+    "s2_awa_qkv_forward", "s2_gelu",
 )
 
 
@@ -130,6 +130,7 @@ def lib() -> ctypes.CDLL:
                                      vp, sz, vp]
         L.s2_awa_qkv_forward.argtypes = [vp, vp, vp, ci, vp, vp, vp, vp, vp, vp, ci, vp, sz, vp]
         L.s2_cast_f32_to_bf16.argtypes = [vp, vp, sz, vp]
+        L.s2_gelu.argtypes = [vp, vp, sz, ci, vp]
         L.s2_cast_bf16_to_f32.argtypes = [vp, vp, sz, vp]
         L.s2_shared_linear_forward.argtypes = [vp, ci, vp, ci, ci, vp, vp, ci, ci, ci, vp, vp, ci, vp]
         L.s2_shared_linear_forward_noalloc.argtypes = L.s2_shared_linear_forward.argtypes
@@ -384,6 +385,16 @@ def cast_f32_to_bf16(src, dst=None, stream=None):
     check(lib().s2_cast_f32_to_bf16(_ptr(src), _ptr(dst), src.numel(), _stream(stream)),
           "s2_cast_f32_to_bf16")
     return dst
+
+
+def gelu(x, y=None, stream=None):
+    """s2_gelu: elementwise erf-GELU of a device tensor (fp32, bf16 or fp16)."""
+    import torch
+    if y is None:
+        y = torch.empty_like(x)
+    assert x.is_contiguous() and y.is_contiguous() and y.dtype == x.dtype
+    check(lib().s2_gelu(_ptr(x), _ptr(y), x.numel(), _dtype_code(x), _stream(stream)), "s2_gelu")
+    return y
 
 
 def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, out_dtype=None,

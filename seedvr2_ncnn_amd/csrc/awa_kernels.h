@@ -36,6 +36,7 @@ hipError_t launch_awa_text_broadcast(const s2_awa_plan& plan, uint16_t* q, uint1
                                      uint16_t* vt, hipStream_t stream);
 
 hipError_t launch_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream);
+hipError_t launch_gelu(const void* x, void* y, size_t n, int kind, hipStream_t stream);
 hipError_t launch_cast_bf16_f32(const uint16_t* src, float* dst, size_t n, hipStream_t stream);
 // Grouped y_s = act(x_s W^T + b) over the video and text streams.
 hipError_t launch_shared_linear(const void* x0, int m0, const void* x1, int m1, int x_kind,

@@ -638,6 +638,13 @@ int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream
     return S2_OK;
 }
 
+int s2_gelu(const void* x, void* y, size_t count, s2_dtype dtype, s2_stream_t stream) {
+    if (count && (!x || !y)) return fail(S2_ERR_INVALID, "null argument");
+    if (!dtype_ok(dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    S2_HIP(s2::launch_gelu(x, y, count, (int)dtype, (hipStream_t)stream));
+    return S2_OK;
+}
+
 int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream_t stream) {
     if (count && (!src || !dst)) return S2_ERR_INVALID;
     S2_HIP(s2::launch_cast_bf16_f32(src, dst, count, (hipStream_t)stream));

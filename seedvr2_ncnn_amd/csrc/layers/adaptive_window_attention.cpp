@@ -372,14 +372,17 @@ int AdaptiveWindowAttention::forward_impl(const std::vector<ncnn::Mat>& bottom_b
              text_qkv.w != inner_dim * 3)
         return -1;
 
-    // Runtime shapes: from the shape blobs (reference :799-817), or from the
-    // runtime state when no shape blob is given (the reference device path,
-    // :1090-1100).
+    // Runtime shapes: from host shape blobs (reference :799-817), or from
+    // the runtime state when no shape blob is given or they are device
+    // blobs, which the host cannot read (the reference device path,
+    // :1065-1067, 1090-1100).
     std::vector<int> shapes;
     std::vector<int> text_lengths;
     int expected_video_tokens = 0;
     int expected_text_tokens = 0;
-    if (!video_shape_blob.empty() || !text_length_blob.empty())
+    const bool host_shape_blobs = !device_allocator_of(video_shape_blob) &&
+                                  !device_allocator_of(text_length_blob);
+    if ((!video_shape_blob.empty() || !text_length_blob.empty()) && host_shape_blobs)
     {
         if (video_shape_blob.w != 3)
             return -1;

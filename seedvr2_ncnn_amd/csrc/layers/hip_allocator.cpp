@@ -16,19 +16,49 @@ void HipDeviceAllocator::fastFree(void* ptr) {
     std::lock_guard<std::mutex> lock(mutex_);
     std::vector<void*>::iterator it = std::find(owned_.begin(), owned_.end(), ptr);
     if (it != owned_.end()) {
+        for (size_t i = 0; i < pool_.size(); i++)
+            if (pool_[i].second == ptr) {
+                pool_.erase(pool_.begin() + i);
+                break;
+            }
         s2_free(ptr);
+        owned_bytes_.erase(owned_bytes_.begin() + (it - owned_.begin()));
         owned_.erase(it);
     }
 }
 
-ncnn::Mat HipDeviceAllocator::create_blob(int w, int h, size_t elemsize) {
-    if (w <= 0 || h <= 0 || (elemsize != 2 && elemsize != 4)) return ncnn::Mat();
-    void* p = 0;
-    if (s2_malloc(&p, (size_t)w * h * elemsize) != S2_OK || !p) return ncnn::Mat();
+// A pooled block of exactly `bytes`, or a new allocation.
+void* HipDeviceAllocator::alloc_bytes(size_t bytes) {
     {
         std::lock_guard<std::mutex> lock(mutex_);
-        owned_.push_back(p);
+        for (size_t i = 0; i < pool_.size(); i++)
+            if (pool_[i].first == bytes) {
+                void* p = pool_[i].second;
+                pool_.erase(pool_.begin() + i);
+                return p;
+            }
     }
+    void* p = 0;
+    if (s2_malloc(&p, bytes) != S2_OK || !p) return 0;
+    std::lock_guard<std::mutex> lock(mutex_);
+    owned_.push_back(p);
+    owned_bytes_.push_back(bytes);
+    return p;
+}
+
+void HipDeviceAllocator::release_blob(void* ptr) {
+    std::lock_guard<std::mutex> lock(mutex_);
+    std::vector<void*>::iterator it = std::find(owned_.begin(), owned_.end(), ptr);
+    if (it == owned_.end()) return;
+    for (size_t i = 0; i < pool_.size(); i++)
+        if (pool_[i].second == ptr) return;
+    pool_.push_back(std::make_pair(owned_bytes_[it - owned_.begin()], ptr));
+}
+
+ncnn::Mat HipDeviceAllocator::create_blob(int w, int h, size_t elemsize) {
+    if (w <= 0 || h <= 0 || (elemsize != 2 && elemsize != 4)) return ncnn::Mat();
+    void* p = alloc_bytes((size_t)w * h * elemsize);
+    if (!p) return ncnn::Mat();
     return ncnn::Mat(w, h, p, elemsize, this);
 }
 
@@ -39,12 +69,8 @@ ncnn::Mat HipDeviceAllocator::wrap_blob(int w, int h, void* device_data, size_t 
 ncnn::Mat HipDeviceAllocator::create_blob(int w, int h, int d, int c, size_t elemsize) {
     if (w <= 0 || h <= 0 || d <= 0 || c <= 0 || (elemsize != 2 && elemsize != 4)) return ncnn::Mat();
     ncnn::Mat shape(w, h, d, c, (void*)0, elemsize, this);
-    void* p = 0;
-    if (s2_malloc(&p, shape.cstep * c * elemsize) != S2_OK || !p) return ncnn::Mat();
-    {
-        std::lock_guard<std::mutex> lock(mutex_);
-        owned_.push_back(p);
-    }
+    void* p = alloc_bytes(shape.cstep * c * elemsize);
+    if (!p) return ncnn::Mat();
     return ncnn::Mat(w, h, d, c, p, elemsize, this);
 }
 
@@ -58,6 +84,8 @@ void HipDeviceAllocator::clear() {
     if (!owned_.empty()) s2_stream_synchronize(stream_);
     for (size_t i = 0; i < owned_.size(); i++) s2_free(owned_[i]);
     owned_.clear();
+    owned_bytes_.clear();
+    pool_.clear();
 }
 
 HipDeviceAllocator* device_allocator_of(const ncnn::Mat& m) {

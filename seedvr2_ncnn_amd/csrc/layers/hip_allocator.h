@@ -42,15 +42,25 @@ public:
     // Wraps caller-owned device memory as a device blob (not owned).
     ncnn::Mat wrap_blob(int w, int h, void* device_data, size_t elemsize);
     ncnn::Mat wrap_blob(int w, int h, int d, int c, void* device_data, size_t elemsize);
-    // Frees every blob this allocator created.
+    // Returns a blob this allocator created to its pool of free blocks (a
+    // no-op for other pointers).  The next create_blob of the same byte size
+    // reuses the block without synchronising: safe when every kernel that
+    // touches this allocator's blobs runs on its stream, in order, as the
+    // graph executor's layers do.
+    void release_blob(void* ptr);
+    // Frees every blob this allocator created, pooled blocks included.
     void clear();
 
     void* stream() const { return stream_; }
 
 private:
+    void* alloc_bytes(size_t bytes);
+
     void* stream_;
     std::mutex mutex_;
     std::vector<void*> owned_;
+    std::vector<size_t> owned_bytes_;
+    std::vector<std::pair<size_t, void*> > pool_;   // (bytes, block) free for reuse
 };
 
 // True when m is a device blob (its allocator is a HipDeviceAllocator).

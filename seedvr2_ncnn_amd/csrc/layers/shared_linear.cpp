@@ -63,6 +63,15 @@ int SharedLinear::load_model(const ncnn::ModelBin& mb)
     return 0;
 }
 
+int SharedLinear::set_activation(int act)
+{
+    if (act != S2_ACT_NONE && act != S2_ACT_GELU)
+        return -1;
+    std::lock_guard<std::mutex> lock(mutex);
+    activation = act;
+    return 0;
+}
+
 int SharedLinear::create_pipeline(const ncnn::Option& /*opt*/)
 {
     return layer_status(create_pipeline_impl());

@@ -36,6 +36,10 @@ public:
                         std::vector<ncnn::Mat>& top_blobs,
                         const ncnn::Option& opt) const;
 
+    // Epilogue activation (param 3: S2_ACT_NONE or S2_ACT_GELU), switched by
+    // a graph optimiser that folds a following GELU layer.  Returns 0 or -1.
+    int set_activation(int act);
+
 private:
     // forward and create_pipeline without the mapping of C-ABI codes to the
     // reference's (layer_status)

@@ -924,6 +924,36 @@ __global__ void cast_bf16_f32_kernel(const uint16_t* __restrict__ src, float* __
     if (i < n) dst[i] = bf16_to_f32(src[i]);
 }
 
+// Elementwise erf-GELU (the epilogue's gelu) over fp32, bf16 or fp16 values,
+// four per thread.
+template <typename T>
+__global__ void gelu_kernel(const T* x, T* y, size_t n) {
+    const size_t i0 = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const size_t i = i0 + j;
+        if (i >= n) return;
+        if constexpr (std::is_same<T, float>::value)
+            y[i] = gelu(x[i]);
+        else if constexpr (std::is_same<T, uint16_t>::value)
+            y[i] = __builtin_bit_cast(uint16_t, (__bf16)gelu(bf16_to_f32(x[i])));
+        else
+            y[i] = (_Float16)gelu((float)x[i]);
+    }
+}
+
+hipError_t launch_gelu(const void* x, void* y, size_t n, int kind, hipStream_t stream) {
+    if (n == 0) return hipSuccess;
+    const unsigned blocks = (unsigned)((n + 1023) / 1024);
+    if (kind == 1)
+        gelu_kernel<uint16_t><<<blocks, 256, 0, stream>>>((const uint16_t*)x, (uint16_t*)y, n);
+    else if (kind == 2)
+        gelu_kernel<_Float16><<<blocks, 256, 0, stream>>>((const _Float16*)x, (_Float16*)y, n);
+    else
+        gelu_kernel<float><<<blocks, 256, 0, stream>>>((const float*)x, (float*)y, n);
+    return hipGetLastError();
+}
+
 hipError_t launch_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream) {
     if (n == 0) return hipSuccess;
     cast_f32_bf16_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(src, dst, n);

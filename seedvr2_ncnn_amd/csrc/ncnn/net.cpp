@@ -1,0 +1,476 @@
+// ncnn-compatible subset: Net and Extractor (net.h).
+#include "net.h"
+
+#include <math.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <map>
+#include <sstream>
+
+#include "hip_allocator.h"
+#include "modelbin.h"
+#include "shared_linear.h"
+#include "paramdict.h"
+#include "seedvr2_hip.h"
+
+namespace ncnn {
+
+// ---- built-in layers -------------------------------------------------------
+
+namespace {
+
+// Input: declares a blob the caller provides (params 0/1/2 = w/h/c, unused).
+class InputLayer : public Layer {
+public:
+    InputLayer() {
+        one_blob_only = true;
+        support_inplace = true;
+    }
+    virtual int forward_inplace(Mat&, const Option&) const { return 0; }
+};
+
+// Split: every top is the bottom blob (a shared reference, no copy).
+class SplitLayer : public Layer {
+public:
+    SplitLayer() {
+        one_blob_only = false;
+        support_inplace = false;
+    }
+    virtual int forward(const std::vector<Mat>& bottom_blobs, std::vector<Mat>& top_blobs,
+                        const Option&) const {
+        for (size_t i = 0; i < top_blobs.size(); i++) top_blobs[i] = bottom_blobs[0];
+        return 0;
+    }
+};
+
+// GELU: y = x * Phi(x), erf form (param 0 fast_gelu must be 0).  Device
+// blobs run s2_gelu on the blob allocator's stream; host fp32 Mats run
+// on the CPU.
+class GeluLayer : public Layer {
+public:
+    GeluLayer() : fast_gelu(0), passthrough(false) {
+        one_blob_only = true;
+        support_inplace = false;
+    }
+    virtual int load_param(const ParamDict& pd) {
+        fast_gelu = pd.get(0, 0);
+        return fast_gelu == 0 ? 0 : -1;
+    }
+    virtual int forward(const Mat& bottom, Mat& top, const Option& opt) const {
+        if (passthrough) {
+            top = bottom;
+            return 0;
+        }
+        seedvr2::HipDeviceAllocator* dev = seedvr2::device_allocator_of(bottom);
+        if (dev) {
+            if (bottom.dims != 2 || bottom.elempack != 1) return -1;
+            seedvr2::HipDeviceAllocator* out = dynamic_cast<seedvr2::HipDeviceAllocator*>(opt.blob_allocator);
+            if (!out) out = dev;
+            top = out->create_blob(bottom.w, bottom.h, bottom.elemsize);
+            if (top.empty()) return -100;
+            const int ret = s2_gelu(bottom.data, top.data, (size_t)bottom.w * bottom.h,
+                                    seedvr2::device_blob_dtype(bottom.elemsize, opt), dev->stream());
+            return seedvr2::layer_status(ret);
+        }
+        if (bottom.elemsize != 4) return -1;
+        top.create_like(bottom, opt.blob_allocator);
+        if (top.empty()) return -100;
+        const size_t n = bottom.total();
+        const float* x = (const float*)bottom.data;
+        float* y = (float*)top.data;
+        for (size_t i = 0; i < n; i++) y[i] = 0.5f * x[i] * (1.f + erff(x[i] * 0.70710678118654752f));
+        return 0;
+    }
+    int fast_gelu;
+    bool passthrough;
+};
+
+}  // namespace
+
+// Device blob references held by an extractor's blob slots: a device block
+// goes back to its allocator's pool when the last slot naming it is
+// released (Split tops and Input aliases share one block).
+class DeviceRefs {
+public:
+    void add(const Mat& m) {
+        seedvr2::HipDeviceAllocator* a = seedvr2::device_allocator_of(m);
+        if (a && m.data) ++refs[m.data].count, refs[m.data].alloc = a;
+    }
+    void pin(const Mat& m) {
+        if (seedvr2::device_allocator_of(m) && m.data) refs[m.data].pinned = true;
+    }
+    void drop(const Mat& m) {
+        if (!seedvr2::device_allocator_of(m) || !m.data) return;
+        std::map<void*, Ref>::iterator it = refs.find(m.data);
+        if (it == refs.end()) return;
+        if (--it->second.count <= 0) {
+            if (!it->second.pinned) it->second.alloc->release_blob(it->first);
+            refs.erase(it);
+        }
+    }
+
+private:
+    struct Ref {
+        Ref() : count(0), pinned(false), alloc(0) {}
+        int count;
+        bool pinned;   // given by the caller or handed out by extract: never pooled
+        seedvr2::HipDeviceAllocator* alloc;
+    };
+    std::map<void*, Ref> refs;
+};
+
+// ---- Net -------------------------------------------------------------------
+
+Net::Net() {}
+
+Net::~Net() { clear(); }
+
+int Net::register_custom_layer(const char* type, layer_creator_func creator,
+                               layer_destroyer_func destroyer, void* userdata) {
+    for (size_t i = 0; i < custom_.size(); i++)
+        if (custom_[i].type == type) return -1;
+    CustomLayer c;
+    c.type = type;
+    c.creator = creator;
+    c.destroyer = destroyer;
+    c.userdata = userdata;
+    custom_.push_back(c);
+    return 0;
+}
+
+Layer* Net::create_layer(const std::string& type, int* custom_index) const {
+    *custom_index = -1;
+    for (size_t i = 0; i < custom_.size(); i++)
+        if (custom_[i].type == type) {
+            *custom_index = (int)i;
+            Layer* l = custom_[i].creator(custom_[i].userdata);
+            if (l) l->userdata = custom_[i].userdata;
+            return l;
+        }
+    if (type == "Input") return new InputLayer();
+    if (type == "Split") return new SplitLayer();
+    if (type == "GELU") return new GeluLayer();
+    return 0;
+}
+
+void Net::clear() {
+    for (size_t i = 0; i < layers_.size(); i++) {
+        layers_[i]->destroy_pipeline(opt);
+        const int ci = layer_custom_[i];
+        if (ci >= 0 && custom_[ci].destroyer)
+            custom_[ci].destroyer(layers_[i], custom_[ci].userdata);
+        else
+            delete layers_[i];
+    }
+    layers_.clear();
+    layer_custom_.clear();
+    consumer_count_.clear();
+    passthrough_.clear();
+    blobs_.clear();
+}
+
+int Net::find_blob_index_by_name(const char* name) const {
+    for (size_t i = 0; i < blobs_.size(); i++)
+        if (blobs_[i].name == name) return (int)i;
+    return -1;
+}
+
+int Net::load_param(const char* protopath) {
+    FILE* fp = fopen(protopath, "rb");
+    if (!fp) return -1;
+    std::string text;
+    char buf[65536];
+    size_t n;
+    while ((n = fread(buf, 1, sizeof(buf), fp)) > 0) text.append(buf, n);
+    fclose(fp);
+    return load_param_mem(text.c_str());
+}
+
+int Net::load_param_mem(const char* mem) {
+    clear();
+    std::istringstream in(mem ? mem : "");
+    std::string line;
+    if (!std::getline(in, line)) return -1;
+    if (atoi(line.c_str()) != 7767517) return -1;
+    int layer_count = 0, blob_count = 0;
+    if (!std::getline(in, line) || sscanf(line.c_str(), "%d %d", &layer_count, &blob_count) != 2 ||
+        layer_count <= 0 || blob_count <= 0)
+        return -1;
+    blobs_.reserve(blob_count);
+    while ((int)layers_.size() < layer_count && std::getline(in, line)) {
+        std::istringstream ls(line);
+        std::string type, name;
+        int nb = 0, nt = 0;
+        if (!(ls >> type)) continue;   // blank line
+        if (!(ls >> name >> nb >> nt) || nb < 0 || nt < 0) return -1;
+        int ci = -1;
+        Layer* layer = create_layer(type, &ci);
+        if (!layer) {
+            fprintf(stderr, "layer %s not exists or registered\n", type.c_str());
+            clear();
+            return -1;
+        }
+        layer->type = type;
+        layer->name = name;
+        const int li = (int)layers_.size();
+        layers_.push_back(layer);
+        layer_custom_.push_back(ci);
+        passthrough_.push_back(0);
+        for (int i = 0; i < nb; i++) {
+            std::string b;
+            if (!(ls >> b)) return -1;
+            const int bi = find_blob_index_by_name(b.c_str());
+            if (bi < 0) {
+                fprintf(stderr, "blob %s of layer %s has no producer\n", b.c_str(), name.c_str());
+                clear();
+                return -1;
+            }
+            blobs_[bi].consumer = li;
+            consumer_count_[bi]++;
+            layer->bottoms.push_back(bi);
+        }
+        for (int i = 0; i < nt; i++) {
+            std::string t;
+            if (!(ls >> t)) return -1;
+            if (find_blob_index_by_name(t.c_str()) >= 0 || (int)blobs_.size() >= blob_count) {
+                clear();
+                return -1;
+            }
+            Blob blob;
+            blob.name = t;
+            blob.producer = li;
+            blobs_.push_back(blob);
+            consumer_count_.push_back(0);
+            layer->tops.push_back((int)blobs_.size() - 1);
+        }
+        std::string rest;
+        std::getline(ls, rest);
+        ParamDict pd;
+        if (pd.load_param_text(rest.c_str()) != 0 || layer->load_param(pd) != 0) {
+            fprintf(stderr, "layer %s load_param failed\n", name.c_str());
+            clear();
+            return -1;
+        }
+    }
+    if ((int)layers_.size() != layer_count || (int)blobs_.size() != blob_count) {
+        clear();
+        return -1;
+    }
+    return 0;
+}
+
+int Net::load_model(const char* modelpath) {
+    FILE* fp = fopen(modelpath, "rb");
+    if (!fp) return -1;
+    std::vector<unsigned char> data;
+    unsigned char buf[1 << 16];
+    size_t n;
+    while ((n = fread(buf, 1, sizeof(buf), fp)) > 0) data.insert(data.end(), buf, buf + n);
+    fclose(fp);
+    return load_model(data.empty() ? 0 : &data[0], data.size());
+}
+
+int Net::load_model(const unsigned char* mem, size_t size) {
+    if (layers_.empty()) return -1;
+    ModelBinFromMemory mb(mem, size);
+    for (size_t i = 0; i < layers_.size(); i++) {
+        const int ret = layers_[i]->load_model(mb);
+        if (ret != 0) {
+            fprintf(stderr, "layer %s load_model failed (%d)\n", layers_[i]->name.c_str(), ret);
+            return ret;
+        }
+    }
+    if (mb.consumed() != size) return -1;
+    for (size_t i = 0; i < layers_.size(); i++) {
+        const int ret = layers_[i]->create_pipeline(opt);
+        if (ret != 0) return ret;
+    }
+    return 0;
+}
+
+int Net::fuse_shared_linear_gelu() {
+    int fused = 0;
+    for (size_t li = 0; li < layers_.size(); li++) {
+        Layer* l = layers_[li];
+        if (l->type != "SharedLinear" || l->tops.empty()) continue;
+        std::vector<int> gelus;
+        for (size_t t = 0; t < l->tops.size(); t++) {
+            const int bi = l->tops[t];
+            const int c = blobs_[bi].consumer;
+            if (consumer_count_[bi] != 1 || c < 0 || layers_[c]->type != "GELU") break;
+            gelus.push_back(c);
+        }
+        if (gelus.size() != l->tops.size()) continue;
+        seedvr2::SharedLinear* sl = dynamic_cast<seedvr2::SharedLinear*>(l);
+        if (!sl || sl->set_activation(S2_ACT_GELU) != 0) continue;
+        for (size_t g = 0; g < gelus.size(); g++) {
+            static_cast<GeluLayer*>(layers_[gelus[g]])->passthrough = true;
+            passthrough_[gelus[g]] = 1;
+        }
+        ++fused;
+    }
+    return fused;
+}
+
+Extractor Net::create_extractor() const { return Extractor(this, blobs_.size()); }
+
+// Runs layer `li` after every producer of its bottoms (depth-first with an
+// explicit stack), as ncnn's Extractor does.
+int Net::forward_layer(int li, std::vector<Mat>& blob_mats, std::vector<int>& pending,
+                       const Option& opt, DeviceRefs* refs) const {
+    std::vector<int> stack(1, li);
+    while (!stack.empty()) {
+        const int cur = stack.back();
+        const Layer* layer = layers_[cur];
+        bool ready = true;
+        for (size_t i = 0; i < layer->bottoms.size(); i++) {
+            const int bi = layer->bottoms[i];
+            if (blob_mats[bi].dims == 0) {
+                const int p = blobs_[bi].producer;
+                if (p < 0 || p == cur) return -1;
+                for (size_t s = 0; s < stack.size(); s++)
+                    if (stack[s] == p) return -1;   // a cycle: not a valid graph
+                if (layers_[p]->type == "Input") {
+                    fprintf(stderr, "blob %s has no input\n", blobs_[bi].name.c_str());
+                    return -1;
+                }
+                stack.push_back(p);
+                ready = false;
+                break;
+            }
+        }
+        if (!ready) continue;
+        stack.pop_back();
+        // already computed through another path
+        bool done = !layer->tops.empty();
+        for (size_t i = 0; i < layer->tops.size(); i++)
+            if (blob_mats[layer->tops[i]].dims == 0) done = false;
+        if (done) continue;
+
+        std::vector<Mat> bottoms(layer->bottoms.size());
+        for (size_t i = 0; i < layer->bottoms.size(); i++) bottoms[i] = blob_mats[layer->bottoms[i]];
+        std::vector<Mat> tops(layer->tops.size());
+        int ret = 0;
+        if (layer->one_blob_only) {
+            if (bottoms.size() != 1 || tops.size() != 1) return -1;
+            if (layer->support_inplace) {
+                tops[0] = bottoms[0];
+                ret = layer->forward_inplace(tops[0], opt);
+            } else {
+                ret = layer->forward(bottoms[0], tops[0], opt);
+            }
+        } else if (layer->support_inplace) {
+            tops = bottoms;
+            ret = layer->forward_inplace(tops, opt);
+        } else {
+            ret = layer->forward(bottoms, tops, opt);
+        }
+        if (ret != 0) {
+            fprintf(stderr, "layer %s forward failed (%d)\n", layer->name.c_str(), ret);
+            return ret;
+        }
+        for (size_t i = 0; i < tops.size(); i++) {
+            blob_mats[layer->tops[i]] = tops[i];
+            if (refs) refs->add(tops[i]);
+        }
+        // light mode: a bottom every consumer has taken is released; a device
+        // block no slot names any more returns to its allocator's pool
+        for (size_t i = 0; i < layer->bottoms.size(); i++) {
+            const int bi = layer->bottoms[i];
+            if (--pending[bi] == 0 && opt.lightmode) {
+                if (refs) refs->drop(blob_mats[bi]);
+                blob_mats[bi].release();
+            }
+        }
+    }
+    return 0;
+}
+
+// ---- Extractor ---------------------------------------------------------------
+
+Extractor::Extractor(const Net* net, size_t blob_count)
+    : net_(net), blob_mats_(blob_count), pending_(net->consumer_count_), opt_(net->opt),
+      refs_(new DeviceRefs()) {}
+
+Extractor::~Extractor() {
+    clear();
+    delete refs_;
+}
+
+Extractor::Extractor(const Extractor& rhs)
+    : net_(rhs.net_), blob_mats_(rhs.blob_mats_), pending_(rhs.pending_), opt_(rhs.opt_),
+      refs_(new DeviceRefs()) {
+    // a copy starts without pooling: its blobs stay referenced by rhs
+    for (size_t i = 0; i < blob_mats_.size(); i++) refs_->pin(blob_mats_[i]);
+}
+
+Extractor& Extractor::operator=(const Extractor& rhs) {
+    if (this == &rhs) return *this;
+    clear();
+    net_ = rhs.net_;
+    blob_mats_ = rhs.blob_mats_;
+    pending_ = rhs.pending_;
+    opt_ = rhs.opt_;
+    for (size_t i = 0; i < blob_mats_.size(); i++) refs_->pin(blob_mats_[i]);
+    return *this;
+}
+
+void Extractor::clear() {
+    for (size_t i = 0; i < blob_mats_.size(); i++) blob_mats_[i].release();
+    delete refs_;
+    refs_ = new DeviceRefs();
+    if (net_) pending_ = net_->consumer_count_;
+}
+
+void Extractor::set_light_mode(bool enable) { opt_.lightmode = enable; }
+void Extractor::set_num_threads(int num_threads) { opt_.num_threads = num_threads; }
+void Extractor::set_blob_allocator(Allocator* allocator) { opt_.blob_allocator = allocator; }
+void Extractor::set_workspace_allocator(Allocator* allocator) { opt_.workspace_allocator = allocator; }
+
+int Extractor::input(const char* blob_name, const Mat& in) {
+    const int bi = net_->find_blob_index_by_name(blob_name);
+    if (bi < 0) return -1;
+    return input(bi, in);
+}
+
+int Extractor::input(int blob_index, const Mat& in) {
+    if (blob_index < 0 || blob_index >= (int)blob_mats_.size()) return -1;
+    seedvr2::HipDeviceAllocator* dev =
+        dynamic_cast<seedvr2::HipDeviceAllocator*>(opt_.blob_allocator);
+    Mat m = in;
+    if (dev && !seedvr2::device_allocator_of(in) && in.dims == 2 && !in.empty() &&
+        (in.elemsize == 4 || in.elemsize == 2)) {
+        // host blob into a device graph: one upload on the allocator's stream
+        m = dev->create_blob(in.w, in.h, in.elemsize);
+        if (m.empty()) return -100;
+        if (s2_memcpy_h2d(m.data, in.data, (size_t)in.w * in.h * in.elemsize, dev->stream()) != S2_OK)
+            return -100;
+    }
+    blob_mats_[blob_index] = m;
+    refs_->add(m);
+    refs_->pin(m);
+    return 0;
+}
+
+int Extractor::extract(const char* blob_name, Mat& feat, int type) {
+    const int bi = net_->find_blob_index_by_name(blob_name);
+    if (bi < 0) return -1;
+    return extract(bi, feat, type);
+}
+
+int Extractor::extract(int blob_index, Mat& feat, int /*type*/) {
+    if (blob_index < 0 || blob_index >= (int)blob_mats_.size()) return -1;
+    if (blob_mats_[blob_index].dims == 0) {
+        const int p = net_->blobs_[blob_index].producer;
+        if (p < 0) return -1;
+        const int ret = net_->forward_layer(p, blob_mats_, pending_, opt_, refs_);
+        if (ret != 0) return ret;
+    }
+    feat = blob_mats_[blob_index];
+    refs_->pin(feat);
+    return feat.dims == 0 ? -1 : 0;
+}
+
+}  // namespace ncnn

@@ -15,6 +15,7 @@
 
 #include "adaptive_window_attention.h"
 #include "decomposed_conv3d.h"
+#include "dit_block_graph.h"
 #include "hip_allocator.h"
 #include "seedvr2_hip.h"
 #include "shared_linear.h"
@@ -280,5 +281,84 @@ int h_build_plan(const int* shapes, int batch, const int* target, int shifted, i
     }
     return 0;
 }
+
+// ---- DiT block graph (seedvr2::DiTBlockGraph over ncnn::Net) -------------------
+
+// Loads a block graph from .param text and .bin bytes.  Returns load's code;
+// *out is the graph (destroy with h_graph_destroy) or null.
+int h_graph_create(const char* param_text, const void* model, long model_bytes, int fp32_blobs,
+                   int fuse_gelu, void** out) {
+    *out = 0;
+    seedvr2::DiTBlockGraph* g = new seedvr2::DiTBlockGraph(0);
+    const int ret = g->load_mem(param_text, static_cast<const unsigned char*>(model),
+                                (size_t)model_bytes, fp32_blobs != 0, fuse_gelu != 0);
+    if (ret != 0) {
+        delete g;
+        return ret;
+    }
+    *out = g;
+    return 0;
+}
+
+int h_graph_fused_gelu(void* graph) {
+    return static_cast<seedvr2::DiTBlockGraph*>(graph)->fused_gelu_count();
+}
+
+// Layer count and device bytes the graph's allocator holds (blocks in use
+// plus pooled ones).
+int h_graph_layer_count(void* graph) {
+    return (int)static_cast<seedvr2::DiTBlockGraph*>(graph)->net.layers().size();
+}
+
+// One run: inputs[0..9] = in0..in9 (host or device blobs, dims 1 or 2);
+// out0/out1 and the named checkpoint blobs are copied into the caller's
+// buffers (device when .device), their shapes reported back.
+int h_graph_run(void* graph, const int* shapes, const int* text_lengths, int batch,
+                const h_blob* inputs, h_blob* outs, int n_checkpoints,
+                const char* const* checkpoint_names) {
+    seedvr2::DiTBlockGraph* g = static_cast<seedvr2::DiTBlockGraph*>(graph);
+    std::vector<std::array<int, 3> > vs(batch);
+    for (int b = 0; b < batch; b++)
+        for (int a = 0; a < 3; a++) vs[b][a] = shapes[3 * b + a];
+    std::vector<int> tl(text_lengths, text_lengths + batch);
+    ncnn::Mat ins[10];
+    for (int i = 0; i < 10; i++) {
+        const h_blob& b = inputs[i];
+        if (b.dims == 0) continue;
+        if (b.device) {
+            ins[i] = b.dims == 1 ? g->allocator().wrap_blob(b.w, 1, b.data, (size_t)b.elemsize)
+                                 : g->allocator().wrap_blob(b.w, b.h, b.data, (size_t)b.elemsize);
+            if (b.dims == 1) {
+                ins[i].dims = 1;
+                ins[i].h = 1;
+            }
+        } else {
+            ins[i] = b.dims == 1 ? ncnn::Mat(b.w, b.data, (size_t)b.elemsize)
+                                 : ncnn::Mat(b.w, b.h, b.data, (size_t)b.elemsize);
+        }
+    }
+    std::vector<std::string> names;
+    for (int i = 0; i < n_checkpoints; i++) names.push_back(checkpoint_names[i]);
+    std::vector<ncnn::Mat> cps;
+    std::vector<ncnn::Mat> tops(2);
+    int ret = g->run(vs, tl, ins, tops[0], tops[1], n_checkpoints ? &names : 0, &cps);
+    if (ret != 0) return ret;
+    for (size_t i = 0; i < cps.size(); i++) tops.push_back(cps[i]);
+    for (size_t i = 0; i < tops.size(); i++) {
+        h_blob& o = outs[i];
+        const ncnn::Mat& m = tops[i];
+        const size_t bytes = (size_t)m.w * m.h * m.elemsize;
+        if (bytes > (size_t)o.w * o.h * o.elemsize) return -3;
+        o.dims = m.dims;
+        o.w = m.w;
+        o.h = m.h;
+        o.elemsize = (int)m.elemsize;
+        ret = o.device ? s2_memcpy_d2d(o.data, m.data, bytes, 0) : s2_memcpy_d2h(o.data, m.data, bytes, 0);
+        if (ret != 0) return ret;
+    }
+    return s2_stream_synchronize(0);
+}
+
+void h_graph_destroy(void* graph) { delete static_cast<seedvr2::DiTBlockGraph*>(graph); }
 
 }  // extern "C"

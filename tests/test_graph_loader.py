@@ -1,0 +1,87 @@
+"""The ncnn-compatible graph loader (ncnn::Net over the SeedVR2 layers,
+seedvr2::DiTBlockGraph) on the CPU: parsing, weight loading, the
+SharedLinear -> GELU folding and the error codes.  The loader replaces the
+reference's Net::load_param / load_model of blocks/seedvr2_blocks.ncnn
+(src/seedvr2/seedvr2_dit.cpp:603-633).  Running the graph is
+tests/test_gpu_graph.py."""
+import ctypes
+import os
+import sys
+
+import pytest
+
+from common import harness
+
+sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+import dit_graph  # noqa: E402
+
+
+def _lib():
+    L = harness()
+    P, vp, ci = ctypes.POINTER, ctypes.c_void_p, ctypes.c_int
+    L.h_graph_create.argtypes = [ctypes.c_char_p, vp, ctypes.c_long, ci, ci, P(vp)]
+    L.h_graph_fused_gelu.argtypes = [vp]
+    L.h_graph_layer_count.argtypes = [vp]
+    L.h_graph_destroy.argtypes = [vp]
+    return L
+
+
+def _create(text, model, fuse=1):
+    L = _lib()
+    g = ctypes.c_void_p()
+    buf = ctypes.create_string_buffer(model, max(1, len(model)))
+    ret = L.h_graph_create(text.encode(), buf, len(model), 0, fuse, ctypes.byref(g))
+    info = None
+    if ret == 0:
+        info = (L.h_graph_layer_count(g), L.h_graph_fused_gelu(g))
+        L.h_graph_destroy(g)
+    return ret, info
+
+
+@pytest.fixture(scope="module")
+def graph():
+    with open(dit_graph.PARAM_PATH) as f:
+        text = f.read()
+    return text, dit_graph.model_bytes(dit_graph.block_weights())
+
+
+def test_committed_param_is_the_generators(graph):
+    assert graph[0] == dit_graph.param_text()
+
+
+def test_header_counts_match_the_layer_lines(graph):
+    lines = graph[0].strip().split("\n")
+    assert lines[0] == "7767517"
+    nl, nb = map(int, lines[1].split())
+    body = lines[2:]
+    assert len(body) == nl
+    tops = set()
+    for line in body:
+        f = line.split()
+        b, t = int(f[2]), int(f[3])
+        tops.update(f[4 + b:4 + b + t])
+    assert len(tops) == nb and {"out0", "out1"} <= tops
+
+
+def test_loads_and_folds_gelu(graph):
+    text, model = graph
+    assert _create(text, model) == (0, (42, 2))
+    assert _create(text, model, fuse=0) == (0, (42, 0))
+
+
+@pytest.mark.parametrize("edit, code", [
+    (lambda t: t.replace("7767517", "7767518", 1), -1),                          # magic
+    (lambda t: t.replace("DiTAdaOut ", "NoSuchOp  ", 1), -1),                    # unknown type
+    (lambda t: t.replace(" b0_h_v b0_h_t b0_qkv_v", " b0_h_v b0_h_x b0_qkv_v", 1), -1),  # no producer
+    (lambda t: t.replace("0=256 1=256 2=1", "0=256 1=0 2=1", 1), -1),           # bad SharedLinear param
+    (lambda t: t.replace("42 74", "43 74", 1), -1),                              # layer count
+])
+def test_malformed_param_is_rejected(graph, edit, code):
+    text, model = graph
+    assert _create(edit(text), model)[0] == code
+
+
+def test_weight_file_must_match_the_graph(graph):
+    text, model = graph
+    assert _create(text, model[:-4])[0] == -100     # a layer runs out of weights
+    assert _create(text, model + b"\0\0\0\0")[0] == -1   # bytes left over
