@@ -667,6 +667,109 @@ def stack_7b(steps, warmup):
             "output_finite": finite}
 
 
+V3_MLP = 3456   # SwiGLU gate/up width of v3 manifests (seedvr2_pipeline.cpp:434-438)
+
+
+def v3_block(steps, warmup):
+    """The v3 DiT block shape at 720p (hidden 2560, 20x128 heads): separate
+    q, k and v projections 2560 -> 2560 feeding the attention's split form,
+    out 2560 -> 2560, the SwiGLU gate/up projection 2560 -> 2 x 3456 with
+    silu(gate) * up in the GEMM's epilogue, down 3456 -> 2560.  Also timed:
+    the same block with q/k/v as one fused projection (s2_awa_qkv_forward on
+    the concatenated weights)."""
+    import torch
+    from seedvr2_ncnn_amd import capi
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(11)
+    bf = torch.bfloat16
+    D, F = HIDDEN, V3_MLP
+    lv = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2]
+    lt = TEXT_TOKENS
+    m = lv + lt
+
+    def randn(*shape, std=1.0):
+        return (torch.randn(*shape, generator=gen, device=dev) * std).to(bf)
+
+    def bias(n):
+        return torch.randn(n, generator=gen, device=dev) * 0.02
+
+    x_v, x_t = randn(lv, D), randn(lt, D)
+    wq, wk, wv, wo = (randn(D, D, std=0.02) for _ in range(4))
+    bq, bk, bv, bo = (bias(D) for _ in range(4))
+    w_gu, b_gu = capi.swiglu_pack_weight(randn(F, D, std=0.02), randn(F, D, std=0.02), bias(F), bias(F))
+    w_dn, b_dn = randn(D, F, std=0.02), bias(D)
+    w_qkv, b_qkv = torch.cat([wq, wk, wv]).contiguous(), torch.cat([bq, bk, bv])
+    norms = (1.0 + 0.02 * torch.randn(4, HEAD_DIM, generator=gen, device=dev)).contiguous()
+    freqs = (10000.0 ** (-torch.arange(PAIRS, device=dev, dtype=torch.float64) / PAIRS)).float()
+    plan = capi.AwaPlan(capi.awa_config(HEADS, HEAD_DIM, TARGET, 0, 1e-5, PAIRS), [VIDEO_SHAPE], [lt])
+    ws = torch.empty(plan.info.workspace_bytes, dtype=torch.uint8, device=dev)
+    q = [(torch.empty(lv, D, dtype=bf, device=dev), torch.empty(lt, D, dtype=bf, device=dev))
+         for _ in range(3)]
+    a_v, a_t = torch.empty(lv, D, dtype=bf, device=dev), torch.empty(lt, D, dtype=bf, device=dev)
+    o_v, o_t = torch.empty_like(a_v), torch.empty_like(a_t)
+    h_v, h_t = torch.empty(lv, F, dtype=bf, device=dev), torch.empty(lt, F, dtype=bf, device=dev)
+    y_v, y_t = torch.empty_like(a_v), torch.empty_like(a_t)
+    names = ["q", "k", "v", "attention", "out", "swiglu_gate_up", "down"]
+
+    def step(fused, ev=None):
+        def mark(i):
+            if ev is not None:
+                ev[i].record()
+        mark(0)
+        if fused:
+            capi.awa_qkv_forward(plan, x_v, x_t, w_qkv, b_qkv, norms, freqs, workspace=ws,
+                                 out_video=a_v, out_text=a_t)
+            for i in range(1, 4):
+                mark(i)
+        else:
+            for i, (w, b_) in enumerate(((wq, bq), (wk, bk), (wv, bv))):
+                capi.shared_linear(x_v, x_t, w, b_, capi.ACT_NONE, y_video=q[i][0], y_text=q[i][1])
+                mark(i + 1)
+            capi.awa_forward(plan, norms, freqs, q[0][0], q[1][0], q[2][0], q[0][1], q[1][1],
+                             q[2][1], workspace=ws, out_video=a_v, out_text=a_t)
+        mark(4)
+        capi.shared_linear(a_v, a_t, wo, bo, capi.ACT_NONE, y_video=o_v, y_text=o_t)
+        mark(5)
+        capi.shared_linear(o_v, o_t, w_gu, b_gu, capi.ACT_SWIGLU, y_video=h_v, y_text=h_t)
+        mark(6)
+        capi.shared_linear(h_v, h_t, w_dn, b_dn, capi.ACT_NONE, y_video=y_v, y_text=y_t)
+        mark(7)
+
+    flops = {"q": 2 * m * D * D, "k": 2 * m * D * D, "v": 2 * m * D * D,
+             "attention": attention_flops(0), "out": 2 * m * D * D,
+             "swiglu_gate_up": 2 * m * D * 2 * F, "down": 2 * m * F * D}
+    total = sum(flops.values())
+    out = {"workload": f"v3 block shape at 6x45x80 + {lt} text tokens: q/k/v {D}->{D} each, "
+                       f"window attention (split form, regular windows), out {D}->{D}, SwiGLU "
+                       f"{D}->2x{F} (silu(gate)*up fused), down {F}->{D}",
+           "block_tflop": round(total / 1e12, 4)}
+    for fused in (False, True):
+        for _ in range(warmup):
+            step(fused)
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(8)] for _ in range(steps)]
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for i in range(steps):
+            step(fused, evs[i])
+        end.record()
+        torch.cuda.synchronize()
+        ms = start.elapsed_time(end) / steps
+        per = {n: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, n in enumerate(names)}
+        rec = {"ms_per_block": round(ms, 4), "tflops": round(total / (ms * 1e-3) / 1e12, 1),
+               "pct_bf16_peak": round(100 * total / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 2)}
+        if fused:
+            qa = sum(per[n] for n in ("q", "k", "v", "attention"))
+            rec["qkv_attention_ms"] = round(qa, 4)
+        else:
+            rec["kernels"] = {n: {"ms": round(per[n], 4),
+                                  "tflops": round(flops[n] / (per[n] * 1e-3) / 1e12, 1)}
+                              for n in names}
+        out["fused_qkv" if fused else "separate_qkv"] = rec
+    plan.close()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -681,6 +784,8 @@ def main():
                          "baseline): the run that rocprofv3 counter passes profile")
     ap.add_argument("--cpu-threads", type=int, default=0)
     ap.add_argument("--no-stack", action="store_true", help="skip the 32-block 7B-shaped stack")
+    ap.add_argument("--no-v3", action="store_true",
+                    help="skip the v3-shaped block (split q/k/v, SwiGLU 3456)")
     ap.add_argument("--stack-steps", type=int, default=3)
     ap.add_argument("--no-tail", action="store_true",
                     help="skip the frontend/tail kernels at the 720p latent")
@@ -695,6 +800,7 @@ def main():
     args = ap.parse_args()
     if args.block_only:
         args.no_stack = args.no_tail = args.no_vae = args.no_parity = args.no_cpu_baseline = True
+        args.no_v3 = True
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported by this build "
               "(the multi-GPU sharding is a design, not a measured path)", file=sys.stderr)
@@ -1002,6 +1108,8 @@ def main():
         line["attention_configs"] = awa_configs(args.cpu_threads or job_cpu_threads())
     if not args.no_stack:
         line["stack_7b"] = stack_7b(args.stack_steps, 1)
+    if not args.no_v3:
+        line["v3_block"] = v3_block(max(5, args.steps // 2), 2)
     if not args.no_tail:
         line["sampler_tail"] = sampler_tail()
     if not args.no_vae:

@@ -46,7 +46,9 @@ typedef enum s2_dtype {
 
 typedef enum s2_activation {
     S2_ACT_NONE = 0,
-    S2_ACT_GELU = 1    /* erf-GELU, 0.5 x (1 + erf(x / sqrt 2)) */
+    S2_ACT_GELU = 1,   /* erf-GELU, 0.5 x (1 + erf(x / sqrt 2)) */
+    S2_ACT_SWIGLU = 2  /* silu(gate) * up over a gate/up weight pair, see
+                          s2_shared_linear_forward */
 } s2_activation;
 
 /* One attention window.  Same fields and meaning as the reference
@@ -200,6 +202,14 @@ S2_API int s2_awa_stage_times(float stage_ms[4]);
 S2_API int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream_t stream);
 S2_API int s2_cast_bf16_to_f32(const uint16_t* src, float* dst, size_t count, s2_stream_t stream);
 
+/* The SwiGLU weight layout of s2_shared_linear_forward from a gate and an up
+ * projection: gate, up device bf16 [n][k]; gate_bias, up_bias device fp32
+ * [n] (both or neither); packed bf16 [2n][k] and packed_bias fp32 [2n] (NULL
+ * when there is no bias).  n a multiple of 128.  Device copies on stream. */
+S2_API int s2_swiglu_pack_weight(const uint16_t* gate, const uint16_t* up,
+                                 const float* gate_bias, const float* up_bias, int n, int k,
+                                 uint16_t* packed, float* packed_bias, s2_stream_t stream);
+
 /* Elementwise erf-GELU, y = x * Phi(x), over count values of dtype (fp32
  * arithmetic; y may equal x).  The device path of the ncnn GELU layer
  * (param 0 fast_gelu = 0) when a block graph keeps its MLP activation as a
@@ -220,7 +230,13 @@ S2_API int s2_gelu(const void* x, void* y, size_t count, s2_dtype dtype, s2_stre
  * of partial tiles: the first such call on a (device, stream) pair allocates
  * that pair's scratch (one 256 KB slot per compute unit, 64 MB on MI355X,
  * plus counters), kept until the process ends.  Calls on different streams
- * therefore never share scratch and may run concurrently. */
+ * therefore never share scratch and may run concurrently. *
+ * activation S2_ACT_SWIGLU (v3 graphs' MLP, seedvr2_pipeline.cpp:434-438):
+ * y = silu(x Wg^T + bg) * (x Wu^T + bu) in one launch.  weight is [2n][k]
+ * with the gate and up rows interleaved in blocks of 128 (rows 256j ..
+ * 256j+127 are gate rows 128j .., rows 256j+128 .. 256j+255 up rows 128j ..;
+ * s2_swiglu_pack_weight builds it), bias likewise [2n] or NULL; n (the
+ * output width) a multiple of 128, bf16 activations, k a multiple of 64. */
 S2_API int s2_shared_linear_forward(const void* x_video, int m_video, const void* x_text, int m_text,
                              s2_dtype x_dtype, const uint16_t* weight, const float* bias,
                              int n, int k, int activation,

@@ -24,6 +24,7 @@ DTYPE_BF16 = 1
 DTYPE_F16 = 2
 ACT_NONE = 0
 ACT_GELU = 1
+ACT_SWIGLU = 2
 
 # Every symbol include/seedvr2_hip.h declares.
 EXPORTS = (
@@ -39,7 +40,7 @@ EXPORTS = (
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
     "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded", "s2_shared_linear_forward_noalloc",
-    "s2_awa_qkv_forward", "s2_gelu",
+    "s2_awa_qkv_forward", "s2_gelu", "s2_swiglu_pack_weight",
 )
 
 
@@ -131,6 +132,7 @@ def lib() -> ctypes.CDLL:
         L.s2_awa_qkv_forward.argtypes = [vp, vp, vp, ci, vp, vp, vp, vp, vp, vp, ci, vp, sz, vp]
         L.s2_cast_f32_to_bf16.argtypes = [vp, vp, sz, vp]
         L.s2_gelu.argtypes = [vp, vp, sz, ci, vp]
+        L.s2_swiglu_pack_weight.argtypes = [vp, vp, vp, vp, ci, ci, vp, vp, vp]
         L.s2_cast_bf16_to_f32.argtypes = [vp, vp, sz, vp]
         L.s2_shared_linear_forward.argtypes = [vp, ci, vp, ci, ci, vp, vp, ci, ci, ci, vp, vp, ci, vp]
         L.s2_shared_linear_forward_noalloc.argtypes = L.s2_shared_linear_forward.argtypes
@@ -387,6 +389,19 @@ def cast_f32_to_bf16(src, dst=None, stream=None):
     return dst
 
 
+def swiglu_pack_weight(gate_bf16, up_bf16, gate_bias=None, up_bias=None, stream=None):
+    """s2_swiglu_pack_weight: the interleaved [2n][k] weight (and [2n] bias)
+    of a SwiGLU shared_linear from gate and up projections [n][k]."""
+    import torch
+    n, k = gate_bf16.shape
+    packed = torch.empty(2 * n, k, dtype=torch.bfloat16, device=gate_bf16.device)
+    pb = None if gate_bias is None else torch.empty(2 * n, device=gate_bf16.device)
+    check(lib().s2_swiglu_pack_weight(_ptr(gate_bf16), _ptr(up_bf16), _ptr(gate_bias),
+                                      _ptr(up_bias), n, k, _ptr(packed), _ptr(pb), _stream(stream)),
+          "s2_swiglu_pack_weight")
+    return packed, pb
+
+
 def gelu(x, y=None, stream=None):
     """s2_gelu: elementwise erf-GELU of a device tensor (fp32, bf16 or fp16)."""
     import torch
@@ -403,6 +418,8 @@ def shared_linear(x_video, x_text, weight_bf16, bias=None, activation=ACT_NONE, 
     (s2_shared_linear_forward_noalloc with noalloc=True)."""
     import torch
     n, k = weight_bf16.shape
+    if activation == ACT_SWIGLU:
+        n //= 2   # the interleaved gate/up weight has two rows per output column
     assert weight_bf16.dtype == torch.bfloat16 and weight_bf16.is_contiguous()
     xd = _dtype_code(x_video)
     assert x_text is None or _dtype_code(x_text) == xd

@@ -638,6 +638,29 @@ int s2_cast_f32_to_bf16(const float* src, uint16_t* dst, size_t count, s2_stream
     return S2_OK;
 }
 
+int s2_swiglu_pack_weight(const uint16_t* gate, const uint16_t* up, const float* gate_bias,
+                          const float* up_bias, int n, int k, uint16_t* packed,
+                          float* packed_bias, s2_stream_t stream) {
+    if (!gate || !up || !packed || n <= 0 || k <= 0 || n % 128 != 0 ||
+        ((gate_bias != 0) != (up_bias != 0)) || ((gate_bias != 0) != (packed_bias != 0)))
+        return fail(S2_ERR_INVALID, "invalid SwiGLU weight pair");
+    hipStream_t s = (hipStream_t)stream;
+    const size_t rows = 128, row_bytes = (size_t)k * 2;
+    for (int j = 0; j < n / 128; ++j) {
+        S2_HIP(hipMemcpyAsync(packed + (size_t)(2 * j) * rows * k, gate + (size_t)j * rows * k,
+                              rows * row_bytes, hipMemcpyDeviceToDevice, s));
+        S2_HIP(hipMemcpyAsync(packed + (size_t)(2 * j + 1) * rows * k, up + (size_t)j * rows * k,
+                              rows * row_bytes, hipMemcpyDeviceToDevice, s));
+        if (gate_bias) {
+            S2_HIP(hipMemcpyAsync(packed_bias + (size_t)(2 * j) * rows, gate_bias + (size_t)j * rows,
+                                  rows * 4, hipMemcpyDeviceToDevice, s));
+            S2_HIP(hipMemcpyAsync(packed_bias + (size_t)(2 * j + 1) * rows, up_bias + (size_t)j * rows,
+                                  rows * 4, hipMemcpyDeviceToDevice, s));
+        }
+    }
+    return S2_OK;
+}
+
 int s2_gelu(const void* x, void* y, size_t count, s2_dtype dtype, s2_stream_t stream) {
     if (count && (!x || !y)) return fail(S2_ERR_INVALID, "null argument");
     if (!dtype_ok(dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
@@ -661,9 +684,12 @@ static int linear_args_ok(const void* x_video, int m_video, const void* x_text, 
     if ((m_video > 0 && (!x_video || !y_video)) || (m_text > 0 && (!x_text || !y_text)))
         return fail(S2_ERR_INVALID, "null stream pointer");
     if (k % 8 != 0) return fail(S2_ERR_INVALID, "k must be a multiple of 8");
-    if (activation != S2_ACT_NONE && activation != S2_ACT_GELU)
+    if (activation != S2_ACT_NONE && activation != S2_ACT_GELU && activation != S2_ACT_SWIGLU)
         return fail(S2_ERR_INVALID, "unknown activation");
     if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (activation == S2_ACT_SWIGLU &&
+        (x_dtype != S2_DTYPE_BF16 || k % 64 != 0 || n % 128 != 0 || (long)256 * k * 2 > 0x7fffffffL))
+        return fail(S2_ERR_INVALID, "SwiGLU needs bf16 activations, k % 64 == 0 and n % 128 == 0");
     const size_t xe = dtype_bytes(x_dtype);
     if (((uintptr_t)x_video) % (8 * xe) || ((uintptr_t)x_text) % (8 * xe) ||
         ((uintptr_t)weight) % 16 || ((uintptr_t)y_video) % 16 || ((uintptr_t)y_text) % 16)

@@ -33,7 +33,11 @@ int SharedLinear::load_param(const ncnn::ParamDict& pd)
     params_loaded = false;
     if (num_output <= 0 || num_input <= 0)
         return -1;
-    if (activation != S2_ACT_NONE && activation != S2_ACT_GELU)
+    if (activation != S2_ACT_NONE && activation != S2_ACT_GELU && activation != S2_ACT_SWIGLU)
+        return -1;
+    // SwiGLU (this build's id 3 = 2): num_output gate and num_output up
+    // rows; the fused epilogue needs whole 128-column blocks and 64-wide k steps
+    if (activation == S2_ACT_SWIGLU && (num_output % 128 != 0 || num_input % 64 != 0))
         return -1;
     params_loaded = true;
     weights_dirty = true;
@@ -48,17 +52,48 @@ int SharedLinear::load_model(const ncnn::ModelBin& mb)
     if (!params_loaded)
         return -1;
     weights_dirty = true;
-    weight_data = mb.load(num_input * num_output, 1);
+    // SwiGLU: the gate projection's [N][K] weight, then the up projection's
+    // (and the two biases in the same order)
+    const int rows = activation == S2_ACT_SWIGLU ? 2 * num_output : num_output;
+    weight_data = mb.load(num_input * rows, 1);
     if (weight_data.empty())
         return -100;
-    weight_data = weight_data.reshape(num_input, num_output);
+    weight_data = weight_data.reshape(num_input, rows);
     if (weight_data.empty())
         return -100;
     if (bias_term)
     {
-        bias_data = mb.load(num_output, 1);
+        bias_data = mb.load(rows, 1);
         if (bias_data.empty())
             return -100;
+    }
+    if (activation == S2_ACT_SWIGLU)
+    {
+        // interleave 128-row blocks: gate rows 128j.., then up rows 128j..
+        // (the weight layout of s2_shared_linear_forward's SwiGLU)
+        ncnn::Mat w(num_input, rows);
+        ncnn::Mat b;
+        if (bias_term)
+            b.create(rows);
+        if (w.empty() || (bias_term && b.empty()))
+            return -100;
+        const size_t blk = (size_t)128 * num_input;
+        for (int j = 0; j < num_output / 128; j++)
+        {
+            memcpy((float*)w.data + (2 * j) * blk, (const float*)weight_data.data + j * blk,
+                   blk * sizeof(float));
+            memcpy((float*)w.data + (2 * j + 1) * blk,
+                   (const float*)weight_data.data + (num_output / 128 + j) * blk, blk * sizeof(float));
+            if (bias_term)
+            {
+                memcpy((float*)b.data + 2 * j * 128, (const float*)bias_data.data + j * 128, 512);
+                memcpy((float*)b.data + (2 * j + 1) * 128,
+                       (const float*)bias_data.data + num_output + j * 128, 512);
+            }
+        }
+        weight_data = w;
+        if (bias_term)
+            bias_data = b;
     }
     return 0;
 }
@@ -101,7 +136,8 @@ int SharedLinear::upload_weights_locked() const
 {
     if (!weights_dirty && weight_gpu.get())
         return 0;
-    const size_t count = static_cast<size_t>(num_input) * num_output;
+    const int rows = activation == S2_ACT_SWIGLU ? 2 * num_output : num_output;
+    const size_t count = static_cast<size_t>(num_input) * rows;
     DeviceBuffer tmp;
     int ret = tmp.reserve(count * sizeof(float));
     if (ret == 0)
@@ -113,9 +149,9 @@ int SharedLinear::upload_weights_locked() const
                                   static_cast<uint16_t*>(weight_gpu.get()), count, 0);
     if (ret == 0 && bias_term)
     {
-        ret = bias_gpu.reserve(num_output * sizeof(float));
+        ret = bias_gpu.reserve(rows * sizeof(float));
         if (ret == 0)
-            ret = s2_memcpy_h2d(bias_gpu.get(), bias_data.data, num_output * sizeof(float), 0);
+            ret = s2_memcpy_h2d(bias_gpu.get(), bias_data.data, rows * sizeof(float), 0);
     }
     if (ret == 0)
         ret = s2_stream_synchronize(0);
@@ -185,7 +221,9 @@ int SharedLinear::forward_impl(const std::vector<ncnn::Mat>& bottom_blobs,
     const size_t in1 = static_cast<size_t>(m1) * num_input;
     const size_t out0 = static_cast<size_t>(m0) * num_output;
     const size_t out1 = static_cast<size_t>(m1) * num_output;
-    ret = staging.reserve((in0 + in1 + out0 + out1) * sizeof(float));
+    // (SwiGLU: room for bf16 copies of the inputs after the fp32 buffers)
+    const size_t swiglu_extra = activation == S2_ACT_SWIGLU ? (in0 + in1 + 8) / 2 : 0;
+    ret = staging.reserve((in0 + in1 + out0 + out1 + swiglu_extra + 4) * sizeof(float));
     if (ret != 0)
         return ret;
     float* x0 = static_cast<float*>(staging.get());
@@ -195,7 +233,25 @@ int SharedLinear::forward_impl(const std::vector<ncnn::Mat>& bottom_blobs,
     ret = s2_memcpy_h2d(x0, bottom_blobs[0].data, in0 * sizeof(float), 0);
     if (ret == 0)
         ret = s2_memcpy_h2d(x1, bottom_blobs[1].data, in1 * sizeof(float), 0);
-    if (ret == 0)
+    if (ret == 0 && activation == S2_ACT_SWIGLU)
+    {
+        // the SwiGLU epilogue runs on bf16 operands: round the staged fp32
+        // rows into their own buffer (16-byte aligned), as the MFMA staging
+        // of the other activations rounds them
+        uintptr_t hb = reinterpret_cast<uintptr_t>(y1 + out1);
+        hb = (hb + 15) & ~static_cast<uintptr_t>(15);
+        uint16_t* h0 = reinterpret_cast<uint16_t*>(hb);
+        uint16_t* h1 = h0 + (in0 + 7) / 8 * 8;
+        ret = s2_cast_f32_to_bf16(x0, h0, in0, 0);
+        if (ret == 0)
+            ret = s2_cast_f32_to_bf16(x1, h1, in1, 0);
+        if (ret == 0)
+            ret = s2_shared_linear_forward(h0, m0, h1, m1, S2_DTYPE_BF16,
+                                           static_cast<const uint16_t*>(weight_gpu.get()), bias,
+                                           num_output, num_input, activation, y0, y1,
+                                           S2_DTYPE_F32, 0);
+    }
+    else if (ret == 0)
         ret = s2_shared_linear_forward(x0, m0, x1, m1, S2_DTYPE_F32,
                                        static_cast<const uint16_t*>(weight_gpu.get()), bias,
                                        num_output, num_input, activation, y0, y1, S2_DTYPE_F32, 0);

@@ -349,10 +349,13 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         col0 = nt * BN;
     };
     // output row of tile row rl, or null past either stream
+    // output row pitch: n, or n / 2 for SwiGLU, whose weight has a gate and
+    // an up row per output column
+    const int ny = ACT == S2_ACT_SWIGLU ? n / 2 : n;
     auto out_row = [&](int rl) -> void* {
         const int r = row0 + rl;
-        if (r < m0) return (char*)y0 + (long)r * n * (YK ? 2 : 4);
-        if (r >= mv && r < mv + m1) return (char*)y1 + (long)(r - mv) * n * (YK ? 2 : 4);
+        if (r < m0) return (char*)y0 + (long)r * ny * (YK ? 2 : 4);
+        if (r >= mv && r < mv + m1) return (char*)y1 + (long)(r - mv) * ny * (YK ? 2 : 4);
         return nullptr;
     };
 
@@ -683,10 +686,79 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         }
     };
 
+    // SwiGLU: the weight's rows come in blocks of 256, the first 128 gate
+    // rows and the next 128 up rows of the same 128 output columns, so a
+    // tile's columns 0-127 are gates and 128-255 ups of output columns
+    // col0/2 .. col0/2 + 127.  acc + bias is staged as fp32 in two halves of
+    // 128 rows; each thread then forms silu(g) * u for 4 columns of a row.
+    auto swiglu_epilogue = [&]() {
+        if constexpr (ACT == S2_ACT_SWIGLU) {
+            constexpr int EF = BN * 4 + 16;   // fp32 row pitch (bytes)
+            const int oc0 = col0 / 2;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                __syncthreads();   // the stage (h = 0) or the previous half is no longer read
+                if (wm == h) {
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int cl = wn * 64 + 32 * j + l32;
+                        const float bv = bias ? bias[col0 + cl] : 0.f;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+#pragma unroll
+                            for (int r = 0; r < 16; ++r) {
+                                const int rl = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                                *(float*)(lds + rl * EF + cl * 4) = acc[i][j][r] + bv;
+                            }
+                    }
+                }
+                __syncthreads();
+#pragma unroll 2
+                for (int it = 0; it < 8; ++it) {
+                    const int idx = it * 512 + tid;
+                    const int rl = idx >> 5;
+                    const int c4 = (idx & 31) * 4;
+                    const f32x4 gv = *(const f32x4*)(lds + rl * EF + c4 * 4);
+                    const f32x4 uv = *(const f32x4*)(lds + rl * EF + (c4 + 128) * 4);
+                    float o[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        // silu(g) = g / (1 + e^-g), e^-g = 2^(-g log2 e)
+                        const float gg = gv[e];
+                        const float sig = __builtin_amdgcn_rcpf(
+                            1.f + __builtin_amdgcn_exp2f(-gg * 1.4426950408889634f));
+                        o[e] = gg * sig * uv[e];
+                    }
+                    void* yr = out_row(h * 128 + rl);
+                    const int col = oc0 + c4;
+                    if (!yr || col >= ny) continue;
+                    if (YK == 0) {
+                        const f32x4 ov = {o[0], o[1], o[2], o[3]};
+                        __builtin_nontemporal_store(ov, (f32x4*)((float*)yr + col));
+                    } else {
+                        uint16_t hb[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            hb[e] = YK == 2 ? __builtin_bit_cast(uint16_t, (_Float16)o[e])
+                                            : __builtin_bit_cast(uint16_t, (__bf16)o[e]);
+                        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+                        const u32x2 hv = {hb[0] | ((uint32_t)hb[1] << 16),
+                                          hb[2] | ((uint32_t)hb[3] << 16)};
+                        __builtin_nontemporal_store(hv, (u32x2*)((uint16_t*)yr + col));
+                    }
+                }
+            }
+        }
+    };
+
     // y tile = act(acc + bias)
     auto epilogue = [&]() {
         if constexpr (AWA != 0) {
             awa_epilogue();
+            return;
+        }
+        if constexpr (ACT == S2_ACT_SWIGLU) {
+            swiglu_epilogue();
             return;
         }
         if (YK && (n & 7) == 0) {
@@ -1116,6 +1188,17 @@ template <typename TX, int YK>
 static hipError_t linear_act(int act, const void* x0, int m0, const void* x1, int m1,
                              const uint16_t* w, const float* bias, int n, int k, void* y0,
                              void* y1, hipStream_t stream, SkSource src) {
+    if (act == S2_ACT_SWIGLU) {
+        // bf16 activations on the 256-tile path only (the caller checks);
+        // n is the output width, the weight has 2n interleaved rows
+        if constexpr (std::is_same<TX, uint16_t>::value) {
+            if (k % 64 != 0 || n % 128 != 0 || (long)256 * k * 2 > 0x7fffffffL)
+                return hipErrorInvalidValue;
+            return linear_impl<TX, YK, S2_ACT_SWIGLU>(x0, m0, x1, m1, w, bias, 2 * n, k, y0, y1,
+                                                      stream, src);
+        }
+        return hipErrorInvalidValue;
+    }
     if (act == S2_ACT_GELU)
         return linear_impl<TX, YK, S2_ACT_GELU>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
     return linear_impl<TX, YK, S2_ACT_NONE>(x0, m0, x1, m1, w, bias, n, k, y0, y1, stream, src);
