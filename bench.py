@@ -579,6 +579,8 @@ def stack_7b(steps, warmup):
     h_t = torch.empty(lt, F, dtype=bf, device=dev)
     plans = {s: capi.AwaPlan(capi.awa_config(H, HEAD_DIM, TARGET, s, 1e-5, PAIRS), [VIDEO_SHAPE], [lt])
              for s in (0, 1)}
+    for p in plans.values():
+        p.cache_rope(freqs)   # the layer keeps its frequencies' cos/sin table with the plan
     ws = torch.empty(max(p.info.workspace_bytes for p in plans.values()), dtype=torch.uint8, device=dev)
 
     def forward():
@@ -702,6 +704,7 @@ def v3_block(steps, warmup):
     norms = (1.0 + 0.02 * torch.randn(4, HEAD_DIM, generator=gen, device=dev)).contiguous()
     freqs = (10000.0 ** (-torch.arange(PAIRS, device=dev, dtype=torch.float64) / PAIRS)).float()
     plan = capi.AwaPlan(capi.awa_config(HEADS, HEAD_DIM, TARGET, 0, 1e-5, PAIRS), [VIDEO_SHAPE], [lt])
+    plan.cache_rope(freqs)
     ws = torch.empty(plan.info.workspace_bytes, dtype=torch.uint8, device=dev)
     q = [(torch.empty(lv, D, dtype=bf, device=dev), torch.empty(lt, D, dtype=bf, device=dev))
          for _ in range(3)]
@@ -845,6 +848,10 @@ def main():
 
     plans = {s: capi.AwaPlan(capi.awa_config(HEADS, HEAD_DIM, TARGET, s, 1e-5, PAIRS),
                              [VIDEO_SHAPE], [lt]) for s in (0, 1)}
+    # the RoPE cos/sin table depends only on the plan and the frequency
+    # weights: the plan keeps it, as the layer does (s2_awa_plan_cache_rope)
+    for p in plans.values():
+        p.cache_rope(freqs)
     ws = torch.empty(max(p.info.workspace_bytes for p in plans.values()), dtype=torch.uint8, device=dev)
 
     ops = ["qkv", "attention", "out", "mlp_up", "mlp_down"]
@@ -1080,7 +1087,9 @@ def main():
                                            flops_s["qkv"] + flops_s["attention"]),
         "kernels": kernels,
         "separate_qkv_and_attention": separate_rec,
-        "attention_stages": stages,
+        "attention_stages": dict(stages, rope_table_note=(
+            "the plans keep the RoPE cos/sin table (s2_awa_plan_cache_rope, as the layer does), "
+            "so rope_table_ms is the empty stage between two events")),
         "roofline": {
             "kernel": "s2::shared_linear_256_kernel<true, 1> (MLP up 2560->10240 + GELU, M=21664)",
             "bound": "mfma",

@@ -121,6 +121,18 @@ S2_API int s2_awa_plan_get_windows(const s2_awa_plan* plan, s2_window_slice* win
                             int max_windows, int* sample_window_count);
 S2_API int s2_awa_plan_destroy(s2_awa_plan* plan);
 
+/* Computes the plan's RoPE (cos, sin) table, angle pos * freq[p] for every
+ * position the plan's windows and text tokens use (apply_mm_rope,
+ * adaptive_window_attention.cpp:521-543, which forms the same angles per
+ * token on every forward), once, into memory the plan owns.  Forwards whose
+ * rope_freqs argument is this same pointer then read it instead of
+ * recomputing it in their workspace; other pointers are unaffected.  After
+ * rewriting the frequencies in place, call this again (rope_freqs == NULL
+ * clears the cache).  The table is written on `stream`: it must be complete
+ * before forwards on other streams use it, and no forward may run on the plan
+ * while this call does. */
+S2_API int s2_awa_plan_cache_rope(s2_awa_plan* plan, const float* rope_freqs, s2_stream_t stream);
+
 /* Materialises the plan's per-token tables on the device with the same
  * integer index math the forward kernels use: video_indices[L] (partition ->
  * source token), inverse_video_indices[L], local_positions[L][3]

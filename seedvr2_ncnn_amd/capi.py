@@ -40,7 +40,7 @@ EXPORTS = (
     "s2_mha_weight_bytes", "s2_mha_prepare_weights", "s2_mha_workspace_bytes", "s2_mha_forward",
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
     "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded", "s2_shared_linear_forward_noalloc",
-    "s2_awa_qkv_forward", "s2_gelu", "s2_swiglu_pack_weight",
+    "s2_awa_qkv_forward", "s2_gelu", "s2_swiglu_pack_weight", "s2_awa_plan_cache_rope",
 )
 
 
@@ -127,6 +127,7 @@ def lib() -> ctypes.CDLL:
         L.s2_awa_plan_get_windows.argtypes = [vp, P(WindowSlice), ci, P(ci)]
         L.s2_awa_plan_destroy.argtypes = [vp]
         L.s2_awa_plan_tables.argtypes = [vp, vp, vp, vp, vp]
+        L.s2_awa_plan_cache_rope.argtypes = [vp, vp, vp]
         L.s2_awa_forward.argtypes = [vp, vp, vp, vp, vp, vp, cl, vp, vp, vp, cl, ci, vp, vp, ci,
                                      vp, sz, vp]
         L.s2_awa_qkv_forward.argtypes = [vp, vp, vp, ci, vp, vp, vp, vp, vp, vp, ci, vp, sz, vp]
@@ -271,6 +272,13 @@ class AwaPlan:
         check(lib().s2_awa_plan_tables(self._h, _ptr(idx), _ptr(inv), _ptr(pos), _stream()),
               "s2_awa_plan_tables")
         return idx, inv, pos
+
+    def cache_rope(self, rope_freqs):
+        """s2_awa_plan_cache_rope: the plan keeps the cos/sin table of these
+        frequencies (a device fp32 tensor; None clears the cache).  Forwards
+        given the same tensor then skip recomputing it."""
+        check(lib().s2_awa_plan_cache_rope(self._h, _ptr(rope_freqs), _stream()),
+              "s2_awa_plan_cache_rope")
 
     def close(self):
         if self._h:

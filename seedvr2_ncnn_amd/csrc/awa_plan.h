@@ -119,6 +119,11 @@ struct s2_awa_plan {
     int qkv_rows = 0;
     s2::QkvRow* d_qkv_rows = nullptr;       // [qkv_rows rounded up to 256]
     int text_partial_rows = 0;
+    // (cos, sin) pairs [rope_positions][pairs] of the frequencies at
+    // rope_cache_src, filled by s2_awa_plan_cache_rope; forwards given that
+    // pointer read it instead of recomputing the table in their workspace
+    float* d_rope_cache = nullptr;
+    const float* rope_cache_src = nullptr;
     // workspace layout (byte offsets)
     size_t off_q = 0, off_k = 0, off_vt = 0, off_rope = 0, off_tpart = 0;
     size_t workspace_bytes = 0;

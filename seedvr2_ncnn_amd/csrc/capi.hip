@@ -490,8 +490,26 @@ int s2_awa_plan_destroy(s2_awa_plan* plan) {
     if (!plan) return S2_OK;
     hipError_t e = hipSuccess;
     if (plan->d_meta) e = hipFree(plan->d_meta);
+    if (plan->d_rope_cache) {
+        const hipError_t e2 = hipFree(plan->d_rope_cache);
+        if (e == hipSuccess) e = e2;
+    }
     delete plan;
     if (e != hipSuccess) return fail_hip(e, "hipFree");
+    return S2_OK;
+}
+
+int s2_awa_plan_cache_rope(s2_awa_plan* plan, const float* rope_freqs, s2_stream_t stream) {
+    if (!plan) return fail(S2_ERR_INVALID, "null plan");
+    plan->rope_cache_src = nullptr;
+    const int pairs = plan->config.rope_pairs_per_axis;
+    if (!rope_freqs || pairs == 0) return S2_OK;   // cache cleared / nothing to cache
+    if (!plan->d_rope_cache)
+        S2_HIP(hipMalloc((void**)&plan->d_rope_cache,
+                         sizeof(float2) * (size_t)plan->rope_positions * pairs));
+    S2_HIP(s2::launch_rope_table(rope_freqs, pairs, plan->rope_positions,
+                                 (float2*)plan->d_rope_cache, (hipStream_t)stream));
+    plan->rope_cache_src = rope_freqs;
     return S2_OK;
 }
 
@@ -537,11 +555,12 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
     uint16_t* q = (uint16_t*)(ws + plan->off_q);
     uint16_t* k = (uint16_t*)(ws + plan->off_k);
     uint16_t* vt = (uint16_t*)(ws + plan->off_vt);
-    float2* rope = (float2*)(ws + plan->off_rope);
+    const bool rope_cached = rope_freqs && rope_freqs == plan->rope_cache_src;
+    float2* rope = rope_cached ? (float2*)plan->d_rope_cache : (float2*)(ws + plan->off_rope);
     float* tpart = (float*)(ws + plan->off_tpart);
     StageTimer& tm = stage_timer();
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[0], s));
-    if (plan->config.rope_pairs_per_axis > 0)
+    if (plan->config.rope_pairs_per_axis > 0 && !rope_cached)
         S2_HIP(s2::launch_rope_table(rope_freqs, plan->config.rope_pairs_per_axis,
                                      plan->rope_positions, rope, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[1], s));
@@ -590,11 +609,12 @@ int s2_awa_qkv_forward(const s2_awa_plan* plan, const void* x_video, const void*
     uint16_t* q = (uint16_t*)(ws + plan->off_q);
     uint16_t* k = (uint16_t*)(ws + plan->off_k);
     uint16_t* vt = (uint16_t*)(ws + plan->off_vt);
-    float2* rope = (float2*)(ws + plan->off_rope);
+    const bool rope_cached = rope_freqs && rope_freqs == plan->rope_cache_src;
+    float2* rope = rope_cached ? (float2*)plan->d_rope_cache : (float2*)(ws + plan->off_rope);
     float* tpart = (float*)(ws + plan->off_tpart);
     StageTimer& tm = stage_timer();
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[0], s));
-    if (plan->config.rope_pairs_per_axis > 0)
+    if (plan->config.rope_pairs_per_axis > 0 && !rope_cached)
         S2_HIP(s2::launch_rope_table(rope_freqs, plan->config.rope_pairs_per_axis,
                                      plan->rope_positions, rope, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[1], s));

@@ -120,7 +120,7 @@ AdaptiveWindowAttention::AdaptiveWindowAttention(AdaptiveWindowRuntimeState* new
     : heads(20), head_dim(128), target_windows({{4, 3, 3}}), shifted(false),
       epsilon(1e-5f), rope_pairs_per_axis(21), shared_norm(false),
       shape_values_are_int32(false), official_bf16_attention(false),
-      runtime_state(new_runtime_state), weights_dirty(true), plan(0)
+      runtime_state(new_runtime_state), weights_dirty(true), plan(0), plan_rope_cached(false)
 {
     one_blob_only = false;
     support_inplace = false;
@@ -252,6 +252,7 @@ void AdaptiveWindowAttention::release_device_locked() const
     if (plan)
         s2_awa_plan_destroy(plan);
     plan = 0;
+    plan_rope_cached = false;
     plan_shapes.clear();
     plan_text_lengths.clear();
     workspace.release();
@@ -286,6 +287,7 @@ int AdaptiveWindowAttention::upload_weights_locked() const
         ret = s2_stream_synchronize(0);
     if (ret == 0)
         weights_dirty = false;
+    plan_rope_cached = false;   // new frequencies (or a new buffer)
     return ret;
 }
 
@@ -297,6 +299,7 @@ int AdaptiveWindowAttention::plan_for_locked(const std::vector<int>& shapes,
     if (plan)
         s2_awa_plan_destroy(plan);
     plan = 0;
+    plan_rope_cached = false;
     s2_awa_config config;
     config.heads = heads;
     config.head_dim = head_dim;
@@ -446,6 +449,17 @@ int AdaptiveWindowAttention::forward_impl(const std::vector<ncnn::Mat>& bottom_b
     ret = upload_weights_locked();
     if (ret != 0)
         return ret;
+    if (!plan_rope_cached)
+    {
+        // the frequencies are weights: the plan keeps their cos/sin table
+        // until the plan or the weights change
+        ret = s2_awa_plan_cache_rope(plan, static_cast<const float*>(weights_gpu.get()) + 4 * head_dim, 0);
+        if (ret == 0)
+            ret = s2_stream_synchronize(0);
+        if (ret != 0)
+            return ret;
+        plan_rope_cached = true;
+    }
     s2_awa_plan_info info;
     s2_awa_plan_get_info(plan, &info);
     ret = workspace.reserve(info.workspace_bytes);

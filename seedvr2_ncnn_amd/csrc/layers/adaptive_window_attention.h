@@ -132,6 +132,7 @@ private:
     mutable bool weights_dirty;
     mutable DeviceBuffer weights_gpu;      // [4][d] norms then [P] freqs, fp32
     mutable s2_awa_plan* plan;
+    mutable bool plan_rope_cached;         // the plan holds the table of weights_gpu's freqs
     mutable std::vector<int> plan_shapes;
     mutable std::vector<int> plan_text_lengths;
     mutable DeviceBuffer workspace;

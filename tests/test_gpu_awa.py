@@ -343,3 +343,31 @@ def test_repeated_forward_is_deterministic():
     a = _run_capi(case, 4, 128, (4, 3, 3), 1, 21, shapes, tl, True, torch.float32)
     b = _run_capi(case, 4, 128, (4, 3, 3), 1, 21, shapes, tl, True, torch.float32)
     assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def test_layer_rebuilds_plan_and_rope_table_when_shapes_change():
+    """One layer instance fed three shape sets in turn (A, B, A): each change
+    of shapes rebuilds the plan, whose cached RoPE table the layer fills from
+    its frequency weights before the forward; every result is at the oracle
+    bar."""
+    torch_mod()
+    heads, d, pairs, target = 2, 128, 21, (4, 3, 3)
+    layer = None
+    for shapes, tl, seed in (([(2, 12, 20)], [33], 301), ([(1, 9, 7)], [70], 302),
+                             ([(2, 12, 20)], [33], 303)):
+        case = make_awa_inputs(seed, shapes, tl, heads, d, pairs)
+        if layer is None:
+            weights = dict(norms=case["norms"], freqs=case["freqs"])
+            layer = Layer("AdaptiveWindowAttention", awa_param_string(heads, d, target, 1, 1e-5, pairs),
+                          [weights["norms"][i] for i in range(4)] + [weights["freqs"]])
+            assert layer.create_code == 0
+        case.update(weights)   # the layer keeps its first weights
+        lv = sum(a * b * c for a, b, c in shapes)
+        inner = heads * d
+        blobs = [case["video"], case["text"], np.asarray(shapes[0], np.float32),
+                 np.asarray(tl, np.float32)]
+        code, (ov, ot) = layer.forward(blobs, [((lv, inner), np.float32), ((sum(tl), inner), np.float32)])
+        assert code == 0
+        rv, rt = oracle_awa(case, heads, d, target, 1, 1e-5, pairs, shapes, tl)
+        assert_close(ov, rv, f"video {shapes}")
+        assert_close(ot, rt, f"text {shapes}")

@@ -139,3 +139,59 @@ def test_fused_qkv_rejects_unsupported_shapes():
         with pytest.raises(capi.S2Error) as e:
             capi.awa_qkv_forward(plan, xv, xt, w, None, norms, freqs)
         assert e.value.code == capi.S2_ERR_INVALID
+
+
+def test_plan_rope_cache():
+    """s2_awa_plan_cache_rope: forwards given the cached frequencies read the
+    plan's table and match the uncached forward bit for bit (both the fused
+    and the separate path); a different frequency tensor is not served from
+    the cache; after the cached tensor is rewritten in place, caching again
+    picks up the new values; a NULL pointer clears the cache."""
+    torch = torch_mod()
+    heads, d, pairs, hidden = 2, 128, 21, 256
+    shapes, tl = [(3, 16, 20)], [24]
+    lv = 3 * 16 * 20
+    case = _inputs(91, lv, 24, hidden, heads, d, pairs)
+    bf = torch.bfloat16
+    xv = torch.from_numpy(case["xv"]).cuda().to(bf)
+    xt = torch.from_numpy(case["xt"]).cuda().to(bf)
+    w = torch.from_numpy(case["w"]).cuda().to(bf)
+    b = torch.from_numpy(case["b"]).cuda()
+    norms = torch.from_numpy(case["norms"]).cuda()
+    f1 = torch.from_numpy(case["freqs"]).cuda()
+    f2 = (f1 * 0.5).contiguous()
+    inner = heads * d
+    cfg = capi.awa_config(heads, d, (4, 3, 3), 1, 1e-5, pairs)
+    qv, qt = capi.shared_linear(xv, xt, w, b, capi.ACT_NONE, out_dtype=bf)
+
+    def both(plan, freqs):
+        fv, ft = capi.awa_qkv_forward(plan, xv, xt, w, b, norms, freqs, out_dtype=torch.float32)
+        sv, st = capi.awa_forward(plan, norms, freqs, qv[:, :inner], qv[:, inner:2 * inner],
+                                  qv[:, 2 * inner:], qt[:, :inner], qt[:, inner:2 * inner],
+                                  qt[:, 2 * inner:], out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        return [t.cpu().numpy() for t in (fv, ft, sv, st)]
+
+    def same(a, b):
+        for x, y in zip(a, b):
+            np.testing.assert_array_equal(x, y)
+
+    with capi.AwaPlan(cfg, shapes, tl) as ref_plan, capi.AwaPlan(cfg, shapes, tl) as plan:
+        ref1, ref2 = both(ref_plan, f1), both(ref_plan, f2)
+        assert not np.array_equal(ref1[0], ref2[0])
+        plan.cache_rope(f1)
+        same(both(plan, f1), ref1)           # served from the cache
+        same(both(plan, f2), ref2)           # another tensor: computed per call
+        f1.copy_(f2)                          # rewritten in place ...
+        plan.cache_rope(f1)                   # ... and cached again
+        same(both(plan, f1), ref2)
+        plan.cache_rope(None)                 # cleared: computed per call again
+        f1.mul_(2.0)
+        same(both(plan, f1), ref1)
+    # the cached table feeds an oracle-checked result as well
+    rv, rt = oracle_awa(dict(video=oracle.linear(case["xv"], case["w"], case["b"], 0, threads=8),
+                             text=oracle.linear(case["xt"], case["w"], case["b"], 0, threads=8),
+                             norms=case["norms"], freqs=case["freqs"]),
+                        heads, d, (4, 3, 3), 1, 1e-5, pairs, shapes, tl)
+    assert_close(ref1[0], rv, "cached rope video")
+    assert_close(ref1[1], rt, "cached rope text")
