@@ -120,7 +120,8 @@ AdaptiveWindowAttention::AdaptiveWindowAttention(AdaptiveWindowRuntimeState* new
     : heads(20), head_dim(128), target_windows({{4, 3, 3}}), shifted(false),
       epsilon(1e-5f), rope_pairs_per_axis(21), shared_norm(false),
       shape_values_are_int32(false), official_bf16_attention(false),
-      runtime_state(new_runtime_state), weights_dirty(true), plan(0), plan_rope_cached(false)
+      runtime_state(new_runtime_state), weights_dirty(true), plan(0), plan_rope_cached(false),
+      qkv_projection(0)
 {
     one_blob_only = false;
     support_inplace = false;
@@ -320,6 +321,21 @@ int AdaptiveWindowAttention::plan_for_locked(const std::vector<int>& shapes,
     return 0;
 }
 
+int AdaptiveWindowAttention::set_qkv_projection(const SharedLinear* qkv)
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    if (qkv)
+    {
+        const int inner = heads * head_dim;
+        if ((head_dim != 64 && head_dim != 128) || inner % 256 != 0 ||
+            qkv->output_width() != 3 * inner || qkv->activation_kind() != S2_ACT_NONE ||
+            qkv->input_width() <= 0 || qkv->input_width() % 64 != 0)
+            return -1;
+    }
+    qkv_projection = qkv;
+    return 0;
+}
+
 int AdaptiveWindowAttention::forward(const std::vector<ncnn::Mat>& bottom_blobs,
                                      std::vector<ncnn::Mat>& top_blobs,
                                      const ncnn::Option& opt) const
@@ -361,6 +377,11 @@ int AdaptiveWindowAttention::forward_impl(const std::vector<ncnn::Mat>& bottom_b
         return -1;
     if (device && elemsize != 4 && elemsize != 2)
         return -1;
+    // fused QKV projection: the first two blobs are its device bf16 inputs
+    const SharedLinear* qkv = split_qkv ? 0 : qkv_projection;
+    if (qkv && (!device || elemsize != 2 || device_blob_dtype(elemsize, opt) != S2_DTYPE_BF16))
+        return -1;
+    const int in_width = qkv ? qkv->input_width() : inner_dim * 3;
 
     // Blob shapes (reference :783-797).
     if (split_qkv)
@@ -371,8 +392,8 @@ int AdaptiveWindowAttention::forward_impl(const std::vector<ncnn::Mat>& bottom_b
                 return -1;
         }
     }
-    else if (video_qkv.dims != 2 || text_qkv.dims != 2 || video_qkv.w != inner_dim * 3 ||
-             text_qkv.w != inner_dim * 3)
+    else if (video_qkv.dims != 2 || text_qkv.dims != 2 || video_qkv.w != in_width ||
+             text_qkv.w != in_width)
         return -1;
 
     // Runtime shapes: from host shape blobs (reference :799-817), or from
@@ -491,6 +512,17 @@ int AdaptiveWindowAttention::forward_impl(const std::vector<ncnn::Mat>& bottom_b
         const void* tv = split_qkv ? bottom_blobs[5].data : t + 2 * inner_dim * elemsize;
         const long vstride = split_qkv ? inner_dim : 3 * inner_dim;
         const s2_dtype dtype = device_blob_dtype(elemsize, opt);
+        if (qkv)
+        {
+            const uint16_t* w = 0;
+            const float* b = 0;
+            ret = qkv->device_weights(&w, &b);
+            if (ret != 0)
+                return ret;
+            return s2_awa_qkv_forward(plan, video_qkv.data, text_qkv.data, in_width, w, b, norms, freqs,
+                                      top_blobs[0].data, top_blobs[1].data, dtype, workspace.get(),
+                                      workspace.size(), device->stream());
+        }
         return s2_awa_forward(plan, norms, freqs, vq, vk, vv, vstride, tq, tk, tv, vstride, dtype,
                               top_blobs[0].data, top_blobs[1].data, dtype, workspace.get(),
                               workspace.size(), device->stream());

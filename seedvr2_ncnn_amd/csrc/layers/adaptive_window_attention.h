@@ -20,6 +20,7 @@
 #include <layer.h>
 
 #include "hip_allocator.h"
+#include "shared_linear.h"
 
 struct s2_awa_plan;
 
@@ -97,6 +98,15 @@ public:
     void set_runtime_shapes(const std::vector<std::array<int, 3> >& video_shapes,
                             const std::vector<int>& text_lengths);
 
+    // Fused QKV projection (s2_awa_qkv_forward), set by a graph optimiser:
+    // the 4-input form's first two blobs are then the projection's inputs
+    // (width qkv->input_width(), device bf16), and `qkv` supplies the
+    // weights.  Requires a bias-free or biased SharedLinear of width
+    // 3 * heads * head_dim without activation, head_dim 64 or 128,
+    // heads * head_dim a multiple of 256 and an input width that is a
+    // multiple of 64; returns -1 otherwise.  nullptr undoes it.
+    int set_qkv_projection(const SharedLinear* qkv);
+
 private:
     // forward and create_pipeline without the mapping of C-ABI codes to the
     // reference's (layer_status)
@@ -133,6 +143,7 @@ private:
     mutable DeviceBuffer weights_gpu;      // [4][d] norms then [P] freqs, fp32
     mutable s2_awa_plan* plan;
     mutable bool plan_rope_cached;         // the plan holds the table of weights_gpu's freqs
+    const SharedLinear* qkv_projection;    // fused QKV projection, or null
     mutable std::vector<int> plan_shapes;
     mutable std::vector<int> plan_text_lengths;
     mutable DeviceBuffer workspace;

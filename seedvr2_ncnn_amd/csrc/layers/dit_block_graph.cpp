@@ -9,7 +9,7 @@
 
 namespace seedvr2 {
 
-DiTBlockGraph::DiTBlockGraph(void* stream) : alloc(stream), fused_gelu(0) {}
+DiTBlockGraph::DiTBlockGraph(void* stream) : alloc(stream), fused_gelu(0), fused_qkv(0) {}
 
 DiTBlockGraph::~DiTBlockGraph()
 {
@@ -40,7 +40,7 @@ int DiTBlockGraph::register_layers()
 }
 
 int DiTBlockGraph::load(const char* param_path, const char* model_path, bool fp32_blobs,
-                        bool fuse_gelu)
+                        bool fuse_gelu, bool fuse_qkv)
 {
     net.clear();
     net.opt.use_bf16_storage = !fp32_blobs;
@@ -51,11 +51,12 @@ int DiTBlockGraph::load(const char* param_path, const char* model_path, bool fp3
     if (ret == 0)
         ret = net.load_model(model_path);
     fused_gelu = (ret == 0 && fuse_gelu) ? net.fuse_shared_linear_gelu() : 0;
+    fused_qkv = (ret == 0 && fuse_qkv && !fp32_blobs) ? net.fuse_qkv_attention() : 0;
     return ret;
 }
 
 int DiTBlockGraph::load_mem(const char* param_text, const unsigned char* model,
-                            size_t model_bytes, bool fp32_blobs, bool fuse_gelu)
+                            size_t model_bytes, bool fp32_blobs, bool fuse_gelu, bool fuse_qkv)
 {
     net.clear();
     net.opt.use_bf16_storage = !fp32_blobs;
@@ -66,6 +67,7 @@ int DiTBlockGraph::load_mem(const char* param_text, const unsigned char* model,
     if (ret == 0)
         ret = net.load_model(model, model_bytes);
     fused_gelu = (ret == 0 && fuse_gelu) ? net.fuse_shared_linear_gelu() : 0;
+    fused_qkv = (ret == 0 && fuse_qkv && !fp32_blobs) ? net.fuse_qkv_attention() : 0;
     return ret;
 }
 

@@ -36,12 +36,15 @@ public:
 
     // Registers the layers and loads the graph; the 16-bit storage option
     // (bf16 blobs between the GEMMs and the attention) is on unless
-    // fp32_blobs.  fuse_gelu folds SharedLinear -> GELU pairs.  Returns 0 or
-    // the first failing code of load_param / load_model.
+    // fp32_blobs.  fuse_gelu folds SharedLinear -> GELU pairs; fuse_qkv (bf16
+    // blobs only) folds each QKV SharedLinear into the attention layer it
+    // feeds (ncnn::Net::fuse_qkv_attention), so the QKV blobs cannot be
+    // extracted as checkpoints.  Returns 0 or the first failing code of
+    // load_param / load_model.
     int load(const char* param_path, const char* model_path, bool fp32_blobs = false,
-             bool fuse_gelu = true);
+             bool fuse_gelu = true, bool fuse_qkv = true);
     int load_mem(const char* param_text, const unsigned char* model, size_t model_bytes,
-                 bool fp32_blobs = false, bool fuse_gelu = true);
+                 bool fp32_blobs = false, bool fuse_gelu = true, bool fuse_qkv = true);
 
     // One pass of the graph.  inputs[0..9] are in0..in9 (host or device
     // Mats); out_video / out_text receive out0 / out1 as device blobs of this
@@ -58,6 +61,7 @@ public:
     void clear_blobs();
 
     int fused_gelu_count() const { return fused_gelu; }
+    int fused_qkv_count() const { return fused_qkv; }
     HipDeviceAllocator& allocator() { return alloc; }
     ncnn::Net net;
     AdaptiveWindowRuntimeState runtime_state;
@@ -67,6 +71,7 @@ private:
 
     HipDeviceAllocator alloc;
     int fused_gelu;
+    int fused_qkv;
     std::vector<void*> last_blocks;   // uploads and outputs of the last run
 };
 

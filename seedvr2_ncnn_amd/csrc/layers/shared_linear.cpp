@@ -160,6 +160,19 @@ int SharedLinear::upload_weights_locked() const
     return ret;
 }
 
+int SharedLinear::device_weights(const uint16_t** weight, const float** bias) const
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    if (!params_loaded || weight_data.empty())
+        return -1;
+    const int ret = upload_weights_locked();
+    if (ret != 0)
+        return ret;
+    *weight = static_cast<const uint16_t*>(weight_gpu.get());
+    *bias = bias_term ? static_cast<const float*>(bias_gpu.get()) : 0;
+    return 0;
+}
+
 int SharedLinear::forward(const std::vector<ncnn::Mat>& bottom_blobs,
                           std::vector<ncnn::Mat>& top_blobs,
                           const ncnn::Option& opt) const

@@ -40,6 +40,15 @@ public:
     // a graph optimiser that folds a following GELU layer.  Returns 0 or -1.
     int set_activation(int act);
 
+    // For a graph optimiser that fuses this projection into the attention
+    // layer consuming it: the widths, the activation, and the device copy of
+    // the weights (bf16 [N][K], uploaded first if needed) and bias (fp32 [N],
+    // or null without a bias term).  device_weights returns 0 or an error code.
+    int input_width() const { return num_input; }
+    int output_width() const { return num_output; }
+    int activation_kind() const { return activation; }
+    int device_weights(const uint16_t** weight, const float** bias) const;
+
 private:
     // forward and create_pipeline without the mapping of C-ABI codes to the
     // reference's (layer_status)

@@ -11,6 +11,7 @@
 
 #include "hip_allocator.h"
 #include "modelbin.h"
+#include "adaptive_window_attention.h"
 #include "shared_linear.h"
 #include "paramdict.h"
 #include "seedvr2_hip.h"
@@ -308,6 +309,38 @@ int Net::fuse_shared_linear_gelu() {
         for (size_t g = 0; g < gelus.size(); g++) {
             static_cast<GeluLayer*>(layers_[gelus[g]])->passthrough = true;
             passthrough_[gelus[g]] = 1;
+        }
+        ++fused;
+    }
+    return fused;
+}
+
+int Net::fuse_qkv_attention() {
+    int fused = 0;
+    for (size_t ai = 0; ai < layers_.size(); ai++) {
+        Layer* a = layers_[ai];
+        if (a->type != "AdaptiveWindowAttention" || a->bottoms.size() != 4) continue;
+        const int b0 = a->bottoms[0], b1 = a->bottoms[1];
+        const int pi = blobs_[b0].producer;
+        if (pi < 0 || blobs_[b1].producer != pi) continue;
+        Layer* p = layers_[pi];
+        if (p->type != "SharedLinear" || p->bottoms.size() != 2 || p->tops.size() != 2 ||
+            p->tops[0] != b0 || p->tops[1] != b1 || consumer_count_[b0] != 1 ||
+            consumer_count_[b1] != 1)
+            continue;
+        seedvr2::SharedLinear* sl = dynamic_cast<seedvr2::SharedLinear*>(p);
+        seedvr2::AdaptiveWindowAttention* awa = dynamic_cast<seedvr2::AdaptiveWindowAttention*>(a);
+        if (!sl || !awa || awa->set_qkv_projection(sl) != 0) continue;
+        // the attention layer reads the projection's inputs in its place
+        for (int i = 0; i < 2; i++) {
+            const int in = p->bottoms[i];
+            a->bottoms[i] = in;
+            blobs_[in].consumer = (int)ai;
+        }
+        p->bottoms.clear();
+        for (int i = 0; i < 2; i++) {
+            blobs_[p->tops[i]].producer = -1;
+            consumer_count_[p->tops[i]] = 0;
         }
         ++fused;
     }

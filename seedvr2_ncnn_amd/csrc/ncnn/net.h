@@ -78,6 +78,16 @@ public:
     // of SharedLinear layers folded.
     int fuse_shared_linear_gelu();
 
+    // This build: SharedLinear -> AdaptiveWindowAttention fusion.  When the
+    // two tops of a SharedLinear are exactly the video and text QKV blobs of
+    // an attention layer (4-input form) and nothing else reads them, the
+    // attention layer takes the projection's inputs and runs the projection
+    // in its own kernel (s2_awa_qkv_forward): the QKV blobs are never formed.
+    // The projection's tops then have no producer (extracting them fails).
+    // Device bf16 blobs only (the attention layer returns -1 otherwise).
+    // Call after load_model; returns the number of pairs fused.
+    int fuse_qkv_attention();
+
 protected:
     friend class Extractor;
     int forward_layer(int layer_index, std::vector<Mat>& blob_mats, std::vector<int>& pending,

@@ -284,14 +284,17 @@ int h_build_plan(const int* shapes, int batch, const int* target, int shifted, i
 
 // ---- DiT block graph (seedvr2::DiTBlockGraph over ncnn::Net) -------------------
 
-// Loads a block graph from .param text and .bin bytes.  Returns load's code;
-// *out is the graph (destroy with h_graph_destroy) or null.
+// Loads a block graph from .param text and .bin bytes; fuse: bit 0 folds
+// SharedLinear -> GELU, bit 1 folds the QKV SharedLinear into the attention.
+// Returns load's code; *out is the graph (destroy with h_graph_destroy) or
+// null.
 int h_graph_create(const char* param_text, const void* model, long model_bytes, int fp32_blobs,
-                   int fuse_gelu, void** out) {
+                   int fuse, void** out) {
     *out = 0;
     seedvr2::DiTBlockGraph* g = new seedvr2::DiTBlockGraph(0);
     const int ret = g->load_mem(param_text, static_cast<const unsigned char*>(model),
-                                (size_t)model_bytes, fp32_blobs != 0, fuse_gelu != 0);
+                                (size_t)model_bytes, fp32_blobs != 0, (fuse & 1) != 0,
+                                (fuse & 2) != 0);
     if (ret != 0) {
         delete g;
         return ret;
@@ -302,6 +305,10 @@ int h_graph_create(const char* param_text, const void* model, long model_bytes, 
 
 int h_graph_fused_gelu(void* graph) {
     return static_cast<seedvr2::DiTBlockGraph*>(graph)->fused_gelu_count();
+}
+
+int h_graph_fused_qkv(void* graph) {
+    return static_cast<seedvr2::DiTBlockGraph*>(graph)->fused_qkv_count();
 }
 
 // Layer count and device bytes the graph's allocator holds (blocks in use

@@ -15,7 +15,9 @@ reference's BlockGraph is (src/seedvr2/seedvr2_dit.cpp:722-833) and checked
     764-978, oracle.ada_out) at max-abs <= 2e-2 and cosine >= 0.9999;
  3. with the GELU layers left as layers (no folding into SharedLinear), bit
     for bit against the chain with s2_gelu, and a second run of the same
-    graph, which reuses pooled device blocks, against the first."""
+    graph, which reuses pooled device blocks, against the first;
+ 4. with each QKV SharedLinear folded into its attention layer
+    (s2_awa_qkv_forward), bit for bit against the unfused graph."""
 import ctypes
 import os
 import sys
@@ -42,6 +44,7 @@ def _lib():
     P, vp, ci = ctypes.POINTER, ctypes.c_void_p, ctypes.c_int
     L.h_graph_create.argtypes = [ctypes.c_char_p, vp, ctypes.c_long, ci, ci, P(vp)]
     L.h_graph_fused_gelu.argtypes = [vp]
+    L.h_graph_fused_qkv.argtypes = [vp]
     L.h_graph_destroy.argtypes = [vp]
     L.h_graph_run.argtypes = [vp, P(ci), P(ci), ci, P(HBlob), P(HBlob), ci,
                               P(ctypes.c_char_p)]
@@ -49,7 +52,9 @@ def _lib():
 
 
 class Graph:
-    def __init__(self, fuse=True):
+    def __init__(self, fuse=1):
+        """fuse: bit 0 folds SharedLinear -> GELU, bit 1 the QKV SharedLinear
+        into the attention layer."""
         with open(dit_graph.PARAM_PATH) as f:
             text = f.read()
         self.weights = dit_graph.block_weights()
@@ -59,6 +64,7 @@ class Graph:
         assert _lib().h_graph_create(text.encode(), self._buf, len(model), 0, int(fuse),
                                      ctypes.byref(self.h)) == 0
         self.fused = _lib().h_graph_fused_gelu(self.h)
+        self.fused_qkv = _lib().h_graph_fused_qkv(self.h)
 
     def run(self, inputs, checkpoints=()):
         """inputs: 10 torch tensors (device) or numpy arrays (host) for in0..in9.
@@ -239,3 +245,29 @@ def test_s2_gelu_against_the_erf_closed_form():
         tol = 2e-6 if dt == torch.float32 else 1e-2
         assert float((y - want).abs().max()) <= tol * max(1.0, float(want.abs().max())), dt
     assert float((capi.gelu(x) - ref).abs().max()) < 2e-6
+
+
+def test_graph_with_qkv_folded_into_the_attention_matches_the_unfused_graph():
+    """ncnn::Net::fuse_qkv_attention: each block's QKV projection runs inside
+    its attention layer (s2_awa_qkv_forward, which rounds the projection to
+    bf16 exactly as the QKV blob holds it; k = 256 is not split, so every
+    element accumulates in the same order).  Outputs equal the unfused
+    graph's bit for bit, on a first run and on a second one over pooled
+    device blocks; the folded QKV blob can no longer be extracted."""
+    import torch
+    x_v, x_t, shape_blob, tl_blob, mods = _inputs(3)
+    inputs = [x_v, x_t, shape_blob, tl_blob] + mods
+    plain, fused = Graph(fuse=1), Graph(fuse=3)
+    try:
+        assert plain.fused_qkv == 0 and fused.fused_qkv == 2 and fused.fused == 2
+        ref = plain.run(inputs)
+        for _ in range(2):
+            got = fused.run(inputs)
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(got[0].cpu().numpy(), ref[0].cpu().numpy())
+            np.testing.assert_array_equal(got[1].cpu().numpy(), ref[1].cpu().numpy())
+        with pytest.raises(AssertionError):
+            fused.run(inputs, checkpoints=["b0_qkv_v"])
+    finally:
+        plain.close()
+        fused.close()

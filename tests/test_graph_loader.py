@@ -22,18 +22,21 @@ def _lib():
     L.h_graph_create.argtypes = [ctypes.c_char_p, vp, ctypes.c_long, ci, ci, P(vp)]
     L.h_graph_fused_gelu.argtypes = [vp]
     L.h_graph_layer_count.argtypes = [vp]
+    L.h_graph_fused_qkv.argtypes = [vp]
     L.h_graph_destroy.argtypes = [vp]
     return L
 
 
-def _create(text, model, fuse=1):
+def _create(text, model, fuse=1, fp32_blobs=0, qkv=False):
     L = _lib()
     g = ctypes.c_void_p()
     buf = ctypes.create_string_buffer(model, max(1, len(model)))
-    ret = L.h_graph_create(text.encode(), buf, len(model), 0, fuse, ctypes.byref(g))
+    ret = L.h_graph_create(text.encode(), buf, len(model), fp32_blobs, fuse, ctypes.byref(g))
     info = None
     if ret == 0:
         info = (L.h_graph_layer_count(g), L.h_graph_fused_gelu(g))
+        if qkv:
+            info += (L.h_graph_fused_qkv(g),)
         L.h_graph_destroy(g)
     return ret, info
 
@@ -67,6 +70,15 @@ def test_loads_and_folds_gelu(graph):
     text, model = graph
     assert _create(text, model) == (0, (42, 2))
     assert _create(text, model, fuse=0) == (0, (42, 0))
+
+
+def test_folds_the_qkv_projection_into_the_attention(graph):
+    # both blocks' QKV SharedLinear -> AdaptiveWindowAttention pairs, on bf16
+    # blobs only; the GELU folding is independent of it
+    text, model = graph
+    assert _create(text, model, fuse=3, qkv=True) == (0, (42, 2, 2))
+    assert _create(text, model, fuse=2, qkv=True) == (0, (42, 0, 2))
+    assert _create(text, model, fuse=3, fp32_blobs=1, qkv=True) == (0, (42, 2, 0))
 
 
 @pytest.mark.parametrize("edit, code", [
