@@ -289,11 +289,15 @@ __device__ __forceinline__ float sum_with_lane_xor32(float x) {
 //
 // LDS swizzles (16-byte chunk c of row r stored at position c ^ f(r)) keep
 // the rows one ds_read_b128 phase reads on distinct banks:
-//   K rows (D*2 bytes):  f(r) = r & 15 for D = 128, (r ^ (r >> 3)) & 7 for D = 64
+//   K rows (D*2 bytes):  f(r) = r with bits 2 and 3 swapped, its low three
+//     bits for D = 64.  A ds_read_b128 phase covers 8 lanes; the A-operand
+//     row of lane l32 is l32 with bits 2 and 3 swapped, so f of its row is
+//     l32 & 15, and the 8 lanes of a phase read 8 distinct chunk positions.
 //   V^T rows (64 bytes): f(r) = ((r >> 1) ^ (r >> 3)) & 3
 template <int D>
 __device__ __forceinline__ int k_swizzle(int r) {
-    return D == 128 ? (r & 15) : ((r ^ (r >> 3)) & 7);
+    const int f = (r & 3) | ((r >> 1) & 4) | ((r << 1) & 8);
+    return D == 128 ? f : (f & 7);
 }
 __device__ __forceinline__ int vt_swizzle(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
