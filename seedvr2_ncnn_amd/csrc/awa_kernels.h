@@ -18,7 +18,7 @@ hipError_t launch_awa_prologue(const s2_awa_plan& plan, const void* vq, const vo
                                uint16_t* vt_out, hipStream_t stream);
 hipError_t launch_awa_attention(const s2_awa_plan& plan, const uint16_t* q, const uint16_t* k,
                                 const uint16_t* vt, void* out_video, int out_kind,
-                                float* text_partial, hipStream_t stream);
+                                float* text_partial, const float* norm, hipStream_t stream);
 hipError_t launch_awa_text_pool(const s2_awa_plan& plan, const float* partial, void* out_text,
                                 int out_kind, hipStream_t stream);
 hipError_t launch_awa_plan_tables(const s2_awa_plan& plan, int* indices, int* inverse,

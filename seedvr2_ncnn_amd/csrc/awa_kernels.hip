@@ -280,12 +280,15 @@ __device__ __forceinline__ float sum_with_lane_xor32(float x) {
 // i = 8s+j of lane group g then holds key 16s + 8g + j, which is exactly the
 // B-operand slot 8g+j of the 16-key PV step s.
 //
-// Online softmax in the log2 domain with a lazily updated row max: the
-// running max only moves when a tile's max exceeds it by more than 8, so
-// un-normalised probabilities stay below 2^8 and the accumulator rescale is
-// skipped for the many tiles that do not raise any row max of the wave.
-// The result is the same softmax; only the reference point of the
-// exponentials changes.
+// Softmax in the log2 domain.  When the norm weights bound every exponent
+// (|s| * log2(e) / sqrt(D) <= B <= 60, see the score bound below) the
+// exponentials are taken relative to the fixed reference B: no row maximum,
+// rescale or wave vote per tile.  Otherwise it is an online softmax with a
+// lazily updated row max: the running max only moves when a tile's max
+// exceeds it by more than 8, so un-normalised probabilities stay below 2^8
+// and the accumulator rescale is skipped for the many tiles that do not
+// raise any row max of the wave.  Either way the result is the same softmax;
+// only the reference point of the exponentials changes.
 //
 // LDS swizzles (16-byte chunk c of row r stored at position c ^ f(r)) keep
 // the rows one ds_read_b128 phase reads on distinct banks:
@@ -306,7 +309,8 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     const WinMeta* __restrict__ wins, const AttnItem* __restrict__ items, int slots_per_xcd,
     const uint16_t* __restrict__ q_in, const uint16_t* __restrict__ k_in,
     const uint16_t* __restrict__ vt_in, long seg_total, float scale_log2, int official_bf16,
-    void* __restrict__ out_video, int out_kind, int inner, float* __restrict__ text_partial) {
+    void* __restrict__ out_video, int out_kind, int inner, float* __restrict__ text_partial,
+    const float* __restrict__ norm) {
     constexpr int KT = 32;                  // keys per tile
     constexpr int STAGES = 3;
     constexpr int KB = KT * D * 2;          // K tile bytes
@@ -320,7 +324,9 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     constexpr int VI_W = VB / 1024 / 4;     // V^T DMA instructions per wave per tile
     constexpr int DMA_W = KI_W + VI_W;
     constexpr float kLazy = 8.f;            // max growth (log2) tolerated before rescaling
+    constexpr float kFixedMax = 60.f;       // largest score bound taken as the fixed reference
     __shared__ __attribute__((aligned(1024))) uint8_t lds[STAGES * SB];
+    __shared__ float wmax[4];
 
     const int bid = blockIdx.x;
     const AttnItem it = items[(bid % kNumXcd) * slots_per_xcd + bid / kNumXcd];
@@ -351,6 +357,24 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
         }
     }
 
+    // Score bound.  q and k rows are RMS-normalised (norm <= sqrt(D)),
+    // scaled by the norm weights, rotated and rounded to bf16, so
+    // |q.k| <= D * Wq * Wk * (1 + 2^-7) with Wq (Wk) the largest |weight| of
+    // the video and text q (k) norms, and every exponent s * scale_log2 lies
+    // within +-B, B = sqrt(D) log2(e) Wq Wk (1 + 2^-6).  For B <= kFixedMax the
+    // softmax is taken relative to the fixed reference B instead of a running
+    // row maximum: every exponential lies in [2^-2B, 1] (normal floats, also
+    // as bf16), so no maximum, rescale or vote is needed.  A NaN weight gives
+    // a NaN bound and the running-maximum path.
+    {
+        float a = norm[tid];
+        if (D == 128) a = __builtin_elementwise_maximum(fabsf(a), fabsf(norm[256 + tid]));
+        a = fabsf(a);
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1)
+            a = __builtin_elementwise_maximum(a, __shfl_xor(a, off));
+        if (lane == 0) wmax[wave] = a;
+    }
     // DMA sources: this (window, head)'s K rows [padded][D] and V^T rows
     // [D][seg_total] starting at the window's segment.
     const i32x4 rk = buffer_rsrc(k_in + head_rows * D, (uint32_t)(padded * D * 2));
@@ -404,8 +428,20 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     // the first MFMA of every tile, which also waits for the DMA issued two
     // tiles ahead.  The first tile needs its DMA anyway.
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    __syncthreads();
+    // [vq | vk | tq | tk]: D = 128, waves 0-1 hold q weights, 2-3 k weights;
+    // D = 64, waves 0 and 2 q, 1 and 3 k
+    const float wq = D == 128 ? __builtin_elementwise_maximum(wmax[0], wmax[1])
+                              : __builtin_elementwise_maximum(wmax[0], wmax[2]);
+    const float wk = D == 128 ? __builtin_elementwise_maximum(wmax[2], wmax[3])
+                              : __builtin_elementwise_maximum(wmax[1], wmax[3]);
+    const float bound = sqrtf((float)D) * 1.4426950408889634f * 1.015625f * wq * wk;
+    const bool fixed_ref = bound <= kFixedMax;   // false for a NaN bound
+    if (fixed_ref) m_run = bound;
     // The tile loop is unrolled by the stage count so that every LDS
     // address is a loop-invariant register plus a constant stage offset.
+    auto tiles = [&](auto fixed_tag) {
+    constexpr bool FIXED = decltype(fixed_tag)::value;
 #pragma unroll 1
     for (int kt0 = 0; kt0 < nkt; kt0 += STAGES) {
 #pragma unroll
@@ -461,15 +497,17 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
                     if (key >= w.seq) s[i] = -INFINITY;
                 }
             }
-            float mx = max3_scores(s[0], s[1], s[2]);
-#pragma unroll
-            for (int i = 3; i < 15; i += 2) mx = max3_scores(mx, s[i], s[i + 1]);
-            mx = max3_scores(mx, mx, s[15]);
-            mx = max_with_lane_xor32(mx) * scale_log2;
             float alpha = 1.f;
-            if (mx > m_run + kLazy) {
-                alpha = __builtin_amdgcn_exp2f(m_run - mx);   // 0 on the first tile
-                m_run = mx;
+            if constexpr (!FIXED) {
+                float mx = max3_scores(s[0], s[1], s[2]);
+#pragma unroll
+                for (int i = 3; i < 15; i += 2) mx = max3_scores(mx, s[i], s[i + 1]);
+                mx = max3_scores(mx, mx, s[15]);
+                mx = max_with_lane_xor32(mx) * scale_log2;
+                if (mx > m_run + kLazy) {
+                    alpha = __builtin_amdgcn_exp2f(m_run - mx);   // 0 on the first tile
+                    m_run = mx;
+                }
             }
             float p[16];
 #pragma unroll
@@ -484,12 +522,16 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
             for (int w2 = 8; w2 >= 1; w2 >>= 1)
 #pragma unroll
                 for (int i = 0; i < w2; ++i) p[i] += p[i + w2];
-            l_run = l_run * alpha + p[0];
-            if (__any(alpha != 1.f)) {
+            if constexpr (FIXED) {
+                l_run += p[0];
+            } else {
+                l_run = l_run * alpha + p[0];
+                if (__any(alpha != 1.f)) {
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt)
+                    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+                        for (int i = 0; i < 16; ++i) o[dt][i] *= alpha;
+                }
             }
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt) {
@@ -502,6 +544,11 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
             }
         }
     }
+    };
+    if (fixed_ref)
+        tiles(std::true_type{});
+    else
+        tiles(std::false_type{});
 
     const float l_tot = sum_with_lane_xor32(l_run);
     const float inv_l = 1.f / l_tot;
@@ -715,7 +762,7 @@ hipError_t launch_awa_prologue(const s2_awa_plan& plan, const void* vq, const vo
 
 hipError_t launch_awa_attention(const s2_awa_plan& plan, const uint16_t* q, const uint16_t* k,
                                 const uint16_t* vt, void* out_video, int out_kind,
-                                float* text_partial, hipStream_t stream) {
+                                float* text_partial, const float* norm, hipStream_t stream) {
     const int d = plan.config.head_dim;
     const int inner = plan.config.heads * d;
     const float scale_log2 = 1.4426950408889634f / sqrtf((float)d);
@@ -724,11 +771,11 @@ hipError_t launch_awa_attention(const s2_awa_plan& plan, const uint16_t* q, cons
     if (d == 128)
         awa_attention_kernel<128><<<grid, 256, 0, stream>>>(
             plan.d_wins, plan.d_items, plan.slots_per_xcd, q, k, vt, plan.seg_total, scale_log2,
-            plan.config.official_bf16_attention, out_video, out_kind, inner, text_partial);
+            plan.config.official_bf16_attention, out_video, out_kind, inner, text_partial, norm);
     else if (d == 64)
         awa_attention_kernel<64><<<grid, 256, 0, stream>>>(
             plan.d_wins, plan.d_items, plan.slots_per_xcd, q, k, vt, plan.seg_total, scale_log2,
-            plan.config.official_bf16_attention, out_video, out_kind, inner, text_partial);
+            plan.config.official_bf16_attention, out_video, out_kind, inner, text_partial, norm);
     else
         return hipErrorInvalidValue;
     return hipGetLastError();

@@ -568,7 +568,8 @@ int s2_awa_forward(const s2_awa_plan* plan, const float* norm_weights, const flo
                                    text_k, text_v, text_row_stride, (int)in_dtype, norm_weights, rope, q,
                                    k, vt, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[2], s));
-    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart, s));
+    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart,
+                                    norm_weights, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[3], s));
     S2_HIP(s2::launch_awa_text_pool(*plan, tpart, out_text, (int)out_dtype, s));
     if (tm.on) {
@@ -622,7 +623,8 @@ int s2_awa_qkv_forward(const s2_awa_plan* plan, const void* x_video, const void*
                               qkv_weight, qkv_bias, norm_weights, rope, q, k, vt, s));
     S2_HIP(s2::launch_awa_text_broadcast(*plan, q, k, vt, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[2], s));
-    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart, s));
+    S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart,
+                                    norm_weights, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[3], s));
     S2_HIP(s2::launch_awa_text_pool(*plan, tpart, out_text, (int)out_dtype, s));
     if (tm.on) {

@@ -371,3 +371,38 @@ def test_layer_rebuilds_plan_and_rope_table_when_shapes_change():
         rv, rt = oracle_awa(case, heads, d, target, 1, 1e-5, pairs, shapes, tl)
         assert_close(ov, rv, f"video {shapes}")
         assert_close(ot, rt, f"text {shapes}")
+
+
+# ---- softmax reference: fixed score bound and running maximum ---------------------------
+# The attention kernel takes the softmax relative to a fixed reference when the
+# norm weights bound every exponent to |s * log2(e) / sqrt(d)| <= 60, and
+# relative to a running row maximum otherwise.  The official bf16 mode rounds
+# q and k to bf16 in the oracle as on the device, so even very sharp softmaxes
+# compare at the usual bar.
+NORM_CASES = {
+    "unit": (1.0, 1.0, 1.0, 1.0),          # bound ~18 (d = 128): fixed reference
+    "near_limit": (1.7, 1.7, 1.7, 1.7),    # bound ~54: fixed reference
+    "large": (2.4, 2.4, 2.4, 2.4),         # bound ~100: running maximum
+    "text_q_only": (1.0, 1.0, 40.0, 1.0),  # only the text q weights are large
+    "text_k_only": (1.0, 1.0, 1.0, 30.0),
+}
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("name", list(NORM_CASES))
+def test_softmax_reference_paths(name, d):
+    import torch
+    shapes, tl = [(2, 16, 24), (1, 9, 13)], [64, 7]
+    heads, pairs = 4, (21 if d == 128 else 10)
+    case = make_awa_inputs(1200 + d + len(name), shapes, tl, heads, d, pairs, bf16=True)
+    g = np.random.default_rng(1300 + d)
+    scales = np.asarray(NORM_CASES[name], np.float32)[:, None]
+    case["norms"] = (scales * (1.0 + 0.02 * g.standard_normal((4, d)))).astype(np.float32)
+    for shifted in (0, 1):
+        ov, ot = _run_capi(case, heads, d, (4, 3, 3), shifted, pairs, shapes, tl, True,
+                           torch.float32, official=True)
+        rv, rt = oracle_awa(case, heads, d, (4, 3, 3), shifted, 1e-5, pairs, shapes, tl,
+                            official_bf16=True)
+        assert np.isfinite(ov).all() and np.isfinite(ot).all()
+        assert_close(ov, rv, f"{name} video (shifted={shifted})")
+        assert_close(ot, rt, f"{name} text (shifted={shifted})")
