@@ -341,6 +341,11 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     const int padded = (w.seq + kSegAlign - 1) / kSegAlign * kSegAlign;
     const int nkt = (w.seq + KT - 1) / KT;
 
+    // this thread's norm weights for the score bound below (their latency
+    // overlaps that of the Q loads and the first DMAs)
+    const float nw0 = norm[tid];
+    const float nw1 = D == 128 ? norm[256 + tid] : 0.f;
+
     // Q fragment (B operand of S^T = K Q^T): query row l32 of this wave,
     // channels 16kk + 8g .. +7.
     const int qrow = it.q_row0 + wave * 32 + l32;
@@ -357,24 +362,6 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
         }
     }
 
-    // Score bound.  q and k rows are RMS-normalised (norm <= sqrt(D)),
-    // scaled by the norm weights, rotated and rounded to bf16, so
-    // |q.k| <= D * Wq * Wk * (1 + 2^-7) with Wq (Wk) the largest |weight| of
-    // the video and text q (k) norms, and every exponent s * scale_log2 lies
-    // within +-B, B = sqrt(D) log2(e) Wq Wk (1 + 2^-6).  For B <= kFixedMax the
-    // softmax is taken relative to the fixed reference B instead of a running
-    // row maximum: every exponential lies in [2^-2B, 1] (normal floats, also
-    // as bf16), so no maximum, rescale or vote is needed.  A NaN weight gives
-    // a NaN bound and the running-maximum path.
-    {
-        float a = norm[tid];
-        if (D == 128) a = __builtin_elementwise_maximum(fabsf(a), fabsf(norm[256 + tid]));
-        a = fabsf(a);
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1)
-            a = __builtin_elementwise_maximum(a, __shfl_xor(a, off));
-        if (lane == 0) wmax[wave] = a;
-    }
     // DMA sources: this (window, head)'s K rows [padded][D] and V^T rows
     // [D][seg_total] starting at the window's segment.
     const i32x4 rk = buffer_rsrc(k_in + head_rows * D, (uint32_t)(padded * D * 2));
@@ -428,6 +415,35 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     // the first MFMA of every tile, which also waits for the DMA issued two
     // tiles ahead.  The first tile needs its DMA anyway.
     __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    // Score bound.  q and k rows are RMS-normalised (norm <= sqrt(D)),
+    // scaled by the norm weights, rotated and rounded to bf16, so
+    // |q.k| <= D * Wq * Wk * (1 + 2^-7) with Wq (Wk) the largest |weight| of
+    // the video and text q (k) norms, and every exponent s * scale_log2 lies
+    // within +-B, B = sqrt(D) log2(e) Wq Wk (1 + 2^-6).  For B <= kFixedMax the
+    // softmax is taken relative to the fixed reference B instead of a running
+    // row maximum: every exponential lies in [2^-2B, 1] (normal floats, also
+    // as bf16), so no maximum, rescale or vote is needed.  A NaN weight gives
+    // a NaN bound and the running-maximum path.
+    {
+        // wave maximum of |weight|: DPP within rows of 16 lanes, then the
+        // four row results (NaN-propagating throughout)
+        float a = D == 128 ? __builtin_elementwise_maximum(fabsf(nw0), fabsf(nw1)) : fabsf(nw0);
+        a = __builtin_elementwise_maximum(
+            a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0xB1, 0xF, 0xF, false)));
+        a = __builtin_elementwise_maximum(
+            a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x4E, 0xF, 0xF, false)));
+        a = __builtin_elementwise_maximum(
+            a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x141, 0xF, 0xF, false)));
+        a = __builtin_elementwise_maximum(
+            a, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(a), 0x140, 0xF, 0xF, false)));
+        const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 0));
+        const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 16));
+        const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 32));
+        const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(a), 48));
+        if (lane == 0)
+            wmax[wave] = __builtin_elementwise_maximum(__builtin_elementwise_maximum(r0, r1),
+                                                       __builtin_elementwise_maximum(r2, r3));
+    }
     __syncthreads();
     // [vq | vk | tq | tk]: D = 128, waves 0-1 hold q weights, 2-3 k weights;
     // D = 64, waves 0 and 2 q, 1 and 3 k
