@@ -369,6 +369,26 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 
     f32x16 acc[4][2];
 
+    // Thread coordinates for the epilogues, derived from an opaque copy of
+    // the thread index: addresses computed from them are not hoisted above
+    // the main loop, where every register is taken and hoisted values would
+    // be spilled and reloaded one scratch round trip at a time.
+    struct EpiIds {
+        int tid, l32, g, wm, wn;
+    };
+    auto epi_ids = [&]() {
+        EpiIds e;
+        int t = tid;
+        asm volatile("" : "+v"(t));
+        const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+        e.tid = t;
+        e.l32 = t & 31;
+        e.g = (t >> 5) & 1;
+        e.wm = w >> 2;
+        e.wn = w & 3;
+        return e;
+    };
+
     // acc = sum over 64-k iterations [kb, ke) of the current tile.
     //
     // Ping-pong main loop.  The two waves of each SIMD (wave w and w + 4:
@@ -532,21 +552,21 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             // an opaque copy of the thread index: nothing the epilogue derives
             // from it is hoisted above the main loop, where every register is
             // taken
-            int etid = tid;
-            asm volatile("" : "+v"(etid));
+            const EpiIds ei = epi_ids();
+            const int etid = ei.tid;
             const int part = col0 / awa.inner;   // 0 q, 1 k, 2 v
             const int hbase = (col0 - part * awa.inner) / D;
             __syncthreads();   // every wave is done reading the last stage
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int cl = wn * 64 + 32 * j + l32;
+                const int cl = ei.wn * 64 + 32 * j + ei.l32;
                 const float bv = bias ? bias[col0 + cl] : 0.f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int q4 = 0; q4 < 4; ++q4) {
                         // registers 4 q4 .. 4 q4 + 3: rows rl .. rl + 3 of column cl
-                        const int rl = wm * 128 + 32 * i + 8 * q4 + 4 * g;
+                        const int rl = ei.wm * 128 + 32 * i + 8 * q4 + 4 * ei.g;
                         uint16_t hv[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
@@ -693,21 +713,22 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     // 128 rows; each thread then forms silu(g) * u for 4 columns of a row.
     auto swiglu_epilogue = [&]() {
         if constexpr (ACT == S2_ACT_SWIGLU) {
+            const EpiIds ei = epi_ids();
             constexpr int EF = BN * 4 + 16;   // fp32 row pitch (bytes)
             const int oc0 = col0 / 2;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 __syncthreads();   // the stage (h = 0) or the previous half is no longer read
-                if (wm == h) {
+                if (ei.wm == h) {
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const int cl = wn * 64 + 32 * j + l32;
+                        const int cl = ei.wn * 64 + 32 * j + ei.l32;
                         const float bv = bias ? bias[col0 + cl] : 0.f;
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
 #pragma unroll
                             for (int r = 0; r < 16; ++r) {
-                                const int rl = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                                const int rl = 32 * i + 8 * (r >> 2) + 4 * ei.g + (r & 3);
                                 *(float*)(lds + rl * EF + cl * 4) = acc[i][j][r] + bv;
                             }
                     }
@@ -715,7 +736,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 __syncthreads();
 #pragma unroll 2
                 for (int it = 0; it < 8; ++it) {
-                    const int idx = it * 512 + tid;
+                    const int idx = it * 512 + ei.tid;
                     const int rl = idx >> 5;
                     const int c4 = (idx & 31) * 4;
                     const f32x4 gv = *(const f32x4*)(lds + rl * EF + c4 * 4);
@@ -761,11 +782,12 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             swiglu_epilogue();
             return;
         }
+        const EpiIds ei = epi_ids();
         if (YK && (n & 7) == 0) {
             __syncthreads();   // every wave is done reading the last stage
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
-                const int cl = wn * 64 + 32 * j + l32;
+                const int cl = ei.wn * 64 + 32 * j + ei.l32;
                 const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
@@ -773,7 +795,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                     for (int r = 0; r < 16; ++r) {
                         float v = acc[i][j][r] + bv;
                         if (ACT == S2_ACT_GELU) v = gelu(v);
-                        const int rl = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                        const int rl = ei.wm * 128 + 32 * i + 8 * (r >> 2) + 4 * ei.g + (r & 3);
                         if (YK == 2)
                             *(_Float16*)(lds + rl * EP + cl * 2) = (_Float16)v;
                         else
@@ -786,7 +808,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             // stores are non-temporal, leaving the L2 to the operand tiles.
 #pragma unroll 4
             for (int c = 0; c < 16; ++c) {
-                const int idx = c * 512 + tid;
+                const int idx = c * 512 + ei.tid;
                 const int rl = idx >> 5;
                 const int ch = idx & 31;
                 const int col = col0 + ch * 8;
@@ -806,10 +828,10 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 __syncthreads();   // the stage (h = 0) or the previous half is no longer read
-                if (wm == h) {
+                if (ei.wm == h) {
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const int cl = wn * 64 + 32 * j + l32;
+                        const int cl = ei.wn * 64 + 32 * j + ei.l32;
                         const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
 #pragma unroll
                         for (int i = 0; i < 4; ++i)
@@ -817,7 +839,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                             for (int r = 0; r < 16; ++r) {
                                 float v = acc[i][j][r] + bv;
                                 if (ACT == S2_ACT_GELU) v = gelu(v);
-                                const int rl = 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+                                const int rl = 32 * i + 8 * (r >> 2) + 4 * ei.g + (r & 3);
                                 *(float*)(lds + rl * EF + cl * 4) = v;
                             }
                     }
@@ -827,8 +849,8 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 // t/64 + 8c
 #pragma unroll 4
                 for (int c = 0; c < 16; ++c) {
-                    const int rl = (tid >> 6) + 8 * c;
-                    const int ch = tid & 63;
+                    const int rl = (ei.tid >> 6) + 8 * c;
+                    const int ch = ei.tid & 63;
                     const int col = col0 + ch * 4;
                     float* yr = (float*)out_row(h * 128 + rl);
                     if (yr && col < n)
@@ -842,14 +864,14 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         // 8(r/4) + 4g + r%4, column l32
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const int col = col0 + wn * 64 + 32 * j + l32;
+            const int col = col0 + ei.wn * 64 + 32 * j + ei.l32;
             if (col >= n) continue;
             const float bv = bias ? bias[col] : 0.f;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    void* yr = out_row(wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3));
+                    void* yr = out_row(ei.wm * 128 + 32 * i + 8 * (r >> 2) + 4 * ei.g + (r & 3));
                     if (!yr) continue;
                     float v = acc[i][j][r] + bv;
                     if (ACT == S2_ACT_GELU) v = gelu(v);
