@@ -55,6 +55,10 @@ struct AttnItem {
 // Segment rows are padded to this multiple so every key tile is whole.
 constexpr int kSegAlign = 64;
 
+// Entries of slack after a cos/sin table: a reader may fetch the three
+// entries after any (position, pair) entry without using them.
+constexpr int kRopePad = 4;
+
 // MI355X has 8 XCDs; workgroups are dealt to them round-robin.
 constexpr int kNumXcd = 8;
 

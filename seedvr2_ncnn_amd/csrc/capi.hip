@@ -450,14 +450,17 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
     plan->d_qkv_rows = (s2::QkvRow*)(base + sz_w + sz_s + sz_t + sz_c + sz_i);
 
     // Workspace layout: Q and K [heads][seg_total][d], V^T [heads][d][seg_total]
-    // (bf16), the cos/sin table, and fp32 text partials [rows][inner].
+    // (bf16), the cos/sin table (with kRopePad entries of slack: the fused QKV
+    // epilogue reads up to three entries past a row's last pair for pairs it
+    // does not rotate), and fp32 text partials [rows][inner].
     const size_t qkv = align256((size_t)heads * plan->seg_total * d * 2);
     plan->off_q = 0;
     plan->off_k = qkv;
     plan->off_vt = 2 * qkv;
     plan->off_rope = 3 * qkv;
     plan->off_tpart =
-        plan->off_rope + align256(sizeof(float2) * (size_t)rope_pos * config->rope_pairs_per_axis);
+        plan->off_rope +
+        align256(sizeof(float2) * ((size_t)rope_pos * config->rope_pairs_per_axis + s2::kRopePad));
     plan->workspace_bytes = plan->off_tpart + align256(sizeof(float) * (size_t)tpart * inner);
     *out = plan;
     return S2_OK;
@@ -506,7 +509,7 @@ int s2_awa_plan_cache_rope(s2_awa_plan* plan, const float* rope_freqs, s2_stream
     if (!rope_freqs || pairs == 0) return S2_OK;   // cache cleared / nothing to cache
     if (!plan->d_rope_cache)
         S2_HIP(hipMalloc((void**)&plan->d_rope_cache,
-                         sizeof(float2) * (size_t)plan->rope_positions * pairs));
+                         sizeof(float2) * ((size_t)plan->rope_positions * pairs + s2::kRopePad)));
     S2_HIP(s2::launch_rope_table(rope_freqs, pairs, plan->rope_positions,
                                  (float2*)plan->d_rope_cache, (hipStream_t)stream));
     plan->rope_cache_src = rope_freqs;

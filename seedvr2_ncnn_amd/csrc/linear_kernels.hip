@@ -595,34 +595,38 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 }
                 // RoPE slots of this thread's four channel pairs: pair
                 // (2p, 2p+1) of axis a lies in [a*2P, (a+1)*2P); 6P <= D.
-                // A row's position on axis a is bits [sh, sh+16) of one of
-                // its two position words.
+                // The four pairs are consecutive, so they lie on axis axA
+                // from pair pairA on, then (pairs split.. of a chunk that
+                // crosses an axis boundary) on axis axA + 1 from pair 0.  A
+                // row's position on axis a is bits [16(a & 1), +16) of
+                // position word a / 2.
                 const int P = awa.pairs;
-                int pair[4], sh[4], rmask[4];
-                bool rot[4], word2[4];
+                bool rot[4];
 #pragma unroll
-                for (int pp = 0; pp < 4; ++pp) {
-                    const int d = d0 + 2 * pp;
-                    rot[pp] = d < 6 * P;
-                    const int axis = rot[pp] ? d / (2 * P) : 0;
-                    pair[pp] = rot[pp] ? (d - axis * 2 * P) >> 1 : 0;
-                    word2[pp] = axis == 2;
-                    sh[pp] = axis == 1 ? 16 : 0;
-                    rmask[pp] = rot[pp] ? -1 : 0;
-                }
+                for (int pp = 0; pp < 4; ++pp) rot[pp] = d0 + 2 * pp < 6 * P;
+                const int axA = P > 0 ? min(d0 / (2 * P), 2) : 0;
+                const int pairA = rot[0] ? (d0 - axA * 2 * P) >> 1 : 0;
+                const int split = rot[0] ? min(P - pairA, 4) : 4;
+                const int axB = min(axA + 1, 2);
                 // (cos, sin) of the four pairs at a row's position, without
-                // branches (so that the wait for these loads is exact): rows
-                // and pairs without rotation read entry 0 of the table, which
-                // is always inside the workspace, and do not use it.  The
-                // loads of pass p + 1 are issued before pass p computes.
+                // branches (so that the wait for these loads is exact): gap
+                // rows hold position 0, and a pair past the rotated width
+                // reads an entry at most three past its row's (the table has
+                // kRopePad entries of slack) and does not use it.  The loads
+                // of pass p + 1 are issued before pass p computes.
+                const char* rope_b = reinterpret_cast<const char*>(awa.rope);
                 auto rope_load = [&](const QkvRow& ri, float2 (&cs)[4]) {
-                    const int live = (ri.pos2 >> 16) != 0 ? -1 : 0;
+                    const uint32_t wa = axA == 2 ? ri.pos2 : ri.pos01;
+                    const uint32_t wb = axB == 2 ? ri.pos2 : ri.pos01;
+                    const uint32_t posA = (wa >> (16 * (axA & 1))) & 0xffff;
+                    const uint32_t posB = (wb >> (16 * (axB & 1))) & 0xffff;
+                    // byte offsets of pair 0 of the chunk on each axis
+                    const uint32_t offA = (__umul24(posA, (uint32_t)P) + pairA) * 8;
+                    const uint32_t offB = __umul24(posB, (uint32_t)P) * 8 - split * 8;
 #pragma unroll
                     for (int pp = 0; pp < 4; ++pp) {
-                        const int wv2 = word2[pp] ? ri.pos2 : ri.pos01;
-                        const int pos = (wv2 >> sh[pp]) & 0xffff;
-                        const int idx = (pos * P + pair[pp]) & rmask[pp] & live;
-                        cs[pp] = awa.rope[idx];
+                        const uint32_t off = (pp < split ? offA : offB) + 8 * pp;
+                        cs[pp] = *reinterpret_cast<const float2*>(rope_b + off);
                     }
                 };
                 // The results of all passes stay in registers (the
