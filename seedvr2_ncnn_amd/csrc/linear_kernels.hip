@@ -265,6 +265,10 @@ constexpr int kSlotFloats = 128 * 512;   // one workgroup's accumulators
 // XCDs' L2s (stores write through, loads do not hit a stale L2 line), so the
 // parts of a tile can meet without cache-wide writeback or invalidation.
 constexpr int kCoherent = 1 | 16;
+// nt: a streaming store, not kept in the L2
+constexpr int kNonTemporal = 2;
+// word 3 of a raw (untyped, stride 0) buffer descriptor
+constexpr int kRawBufferFormat = 0x00020000;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
@@ -808,18 +812,37 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             }
             __syncthreads();
             // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows
-            // t/32 + 16c.  The output is not read again by this launch: the
-            // stores are non-temporal, leaving the L2 to the operand tiles.
-#pragma unroll 4
+            // t/32 + 16c, all sixteen LDS reads issued before the first store.
+            // Each stream's rows of the tile go through a buffer descriptor
+            // bounded by those rows, so the range check drops a row past its
+            // stream, and a chunk past n (given an offset past every bound),
+            // without a branch per store.  A wave's two rows lie in one 8-row
+            // group, hence in one stream.  The output is not read again by
+            // this launch: the stores are non-temporal, leaving the L2 to the
+            // operand tiles.
+            const int ch = ei.tid & 31;
+            const int sub = ei.tid >> 5;
+            const int wv = ei.wm * 4 + ei.wn;
+            const int pitch = ny * 2;
+            const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+                (char*)y0 + (long)row0 * pitch, (short)0, max(min(m0 - row0, BM), 0) * pitch,
+                kRawBufferFormat);
+            const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+                (char*)y1 + (long)(row0 - mv) * pitch, (short)0,
+                row0 + BM > mv ? min(mv + m1 - row0, BM) * pitch : 0, kRawBufferFormat);
+            // offsets are below 2^31 (the launcher checks 256 rows of output):
+            // bit 31 takes a chunk past n out of every range
+            const uint32_t drop = col0 + ch * 8 < n ? 0u : 0x80000000u;
+            u32x4 sv[16];
+#pragma unroll
+            for (int c = 0; c < 16; ++c) sv[c] = *(const u32x4*)(lds + (16 * c + sub) * EP + ch * 16);
+#pragma unroll
             for (int c = 0; c < 16; ++c) {
-                const int idx = c * 512 + ei.tid;
-                const int rl = idx >> 5;
-                const int ch = idx & 31;
-                const int col = col0 + ch * 8;
-                uint16_t* yr = (uint16_t*)out_row(rl);
-                if (yr && col < n)
-                    __builtin_nontemporal_store(*(const u32x4*)(lds + rl * EP + ch * 16),
-                                                (u32x4*)(yr + col));
+                const uint32_t off = (uint32_t)((16 * c + sub) * pitch + col0 * 2 + ch * 16) | drop;
+                if (row0 + 16 * c + 2 * wv < mv)
+                    __builtin_amdgcn_raw_buffer_store_b128(sv[c], rs0, off, 0, kNonTemporal);
+                else
+                    __builtin_amdgcn_raw_buffer_store_b128(sv[c], rs1, off, 0, kNonTemporal);
             }
             return;
         }
@@ -924,7 +947,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             // slot layout: float4 c (4 accumulator registers) of thread tid
             // at byte (c * 512 + tid) * 16; the chunk index goes in soffset
             const __amdgpu_buffer_rsrc_t mine = __builtin_amdgcn_make_buffer_rsrc(
-                sk.slots + (long)s * kSlotFloats, (short)0, kSlotFloats * 4, 0x00020000);
+                sk.slots + (long)s * kSlotFloats, (short)0, kSlotFloats * 4, kRawBufferFormat);
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
@@ -963,7 +986,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 #pragma unroll 1
                 for (int q = lo; q <= hi; ++q) {
                     const __amdgpu_buffer_rsrc_t other = __builtin_amdgcn_make_buffer_rsrc(
-                        sk.slots + (long)q * kSlotFloats, (short)0, kSlotFloats * 4, 0x00020000);
+                        sk.slots + (long)q * kSlotFloats, (short)0, kSlotFloats * 4, kRawBufferFormat);
                     // sixteen 16-byte loads in flight per batch (four
                     // accumulators; the fragment registers are free here)
 #pragma unroll
@@ -1184,7 +1207,8 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
     // bf16 activations (the operand type of the MFMAs) go straight to LDS;
     // fp32 and fp16 ones are rounded to bf16 while staged by the 128 kernel
     if (std::is_same<TX, uint16_t>::value && k % 64 == 0 &&
-        (long)256 * k * 2 <= 0x7fffffffL) {   // buffer offsets are 32-bit
+        (long)256 * k * 2 <= 0x7fffffffL &&   // buffer offsets are 32-bit
+        (long)256 * n * 4 <= 0x7fffffffL) {
         const int mv = (m0 + 7) / 8 * 8;   // first text row in the joint row space
         const int ntiles = (n + 255) / 256;
         const int mtiles = (mv + m1 + 255) / 256;
