@@ -296,13 +296,17 @@ __device__ __forceinline__ float sum_with_lane_xor32(float x) {
 //     bits for D = 64.  A ds_read_b128 phase covers 8 lanes; the A-operand
 //     row of lane l32 is l32 with bits 2 and 3 swapped, so f of its row is
 //     l32 & 15, and the 8 lanes of a phase read 8 distinct chunk positions.
-//   V^T rows (64 bytes): f(r) = ((r >> 1) ^ (r >> 3)) & 3
+//   V^T rows (64 bytes): f(r) = (r >> 2) & 3.  Rows four apart share
+//     their banks; the fragment read of a 16-lane group covers rows r..r+15,
+//     so rows r, r+4, r+8, r+12 must take distinct chunk positions.  (The
+//     LDS conflict counter reads 4 cycles per ds_read_b128 for
+//     ((r >> 1) ^ (r >> 3)) & 3, 12 without a swizzle, 0 for this one.)
 template <int D>
 __device__ __forceinline__ int k_swizzle(int r) {
     const int f = (r & 3) | ((r >> 1) & 4) | ((r << 1) & 8);
     return D == 128 ? f : (f & 7);
 }
-__device__ __forceinline__ int vt_swizzle(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+__device__ __forceinline__ int vt_swizzle(int r) { return (r >> 2) & 3; }
 
 template <int D>
 __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
