@@ -1091,7 +1091,7 @@ def main():
             "the plans keep the RoPE cos/sin table (s2_awa_plan_cache_rope, as the layer does), "
             "so rope_table_ms is the empty stage between two events")),
         "roofline": {
-            "kernel": "s2::shared_linear_256_kernel<true, 1> (MLP up 2560->10240 + GELU, M=21664)",
+            "kernel": "s2::shared_linear_256_kernel<1, 1, 0> (MLP up 2560->10240 + GELU, bf16 out, M=21664)",
             "bound": "mfma",
             "achieved": round(up_tf, 1),
             "peak": PEAK_BF16_TFLOPS,
