@@ -171,11 +171,13 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
             rq[pass].to_float(q);
             rk[pass].to_float(k);
             rv[pass].to_float(v);
-            float sq2 = 0.f, sk2 = 0.f;
+            // sums of squares as one fma chain per row (the fused QKV
+            // epilogue takes the same operation order)
+            float sq2 = q[0] * q[0], sk2 = k[0] * k[0];
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                sq2 += q[i] * q[i];
-                sk2 += k[i] * k[i];
+            for (int i = 1; i < 8; ++i) {
+                sq2 = fmaf(q[i], q[i], sq2);
+                sk2 = fmaf(k[i], k[i], sk2);
             }
 #pragma unroll
             for (int off = 1; off < TPR; off <<= 1) {
@@ -198,10 +200,10 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
                     const float2 c = cs[pass][pp];
                     const float q0 = q[2 * pp], q1 = q[2 * pp + 1];
                     const float k0 = k[2 * pp], k1 = k[2 * pp + 1];
-                    q[2 * pp] = q0 * c.x - q1 * c.y;
-                    q[2 * pp + 1] = q0 * c.y + q1 * c.x;
-                    k[2 * pp] = k0 * c.x - k1 * c.y;
-                    k[2 * pp + 1] = k0 * c.y + k1 * c.x;
+                    q[2 * pp] = fmaf(q0, c.x, -(q1 * c.y));
+                    q[2 * pp + 1] = fmaf(q0, c.y, q1 * c.x);
+                    k[2 * pp] = fmaf(k0, c.x, -(k1 * c.y));
+                    k[2 * pp + 1] = fmaf(k0, c.y, k1 * c.x);
                 }
             }
 #pragma unroll

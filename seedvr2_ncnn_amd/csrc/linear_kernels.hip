@@ -638,10 +638,15 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 // loop, so the loop holds loads only and each pass waits for
                 // its own loads, not for earlier stores.
                 constexpr int PASSES = BM / 16;
+                uint4 res[PASSES];
+                // Only the tile holding the first text row (the row space is
+                // the video rows in window order, then the text rows) selects
+                // between the video and text weights per row.
+                auto passes = [&](auto text_tag) {
+                constexpr bool TEXT = decltype(text_tag)::value;
                 QkvRow ri_next = qrows[etid >> 5];
                 float2 cs_next[4];
                 rope_load(ri_next, cs_next);
-                uint4 res[PASSES];
 #pragma unroll
                 for (int pass = 0; pass < PASSES; ++pass) {
                     const int rl = pass * 16 + (etid >> 5);
@@ -662,32 +667,36 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                         x[2 * i] = __uint_as_float(wd[i] << 16);
                         x[2 * i + 1] = __uint_as_float(wd[i] & 0xffff0000u);
                     }
-                    float ss = 0.f;
+                    float ss = x[0] * x[0];
 #pragma unroll
-                    for (int i = 0; i < 8; ++i) ss += x[i] * x[i];
+                    for (int i = 1; i < 8; ++i) ss = fmaf(x[i], x[i], ss);
                     ss = row_sum<TPR>(ss);
                     const float inv = __builtin_amdgcn_rsqf(ss / (float)D + awa.eps);
-                    const bool video = kind == 1;
+                    const bool video = !TEXT || kind == 1;
 #pragma unroll
                     for (int i = 0; i < 8; ++i) x[i] = x[i] * inv * (video ? wv[i] : wt[i]);
 #pragma unroll
                     for (int pp = 0; pp < 4; ++pp) {
                         if (rot[pp]) {
                             const float a0 = x[2 * pp], a1 = x[2 * pp + 1];
-                            x[2 * pp] = a0 * cs[pp].x - a1 * cs[pp].y;
-                            x[2 * pp + 1] = a0 * cs[pp].y + a1 * cs[pp].x;
+                            x[2 * pp] = fmaf(a0, cs[pp].x, -(a1 * cs[pp].y));
+                            x[2 * pp + 1] = fmaf(a0, cs[pp].y, a1 * cs[pp].x);
                         }
                     }
-                    uint16_t hb[8];
                     if (awa.official_bf16) {
+                        uint16_t hb[8];
 #pragma unroll
                         for (int i = 0; i < 8; ++i) hb[i] = round_bf16_ref_bits(x[i]);
+                        res[pass] = pack8_bf16(hb);
                     } else {
-#pragma unroll
-                        for (int i = 0; i < 8; ++i) hb[i] = __builtin_bit_cast(uint16_t, (__bf16)x[i]);
+                        res[pass] = cvt8_bf16(x);
                     }
-                    res[pass] = pack8_bf16(hb);
                 }
+                };
+                if (row0 + BM > mv)
+                    passes(std::true_type{});
+                else
+                    passes(std::false_type{});
 #pragma unroll
                 for (int pass = 0; pass < PASSES; ++pass) {
                     const QkvRow ri = qrows[pass * 16 + (etid >> 5)];

@@ -95,6 +95,20 @@ __device__ __forceinline__ uint4 pack8_bf16(const uint16_t (&h)[8]) {
     return r;
 }
 
+// eight floats to bf16 (round to nearest even), as four pair conversions
+// (v_cvt_pk_bf16_f32), packed in element order
+__device__ __forceinline__ uint4 cvt8_bf16(const float (&x)[8]) {
+    typedef float f32x2_t __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const f32x2_t f = {x[2 * i], x[2 * i + 1]};
+        w[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+    }
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
     return __builtin_bit_cast(bf16x8, v);
 }
