@@ -446,8 +446,10 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                     go[j] = (uint32_t)rr * (uint32_t)(k * 2) +
                             (uint32_t)((((lane & 7) ^ lds_swizzle(row_a) ^ ((j & 1) << 2))) * 16);
                 }
-                goff_lds[(wq * 64 + lane) * 2] = make_uint4(go[0], go[1], go[2], go[3]);
-                goff_lds[(wq * 64 + lane) * 2 + 1] = make_uint4(go[4], go[5], go[6], go[7]);
+                // lanes 16 bytes apart in each half, so a 16-lane read
+                // phase covers all banks once
+                goff_lds[wq * 64 + lane] = make_uint4(go[0], go[1], go[2], go[3]);
+                goff_lds[256 + wq * 64 + lane] = make_uint4(go[4], go[5], go[6], go[7]);
             }
         }
         auto issue = [&](int stage, int kt, int operand) {
@@ -456,8 +458,8 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             uint32_t go[8];
             if constexpr (AWA != 0) {
                 if (!operand) {
-                    const uint4 g0 = goff_lds[(wq * 64 + lane) * 2];
-                    const uint4 g1 = goff_lds[(wq * 64 + lane) * 2 + 1];
+                    const uint4 g0 = goff_lds[wq * 64 + lane];
+                    const uint4 g1 = goff_lds[256 + wq * 64 + lane];
                     go[0] = g0.x; go[1] = g0.y; go[2] = g0.z; go[3] = g0.w;
                     go[4] = g1.x; go[5] = g1.y; go[6] = g1.z; go[7] = g1.w;
                 }
@@ -553,6 +555,9 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 #pragma clang fp contract(off)
             constexpr int D = AWA;
             constexpr int SP = BN * 2 + 16;   // bytes per staged row
+            // transposed (v) staging: 8-byte writes of 32 lanes to 32 rows;
+            // a pitch of 130 dwords puts them on distinct bank pairs
+            constexpr int SPV = BN * 2 + 8;
             // an opaque copy of the thread index: nothing the epilogue derives
             // from it is hoisted above the main loop, where every register is
             // taken
@@ -579,7 +584,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 #pragma unroll
                             for (int e = 0; e < 4; ++e) *(uint16_t*)(lds + (rl + e) * SP + cl * 2) = hv[e];
                         } else {
-                            *(uint2*)(lds + cl * SP + rl * 2) =
+                            *(uint2*)(lds + cl * SPV + rl * 2) =
                                 make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
                         }
                     }
@@ -715,7 +720,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
 #pragma unroll 8
                     for (int c = 0; c < 64; ++c) {
                         const int cl = (etid >> 7) + 4 * c;
-                        const uint32_t v = *(const uint32_t*)(lds + cl * SP + qp * 4);
+                        const uint32_t v = *(const uint32_t*)(lds + cl * SPV + qp * 4);
                         __builtin_nontemporal_store(v, (uint32_t*)(base + (long)cl * awa.seg_total));
                     }
                 }
