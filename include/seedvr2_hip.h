@@ -95,6 +95,24 @@ S2_API int s2_memcpy_h2d(void* dst, const void* src, size_t bytes, s2_stream_t s
 S2_API int s2_memcpy_d2h(void* dst, const void* src, size_t bytes, s2_stream_t stream);
 S2_API int s2_memcpy_d2d(void* dst, const void* src, size_t bytes, s2_stream_t stream);
 S2_API int s2_stream_synchronize(s2_stream_t stream);
+/* Orders `waiter` after the work enqueued on `producer` so far, without a
+ * host wait (an event recorded on producer and waited for on waiter).  No
+ * counterpart in the reference (one Vulkan queue there): the layers use it
+ * when a blob produced on one stream is consumed on another. */
+S2_API int s2_stream_wait(s2_stream_t waiter, s2_stream_t producer);
+/* Scratch that the split-k GEMM tail and the guidance statistics share
+ * between the workgroups of one launch, one allocation per (device, stream)
+ * (about 64 MB on MI355X).  An owner of a stream -- a device allocator, a
+ * layer whose host path runs on the default stream -- acquires it when it is
+ * created: it is allocated then and zeroed on that stream, with no host wait.
+ * Each acquire takes one reference; the last release waits for that stream
+ * and frees it.  Forward calls only look it up; on a stream nobody acquired,
+ * the first forward that needs it makes it the same way (zeroed on its
+ * stream, no device-wide synchronisation) and it is kept until the process
+ * ends.  No counterpart in the reference (ncnn's Vulkan allocators own their
+ * workspaces). */
+S2_API int s2_stream_scratch_acquire(s2_stream_t stream);
+S2_API int s2_stream_scratch_release(s2_stream_t stream);
 /* Last HIP error string recorded by this library on the calling thread. */
 S2_API const char* s2_last_error(void);
 
@@ -228,6 +246,53 @@ S2_API int s2_swiglu_pack_weight(const uint16_t* gate, const uint16_t* up,
  * layer of its own instead of SharedLinear's fused epilogue (param 3). */
 S2_API int s2_gelu(const void* x, void* y, size_t count, s2_dtype dtype, s2_stream_t stream);
 
+/* ---- ncnn built-in layers of exported graphs ----------------------------- */
+/* The device paths of the ncnn built-ins that exported SeedVR2 graphs place
+ * around the custom layers (the graphs the reference loads at
+ * src/seedvr2/seedvr2_dit.cpp:603-633, 1424-1449): BinaryOp, UnaryOp,
+ * Sigmoid, Swish, Reduction (whose Vulkan path the reference patches for
+ * large row counts, patches/ncnn/0002-seedvr2-large-vulkan-workloads.patch:
+ * 256-284), RMSNorm, and the copies behind Slice, Concat, Crop and Reshape.
+ * Operands are 2-D [rows][cols] views with a row stride in elements; element
+ * types fp32 / bf16 / fp16, fp32 arithmetic; outputs must not overlap
+ * inputs. */
+
+/* ncnn BinaryOp (op: 0 add, 1 sub, 2 mul, 3 div, 4 max, 5 min, 6 pow, 7 rsub,
+ * 8 rdiv, 9 rpow, 10 atan2, 11 ratan2): y[r][c] = op(a[r][c], b[r][c]) over
+ * [rows][cols], each operand broadcast numpy-style: a_rows (b_rows) is rows
+ * or 1, a_cols (b_cols) is cols or 1.  b == NULL: the scalar b_scalar
+ * (ncnn's with_scalar). */
+S2_API int s2_binary_op(int op, const void* a, s2_dtype a_dtype, int a_rows, int a_cols,
+                        long a_stride, const void* b, s2_dtype b_dtype, int b_rows, int b_cols,
+                        long b_stride, float b_scalar, void* y, s2_dtype y_dtype, int rows,
+                        int cols, long y_stride, s2_stream_t stream);
+
+/* ncnn UnaryOp (op 0 abs, 1 neg, 2 floor, 3 ceil, 4 square, 5 sqrt, 6 rsqrt,
+ * 7 exp, 8 log, 9 sin, 10 cos, 11 tan, 12 asin, 13 acos, 14 atan,
+ * 15 reciprocal, 16 tanh, 17 log10, 18 round (half to even), 19 trunc), and
+ * this build's 100 Sigmoid (1 / (1 + e^-x)) and 101 Swish (x / (1 + e^-x)),
+ * over count contiguous values. */
+S2_API int s2_unary_op(int op, const void* x, s2_dtype x_dtype, void* y, s2_dtype y_dtype,
+                       size_t count, s2_stream_t stream);
+
+/* ncnn Reduction (op 0 sum, 1 asum, 2 sumsq, 3 mean, 4 max, 5 min, 6 prod,
+ * 7 l1, 8 l2, 9 logsum, 10 logsumexp; the result times coeff) of a
+ * [rows][cols] view: axis 1 reduces each row (y: rows values), axis 0 each
+ * column (y: cols values).  y is contiguous. */
+S2_API int s2_reduce(int op, float coeff, int axis, const void* x, s2_dtype x_dtype, int rows,
+                     int cols, long x_stride, void* y, s2_dtype y_dtype, s2_stream_t stream);
+
+/* ncnn RMSNorm over each row: y = x / sqrt(mean(x^2) + epsilon), times
+ * gamma[cols] (fp32, device) when gamma is not NULL. */
+S2_API int s2_rms_norm(const void* x, s2_dtype x_dtype, int rows, int cols, long x_stride,
+                       const float* gamma, float epsilon, void* y, s2_dtype y_dtype,
+                       long y_stride, s2_stream_t stream);
+
+/* dst[r][c] = src[r][c] over [rows][cols], converting the element type. */
+S2_API int s2_copy_2d(const void* src, s2_dtype src_dtype, long src_stride, void* dst,
+                      s2_dtype dst_dtype, long dst_stride, int rows, int cols,
+                      s2_stream_t stream);
+
 /* SharedLinear::forward (shared_linear.cpp:83-96): one projection applied to
  * two token streams in ONE grouped launch sharing the weight:
  *   y_video = act(x_video W^T + b),  y_text = act(x_text W^T + b).
@@ -238,11 +303,10 @@ S2_API int s2_gelu(const void* x, void* y, size_t count, s2_dtype dtype, s2_stre
  * they are staged.  Either stream may have m == 0 (its pointers are then
  * ignored).  k must be a multiple of 8; x, y and weight 16-byte aligned.
  * When the last wave of output tiles would leave the chip mostly idle, its
- * tiles are split along k over several workgroups, which meet in a scratch
- * of partial tiles: the first such call on a (device, stream) pair allocates
- * that pair's scratch (one 256 KB slot per compute unit, 64 MB on MI355X,
- * plus counters), kept until the process ends.  Calls on different streams
- * therefore never share scratch and may run concurrently. *
+ * tiles are split along k over several workgroups, which meet in the
+ * stream's scratch of partial tiles (one 256 KB slot per compute unit, 64 MB
+ * on MI355X, plus counters; see s2_stream_scratch_acquire).  Calls on
+ * different streams therefore never share scratch and may run concurrently. *
  * activation S2_ACT_SWIGLU (v3 graphs' MLP, seedvr2_pipeline.cpp:434-438):
  * y = silu(x Wg^T + bg) * (x Wu^T + bu) in one launch.  weight is [2n][k]
  * with the gate and up rows interleaved in blocks of 128 (rows 256j ..
@@ -315,9 +379,8 @@ S2_API int s2_unpatchify_prediction(const float* patches, long patch_count,
  * rescale != 0 and count >= 2, output *= (float)(rescale std(positive) /
  * std(output) + (1 - rescale)) (sample standard deviations, accumulated in
  * fp64), unless std(output) is 0.  16-byte aligned operands.  The rescale
- * uses a per-device statistics scratch (40 KB, allocated by the first such
- * call on a device and kept until the process ends); calls whose kernels
- * overlap in time on one device must not both rescale. */
+ * uses the stream's statistics scratch (40 KB, s2_stream_scratch_acquire),
+ * so rescaling calls on different streams never share it. */
 S2_API int s2_apply_cfg(const float* positive, const float* negative, long count, float scale,
                         float rescale, float* output, s2_stream_t stream);
 

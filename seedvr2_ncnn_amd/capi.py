@@ -41,6 +41,8 @@ EXPORTS = (
     "s2_conv3d_forward_padded", "s2_vae_pixel_shuffle", "s2_dit_ada_in", "s2_dit_ada_out",
     "s2_dit_ada_out_in", "s2_conv3d_workspace_bytes_padded", "s2_shared_linear_forward_noalloc",
     "s2_awa_qkv_forward", "s2_gelu", "s2_swiglu_pack_weight", "s2_awa_plan_cache_rope",
+    "s2_stream_wait", "s2_stream_scratch_acquire", "s2_stream_scratch_release",
+    "s2_binary_op", "s2_unary_op", "s2_reduce", "s2_rms_norm", "s2_copy_2d",
 )
 
 

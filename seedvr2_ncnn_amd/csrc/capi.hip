@@ -11,9 +11,11 @@
 #include "awa_plan.h"
 #include "block_kernels.h"
 #include "conv3d_kernels.h"
+#include "graph_ops_kernels.h"
 #include "mha_kernels.h"
 #include "pipeline_kernels.h"
 #include "seedvr2_hip.h"
+#include "stream_scratch.h"
 
 namespace {
 
@@ -239,6 +241,118 @@ int s2_memcpy_d2d(void* dst, const void* src, size_t bytes, s2_stream_t stream) 
 
 int s2_stream_synchronize(s2_stream_t stream) {
     S2_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return S2_OK;
+}
+
+// ---- ncnn built-in layers of exported graphs --------------------------------
+
+namespace {
+
+bool view_ok(const void* p, int rows, int cols, long stride) {
+    return p && rows > 0 && cols > 0 && stride >= cols;
+}
+
+}  // namespace
+
+int s2_binary_op(int op, const void* a, s2_dtype a_dtype, int a_rows, int a_cols, long a_stride,
+                 const void* b, s2_dtype b_dtype, int b_rows, int b_cols, long b_stride,
+                 float b_scalar, void* y, s2_dtype y_dtype, int rows, int cols, long y_stride,
+                 s2_stream_t stream) {
+    if (op < 0 || op > 11) return fail(S2_ERR_INVALID, "binary op type 0..11");
+    if (rows <= 0 || cols <= 0 || !y || y_stride < cols)
+        return fail(S2_ERR_INVALID, "output shape or stride");
+    if (!dtype_ok(a_dtype) || !dtype_ok(y_dtype) || (b && !dtype_ok(b_dtype)))
+        return fail(S2_ERR_INVALID, "unsupported dtype");
+    auto bcast_ok = [&](int r, int c, long stride, const void* p) {
+        return p && (r == rows || r == 1) && (c == cols || c == 1) && stride >= c;
+    };
+    if (!bcast_ok(a_rows, a_cols, a_stride, a) || (b && !bcast_ok(b_rows, b_cols, b_stride, b)))
+        return fail(S2_ERR_INVALID, "operand shapes do not broadcast to the output");
+    s2::BinaryArgs p = {};
+    p.op = op;
+    p.a = a;
+    p.a_kind = (int)a_dtype;
+    p.a_rs = a_rows == 1 ? 0 : a_stride;
+    p.a_cs = a_cols == 1 ? 0 : 1;
+    p.b = b;
+    p.b_kind = b ? (int)b_dtype : 0;
+    p.b_rs = b && b_rows != 1 ? b_stride : 0;
+    p.b_cs = b && b_cols != 1 ? 1 : 0;
+    p.b_scalar = b_scalar;
+    p.y = y;
+    p.y_kind = (int)y_dtype;
+    p.y_rs = y_stride;
+    p.rows = rows;
+    p.cols = cols;
+    S2_HIP(s2::launch_binary(p, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_unary_op(int op, const void* x, s2_dtype x_dtype, void* y, s2_dtype y_dtype, size_t count,
+                s2_stream_t stream) {
+    if (!((op >= 0 && op <= 19) || op == 100 || op == 101))
+        return fail(S2_ERR_INVALID, "unary op type 0..19, 100 sigmoid or 101 swish");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (count == 0) return S2_OK;
+    if (!x || !y) return fail(S2_ERR_INVALID, "null operand");
+    S2_HIP(s2::launch_unary(op, x, (int)x_dtype, y, (int)y_dtype, count, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_reduce(int op, float coeff, int axis, const void* x, s2_dtype x_dtype, int rows, int cols,
+              long x_stride, void* y, s2_dtype y_dtype, s2_stream_t stream) {
+    if (op < 0 || op > 10) return fail(S2_ERR_INVALID, "reduction op type 0..10");
+    if (axis != 0 && axis != 1) return fail(S2_ERR_INVALID, "reduction axis 0 (columns) or 1 (rows)");
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (!view_ok(x, rows, cols, x_stride) || !y) return fail(S2_ERR_INVALID, "operand shape or stride");
+    S2_HIP(s2::launch_reduce(op, coeff, axis, x, (int)x_dtype, x_stride, rows, cols, y, (int)y_dtype,
+                             (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_rms_norm(const void* x, s2_dtype x_dtype, int rows, int cols, long x_stride,
+                const float* gamma, float epsilon, void* y, s2_dtype y_dtype, long y_stride,
+                s2_stream_t stream) {
+    if (!dtype_ok(x_dtype) || !dtype_ok(y_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (!view_ok(x, rows, cols, x_stride) || !view_ok(y, rows, cols, y_stride))
+        return fail(S2_ERR_INVALID, "operand shape or stride");
+    if (!(epsilon >= 0.f)) return fail(S2_ERR_INVALID, "epsilon must be >= 0");
+    S2_HIP(s2::launch_rms_norm(x, (int)x_dtype, x_stride, rows, cols, gamma, epsilon, y, (int)y_dtype,
+                               y_stride, (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_copy_2d(const void* src, s2_dtype src_dtype, long src_stride, void* dst, s2_dtype dst_dtype,
+               long dst_stride, int rows, int cols, s2_stream_t stream) {
+    if (!dtype_ok(src_dtype) || !dtype_ok(dst_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    if (rows == 0 || cols == 0) return S2_OK;
+    if (!view_ok(src, rows, cols, src_stride) || !view_ok(dst, rows, cols, dst_stride))
+        return fail(S2_ERR_INVALID, "operand shape or stride");
+    S2_HIP(s2::launch_copy2d(src, (int)src_dtype, src_stride, dst, (int)dst_dtype, dst_stride, rows, cols,
+                             (hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_stream_wait(s2_stream_t waiter, s2_stream_t producer) {
+    if (waiter == producer) return S2_OK;
+    hipEvent_t ev;
+    S2_HIP(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    hipError_t e = hipEventRecord(ev, (hipStream_t)producer);
+    if (e == hipSuccess) e = hipStreamWaitEvent((hipStream_t)waiter, ev, 0);
+    // the wait holds what it needs: the event may go now
+    const hipError_t d = hipEventDestroy(ev);
+    S2_HIP(e);
+    S2_HIP(d);
+    return S2_OK;
+}
+
+int s2_stream_scratch_acquire(s2_stream_t stream) {
+    S2_HIP(s2::stream_scratch_acquire((hipStream_t)stream));
+    return S2_OK;
+}
+
+int s2_stream_scratch_release(s2_stream_t stream) {
+    S2_HIP(s2::stream_scratch_release((hipStream_t)stream));
     return S2_OK;
 }
 

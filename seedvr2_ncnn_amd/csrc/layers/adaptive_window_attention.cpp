@@ -233,6 +233,10 @@ int AdaptiveWindowAttention::create_pipeline(const ncnn::Option& /*opt*/)
 int AdaptiveWindowAttention::create_pipeline_impl()
 {
     std::lock_guard<std::mutex> lock(mutex);
+    // the host-blob path runs on the default stream: own its scratch
+    const int sret = host_scratch.take(0);
+    if (sret != S2_OK)
+        return sret;
     int devices = 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0)
         return 0;   // nothing to prepare without a device; forward reports it
@@ -244,6 +248,7 @@ int AdaptiveWindowAttention::create_pipeline_impl()
 int AdaptiveWindowAttention::destroy_pipeline(const ncnn::Option& /*opt*/)
 {
     std::lock_guard<std::mutex> lock(mutex);
+    host_scratch.drop();
     release_device_locked();
     return 0;
 }

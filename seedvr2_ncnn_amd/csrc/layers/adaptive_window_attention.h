@@ -139,6 +139,7 @@ private:
     // Device state (guarded by mutex; forward is const and may be called
     // from several threads).
     mutable std::mutex mutex;
+    StreamScratchRef host_scratch;   // the default stream's kernel scratch
     mutable bool weights_dirty;
     mutable DeviceBuffer weights_gpu;      // [4][d] norms then [P] freqs, fp32
     mutable s2_awa_plan* plan;

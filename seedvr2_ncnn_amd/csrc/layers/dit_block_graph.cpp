@@ -78,39 +78,38 @@ int DiTBlockGraph::run(const std::vector<std::array<int, 3> >& video_shapes,
                        const std::vector<std::string>* checkpoints,
                        std::vector<ncnn::Mat>* checkpoint_blobs)
 {
-    // the previous run's uploads and outputs go back to the pool (the
-    // kernels that will reuse them run after that run's, on the same stream)
+    // The previous run's outputs go back to the pool (the kernels that will
+    // reuse them run after that run's, on the same stream), except those fed
+    // back as inputs of this run (a denoising loop's out0 -> in0): they are
+    // released after the run that reads them.
+    std::vector<void*> still_read;
     for (size_t i = 0; i < last_blocks.size(); i++)
-        alloc.release_blob(last_blocks[i]);
-    last_blocks.clear();
+    {
+        bool input = false;
+        for (int j = 0; j < 10; j++)
+            input = input || inputs[j].data == last_blocks[i];
+        if (input)
+            still_read.push_back(last_blocks[i]);
+        else
+            alloc.release_blob(last_blocks[i]);
+    }
+    last_blocks.swap(still_read);
     runtime_state.video_shapes = video_shapes;
     runtime_state.text_lengths = text_lengths;
     ncnn::Extractor ex = net.create_extractor();
     ex.set_light_mode(true);
     ex.set_blob_allocator(&alloc);
     ex.set_workspace_allocator(&alloc);
+    // Host inputs are uploaded once by the extractor on this graph's stream,
+    // except in2 / in3 (video_shape, text_length), which the attention layers
+    // read on the host; device inputs of another allocator are ordered
+    // behind that allocator's stream (ncnn::Extractor::input).
     int ret = 0;
     for (int i = 0; ret == 0 && i < 10; i++)
     {
         char name[8];
         snprintf(name, sizeof(name), "in%d", i);
-        ncnn::Mat m = inputs[i];
-        // in2 / in3 (video_shape, text_length) stay where they are: the
-        // attention layers read host shape blobs on the host
-        if (i != 2 && i != 3 && !device_allocator_of(m) && m.dims == 2 && !m.empty() &&
-            (m.elemsize == 4 || m.elemsize == 2))
-        {
-            // a host blob: one upload on the graph's stream
-            m = alloc.create_blob(m.w, m.h, m.elemsize);
-            if (m.empty())
-                return -100;
-            last_blocks.push_back(m.data);
-            ret = s2_memcpy_h2d(m.data, inputs[i].data, (size_t)m.w * m.h * m.elemsize,
-                                alloc.stream());
-            if (ret != 0)
-                return layer_status(ret);
-        }
-        ret = ex.input(name, m);
+        ret = ex.input(name, inputs[i]);
     }
     if (ret == 0 && checkpoints)
     {

@@ -10,9 +10,13 @@
 // boundary blobs of chosen blocks (:722-833).  This class does the same with
 // its own HipDeviceAllocator as the extractor's blob allocator, so every
 // blob between two layers stays in HBM and only in0..in9 are uploaded when
-// they are host Mats.  It also registers the block's norm/modulation layers
-// (DiTAdaIn, DiTAdaOut, DiTAdaOutIn, dit_block_ops.h) with the same runtime
-// state, and folds SharedLinear -> GELU pairs into the GEMM epilogue.
+// they are host Mats (in2 / in3 stay on the host).  Device inputs of another
+// HipDeviceAllocator may come from another stream: the graph's stream waits
+// for that stream's work enqueued before run(), and every layer runs on the
+// graph's stream.  Outputs are ready once the graph's stream has run.  It
+// also registers the block's norm/modulation layers (DiTAdaIn, DiTAdaOut,
+// DiTAdaOutIn, dit_block_ops.h) with the same runtime state, and folds
+// SharedLinear -> GELU pairs into the GEMM epilogue.
 #ifndef SEEDVR2_DIT_BLOCK_GRAPH_H
 #define SEEDVR2_DIT_BLOCK_GRAPH_H
 

@@ -6,9 +6,33 @@
 
 namespace seedvr2 {
 
-HipDeviceAllocator::HipDeviceAllocator(void* stream) : stream_(stream) {}
+int StreamScratchRef::take(void* stream) {
+    if (held_) {
+        if (stream == stream_) return S2_OK;
+        drop();
+    }
+    int devices = 0;
+    if (s2_device_count(&devices) != S2_OK || devices == 0) return S2_OK;
+    const int ret = s2_stream_scratch_acquire(stream);
+    if (ret != S2_OK) return ret;
+    stream_ = stream;
+    held_ = true;
+    return S2_OK;
+}
 
-HipDeviceAllocator::~HipDeviceAllocator() { clear(); }
+void StreamScratchRef::drop() {
+    if (!held_) return;
+    held_ = false;
+    (void)s2_stream_scratch_release(stream_);
+}
+
+// (a failed acquire leaves the scratch to the first forward that needs it)
+HipDeviceAllocator::HipDeviceAllocator(void* stream) : stream_(stream) { (void)scratch_.take(stream); }
+
+HipDeviceAllocator::~HipDeviceAllocator() {
+    clear();
+    scratch_.drop();
+}
 
 void* HipDeviceAllocator::fastMalloc(size_t) { return 0; }
 

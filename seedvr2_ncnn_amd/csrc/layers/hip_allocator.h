@@ -24,9 +24,32 @@
 
 namespace seedvr2 {
 
+// One owner reference to a stream's kernel scratch (split-k partial tiles,
+// guidance statistics; s2_stream_scratch_acquire): taken by take() when a
+// gfx950 device is present (a no-op without one), dropped by drop() or the
+// destructor.  Owners: every HipDeviceAllocator for its stream, and each
+// layer whose host-blob path runs on the default stream, from
+// create_pipeline to destroy_pipeline.  So the scratch is allocated and
+// zeroed when an owner is made, never inside a forward.
+class StreamScratchRef {
+public:
+    StreamScratchRef() : stream_(0), held_(false) {}
+    ~StreamScratchRef() { drop(); }
+    int take(void* stream);   // S2_OK, or the acquire's error code
+    void drop();
+    bool held() const { return held_; }
+
+private:
+    StreamScratchRef(const StreamScratchRef&);
+    StreamScratchRef& operator=(const StreamScratchRef&);
+    void* stream_;
+    bool held_;
+};
+
 class HipDeviceAllocator : public ncnn::Allocator {
 public:
-    // stream: a hipStream_t (as void*), 0 = the default stream.
+    // stream: a hipStream_t (as void*), 0 = the default stream.  Takes the
+    // stream's kernel scratch (StreamScratchRef) for as long as it lives.
     explicit HipDeviceAllocator(void* stream = 0);
     virtual ~HipDeviceAllocator();
 
@@ -52,12 +75,18 @@ public:
     void clear();
 
     void* stream() const { return stream_; }
+    // Blocks this allocator holds, in use or pooled (for tests).
+    size_t owned_count() const {
+        std::lock_guard<std::mutex> lock(mutex_);
+        return owned_.size();
+    }
 
 private:
     void* alloc_bytes(size_t bytes);
 
     void* stream_;
-    std::mutex mutex_;
+    StreamScratchRef scratch_;
+    mutable std::mutex mutex_;
     std::vector<void*> owned_;
     std::vector<size_t> owned_bytes_;
     std::vector<std::pair<size_t, void*> > pool_;   // (bytes, block) free for reuse

@@ -103,6 +103,8 @@ int SharedLinear::set_activation(int act)
     if (act != S2_ACT_NONE && act != S2_ACT_GELU)
         return -1;
     std::lock_guard<std::mutex> lock(mutex);
+    if (act != activation && activation != S2_ACT_NONE)
+        return -1;
     activation = act;
     return 0;
 }
@@ -115,6 +117,10 @@ int SharedLinear::create_pipeline(const ncnn::Option& /*opt*/)
 int SharedLinear::create_pipeline_impl()
 {
     std::lock_guard<std::mutex> lock(mutex);
+    // the host-blob path runs on the default stream: own its scratch
+    const int sret = host_scratch.take(0);
+    if (sret != S2_OK)
+        return sret;
     int devices = 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0 || weight_data.empty())
         return 0;
@@ -124,6 +130,7 @@ int SharedLinear::create_pipeline_impl()
 int SharedLinear::destroy_pipeline(const ncnn::Option& /*opt*/)
 {
     std::lock_guard<std::mutex> lock(mutex);
+    host_scratch.drop();
     weight_gpu.release();
     bias_gpu.release();
     staging.release();

@@ -36,8 +36,10 @@ public:
                         std::vector<ncnn::Mat>& top_blobs,
                         const ncnn::Option& opt) const;
 
-    // Epilogue activation (param 3: S2_ACT_NONE or S2_ACT_GELU), switched by
-    // a graph optimiser that folds a following GELU layer.  Returns 0 or -1.
+    // Epilogue activation, switched by a graph optimiser that folds a
+    // following GELU layer: S2_ACT_GELU on a layer without one (param 3 = 0),
+    // or the activation the layer already has.  Returns 0, or -1 for any
+    // other change (a GELU or SwiGLU epilogue loaded from param 3 is kept).
     int set_activation(int act);
 
     // For a graph optimiser that fuses this projection into the attention
@@ -66,6 +68,7 @@ private:
     ncnn::Mat bias_data;
 
     mutable std::mutex mutex;
+    StreamScratchRef host_scratch;   // the default stream's kernel scratch
     mutable bool weights_dirty;
     mutable DeviceBuffer weight_gpu;   // bf16 [N][K]
     mutable DeviceBuffer bias_gpu;     // fp32 [N]

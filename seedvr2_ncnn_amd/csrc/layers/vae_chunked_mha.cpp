@@ -73,6 +73,10 @@ int VAEChunkedMHA::create_pipeline(const ncnn::Option& /*opt*/)
 int VAEChunkedMHA::create_pipeline_impl()
 {
     std::lock_guard<std::mutex> lock(mutex);
+    // the host-blob path runs on the default stream: own its scratch
+    const int sret = host_scratch.take(0);
+    if (sret != S2_OK)
+        return sret;
     int devices = 0;
     const int qdim = embed_dim > 0 ? weight_data_size / embed_dim : 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0 || weights[0].empty() ||
@@ -84,6 +88,7 @@ int VAEChunkedMHA::create_pipeline_impl()
 int VAEChunkedMHA::destroy_pipeline(const ncnn::Option& /*opt*/)
 {
     std::lock_guard<std::mutex> lock(mutex);
+    host_scratch.drop();
     prepared.release();
     workspace.release();
     staging.release();

@@ -53,6 +53,7 @@ private:
     ncnn::Mat weights[8];
 
     mutable std::mutex mutex;
+    StreamScratchRef host_scratch;   // the default stream's kernel scratch
     mutable bool weights_dirty;
     mutable DeviceBuffer prepared;
     mutable DeviceBuffer workspace;

@@ -1130,6 +1130,18 @@ size_t sk_scratch_bytes(int groups) {
     return (size_t)groups * kSlotFloats * sizeof(float) + (size_t)groups * sizeof(int);
 }
 
+}  // namespace
+
+// Split-k scratch of a stream on the current device: a slot per compute unit.
+hipError_t splitk_scratch_bytes(size_t* bytes) {
+    int G = 0;
+    const hipError_t e = device_cus(&G);
+    if (e == hipSuccess) *bytes = sk_scratch_bytes(G);
+    return e;
+}
+
+namespace {
+
 // The no-allocation entry point's scratch: slots and counters for up to
 // kNoallocGroups sharing workgroups (the split of a 256-CU device), about
 // 64 MB that every GPU the library runs on holds until the process ends.

@@ -9,6 +9,7 @@
 #include <map>
 #include <sstream>
 
+#include "builtin_layers.h"
 #include "hip_allocator.h"
 #include "modelbin.h"
 #include "adaptive_window_attention.h"
@@ -90,9 +91,11 @@ public:
 
 }  // namespace
 
-// Device blob references held by an extractor's blob slots: a device block
-// goes back to its allocator's pool when the last slot naming it is
-// released (Split tops and Input aliases share one block).
+// Device blob references held by the blob slots of an extractor and of its
+// copies (which share one table): a device block goes back to its
+// allocator's pool when the last slot naming it is released (Split tops and
+// Input aliases share one block) unless it is pinned (the caller's own, or
+// handed out by extract).
 class DeviceRefs {
 public:
     void add(const Mat& m) {
@@ -153,7 +156,7 @@ Layer* Net::create_layer(const std::string& type, int* custom_index) const {
     if (type == "Input") return new InputLayer();
     if (type == "Split") return new SplitLayer();
     if (type == "GELU") return new GeluLayer();
-    return 0;
+    return create_builtin_layer(type);
 }
 
 void Net::clear() {
@@ -170,6 +173,29 @@ void Net::clear() {
     consumer_count_.clear();
     passthrough_.clear();
     blobs_.clear();
+}
+
+bool Net::host_only_blob(int bi, int depth) const {
+    if (bi < 0 || bi >= (int)blobs_.size() || depth > 16) return false;
+    bool any = false;
+    for (size_t li = 0; li < layers_.size(); li++) {
+        const Layer* l = layers_[li];
+        for (size_t k = 0; k < l->bottoms.size(); k++) {
+            if (l->bottoms[k] != bi) continue;
+            any = true;
+            // the video_shape / text_length blobs of either input form
+            if (l->type == "AdaptiveWindowAttention" && l->bottoms.size() >= 4 &&
+                k + 2 >= l->bottoms.size())
+                continue;
+            if (l->type == "Split") {
+                for (size_t t = 0; t < l->tops.size(); t++)
+                    if (!host_only_blob(l->tops[t], depth + 1)) return false;
+                continue;
+            }
+            return false;
+        }
+    }
+    return any;
 }
 
 int Net::find_blob_index_by_name(const char* name) const {
@@ -205,7 +231,10 @@ int Net::load_param_mem(const char* mem) {
         std::string type, name;
         int nb = 0, nt = 0;
         if (!(ls >> type)) continue;   // blank line
-        if (!(ls >> name >> nb >> nt) || nb < 0 || nt < 0) return -1;
+        if (!(ls >> name >> nb >> nt) || nb < 0 || nt < 0) {
+            clear();
+            return -1;
+        }
         int ci = -1;
         Layer* layer = create_layer(type, &ci);
         if (!layer) {
@@ -221,7 +250,10 @@ int Net::load_param_mem(const char* mem) {
         passthrough_.push_back(0);
         for (int i = 0; i < nb; i++) {
             std::string b;
-            if (!(ls >> b)) return -1;
+            if (!(ls >> b)) {
+                clear();
+                return -1;
+            }
             const int bi = find_blob_index_by_name(b.c_str());
             if (bi < 0) {
                 fprintf(stderr, "blob %s of layer %s has no producer\n", b.c_str(), name.c_str());
@@ -234,7 +266,10 @@ int Net::load_param_mem(const char* mem) {
         }
         for (int i = 0; i < nt; i++) {
             std::string t;
-            if (!(ls >> t)) return -1;
+            if (!(ls >> t)) {
+                clear();
+                return -1;
+            }
             if (find_blob_index_by_name(t.c_str()) >= 0 || (int)blobs_.size() >= blob_count) {
                 clear();
                 return -1;
@@ -304,8 +339,11 @@ int Net::fuse_shared_linear_gelu() {
             gelus.push_back(c);
         }
         if (gelus.size() != l->tops.size()) continue;
+        // only a projection without an epilogue activation of its own: a
+        // GELU after a GELU or SwiGLU epilogue stays a layer
         seedvr2::SharedLinear* sl = dynamic_cast<seedvr2::SharedLinear*>(l);
-        if (!sl || sl->set_activation(S2_ACT_GELU) != 0) continue;
+        if (!sl || sl->activation_kind() != S2_ACT_NONE || sl->set_activation(S2_ACT_GELU) != 0)
+            continue;
         for (size_t g = 0; g < gelus.size(); g++) {
             static_cast<GeluLayer*>(layers_[gelus[g]])->passthrough = true;
             passthrough_[gelus[g]] = 1;
@@ -427,16 +465,15 @@ Extractor::Extractor(const Net* net, size_t blob_count)
     : net_(net), blob_mats_(blob_count), pending_(net->consumer_count_), opt_(net->opt),
       refs_(new DeviceRefs()) {}
 
-Extractor::~Extractor() {
-    clear();
-    delete refs_;
-}
+Extractor::~Extractor() { clear(); }
 
+// A copy shares rhs's reference table and adds its own references to the
+// blobs it names, so a block goes back to the pool only when neither
+// extractor names it any more.
 Extractor::Extractor(const Extractor& rhs)
     : net_(rhs.net_), blob_mats_(rhs.blob_mats_), pending_(rhs.pending_), opt_(rhs.opt_),
-      refs_(new DeviceRefs()) {
-    // a copy starts without pooling: its blobs stay referenced by rhs
-    for (size_t i = 0; i < blob_mats_.size(); i++) refs_->pin(blob_mats_[i]);
+      refs_(rhs.refs_) {
+    for (size_t i = 0; i < blob_mats_.size(); i++) refs_->add(blob_mats_[i]);
 }
 
 Extractor& Extractor::operator=(const Extractor& rhs) {
@@ -446,14 +483,19 @@ Extractor& Extractor::operator=(const Extractor& rhs) {
     blob_mats_ = rhs.blob_mats_;
     pending_ = rhs.pending_;
     opt_ = rhs.opt_;
-    for (size_t i = 0; i < blob_mats_.size(); i++) refs_->pin(blob_mats_[i]);
+    refs_ = rhs.refs_;
+    for (size_t i = 0; i < blob_mats_.size(); i++) refs_->add(blob_mats_[i]);
     return *this;
 }
 
+// Releases every slot; device blocks this extractor alone still named (its
+// intermediates and uploads) go back to their allocator's pool.
 void Extractor::clear() {
-    for (size_t i = 0; i < blob_mats_.size(); i++) blob_mats_[i].release();
-    delete refs_;
-    refs_ = new DeviceRefs();
+    for (size_t i = 0; i < blob_mats_.size(); i++) {
+        if (refs_) refs_->drop(blob_mats_[i]);
+        blob_mats_[i].release();
+    }
+    refs_.reset(new DeviceRefs());
     if (net_) pending_ = net_->consumer_count_;
 }
 
@@ -472,18 +514,33 @@ int Extractor::input(int blob_index, const Mat& in) {
     if (blob_index < 0 || blob_index >= (int)blob_mats_.size()) return -1;
     seedvr2::HipDeviceAllocator* dev =
         dynamic_cast<seedvr2::HipDeviceAllocator*>(opt_.blob_allocator);
+    seedvr2::HipDeviceAllocator* src = seedvr2::device_allocator_of(in);
     Mat m = in;
-    if (dev && !seedvr2::device_allocator_of(in) && in.dims == 2 && !in.empty() &&
-        (in.elemsize == 4 || in.elemsize == 2)) {
-        // host blob into a device graph: one upload on the allocator's stream
-        m = dev->create_blob(in.w, in.h, in.elemsize);
+    bool upload = false;
+    if (dev && src && src != dev) {
+        // a device blob of another allocator: this graph's stream waits for
+        // the work its producer enqueued, and its consumers run on this
+        // graph's stream (layers launch on their bottom blob's allocator's)
+        if (s2_stream_wait(dev->stream(), src->stream()) != S2_OK) return -100;
+        m.allocator = dev;
+    } else if (dev && !src && (in.dims == 1 || in.dims == 2) && !in.empty() &&
+               (in.elemsize == 4 || in.elemsize == 2) && !net_->host_only_blob(blob_index)) {
+        // host blob into a device graph: one upload on the allocator's
+        // stream, owned by this extractor (pooled again once consumed)
+        m = dev->create_blob(in.w, in.dims == 1 ? 1 : in.h, in.elemsize);
         if (m.empty()) return -100;
+        if (in.dims == 1) m.dims = 1;
         if (s2_memcpy_h2d(m.data, in.data, (size_t)in.w * in.h * in.elemsize, dev->stream()) != S2_OK)
             return -100;
+        upload = true;
+    }
+    if (blob_mats_[blob_index].dims) {
+        refs_->drop(blob_mats_[blob_index]);
+        blob_mats_[blob_index].release();
     }
     blob_mats_[blob_index] = m;
     refs_->add(m);
-    refs_->pin(m);
+    if (!upload) refs_->pin(m);
     return 0;
 }
 
@@ -498,7 +555,7 @@ int Extractor::extract(int blob_index, Mat& feat, int /*type*/) {
     if (blob_mats_[blob_index].dims == 0) {
         const int p = net_->blobs_[blob_index].producer;
         if (p < 0) return -1;
-        const int ret = net_->forward_layer(p, blob_mats_, pending_, opt_, refs_);
+        const int ret = net_->forward_layer(p, blob_mats_, pending_, opt_, refs_.get());
         if (ret != 0) return ret;
     }
     feat = blob_mats_[blob_index];

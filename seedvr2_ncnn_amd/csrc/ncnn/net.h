@@ -7,18 +7,22 @@
 // reads its own weights, in layer order), and runs it through an Extractor
 // that computes a requested blob from the blobs it depends on, as ncnn's
 // does.  Layer types come from the registered custom layers first, then the
-// built-ins Input, Split and GELU.
+// built-ins Input, Split and GELU and those of builtin_layers.h.
 //
 // Device residency (this build): when the extractor's blob allocator is a
 // HipDeviceAllocator (layers/hip_allocator.h), every layer output is a
-// device blob of that allocator, host Mats given to input() are uploaded
-// once, and in light mode a device blob no slot references any more goes
-// back to the allocator's pool for a later layer to reuse.
+// device blob of that allocator; host Mats given to input() are uploaded
+// once (except blobs only read on the host, Net::host_only_blob), and device
+// blobs of another allocator are re-tagged to this one after its stream has
+// been ordered behind theirs (s2_stream_wait), so every layer runs on the
+// extractor's stream.  In light mode a device blob no slot references any
+// more goes back to the allocator's pool for a later layer to reuse.
 #ifndef NCNN_NET_H
 #define NCNN_NET_H
 
 #include <stddef.h>
 
+#include <memory>
 #include <string>
 #include <vector>
 
@@ -66,6 +70,12 @@ public:
     void clear();
 
     Extractor create_extractor() const;
+
+    // This build: true when every consumer of blob bi reads it on the host
+    // (the video_shape / text_length bottoms of AdaptiveWindowAttention,
+    // directly or through Split layers).  A device extractor does not upload
+    // such a blob when it is given as a host Mat.
+    bool host_only_blob(int bi, int depth = 0) const;
 
     const std::vector<Blob>& blobs() const { return blobs_; }
     const std::vector<Layer*>& layers() const { return layers_; }
@@ -141,7 +151,7 @@ private:
     std::vector<Mat> blob_mats_;
     std::vector<int> pending_;   // consumers of each blob that have not run yet
     Option opt_;
-    class DeviceRefs* refs_;
+    std::shared_ptr<class DeviceRefs> refs_;   // shared with copies of this extractor
 };
 
 }  // namespace ncnn

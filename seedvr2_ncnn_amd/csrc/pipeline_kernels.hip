@@ -417,6 +417,8 @@ bool fits_int(long v) { return v >= 0 && v <= 0x7fffffffL; }
 
 }  // namespace
 
+size_t cfg_scratch_bytes() { return sizeof(CfgScratch); }
+
 hipError_t launch_patchify(const float* tokens, int frames, int height, int width, float* patches,
                            hipStream_t stream) {
     const int pw = width / 2;

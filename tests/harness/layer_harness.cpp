@@ -10,6 +10,7 @@
 #include <vector>
 
 #include <layer.h>
+#include <net.h>
 #include <modelbin.h>
 #include <paramdict.h>
 
@@ -320,10 +321,31 @@ int h_graph_layer_count(void* graph) {
 // One run: inputs[0..9] = in0..in9 (host or device blobs, dims 1 or 2);
 // out0/out1 and the named checkpoint blobs are copied into the caller's
 // buffers (device when .device), their shapes reported back.
+static int graph_run(void* graph, const int* shapes, const int* text_lengths, int batch,
+                     const h_blob* inputs, h_blob* outs, int n_checkpoints,
+                     const char* const* checkpoint_names, seedvr2::HipDeviceAllocator* wrap);
+
 int h_graph_run(void* graph, const int* shapes, const int* text_lengths, int batch,
                 const h_blob* inputs, h_blob* outs, int n_checkpoints,
                 const char* const* checkpoint_names) {
+    return graph_run(graph, shapes, text_lengths, batch, inputs, outs, n_checkpoints,
+                     checkpoint_names, 0);
+}
+
+// h_graph_run with the device inputs tagged as blobs of an allocator on
+// `input_stream` (a hipStream_t), as a caller whose producer kernels ran
+// there hands them over: the graph must order its stream behind that one.
+int h_graph_run_from_stream(void* graph, const int* shapes, const int* text_lengths, int batch,
+                            const h_blob* inputs, h_blob* outs, void* input_stream) {
+    seedvr2::HipDeviceAllocator producer(input_stream);
+    return graph_run(graph, shapes, text_lengths, batch, inputs, outs, 0, 0, &producer);
+}
+
+static int graph_run(void* graph, const int* shapes, const int* text_lengths, int batch,
+                     const h_blob* inputs, h_blob* outs, int n_checkpoints,
+                     const char* const* checkpoint_names, seedvr2::HipDeviceAllocator* wrap) {
     seedvr2::DiTBlockGraph* g = static_cast<seedvr2::DiTBlockGraph*>(graph);
+    seedvr2::HipDeviceAllocator& tag = wrap ? *wrap : g->allocator();
     std::vector<std::array<int, 3> > vs(batch);
     for (int b = 0; b < batch; b++)
         for (int a = 0; a < 3; a++) vs[b][a] = shapes[3 * b + a];
@@ -333,8 +355,8 @@ int h_graph_run(void* graph, const int* shapes, const int* text_lengths, int bat
         const h_blob& b = inputs[i];
         if (b.dims == 0) continue;
         if (b.device) {
-            ins[i] = b.dims == 1 ? g->allocator().wrap_blob(b.w, 1, b.data, (size_t)b.elemsize)
-                                 : g->allocator().wrap_blob(b.w, b.h, b.data, (size_t)b.elemsize);
+            ins[i] = b.dims == 1 ? tag.wrap_blob(b.w, 1, b.data, (size_t)b.elemsize)
+                                 : tag.wrap_blob(b.w, b.h, b.data, (size_t)b.elemsize);
             if (b.dims == 1) {
                 ins[i].dims = 1;
                 ins[i].h = 1;
@@ -367,5 +389,80 @@ int h_graph_run(void* graph, const int* shapes, const int* text_lengths, int bat
 }
 
 void h_graph_destroy(void* graph) { delete static_cast<seedvr2::DiTBlockGraph*>(graph); }
+
+// Blocks the graph's device allocator holds, in use or pooled.
+long h_graph_owned_blocks(void* graph) {
+    return (long)static_cast<seedvr2::DiTBlockGraph*>(graph)->allocator().owned_count();
+}
+
+// Runs a graph of built-in layers through ncnn::Net: load_param_mem /
+// load_model, then one extractor fed n_in named blobs and asked for n_out
+// named blobs.  device != 0: the extractor's blob allocator is a device
+// allocator (host inputs are uploaded, device inputs used in place) and
+// outputs are copied back into the caller's buffers (host or device per
+// h_blob.device); otherwise everything runs on the host.  Returns the first
+// failing code.
+int h_net_run(const char* param_text, const void* model, long model_bytes, int device, int n_in,
+              const char* const* in_names, const h_blob* ins, int n_out,
+              const char* const* out_names, h_blob* outs) {
+    ncnn::Net net;
+    net.opt.use_bf16_storage = false;
+    net.opt.use_fp16_storage = false;
+    int ret = net.load_param_mem(param_text);
+    if (ret == 0) ret = net.load_model(static_cast<const unsigned char*>(model), (size_t)model_bytes);
+    if (ret != 0) return ret;
+    seedvr2::HipDeviceAllocator alloc(0);
+    ncnn::Extractor ex = net.create_extractor();
+    if (device) ex.set_blob_allocator(&alloc);
+    for (int i = 0; ret == 0 && i < n_in; i++) {
+        const h_blob& b = ins[i];
+        ncnn::Mat m;
+        if (b.device)
+            m = b.dims == 1 ? alloc.wrap_blob(b.w, 1, b.data, (size_t)b.elemsize)
+                            : alloc.wrap_blob(b.w, b.h, b.data, (size_t)b.elemsize);
+        else
+            m = b.dims == 1 ? ncnn::Mat(b.w, b.data, (size_t)b.elemsize)
+                            : ncnn::Mat(b.w, b.h, b.data, (size_t)b.elemsize);
+        if (b.dims == 1) {
+            m.dims = 1;
+            m.h = 1;
+        }
+        ret = ex.input(in_names[i], m);
+    }
+    for (int i = 0; ret == 0 && i < n_out; i++) {
+        ncnn::Mat m;
+        ret = ex.extract(out_names[i], m);
+        if (ret != 0) break;
+        h_blob& o = outs[i];
+        const size_t bytes = (size_t)m.w * (m.dims == 2 ? m.h : 1) * m.elemsize;
+        if (bytes > (size_t)o.w * o.h * o.elemsize) return -3;
+        const bool on_device = seedvr2::device_allocator_of(m) != 0;
+        if (on_device)
+            ret = o.device ? s2_memcpy_d2d(o.data, m.data, bytes, 0) : s2_memcpy_d2h(o.data, m.data, bytes, 0);
+        else if (o.device)
+            ret = s2_memcpy_h2d(o.data, m.data, bytes, 0);
+        else
+            memcpy(o.data, m.data, bytes);
+        o.dims = m.dims;
+        o.w = m.w;
+        o.h = m.dims == 2 ? m.h : 1;
+        o.elemsize = (int)m.elemsize;
+    }
+    if (ret == 0 && device) ret = s2_stream_synchronize(0);
+    return ret;
+}
+
+// An ncnn::Net with SharedLinear registered: load_param_mem, then load_model
+// on the same net whatever load_param returned.  Returns the layer count
+// left in the net; *param_ret / *model_ret receive the two codes.
+int h_net_load(const char* param_text, const void* model, long model_bytes, int* param_ret,
+               int* model_ret) {
+    ncnn::Net net;
+    net.register_custom_layer("SharedLinear", seedvr2::shared_linear_layer_creator,
+                              seedvr2::shared_linear_layer_destroyer);
+    *param_ret = net.load_param_mem(param_text);
+    *model_ret = net.load_model(static_cast<const unsigned char*>(model), (size_t)model_bytes);
+    return (int)net.layers().size();
+}
 
 }  // extern "C"

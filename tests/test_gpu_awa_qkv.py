@@ -195,3 +195,66 @@ def test_plan_rope_cache():
                         heads, d, (4, 3, 3), 1, 1e-5, pairs, shapes, tl)
     assert_close(ref1[0], rv, "cached rope video")
     assert_close(ref1[1], rt, "cached rope text")
+
+
+@pytest.mark.parametrize("shifted", [0, 1])
+def test_fused_qkv_720p_against_the_oracle(shifted):
+    """The headline kernel at the shape it is timed on: s2_awa_qkv_forward at
+    6x45x80 + 64 text tokens, hidden 2560, 20x128 heads, against the oracle's
+    attention forward (adaptive_window_attention.cpp:886-945) on every video
+    and text row, at max-abs <= 2e-2 and cosine >= 0.9999.
+
+    The projection feeding the oracle is X W^T + b in fp32.  For all 21,664
+    rows it is torch's CPU matmul (a library GEMM; the oracle's textbook
+    loop would take minutes here), tied to oracle.linear (the SharedLinear
+    forward of shared_linear.cpp:83-96) on every row of two windows -- the
+    first and a ragged edge window -- and every text row, where both must
+    agree to 1e-5 of the output scale."""
+    import torch
+    shapes, tl = [(6, 45, 80)], [64]
+    heads, d, pairs, hidden, target = 20, 128, 21, 2560, (4, 3, 3)
+    inner = heads * d
+    case = _inputs(71 + shifted, 21600, 64, hidden, heads, d, pairs)
+    bf = torch.bfloat16
+    cfg = capi.awa_config(heads, d, target, shifted, 1e-5, pairs)
+    with capi.AwaPlan(cfg, shapes, tl) as plan:
+        windows = plan.windows()[0]
+        fv, ft = capi.awa_qkv_forward(plan, torch.from_numpy(case["xv"]).cuda().to(bf),
+                                      torch.from_numpy(case["xt"]).cuda().to(bf),
+                                      torch.from_numpy(case["w"]).cuda().to(bf),
+                                      torch.from_numpy(case["b"]).cuda(),
+                                      torch.from_numpy(case["norms"]).cuda(),
+                                      torch.from_numpy(case["freqs"]).cuda(),
+                                      out_dtype=torch.float32)
+        torch.cuda.synchronize()
+    fv, ft = fv.cpu().numpy(), ft.cpu().numpy()
+    assert np.all(np.isfinite(fv)) and np.all(np.isfinite(ft))
+
+    w = torch.from_numpy(case["w"])
+    b = torch.from_numpy(case["b"])
+    qv = torch.addmm(b, torch.from_numpy(case["xv"]), w.t()).numpy()
+    qt = torch.addmm(b, torch.from_numpy(case["xt"]), w.t()).numpy()
+
+    # pin the library GEMM to the oracle's on the rows of two windows: the
+    # first, and the last one, a ragged edge window in both modes
+    def window_rows(win):
+        _, t0, t1, h0, h1, w0, w1, _, count = win
+        assert count == (t1 - t0) * (h1 - h0) * (w1 - w0)
+        return [(t * 45 + h) * 80 + x for t in range(t0, t1) for h in range(h0, h1)
+                for x in range(w0, w1)]
+    first, edge = windows[0], windows[-1]
+    assert edge[6] == 80 and edge[8] < 810       # ends at the grid's edge, not full size
+    rows = np.asarray(window_rows(first) + window_rows(edge), np.int32)
+    ov = oracle.linear(case["xv"], case["w"], case["b"], 0, rows=rows, threads=16, fast=True)
+    ot = oracle.linear(case["xt"], case["w"], case["b"], 0, threads=16, fast=True)
+    scale = max(float(np.abs(ov).max()), float(np.abs(ot).max()))
+    assert float(np.abs(qv[rows] - ov).max()) <= 1e-5 * scale
+    assert float(np.abs(qt - ot).max()) <= 1e-5 * scale
+
+    oc = dict(video=qv, text=qt, norms=case["norms"], freqs=case["freqs"])
+    rv, rt = oracle_awa(oc, heads, d, target, shifted, 1e-5, pairs, shapes, tl, fast=True)
+    assert_close(fv, rv, f"fused 720p video shifted={shifted}")
+    assert_close(ft, rt, f"fused 720p text shifted={shifted}")
+    # the two windows' rows on their own (a mistake confined to a window
+    # would be diluted in the whole-array cosine)
+    assert_close(fv[rows], rv[rows], f"fused 720p two windows shifted={shifted}")

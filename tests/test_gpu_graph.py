@@ -112,8 +112,11 @@ def _inputs(seed):
     lt = sum(TEXT)
     x_v = g.standard_normal((lv, D)).astype(np.float32)
     x_t = g.standard_normal((lt, D)).astype(np.float32)
+    # the reference's shape blobs: video_shape Mat(3, batch), text_length
+    # Mat(1, batch) (src/seedvr2/seedvr2_dit.cpp:143-161), which the
+    # attention layers decode on the host
     shape_blob = np.asarray(SHAPES, np.float32)
-    tl_blob = np.asarray(TEXT, np.float32)
+    tl_blob = np.asarray(TEXT, np.float32).reshape(-1, 1)
     mods = [(0.1 * g.standard_normal((len(SHAPES), D)) + (1.0 if k in (1, 4) else 0.0)).astype(np.float32)
             for k in range(6)]   # a_shift a_scale a_gate m_shift m_scale m_gate
     return x_v, x_t, shape_blob, tl_blob, mods
@@ -271,3 +274,84 @@ def test_graph_with_qkv_folded_into_the_attention_matches_the_unfused_graph():
     finally:
         plain.close()
         fused.close()
+
+
+def test_graph_orders_itself_behind_inputs_from_another_stream():
+    """Device inputs produced on another stream, by an allocator of that
+    stream, and handed over without a host synchronisation: the graph's
+    stream waits for that stream (ncnn::Extractor::input, s2_stream_wait)
+    and every layer runs on the graph's stream.  The producer stream first
+    spins, then writes the real inputs over garbage, so a graph that did not
+    wait would read the garbage."""
+    import torch
+    x_v, x_t, shape_blob, tl_blob, mods = _inputs(4)
+    host = [x_v, x_t, shape_blob, tl_blob] + mods
+    g = Graph(fuse=3)
+    try:
+        ref = g.run(host)
+        torch.cuda.synchronize()
+        ref = [r.clone() for r in ref]
+        side = torch.cuda.Stream()
+        dev = [torch.full(a.shape, float("nan"), device="cuda") if i not in (2, 3) else a
+               for i, a in enumerate(host)]
+        src = [torch.from_numpy(a).cuda() if i not in (2, 3) else None for i, a in enumerate(host)]
+        torch.cuda.synchronize()
+        with torch.cuda.stream(side):
+            torch.cuda._sleep(20_000_000)   # a bounded spin (cycles) on the producer stream
+            for i, t in enumerate(dev):
+                if i not in (2, 3):
+                    t.copy_(src[i])
+        blobs = (HBlob * 10)()
+        keep = []
+        for i, t in enumerate(dev):
+            if isinstance(t, np.ndarray):
+                keep.append(t)
+                blobs[i] = HBlob(t.ndim, t.shape[-1], t.shape[0] if t.ndim == 2 else 1, 4, 0,
+                                 t.ctypes.data)
+            else:
+                blobs[i] = HBlob(t.dim(), t.shape[-1], t.shape[0], 4, 1, t.data_ptr())
+        lv, lt = sum(a * b * c for a, b, c in SHAPES), sum(TEXT)
+        outs_t = [torch.empty(lv, D, device="cuda"), torch.empty(lt, D, device="cuda")]
+        outs = (HBlob * 2)()
+        for i, t in enumerate(outs_t):
+            outs[i] = HBlob(2, t.shape[1], t.shape[0], 4, 1, t.data_ptr())
+        shapes = np.asarray(SHAPES, np.int32).ravel()
+        tl = np.asarray(TEXT, np.int32)
+        L = _lib()
+        L.h_graph_run_from_stream.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
+                                              ctypes.POINTER(ctypes.c_int), ctypes.c_int,
+                                              ctypes.POINTER(HBlob), ctypes.POINTER(HBlob),
+                                              ctypes.c_void_p]
+        ret = L.h_graph_run_from_stream(g.h, shapes.ctypes.data_as(ctypes.POINTER(ctypes.c_int)),
+                                        tl.ctypes.data_as(ctypes.POINTER(ctypes.c_int)), len(SHAPES),
+                                        blobs, outs, ctypes.c_void_p(side.cuda_stream))
+        assert ret == 0, ret
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(outs_t[0].cpu().numpy(), ref[0].cpu().numpy())
+        np.testing.assert_array_equal(outs_t[1].cpu().numpy(), ref[1].cpu().numpy())
+    finally:
+        g.close()
+
+
+def test_repeated_runs_keep_a_fixed_set_of_device_blocks():
+    """Host inputs are uploaded into blocks the extractor owns and pools
+    again once consumed (the shape blobs in2 / in3 are read on the host and
+    never uploaded), and each run's outputs go back to the pool at the next
+    run: the graph's allocator holds the same number of blocks after every
+    run from the second on."""
+    import torch
+    x_v, x_t, shape_blob, tl_blob, mods = _inputs(5)
+    host = [x_v, x_t, shape_blob, tl_blob] + mods
+    L = _lib()
+    L.h_graph_owned_blocks.argtypes = [ctypes.c_void_p]
+    L.h_graph_owned_blocks.restype = ctypes.c_long
+    g = Graph(fuse=3)
+    try:
+        counts = []
+        for _ in range(4):
+            g.run(host)
+            torch.cuda.synchronize()
+            counts.append(L.h_graph_owned_blocks(g.h))
+        assert counts[1] == counts[2] == counts[3], counts
+    finally:
+        g.close()

@@ -97,3 +97,47 @@ def test_weight_file_must_match_the_graph(graph):
     text, model = graph
     assert _create(text, model[:-4])[0] == -100     # a layer runs out of weights
     assert _create(text, model + b"\0\0\0\0")[0] == -1   # bytes left over
+
+
+def _linear_gelu_graph(act):
+    """Two inputs -> SharedLinear (param 3 = act) -> GELU on both tops."""
+    return ("7767517\n5 6\n"
+            "Input in0 0 1 in0\n"
+            "Input in1 0 1 in1\n"
+            f"SharedLinear lin 2 2 in0 in1 a b 0=256 1=256 2=1 3={act}\n"
+            "GELU g0 1 1 a ga 0=0\n"
+            "GELU g1 1 1 b gb 0=0\n")
+
+
+@pytest.mark.parametrize("act, folded", [(0, 1), (1, 0), (2, 0)])
+def test_gelu_folds_only_into_a_projection_without_an_activation(act, folded):
+    """A GELU after a projection that already has a GELU (param 3 = 1) or
+    SwiGLU (3 = 2) epilogue stays a layer: folding it would drop one GELU,
+    or run the interleaved gate/up weight as a plain GELU GEMM."""
+    import numpy as np
+    rows = 512 if act == 2 else 256
+    model = np.zeros(rows * 256 + rows, np.float32).tobytes()
+    ret, info = _create(_linear_gelu_graph(act), model)
+    assert ret == 0 and info == (5, folded)
+
+
+@pytest.mark.parametrize("edit", [
+    lambda t: t.replace("Input                    in9              0 1 in9",
+                        "Input                    in9              0 2 in9", 1),       # short top list
+    lambda t: t.replace("Split                    split_in2        1 2 in2 in2_s0 in2_s1",
+                        "Split                    split_in2        3 2", 1),           # short bottom list
+])
+def test_short_blob_lists_leave_an_empty_net(graph, edit):
+    """A line whose bottom or top list ends early is refused and leaves no
+    half-built net behind: load_model on the same net then fails too."""
+    text, model = graph
+    edited = edit(text)
+    assert edited != text
+    L = harness()
+    P = ctypes.POINTER
+    L.h_net_load.argtypes = [ctypes.c_char_p, ctypes.c_void_p, ctypes.c_long, P(ctypes.c_int),
+                             P(ctypes.c_int)]
+    pr, mr = ctypes.c_int(), ctypes.c_int()
+    buf = ctypes.create_string_buffer(model, len(model))
+    layers = L.h_net_load(edited.encode(), buf, len(model), ctypes.byref(pr), ctypes.byref(mr))
+    assert pr.value == -1 and mr.value == -1 and layers == 0
