@@ -44,7 +44,7 @@ LAYER_SOURCES = ["ncnn/mat.cpp", "ncnn/layer.cpp", "ncnn/net.cpp", "ncnn/builtin
                  "layers/adaptive_window_attention.cpp", "layers/shared_linear.cpp",
                  "layers/decomposed_conv3d.cpp", "layers/vae_chunked_mha.cpp",
                  "layers/vae_resample3d.cpp", "layers/dit_block_ops.cpp",
-                 "layers/dit_block_graph.cpp"]
+                 "layers/dit_block_fold.cpp", "layers/dit_block_graph.cpp"]
 
 HIP_LIB = os.path.join(LIB, "libseedvr2_hip.so")
 LAYER_LIB = os.path.join(LIB, "libseedvr2_layers.so")

@@ -3,13 +3,17 @@
 
 #include <stdio.h>
 
+#include "dit_block_fold.h"
 #include "dit_block_ops.h"
 #include "seedvr2_hip.h"
 #include "shared_linear.h"
 
 namespace seedvr2 {
 
-DiTBlockGraph::DiTBlockGraph(void* stream) : alloc(stream), fused_gelu(0), fused_qkv(0) {}
+DiTBlockGraph::DiTBlockGraph(void* stream)
+    : alloc(stream), fused_gelu(0), fused_qkv(0), folded_modulation(0)
+{
+}
 
 DiTBlockGraph::~DiTBlockGraph()
 {
@@ -40,7 +44,7 @@ int DiTBlockGraph::register_layers()
 }
 
 int DiTBlockGraph::load(const char* param_path, const char* model_path, bool fp32_blobs,
-                        bool fuse_gelu, bool fuse_qkv)
+                        bool fuse_gelu, bool fuse_qkv, bool fold_modulation)
 {
     net.clear();
     net.opt.use_bf16_storage = !fp32_blobs;
@@ -50,13 +54,12 @@ int DiTBlockGraph::load(const char* param_path, const char* model_path, bool fp3
         ret = net.load_param(param_path);
     if (ret == 0)
         ret = net.load_model(model_path);
-    fused_gelu = (ret == 0 && fuse_gelu) ? net.fuse_shared_linear_gelu() : 0;
-    fused_qkv = (ret == 0 && fuse_qkv && !fp32_blobs) ? net.fuse_qkv_attention() : 0;
-    return ret;
+    return finish_load(ret, fp32_blobs, fuse_gelu, fuse_qkv, fold_modulation);
 }
 
 int DiTBlockGraph::load_mem(const char* param_text, const unsigned char* model,
-                            size_t model_bytes, bool fp32_blobs, bool fuse_gelu, bool fuse_qkv)
+                            size_t model_bytes, bool fp32_blobs, bool fuse_gelu, bool fuse_qkv,
+                            bool fold_modulation)
 {
     net.clear();
     net.opt.use_bf16_storage = !fp32_blobs;
@@ -66,9 +69,23 @@ int DiTBlockGraph::load_mem(const char* param_text, const unsigned char* model,
         ret = net.load_param_mem(param_text);
     if (ret == 0)
         ret = net.load_model(model, model_bytes);
-    fused_gelu = (ret == 0 && fuse_gelu) ? net.fuse_shared_linear_gelu() : 0;
-    fused_qkv = (ret == 0 && fuse_qkv && !fp32_blobs) ? net.fuse_qkv_attention() : 0;
-    return ret;
+    return finish_load(ret, fp32_blobs, fuse_gelu, fuse_qkv, fold_modulation);
+}
+
+// The graph folds, in an order where none hides another's pattern.
+int DiTBlockGraph::finish_load(int ret, bool fp32_blobs, bool fuse_gelu, bool fuse_qkv,
+                               bool fold_modulation)
+{
+    fused_gelu = fused_qkv = folded_modulation = 0;
+    if (ret != 0)
+        return ret;
+    if (fuse_gelu)
+        fused_gelu = net.fuse_shared_linear_gelu();
+    if (fold_modulation)
+        folded_modulation = fold_dit_modulation(net, &runtime_state);
+    if (fuse_qkv && !fp32_blobs)
+        fused_qkv = net.fuse_qkv_attention();
+    return 0;
 }
 
 // The extractor sequence of seedvr2_dit.cpp:722-833 on device blobs.

@@ -43,12 +43,14 @@ public:
     // fp32_blobs.  fuse_gelu folds SharedLinear -> GELU pairs; fuse_qkv (bf16
     // blobs only) folds each QKV SharedLinear into the attention layer it
     // feeds (ncnn::Net::fuse_qkv_attention), so the QKV blobs cannot be
-    // extracted as checkpoints.  Returns 0 or the first failing code of
-    // load_param / load_model.
+    // extracted as checkpoints; fold_modulation folds norm / modulation /
+    // residual chains written with ncnn built-ins (dit_block_fold.h).
+    // Returns 0 or the first failing code of load_param / load_model.
     int load(const char* param_path, const char* model_path, bool fp32_blobs = false,
-             bool fuse_gelu = true, bool fuse_qkv = true);
+             bool fuse_gelu = true, bool fuse_qkv = true, bool fold_modulation = true);
     int load_mem(const char* param_text, const unsigned char* model, size_t model_bytes,
-                 bool fp32_blobs = false, bool fuse_gelu = true, bool fuse_qkv = true);
+                 bool fp32_blobs = false, bool fuse_gelu = true, bool fuse_qkv = true,
+                 bool fold_modulation = true);
 
     // One pass of the graph.  inputs[0..9] are in0..in9 (host or device
     // Mats); out_video / out_text receive out0 / out1 as device blobs of this
@@ -66,6 +68,7 @@ public:
 
     int fused_gelu_count() const { return fused_gelu; }
     int fused_qkv_count() const { return fused_qkv; }
+    int folded_modulation_count() const { return folded_modulation; }
     HipDeviceAllocator& allocator() { return alloc; }
     ncnn::Net net;
     AdaptiveWindowRuntimeState runtime_state;
@@ -76,6 +79,8 @@ private:
     HipDeviceAllocator alloc;
     int fused_gelu;
     int fused_qkv;
+    int folded_modulation;
+    int finish_load(int ret, bool fp32_blobs, bool fuse_gelu, bool fuse_qkv, bool fold_modulation);
     std::vector<void*> last_blocks;   // uploads and outputs of the last run
 };
 

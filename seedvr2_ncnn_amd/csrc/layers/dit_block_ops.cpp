@@ -204,6 +204,165 @@ int DiTBlockOp::forward(const std::vector<ncnn::Mat>& bottom_blobs,
     return layer_status(ret);
 }
 
+DiTStreamOp::DiTStreamOp(int _kind, int _stream, const AdaptiveWindowRuntimeState* _state,
+                         float _epsilon, const ncnn::Mat& gate, const ncnn::Mat& shift,
+                         const ncnn::Mat& scale)
+    : kind(_kind), stream(_stream), state(_state), epsilon(_epsilon), dirty(true)
+{
+    one_blob_only = false;
+    support_inplace = false;
+    vectors[0] = gate;
+    vectors[1] = shift;
+    vectors[2] = scale;
+}
+
+DiTStreamOp::~DiTStreamOp()
+{
+}
+
+int DiTStreamOp::create_pipeline(const ncnn::Option& /*opt*/)
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    int devices = 0;
+    if (s2_device_count(&devices) != S2_OK || devices == 0)
+        return 0;
+    return layer_status(upload_locked());
+}
+
+int DiTStreamOp::destroy_pipeline(const ncnn::Option& /*opt*/)
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    vectors_gpu.release();
+    dirty = true;
+    return 0;
+}
+
+int DiTStreamOp::upload_locked() const
+{
+    if (!dirty)
+        return S2_OK;
+    int hidden = 0;
+    for (int i = 0; i < 3; i++)
+        if (!vectors[i].empty())
+            hidden = vectors[i].w;
+    if (hidden == 0)
+    {
+        dirty = false;
+        return S2_OK;
+    }
+    const size_t bytes = (size_t)hidden * sizeof(float);
+    int ret = vectors_gpu.reserve(3 * bytes);
+    for (int i = 0; ret == S2_OK && i < 3; i++)
+        if (!vectors[i].empty())
+            ret = s2_memcpy_h2d((char*)vectors_gpu.get() + i * bytes, vectors[i].data, bytes, 0);
+    if (ret == S2_OK)
+        ret = s2_stream_synchronize(0);
+    if (ret == S2_OK)
+        dirty = false;
+    return ret;
+}
+
+int DiTStreamOp::forward(const std::vector<ncnn::Mat>& bottom_blobs,
+                         std::vector<ncnn::Mat>& top_blobs, const ncnn::Option& opt) const
+{
+    std::lock_guard<std::mutex> lock(mutex);
+    const int n_bottoms[3] = {3, 3, 5};
+    const int n_tops[3] = {1, 1, 2};
+    if (!state || (int)bottom_blobs.size() != n_bottoms[kind] || (int)top_blobs.size() != n_tops[kind])
+        return -1;
+    const int batch = (int)state->video_shapes.size();
+    if (batch <= 0 || batch > 64 || (int)state->text_lengths.size() != batch)
+        return -1;
+    // this stream's rows per sample; the other stream has none
+    std::vector<int> rows(batch), none(batch, 0);
+    int total = 0;
+    for (int b = 0; b < batch; b++)
+    {
+        const std::array<int, 3>& s = state->video_shapes[b];
+        rows[b] = stream == 0 ? s[0] * s[1] * s[2] : state->text_lengths[b];
+        if (rows[b] < 0)
+            return -1;
+        total += rows[b];
+    }
+    const ncnn::Mat& x = bottom_blobs[0];
+    const int hidden = x.w;
+    for (int i = 0; i < 3; i++)
+        if (!vectors[i].empty() && vectors[i].w != hidden)
+            return -1;
+    if (hidden <= 0 || hidden % 4 != 0 || hidden > 4096 || !rows_ok(x, hidden, total))
+        return -1;
+    HipDeviceAllocator* dev = device_allocator_of(x);
+    HipDeviceAllocator* out = dynamic_cast<HipDeviceAllocator*>(opt.blob_allocator);
+    if (!out)
+        out = dev;
+    int ret = upload_locked();
+    if (ret != S2_OK)
+        return layer_status(ret);
+    const float* sv = vectors_gpu.get() ? static_cast<const float*>(vectors_gpu.get()) : 0;
+    const float* own[3];
+    for (int i = 0; i < 3; i++)
+        own[i] = vectors[i].empty() ? 0 : sv + (size_t)i * hidden;
+    const s2_dtype x_dtype = device_blob_dtype(x.elemsize, opt);
+    const size_t h_elem = (opt.use_bf16_storage || opt.use_fp16_storage) ? 2 : 4;
+    const s2_dtype h_dtype = device_blob_dtype(h_elem, opt);
+    const int* vr = stream == 0 ? &rows[0] : &none[0];
+    const int* tr = stream == 0 ? 0 : &rows[0];
+    void* s = dev->stream();
+    // pointers of this stream in its slot of the two-stream entry points
+    const void* xv = stream == 0 ? x.data : 0;
+    const void* xt = stream == 0 ? 0 : x.data;
+    auto vec = [&](int i, int want_stream) { return stream == want_stream ? own[i] : 0; };
+
+    if (kind == 0)
+    {
+        const ncnn::Mat& shift = bottom_blobs[1];
+        const ncnn::Mat& scale = bottom_blobs[2];
+        if (!modulation_ok(shift, hidden, batch) || !modulation_ok(scale, hidden, batch))
+            return -1;
+        top_blobs[0] = out->create_blob(hidden, total, h_elem);
+        if (top_blobs[0].empty())
+            return -100;
+        void* hv = stream == 0 ? top_blobs[0].data : 0;
+        void* ht = stream == 0 ? 0 : top_blobs[0].data;
+        ret = s2_dit_ada_in(hidden, epsilon, batch, vr, tr, xv, xt, x_dtype, hidden,
+                            (const float*)shift.data, (const float*)scale.data, vec(1, 0), vec(2, 0),
+                            vec(1, 1), vec(2, 1), hv, ht, h_dtype, hidden, s);
+        return layer_status(ret);
+    }
+    const ncnn::Mat& y = bottom_blobs[1];
+    const ncnn::Mat& gate = bottom_blobs[2];
+    if (!rows_ok(y, hidden, total) || !modulation_ok(gate, hidden, batch))
+        return -1;
+    const s2_dtype y_dtype = device_blob_dtype(y.elemsize, opt);
+    const void* yv = stream == 0 ? y.data : 0;
+    const void* yt = stream == 0 ? 0 : y.data;
+    top_blobs[0] = out->create_blob(hidden, total, x.elemsize);
+    if (top_blobs[0].empty())
+        return -100;
+    void* ov = stream == 0 ? top_blobs[0].data : 0;
+    void* ot = stream == 0 ? 0 : top_blobs[0].data;
+    if (kind == 1)
+    {
+        ret = s2_dit_ada_out(hidden, batch, vr, tr, xv, xt, x_dtype, hidden, yv, yt, y_dtype, hidden,
+                             (const float*)gate.data, vec(0, 0), vec(0, 1), ov, ot, hidden, s);
+        return layer_status(ret);
+    }
+    const ncnn::Mat& shift = bottom_blobs[3];
+    const ncnn::Mat& scale = bottom_blobs[4];
+    if (!modulation_ok(shift, hidden, batch) || !modulation_ok(scale, hidden, batch))
+        return -1;
+    top_blobs[1] = out->create_blob(hidden, total, h_elem);
+    if (top_blobs[1].empty())
+        return -100;
+    void* hv = stream == 0 ? top_blobs[1].data : 0;
+    void* ht = stream == 0 ? 0 : top_blobs[1].data;
+    ret = s2_dit_ada_out_in(hidden, batch, vr, tr, xv, xt, x_dtype, hidden, yv, yt, y_dtype, hidden,
+                            (const float*)gate.data, vec(0, 0), vec(0, 1), ov, ot, hidden, epsilon,
+                            (const float*)shift.data, (const float*)scale.data, vec(1, 0), vec(2, 0),
+                            vec(1, 1), vec(2, 1), hv, ht, h_dtype, hidden, s);
+    return layer_status(ret);
+}
+
 ncnn::Layer* dit_ada_in_layer_creator(void* userdata)
 {
     return new DiTBlockOp(0, static_cast<const AdaptiveWindowRuntimeState*>(userdata));

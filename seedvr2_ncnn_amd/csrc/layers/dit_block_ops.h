@@ -69,6 +69,47 @@ private:
     mutable bool dirty;
 };
 
+// One token stream's pass, made by the graph fold (dit_block_fold.h) from
+// a chain of ncnn built-ins:
+//   kind 0 ada_in      bottoms x, shift, scale           top  h
+//   kind 1 ada_out     bottoms x, y, gate                top  out
+//   kind 2 ada_out_in  bottoms x, y, gate, shift, scale  tops out, h
+// with the arithmetic of DiTBlockOp.  stream 0 is the video stream, 1 the
+// text stream: its rows per sample come from the runtime state.  hidden is
+// the width of x.  The block's own [hidden] vectors of the stream (gate,
+// shift, scale; empty Mats for none) come from the chain's MemoryData.
+class DiTStreamOp : public ncnn::Layer
+{
+public:
+    DiTStreamOp(int kind, int stream, const AdaptiveWindowRuntimeState* state, float epsilon,
+                const ncnn::Mat& gate, const ncnn::Mat& shift, const ncnn::Mat& scale);
+    virtual ~DiTStreamOp();
+
+    virtual int create_pipeline(const ncnn::Option& opt);
+    virtual int destroy_pipeline(const ncnn::Option& opt);
+    virtual int forward(const std::vector<ncnn::Mat>& bottom_blobs,
+                        std::vector<ncnn::Mat>& top_blobs,
+                        const ncnn::Option& opt) const;
+
+    int kind_of() const { return kind; }
+    int stream_of() const { return stream; }
+    float epsilon_of() const { return epsilon; }
+    const ncnn::Mat& vector(int i) const { return vectors[i]; }   // 0 gate, 1 shift, 2 scale
+
+private:
+    int upload_locked() const;
+
+    int kind;
+    int stream;
+    const AdaptiveWindowRuntimeState* state;
+    float epsilon;
+    ncnn::Mat vectors[3];
+
+    mutable std::mutex mutex;
+    mutable DeviceBuffer vectors_gpu;   // [3][hidden] fp32, a slot per present vector
+    mutable bool dirty;
+};
+
 ncnn::Layer* dit_ada_in_layer_creator(void* userdata);
 ncnn::Layer* dit_ada_out_layer_creator(void* userdata);
 ncnn::Layer* dit_ada_out_in_layer_creator(void* userdata);

@@ -172,6 +172,7 @@ void Net::clear() {
     layer_custom_.clear();
     consumer_count_.clear();
     passthrough_.clear();
+    removed_.clear();
     blobs_.clear();
 }
 
@@ -248,6 +249,7 @@ int Net::load_param_mem(const char* mem) {
         layers_.push_back(layer);
         layer_custom_.push_back(ci);
         passthrough_.push_back(0);
+        removed_.push_back(0);
         for (int i = 0; i < nb; i++) {
             std::string b;
             if (!(ls >> b)) {
@@ -383,6 +385,66 @@ int Net::fuse_qkv_attention() {
         ++fused;
     }
     return fused;
+}
+
+int Net::replace_layers(const std::vector<int>& remove, Layer* fused, const std::vector<int>& bottoms,
+                        const std::vector<int>& tops) {
+    for (size_t i = 0; i < tops.size(); i++) {
+        const int p = blobs_[tops[i]].producer;
+        bool ok = false;
+        for (size_t r = 0; r < remove.size(); r++) ok = ok || remove[r] == p;
+        if (!ok) return -1;
+    }
+    for (size_t r = 0; r < remove.size(); r++) {
+        Layer* l = layers_[remove[r]];
+        for (size_t i = 0; i < l->bottoms.size(); i++) consumer_count_[l->bottoms[i]]--;
+        for (size_t i = 0; i < l->tops.size(); i++) blobs_[l->tops[i]].producer = -1;
+        l->bottoms.clear();
+        l->tops.clear();
+        removed_[remove[r]] = 1;
+    }
+    const int li = (int)layers_.size();
+    layers_.push_back(fused);
+    layer_custom_.push_back(-1);
+    passthrough_.push_back(0);
+    removed_.push_back(0);
+    fused->bottoms = bottoms;
+    fused->tops = tops;
+    for (size_t i = 0; i < bottoms.size(); i++) {
+        consumer_count_[bottoms[i]]++;
+        blobs_[bottoms[i]].consumer = li;
+    }
+    for (size_t i = 0; i < tops.size(); i++) blobs_[tops[i]].producer = li;
+    return li;
+}
+
+int Net::prune_splits() {
+    int dropped = 0;
+    for (bool again = true; again;) {
+        again = false;
+        for (size_t li = 0; li < layers_.size(); li++) {
+            Layer* l = layers_[li];
+            if (removed_[li] || l->type != "Split") continue;
+            std::vector<int> keep;
+            for (size_t t = 0; t < l->tops.size(); t++) {
+                if (consumer_count_[l->tops[t]] > 0) {
+                    keep.push_back(l->tops[t]);
+                } else {
+                    blobs_[l->tops[t]].producer = -1;
+                    ++dropped;
+                }
+            }
+            if (keep.size() == l->tops.size()) continue;
+            l->tops = keep;
+            if (keep.empty()) {
+                for (size_t i = 0; i < l->bottoms.size(); i++) consumer_count_[l->bottoms[i]]--;
+                l->bottoms.clear();
+                removed_[li] = 1;
+                again = true;
+            }
+        }
+    }
+    return dropped;
 }
 
 Extractor Net::create_extractor() const { return Extractor(this, blobs_.size()); }

@@ -98,6 +98,20 @@ public:
     // Call after load_model; returns the number of pairs fused.
     int fuse_qkv_attention();
 
+    // This build: graph rewriting for fusion passes.  The layers `remove`
+    // stop running (their objects live until clear()); `fused`, owned by the
+    // net from now on, reads `bottoms` and produces `tops`, each a top of a
+    // removed layer, and the removed layers' other tops lose their producer
+    // (they can no longer be extracted).  Returns the new layer's index, or
+    // -1 when a top was not produced by a removed layer.
+    int replace_layers(const std::vector<int>& remove, Layer* fused, const std::vector<int>& bottoms,
+                       const std::vector<int>& tops);
+    // Drops the tops of Split layers that nothing consumes, and Split layers
+    // left without a top; returns the number of tops dropped.
+    int prune_splits();
+    int consumer_count(int blob) const { return consumer_count_[blob]; }
+    bool removed(int layer) const { return removed_[layer] != 0; }
+
 protected:
     friend class Extractor;
     int forward_layer(int layer_index, std::vector<Mat>& blob_mats, std::vector<int>& pending,
@@ -119,6 +133,7 @@ private:
     std::vector<int> layer_custom_;     // index into custom_ or -1 (built-in)
     std::vector<int> consumer_count_;   // per blob
     std::vector<char> passthrough_;     // per layer: forward copies bottom to top
+    std::vector<char> removed_;         // per layer: replaced by a fusion pass
     std::vector<Blob> blobs_;
 };
 

@@ -14,7 +14,8 @@ with Split layers wherever a blob has more than one consumer, as ncnn graphs
 have.  Even blocks use regular windows, odd blocks shifted ones; block 1
 carries the block's own per-stream modulation vectors (param 2 = 1).
 
-Usage: python tests/golden/dit_graph.py  rewrites dit_blocks_2.param here.
+Usage: python tests/golden/dit_graph.py  rewrites dit_blocks_2.param and
+dit_blocks_2_builtin.param here.
 """
 from __future__ import annotations
 
@@ -124,6 +125,144 @@ def param_text(blocks=BLOCKS):
     return "7767517\n" + f"{len(layers)} {len(blobs)}\n" + "\n".join(layers) + "\n"
 
 
+BUILTIN_PARAM_PATH = os.path.join(HERE, "dit_blocks_2_builtin.param")
+
+
+def _with_splits(layers, first_free):
+    """Inserts a Split after the producer of every blob read more than once
+    (tops blob_s0, blob_s1, ... handed to the consumers in order), as ncnn
+    exports write them."""
+    uses = {}
+    for _, _, bottoms, _, _ in layers:
+        for b in bottoms:
+            uses[b] = uses.get(b, 0) + 1
+    taken = {}
+    out = []
+    for type_, name, bottoms, tops, params in layers:
+        nb = []
+        for b in bottoms:
+            if uses[b] > 1:
+                i = taken.get(b, 0)
+                taken[b] = i + 1
+                nb.append(f"{b}_s{i}")
+            else:
+                nb.append(b)
+        out.append((type_, name, nb, tops, params))
+        for t in tops:
+            if uses.get(t, 0) > 1:
+                out.append(("Split", f"split_{t}", [t], [f"{t}_s{i}" for i in range(uses[t])], ""))
+    return out
+
+
+def builtin_layers(blocks=BLOCKS):
+    """The same blocks written with ncnn built-ins in place of DiTAdaIn,
+    DiTAdaOut and DiTAdaOutIn: RMSNorm (block 0 as UnaryOp square ->
+    Reduction mean -> BinaryOp add eps -> UnaryOp rsqrt -> BinaryOp mul,
+    odd blocks as an RMSNorm layer without affine), the modulation as
+    BinaryOp mul / add with the per-sample inputs (plus MemoryData vectors
+    of the block's own, odd blocks), the gated residual as BinaryOp mul /
+    add.  Per stream, as the exported graph keeps the streams apart."""
+    L = []
+
+    def add(type_, name, bottoms, tops, params=""):
+        L.append((type_, name, list(bottoms), list(tops), params))
+
+    for i in range(10):
+        add("Input", f"in{i}", [], [f"in{i}"])
+    rv, rt = "in0", "in1"
+    for b in range(blocks):
+        p = f"b{b}_"
+        own = b % 2 == 1
+
+        def mod(inp, vec_name):
+            """in_k, or in_k + the block's MemoryData vector."""
+            if not own:
+                return inp
+            add("MemoryData", p + vec_name, [], [p + vec_name], f"0={HIDDEN}")
+            add("BinaryOp", p + vec_name + "_add", [inp, p + vec_name], [p + vec_name + "_sum"], "0=0")
+            return p + vec_name + "_sum"
+
+        def norm(x, tag):
+            if b == 0:
+                add("UnaryOp", p + tag + "_sq", [x], [p + tag + "_sq"], "0=4")
+                add("Reduction", p + tag + "_ms", [p + tag + "_sq"], [p + tag + "_ms"],
+                    "0=3 1=0 -23303=1,-1 4=1 5=1")
+                add("BinaryOp", p + tag + "_eps", [p + tag + "_ms"], [p + tag + "_mse"],
+                    "0=0 1=1 2=1.000000e-05")
+                add("UnaryOp", p + tag + "_rs", [p + tag + "_mse"], [p + tag + "_rs"], "0=6")
+                add("BinaryOp", p + tag + "_n", [x, p + tag + "_rs"], [p + tag + "_n"], "0=2")
+            else:
+                add("RMSNorm", p + tag + "_n", [x], [p + tag + "_n"], f"0={HIDDEN} 1=1.000000e-05 2=0")
+            return p + tag + "_n"
+
+        def modulate(x, tag, shift_in, scale_in, shift_vec, scale_vec):
+            n = norm(x, tag)
+            sc = mod(scale_in, scale_vec)
+            sh = mod(shift_in, shift_vec)
+            add("BinaryOp", p + tag + "_scale", [n, sc], [p + tag + "_m1"], "0=2")
+            add("BinaryOp", p + tag + "_shift", [p + tag + "_m1", sh], [p + tag + "_h"], "0=0")
+            return p + tag + "_h"
+
+        def gated(x, y, tag, gate_in, gate_vec, top):
+            g = mod(gate_in, gate_vec)
+            add("BinaryOp", p + tag + "_gate", [y, g], [p + tag + "_g"], "0=2")
+            add("BinaryOp", p + tag + "_res", [x, p + tag + "_g"], [top], "0=0")
+            return top
+
+        h_v = modulate(rv, "an_v", "in4", "in5", "vshift", "vscale")
+        h_t = modulate(rt, "an_t", "in4", "in5", "tshift", "tscale")
+        add("SharedLinear", p + "qkv", [h_v, h_t], [p + "qkv_v", p + "qkv_t"], f"0={3 * HIDDEN} 1={HIDDEN} 2=1")
+        add("AdaptiveWindowAttention", p + "attn", [p + "qkv_v", p + "qkv_t", "in2", "in3"],
+            [p + "a_v", p + "a_t"],
+            f"0={HEADS} 1={HEAD_DIM} 2={TARGET[0]} 3={TARGET[1]} 4={TARGET[2]} 5={b % 2} "
+            f"6=1.000000e-05 7={PAIRS} 8=0 9=0 10=0")
+        add("SharedLinear", p + "out", [p + "a_v", p + "a_t"], [p + "o_v", p + "o_t"], f"0={HIDDEN} 1={HIDDEN} 2=1")
+        r_v = gated(rv, p + "o_v", "ag_v", "in6", "vgate", p + "r_v")
+        r_t = gated(rt, p + "o_t", "ag_t", "in6", "tgate", p + "r_t")
+        m_v = modulate(r_v, "mn_v", "in7", "in8", "m_vshift", "m_vscale")
+        m_t = modulate(r_t, "mn_t", "in7", "in8", "m_tshift", "m_tscale")
+        add("SharedLinear", p + "up", [m_v, m_t], [p + "u_v", p + "u_t"], f"0={MLP} 1={HIDDEN} 2=1")
+        add("GELU", p + "gelu_v", [p + "u_v"], [p + "g_v"], "0=0")
+        add("GELU", p + "gelu_t", [p + "u_t"], [p + "g_t"], "0=0")
+        add("SharedLinear", p + "down", [p + "g_v", p + "g_t"], [p + "y_v", p + "y_t"], f"0={HIDDEN} 1={MLP} 2=1")
+        last = b + 1 == blocks
+        ov, ot = ("out0", "out1") if last else (p + "out_v", p + "out_t")
+        rv = gated(r_v, p + "y_v", "mg_v", "in9", "m_vgate", ov)
+        rt = gated(r_t, p + "y_t", "mg_t", "in9", "m_tgate", ot)
+    return _with_splits(L, 0)
+
+
+def builtin_param_text(blocks=BLOCKS):
+    layers = builtin_layers(blocks)
+    lines = []
+    blobs = set()
+    for type_, name, bottoms, tops, params in layers:
+        line = f"{type_:<24} {name:<16} {len(bottoms)} {len(tops)} " + " ".join(bottoms + tops)
+        lines.append(line + (" " + params if params else ""))
+        blobs.update(tops)
+    return "7767517\n" + f"{len(lines)} {len(blobs)}\n" + "\n".join(lines) + "\n"
+
+
+def builtin_model_bytes(weights, blocks=BLOCKS):
+    """The .bin of builtin_param_text: each layer's weights in layer order
+    (SharedLinear and attention as in model_bytes, MemoryData raw fp32)."""
+    parts = []
+    for type_, name, _, _, _ in builtin_layers(blocks):
+        b = int(name[1:name.index("_")]) if name.startswith("b") and name[1].isdigit() else None
+        if b is None:
+            continue
+        w = weights[b]
+        key = name[name.index("_") + 1:]
+        if type_ == "MemoryData":
+            parts.append(w["stream"][key])
+        elif type_ == "SharedLinear":
+            k = {"qkv": "qkv", "out": "o", "up": "up", "down": "dn"}[key]
+            parts += [w[k], w["b_" + k]]
+        elif type_ == "AdaptiveWindowAttention":
+            parts += [w["norms"][0], w["norms"][1], w["norms"][2], w["norms"][3], w["freqs"]]
+    return b"".join(np.ascontiguousarray(p, dtype="<f4").tobytes() for p in parts)
+
+
 def model_bytes(weights):
     """The .bin: each layer's load_model data in layer order, raw fp32 (the
     type-1 loads of SharedLinear, AdaptiveWindowAttention and the block ops)."""
@@ -146,4 +285,6 @@ def model_bytes(weights):
 if __name__ == "__main__":
     with open(PARAM_PATH, "w") as f:
         f.write(param_text())
-    print("wrote", PARAM_PATH)
+    with open(BUILTIN_PARAM_PATH, "w") as f:
+        f.write(builtin_param_text())
+    print("wrote", PARAM_PATH, BUILTIN_PARAM_PATH)

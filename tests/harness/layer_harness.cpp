@@ -286,16 +286,16 @@ int h_build_plan(const int* shapes, int batch, const int* target, int shifted, i
 // ---- DiT block graph (seedvr2::DiTBlockGraph over ncnn::Net) -------------------
 
 // Loads a block graph from .param text and .bin bytes; fuse: bit 0 folds
-// SharedLinear -> GELU, bit 1 folds the QKV SharedLinear into the attention.
-// Returns load's code; *out is the graph (destroy with h_graph_destroy) or
-// null.
+// SharedLinear -> GELU, bit 1 folds the QKV SharedLinear into the attention,
+// bit 2 folds built-in norm / modulation / residual chains.  Returns load's
+// code; *out is the graph (destroy with h_graph_destroy) or null.
 int h_graph_create(const char* param_text, const void* model, long model_bytes, int fp32_blobs,
                    int fuse, void** out) {
     *out = 0;
     seedvr2::DiTBlockGraph* g = new seedvr2::DiTBlockGraph(0);
     const int ret = g->load_mem(param_text, static_cast<const unsigned char*>(model),
                                 (size_t)model_bytes, fp32_blobs != 0, (fuse & 1) != 0,
-                                (fuse & 2) != 0);
+                                (fuse & 2) != 0, (fuse & 4) != 0);
     if (ret != 0) {
         delete g;
         return ret;
@@ -306,6 +306,10 @@ int h_graph_create(const char* param_text, const void* model, long model_bytes, 
 
 int h_graph_fused_gelu(void* graph) {
     return static_cast<seedvr2::DiTBlockGraph*>(graph)->fused_gelu_count();
+}
+
+int h_graph_folded_modulation(void* graph) {
+    return static_cast<seedvr2::DiTBlockGraph*>(graph)->folded_modulation_count();
 }
 
 int h_graph_fused_qkv(void* graph) {

@@ -141,3 +141,60 @@ def test_short_blob_lists_leave_an_empty_net(graph, edit):
     buf = ctypes.create_string_buffer(model, len(model))
     layers = L.h_net_load(edited.encode(), buf, len(model), ctypes.byref(pr), ctypes.byref(mr))
     assert pr.value == -1 and mr.value == -1 and layers == 0
+
+
+# ---- the same blocks written with ncnn built-ins ------------------------------------
+
+
+@pytest.fixture(scope="module")
+def builtin_graph():
+    with open(dit_graph.BUILTIN_PARAM_PATH) as f:
+        text = f.read()
+    return text, dit_graph.builtin_model_bytes(dit_graph.block_weights())
+
+
+def _create_counts(text, model, fuse):
+    L = _lib()
+    L.h_graph_folded_modulation.argtypes = [ctypes.c_void_p]
+    g = ctypes.c_void_p()
+    buf = ctypes.create_string_buffer(model, max(1, len(model)))
+    ret = L.h_graph_create(text.encode(), buf, len(model), 0, fuse, ctypes.byref(g))
+    if ret != 0:
+        return ret, None
+    counts = (L.h_graph_fused_gelu(g), L.h_graph_folded_modulation(g), L.h_graph_fused_qkv(g))
+    L.h_graph_destroy(g)
+    return 0, counts
+
+
+def test_committed_builtin_param_is_the_generators(builtin_graph):
+    assert builtin_graph[0] == dit_graph.builtin_param_text()
+
+
+def test_builtin_graph_uses_only_ncnn_layer_types(builtin_graph):
+    types = {line.split()[0] for line in builtin_graph[0].strip().split("\n")[2:]}
+    assert types == {"Input", "Split", "UnaryOp", "Reduction", "BinaryOp", "RMSNorm", "MemoryData",
+                     "SharedLinear", "AdaptiveWindowAttention", "GELU"}
+
+
+def test_builtin_graph_folds_its_norm_modulation_and_residual_chains(builtin_graph):
+    """Per block and stream: the attention's ada_in, its gated residual merged
+    with the MLP's ada_in (ada_out_in), and the MLP's gated residual, which
+    for block 0 merges with block 1's attention ada_in: 2 x (2 + 2) + 2
+    passes.  Without the fold the graph loads as written."""
+    text, model = builtin_graph
+    assert _create_counts(text, model, 7) == (0, (2, 10, 2))
+    assert _create_counts(text, model, 1) == (0, (2, 0, 0))
+    assert _create_counts(text, model, 5) == (0, (2, 10, 0))
+
+
+def test_chain_with_an_extra_consumer_is_not_folded(builtin_graph):
+    """A norm whose intermediate blob has a second reader stays as written:
+    here block 0's video mean of squares also feeds an extra layer, so that
+    stream's attention ada_in is not folded (9 passes instead of 10)."""
+    text, model = builtin_graph
+    lines = text.strip().split("\n")
+    nl, nb = map(int, lines[1].split())
+    body = lines[2:] + ["UnaryOp extra 1 1 b0_an_v_ms extra_out 0=0"]
+    edited = "7767517\n" + f"{nl + 1} {nb + 1}\n" + "\n".join(body) + "\n"
+    ret, counts = _create_counts(edited, model, 5)
+    assert ret == 0 and counts[1] == 9
