@@ -11,7 +11,7 @@
 namespace seedvr2 {
 
 DiTBlockGraph::DiTBlockGraph(void* stream)
-    : alloc(stream), fused_gelu(0), fused_qkv(0), folded_modulation(0)
+    : alloc(stream), fused_gelu(0), fused_qkv(0), folded_modulation(0), fused_swiglu(0)
 {
 }
 
@@ -76,15 +76,17 @@ int DiTBlockGraph::load_mem(const char* param_text, const unsigned char* model,
 int DiTBlockGraph::finish_load(int ret, bool fp32_blobs, bool fuse_gelu, bool fuse_qkv,
                                bool fold_modulation)
 {
-    fused_gelu = fused_qkv = folded_modulation = 0;
+    fused_gelu = fused_qkv = folded_modulation = fused_swiglu = 0;
     if (ret != 0)
         return ret;
     if (fuse_gelu)
         fused_gelu = net.fuse_shared_linear_gelu();
+    if (fuse_gelu && !fp32_blobs)   // the SwiGLU epilogue takes bf16 activations
+        fused_swiglu = net.fuse_swiglu();
     if (fold_modulation)
         folded_modulation = fold_dit_modulation(net, &runtime_state);
     if (fuse_qkv && !fp32_blobs)
-        fused_qkv = net.fuse_qkv_attention();
+        fused_qkv = net.fuse_qkv_attention() + net.fuse_split_qkv_attention();
     return 0;
 }
 

@@ -42,8 +42,11 @@ public:
     // (bf16 blobs between the GEMMs and the attention) is on unless
     // fp32_blobs.  fuse_gelu folds SharedLinear -> GELU pairs; fuse_qkv (bf16
     // blobs only) folds each QKV SharedLinear into the attention layer it
-    // feeds (ncnn::Net::fuse_qkv_attention), so the QKV blobs cannot be
-    // extracted as checkpoints; fold_modulation folds norm / modulation /
+    // feeds (ncnn::Net::fuse_qkv_attention), and the split q / k / v
+    // projections of v3 graphs likewise (fuse_split_qkv_attention), so the
+    // QKV blobs cannot be extracted as checkpoints; with bf16 blobs
+    // fuse_gelu also folds gate / up / Swish / mul chains into one SwiGLU
+    // projection (fuse_swiglu); fold_modulation folds norm / modulation /
     // residual chains written with ncnn built-ins (dit_block_fold.h).
     // Returns 0 or the first failing code of load_param / load_model.
     int load(const char* param_path, const char* model_path, bool fp32_blobs = false,
@@ -69,6 +72,7 @@ public:
     int fused_gelu_count() const { return fused_gelu; }
     int fused_qkv_count() const { return fused_qkv; }
     int folded_modulation_count() const { return folded_modulation; }
+    int fused_swiglu_count() const { return fused_swiglu; }
     HipDeviceAllocator& allocator() { return alloc; }
     ncnn::Net net;
     AdaptiveWindowRuntimeState runtime_state;
@@ -80,6 +84,7 @@ private:
     int fused_gelu;
     int fused_qkv;
     int folded_modulation;
+    int fused_swiglu;
     int finish_load(int ret, bool fp32_blobs, bool fuse_gelu, bool fuse_qkv, bool fold_modulation);
     std::vector<void*> last_blocks;   // uploads and outputs of the last run
 };

@@ -98,6 +98,64 @@ int SharedLinear::load_model(const ncnn::ModelBin& mb)
     return 0;
 }
 
+SharedLinear* SharedLinear::stack(const std::vector<const SharedLinear*>& parts, int act)
+{
+    if (parts.empty() || (act != S2_ACT_NONE && act != S2_ACT_SWIGLU) ||
+        (act == S2_ACT_SWIGLU && parts.size() != 2))
+        return 0;
+    const int k = parts[0]->num_input;
+    int n = 0;
+    bool any_bias = false;
+    for (size_t i = 0; i < parts.size(); i++)
+    {
+        const SharedLinear* p = parts[i];
+        std::lock_guard<std::mutex> lock(p->mutex);
+        if (p->num_input != k || p->activation != S2_ACT_NONE || p->weight_data.empty())
+            return 0;
+        n += p->num_output;
+        any_bias = any_bias || p->bias_term;
+    }
+    if (act == S2_ACT_SWIGLU && parts[0]->num_output != parts[1]->num_output)
+        return 0;
+    ncnn::Mat w((int)((size_t)k * n));
+    ncnn::Mat b;
+    if (any_bias)
+        b.create(n);
+    if (w.empty() || (any_bias && b.empty()))
+        return 0;
+    size_t row = 0;
+    for (size_t i = 0; i < parts.size(); i++)
+    {
+        const SharedLinear* p = parts[i];
+        std::lock_guard<std::mutex> lock(p->mutex);
+        memcpy((float*)w.data + row * k, p->weight_data.data, (size_t)p->num_output * k * sizeof(float));
+        if (any_bias)
+        {
+            float* bd = (float*)b.data + row;
+            if (p->bias_term)
+                memcpy(bd, p->bias_data.data, (size_t)p->num_output * sizeof(float));
+            else
+                memset(bd, 0, (size_t)p->num_output * sizeof(float));
+        }
+        row += p->num_output;
+    }
+    ncnn::ParamDict pd;
+    pd.set(0, act == S2_ACT_SWIGLU ? n / 2 : n);
+    pd.set(1, k);
+    pd.set(2, any_bias ? 1 : 0);
+    pd.set(3, act);
+    SharedLinear* s = new SharedLinear();
+    s->type = "SharedLinear";
+    const ncnn::Mat mats[2] = {w, b};
+    ncnn::ModelBinFromMatArray mb(mats);
+    if (s->load_param(pd) != 0 || s->load_model(mb) != 0)
+    {
+        delete s;
+        return 0;
+    }
+    return s;
+}
+
 int SharedLinear::set_activation(int act)
 {
     if (act != S2_ACT_NONE && act != S2_ACT_GELU)

@@ -13,6 +13,7 @@
 #define SEEDVR2_SHARED_LINEAR_H
 
 #include <mutex>
+#include <vector>
 
 #include <layer.h>
 
@@ -50,6 +51,15 @@ public:
     int output_width() const { return num_output; }
     int activation_kind() const { return activation; }
     int device_weights(const uint16_t** weight, const float** bias) const;
+
+    // A new projection whose outputs are these projections' outputs side by
+    // side (their [N][K] weight rows stacked in order; zero bias rows for a
+    // part without a bias term), for graph folds: the q, k and v projections
+    // of split graphs (activation S2_ACT_NONE), or a gate and an up
+    // projection (S2_ACT_SWIGLU, exactly two parts of one width).  The parts
+    // must share num_input, carry no activation and hold their weights.
+    // Null when they do not, or when the result breaks load_param's rules.
+    static SharedLinear* stack(const std::vector<const SharedLinear*>& parts, int activation);
 
 private:
     // forward and create_pipeline without the mapping of C-ABI codes to the

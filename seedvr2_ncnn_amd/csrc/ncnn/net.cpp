@@ -447,6 +447,139 @@ int Net::prune_splits() {
     return dropped;
 }
 
+int Net::split_source(int blob) const {
+    for (int guard = 0; guard < 64 && blob >= 0; guard++) {
+        const int p = blobs_[blob].producer;
+        if (p < 0 || layers_[p]->type != "Split") break;
+        blob = layers_[p]->bottoms[0];
+    }
+    return blob;
+}
+
+int Net::fuse_split_qkv_attention() {
+    int fused = 0;
+    const size_t count = layers_.size();
+    for (size_t ai = 0; ai < count; ai++) {
+        Layer* a = layers_[ai];
+        if (removed_[ai] || a->type != "AdaptiveWindowAttention" || a->bottoms.size() != 8) continue;
+        seedvr2::AdaptiveWindowAttention* awa = dynamic_cast<seedvr2::AdaptiveWindowAttention*>(a);
+        std::vector<const seedvr2::SharedLinear*> parts;
+        std::vector<int> part_layers;
+        bool ok = awa != 0;
+        for (int j = 0; ok && j < 3; j++) {
+            // q, k, v: one projection each, its video top in slot j, its
+            // text top in slot 3 + j, read by nothing else
+            const int bv = a->bottoms[j], bt = a->bottoms[3 + j];
+            const int p = blobs_[bv].producer;
+            const seedvr2::SharedLinear* sl =
+                p >= 0 ? dynamic_cast<const seedvr2::SharedLinear*>(layers_[p]) : 0;
+            ok = sl && blobs_[bt].producer == p && layers_[p]->bottoms.size() == 2 &&
+                 layers_[p]->tops.size() == 2 && layers_[p]->tops[0] == bv && layers_[p]->tops[1] == bt &&
+                 consumer_count_[bv] == 1 && consumer_count_[bt] == 1;
+            if (ok && j > 0)   // all three read the same two token streams
+                ok = split_source(layers_[p]->bottoms[0]) == split_source(layers_[part_layers[0]]->bottoms[0]) &&
+                     split_source(layers_[p]->bottoms[1]) == split_source(layers_[part_layers[0]]->bottoms[1]);
+            if (ok) {
+                parts.push_back(sl);
+                part_layers.push_back(p);
+            }
+        }
+        if (!ok) continue;
+        seedvr2::SharedLinear* qkv = seedvr2::SharedLinear::stack(parts, S2_ACT_NONE);
+        if (!qkv) continue;
+        qkv->name = layers_[part_layers[0]]->name + "_stacked_qkv";
+        if (qkv->create_pipeline(opt) != 0 || awa->set_qkv_projection(qkv) != 0) {
+            qkv->destroy_pipeline(opt);
+            delete qkv;
+            continue;
+        }
+        const int in_v = layers_[part_layers[0]]->bottoms[0];
+        const int in_t = layers_[part_layers[0]]->bottoms[1];
+        // the three projections stop running; the stacked one (owned by the
+        // net, run by the attention layer) takes their place
+        replace_layers(part_layers, qkv, std::vector<int>(), std::vector<int>());
+        // the attention now reads the token streams and the two shape blobs
+        for (int j = 0; j < 6; j++) consumer_count_[a->bottoms[j]]--;
+        const int shape = a->bottoms[6], length = a->bottoms[7];
+        a->bottoms.clear();
+        a->bottoms.push_back(in_v);
+        a->bottoms.push_back(in_t);
+        a->bottoms.push_back(shape);
+        a->bottoms.push_back(length);
+        consumer_count_[in_v]++;
+        consumer_count_[in_t]++;
+        blobs_[in_v].consumer = blobs_[in_t].consumer = (int)ai;
+        ++fused;
+    }
+    if (fused) prune_splits();
+    return fused;
+}
+
+int Net::fuse_swiglu() {
+    int fused = 0;
+    const size_t count = layers_.size();
+    for (size_t gi = 0; gi < count; gi++) {
+        seedvr2::SharedLinear* gate = dynamic_cast<seedvr2::SharedLinear*>(layers_[gi]);
+        if (removed_[gi] || !gate || layers_[gi]->tops.size() != 2 || layers_[gi]->bottoms.size() != 2) continue;
+        // per stream: y = mul(swish(g), u) with g this projection's top and
+        // u the matching top of one other projection of the same inputs
+        std::vector<int> remove(1, (int)gi);
+        std::vector<int> outs;
+        int ui = -1;
+        bool ok = true;
+        for (int t = 0; ok && t < 2; t++) {
+            const int g = layers_[gi]->tops[t];
+            ok = consumer_count_[g] == 1;
+            int si = -1, mi = -1;
+            for (size_t li = 0; ok && li < count && si < 0; li++)
+                if (!removed_[li] && layers_[li]->type == "Swish" && layers_[li]->bottoms.size() == 1 &&
+                    layers_[li]->bottoms[0] == g)
+                    si = (int)li;
+            ok = ok && si >= 0 && consumer_count_[layers_[si]->tops[0]] == 1;
+            const int act = ok ? layers_[si]->tops[0] : -1;
+            int with_scalar = 0;
+            float bs = 0.f;
+            for (size_t li = 0; ok && li < count && mi < 0; li++)
+                if (!removed_[li] && binary_op_of(layers_[li], &with_scalar, &bs) == 2 && !with_scalar &&
+                    layers_[li]->bottoms.size() == 2 &&
+                    (layers_[li]->bottoms[0] == act || layers_[li]->bottoms[1] == act))
+                    mi = (int)li;
+            ok = ok && mi >= 0;
+            if (!ok) break;
+            const int u = layers_[mi]->bottoms[0] == act ? layers_[mi]->bottoms[1] : layers_[mi]->bottoms[0];
+            const int up = blobs_[u].producer;
+            ok = up >= 0 && up != (int)gi && (ui < 0 || ui == up) && consumer_count_[u] == 1 &&
+                 layers_[up]->tops.size() == 2 && layers_[up]->tops[t] == u &&
+                 dynamic_cast<seedvr2::SharedLinear*>(layers_[up]) != 0;
+            ui = up;
+            remove.push_back(si);
+            remove.push_back(mi);
+            outs.push_back(layers_[mi]->tops[0]);
+        }
+        if (!ok || layers_[ui]->bottoms.size() != 2 ||
+            split_source(layers_[ui]->bottoms[0]) != split_source(layers_[gi]->bottoms[0]) ||
+            split_source(layers_[ui]->bottoms[1]) != split_source(layers_[gi]->bottoms[1]))
+            continue;
+        std::vector<const seedvr2::SharedLinear*> parts;
+        parts.push_back(gate);
+        parts.push_back(dynamic_cast<seedvr2::SharedLinear*>(layers_[ui]));
+        seedvr2::SharedLinear* sw = seedvr2::SharedLinear::stack(parts, S2_ACT_SWIGLU);
+        if (!sw) continue;
+        sw->name = layers_[gi]->name + "_swiglu";
+        if (sw->create_pipeline(opt) != 0) {
+            sw->destroy_pipeline(opt);
+            delete sw;
+            continue;
+        }
+        const std::vector<int> bottoms = layers_[gi]->bottoms;
+        remove.push_back(ui);
+        replace_layers(remove, sw, bottoms, outs);
+        ++fused;
+    }
+    if (fused) prune_splits();
+    return fused;
+}
+
 Extractor Net::create_extractor() const { return Extractor(this, blobs_.size()); }
 
 // Runs layer `li` after every producer of its bottoms (depth-first with an

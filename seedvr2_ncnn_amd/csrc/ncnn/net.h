@@ -98,6 +98,20 @@ public:
     // Call after load_model; returns the number of pairs fused.
     int fuse_qkv_attention();
 
+    // This build: the split q / k / v form.  Three SharedLinear layers of
+    // the same two token streams whose tops are exactly the video and text
+    // q, k and v bottoms of an 8-input AdaptiveWindowAttention (and read by
+    // nothing else) become one stacked projection that the attention layer
+    // runs itself (s2_awa_qkv_forward, as fuse_qkv_attention).  Returns the
+    // number of attention layers so fused.
+    int fuse_split_qkv_attention();
+
+    // This build: SwiGLU.  A gate and an up SharedLinear of the same two
+    // token streams, whose tops feed, per stream, mul(Swish(gate), up) and
+    // nothing else, become one SharedLinear with the fused SwiGLU epilogue
+    // (param 3 = 2).  Returns the number of pairs fused.
+    int fuse_swiglu();
+
     // This build: graph rewriting for fusion passes.  The layers `remove`
     // stop running (their objects live until clear()); `fused`, owned by the
     // net from now on, reads `bottoms` and produces `tops`, each a top of a
@@ -110,6 +124,8 @@ public:
     // left without a top; returns the number of tops dropped.
     int prune_splits();
     int consumer_count(int blob) const { return consumer_count_[blob]; }
+    // The blob a Split top aliases, through any number of Splits.
+    int split_source(int blob) const;
     bool removed(int layer) const { return removed_[layer] != 0; }
 
 protected:

@@ -14,8 +14,8 @@ with Split layers wherever a blob has more than one consumer, as ncnn graphs
 have.  Even blocks use regular windows, odd blocks shifted ones; block 1
 carries the block's own per-stream modulation vectors (param 2 = 1).
 
-Usage: python tests/golden/dit_graph.py  rewrites dit_blocks_2.param and
-dit_blocks_2_builtin.param here.
+Usage: python tests/golden/dit_graph.py  rewrites dit_blocks_2.param,
+dit_blocks_2_builtin.param and dit_blocks_2_v3.param here.
 """
 from __future__ import annotations
 
@@ -263,6 +263,106 @@ def builtin_model_bytes(weights, blocks=BLOCKS):
     return b"".join(np.ascontiguousarray(p, dtype="<f4").tobytes() for p in parts)
 
 
+V3_PARAM_PATH = os.path.join(HERE, "dit_blocks_2_v3.param")
+V3_MLP = 384   # SwiGLU width: whole 128-column blocks, not a multiple of 256
+
+
+def v3_block_weights(blocks=BLOCKS, seed=SEED + 3):
+    """Weights of the v3-shaped blocks (seedvr2_pipeline.cpp:434-438): q, k
+    and v projections of their own and a SwiGLU MLP (gate, up, down)."""
+    g = np.random.default_rng(seed)
+    out = []
+    for b in range(blocks):
+        w = {}
+        for name, n, k in (("q", HIDDEN, HIDDEN), ("k", HIDDEN, HIDDEN), ("v", HIDDEN, HIDDEN),
+                           ("o", HIDDEN, HIDDEN), ("gate", V3_MLP, HIDDEN), ("up", V3_MLP, HIDDEN),
+                           ("dn", HIDDEN, V3_MLP)):
+            w[name] = _bf16(0.02 * g.standard_normal((n, k)))
+            w["b_" + name] = (0.02 * g.standard_normal(n)).astype(np.float32)
+        w["norms"] = (1.0 + 0.02 * g.standard_normal((4, HEAD_DIM))).astype(np.float32)
+        w["freqs"] = (10000.0 ** (-np.arange(PAIRS, dtype=np.float64) / PAIRS)).astype(np.float32)
+        w["stream"] = None
+        if b % 2 == 1:
+            w["stream"] = {k: (0.05 * g.standard_normal(HIDDEN)).astype(np.float32)
+                           for k in ("vshift", "vscale", "tshift", "tscale", "vgate", "tgate",
+                                     "m_vshift", "m_vscale", "m_tshift", "m_tscale",
+                                     "m_vgate", "m_tgate")}
+        out.append(w)
+    return out
+
+
+def v3_layers(blocks=BLOCKS):
+    """The v3 graph form: split q / k / v SharedLinear layers feeding the
+    attention's 8-input form (adaptive_window_attention.cpp:783-797), and a
+    SwiGLU MLP written as gate and up SharedLinear layers, Swish on the gate
+    and a BinaryOp mul per stream; the norm / modulation layers as in
+    param_text."""
+    L = []
+
+    def add(type_, name, bottoms, tops, params=""):
+        L.append((type_, name, list(bottoms), list(tops), params))
+
+    for i in range(10):
+        add("Input", f"in{i}", [], [f"in{i}"])
+    rv, rt = "in0", "in1"
+    for b in range(blocks):
+        p = f"b{b}_"
+        sv = 1 if b % 2 == 1 else 0
+        add("DiTAdaIn", p + "ada_in", [rv, rt, "in4", "in5"], [p + "h_v", p + "h_t"],
+            f"0={HIDDEN} 1=1.000000e-05 2={sv}")
+        for part in ("q", "k", "v"):
+            add("SharedLinear", p + part, [p + "h_v", p + "h_t"], [p + part + "_v", p + part + "_t"],
+                f"0={HIDDEN} 1={HIDDEN} 2=1")
+        add("AdaptiveWindowAttention", p + "attn",
+            [p + "q_v", p + "k_v", p + "v_v", p + "q_t", p + "k_t", p + "v_t", "in2", "in3"],
+            [p + "a_v", p + "a_t"],
+            f"0={HEADS} 1={HEAD_DIM} 2={TARGET[0]} 3={TARGET[1]} 4={TARGET[2]} 5={b % 2} "
+            f"6=1.000000e-05 7={PAIRS} 8=0 9=0 10=0")
+        add("SharedLinear", p + "out", [p + "a_v", p + "a_t"], [p + "o_v", p + "o_t"], f"0={HIDDEN} 1={HIDDEN} 2=1")
+        add("DiTAdaOutIn", p + "ada_out_in", [rv, rt, p + "o_v", p + "o_t", "in6", "in7", "in8"],
+            [p + "r_v", p + "r_t", p + "m_v", p + "m_t"], f"0={HIDDEN} 1=1.000000e-05 2={sv}")
+        add("SharedLinear", p + "gate", [p + "m_v", p + "m_t"], [p + "gt_v", p + "gt_t"], f"0={V3_MLP} 1={HIDDEN} 2=1")
+        add("SharedLinear", p + "up", [p + "m_v", p + "m_t"], [p + "u_v", p + "u_t"], f"0={V3_MLP} 1={HIDDEN} 2=1")
+        for s_ in ("v", "t"):
+            add("Swish", p + "silu_" + s_, [p + "gt_" + s_], [p + "sg_" + s_])
+            add("BinaryOp", p + "glu_" + s_, [p + "sg_" + s_, p + "u_" + s_], [p + "gu_" + s_], "0=2")
+        add("SharedLinear", p + "down", [p + "gu_v", p + "gu_t"], [p + "y_v", p + "y_t"], f"0={HIDDEN} 1={V3_MLP} 2=1")
+        last = b + 1 == blocks
+        ov, ot = ("out0", "out1") if last else (p + "out_v", p + "out_t")
+        add("DiTAdaOut", p + "ada_out", [p + "r_v", p + "r_t", p + "y_v", p + "y_t", "in9"], [ov, ot],
+            f"0={HIDDEN} 2={sv}")
+        rv, rt = ov, ot
+    return _with_splits(L, 0)
+
+
+def v3_param_text(blocks=BLOCKS):
+    lines = []
+    blobs = set()
+    for type_, name, bottoms, tops, params in v3_layers(blocks):
+        line = f"{type_:<24} {name:<16} {len(bottoms)} {len(tops)} " + " ".join(bottoms + tops)
+        lines.append(line + (" " + params if params else ""))
+        blobs.update(tops)
+    return "7767517\n" + f"{len(lines)} {len(blobs)}\n" + "\n".join(lines) + "\n"
+
+
+def v3_model_bytes(weights):
+    parts = []
+    for w in weights:
+        s = w["stream"]
+        if s is not None:
+            parts += [s["vshift"], s["vscale"], s["tshift"], s["tscale"]]
+        for k in ("q", "k", "v"):
+            parts += [w[k], w["b_" + k]]
+        parts += [w["norms"][0], w["norms"][1], w["norms"][2], w["norms"][3], w["freqs"]]
+        parts += [w["o"], w["b_o"]]
+        if s is not None:
+            parts += [s["vgate"], s["tgate"], s["m_vshift"], s["m_vscale"], s["m_tshift"], s["m_tscale"]]
+        parts += [w["gate"], w["b_gate"], w["up"], w["b_up"], w["dn"], w["b_dn"]]
+        if s is not None:
+            parts += [s["m_vgate"], s["m_tgate"]]
+    return b"".join(np.ascontiguousarray(p, dtype="<f4").tobytes() for p in parts)
+
+
 def model_bytes(weights):
     """The .bin: each layer's load_model data in layer order, raw fp32 (the
     type-1 loads of SharedLinear, AdaptiveWindowAttention and the block ops)."""
@@ -287,4 +387,6 @@ if __name__ == "__main__":
         f.write(param_text())
     with open(BUILTIN_PARAM_PATH, "w") as f:
         f.write(builtin_param_text())
-    print("wrote", PARAM_PATH, BUILTIN_PARAM_PATH)
+    with open(V3_PARAM_PATH, "w") as f:
+        f.write(v3_param_text())
+    print("wrote", PARAM_PATH, BUILTIN_PARAM_PATH, V3_PARAM_PATH)

@@ -312,6 +312,10 @@ int h_graph_folded_modulation(void* graph) {
     return static_cast<seedvr2::DiTBlockGraph*>(graph)->folded_modulation_count();
 }
 
+int h_graph_fused_swiglu(void* graph) {
+    return static_cast<seedvr2::DiTBlockGraph*>(graph)->fused_swiglu_count();
+}
+
 int h_graph_fused_qkv(void* graph) {
     return static_cast<seedvr2::DiTBlockGraph*>(graph)->fused_qkv_count();
 }

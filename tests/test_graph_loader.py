@@ -198,3 +198,25 @@ def test_chain_with_an_extra_consumer_is_not_folded(builtin_graph):
     edited = "7767517\n" + f"{nl + 1} {nb + 1}\n" + "\n".join(body) + "\n"
     ret, counts = _create_counts(edited, model, 5)
     assert ret == 0 and counts[1] == 9
+
+
+# ---- the v3 graph form: split q / k / v and the SwiGLU MLP --------------------------
+
+
+def test_committed_v3_param_is_the_generators():
+    with open(dit_graph.V3_PARAM_PATH) as f:
+        assert f.read() == dit_graph.v3_param_text()
+
+
+def test_v3_graph_folds_split_qkv_and_swiglu():
+    text = dit_graph.v3_param_text()
+    model = dit_graph.v3_model_bytes(dit_graph.v3_block_weights())
+    L = _lib()
+    L.h_graph_fused_swiglu.argtypes = [ctypes.c_void_p]
+    for fuse, fp32, want in ((3, 0, (2, 2)), (2, 0, (0, 2)), (1, 0, (2, 0)), (0, 0, (0, 0)), (3, 1, (0, 0))):
+        g = ctypes.c_void_p()
+        buf = ctypes.create_string_buffer(model, len(model))
+        assert L.h_graph_create(text.encode(), buf, len(model), fp32, fuse, ctypes.byref(g)) == 0
+        got = (L.h_graph_fused_swiglu(g), L.h_graph_fused_qkv(g))
+        L.h_graph_destroy(g)
+        assert got == want, (fuse, fp32, got)
