@@ -628,6 +628,28 @@ def stack_7b(steps, warmup):
             else:
                 capi.ada_out(res_v, res_t, o_v, o_t, vr, tr, md["m_gate"])
 
+    # The same with the gated residual sums in the epilogues of the out and
+    # MLP-down projections (s2_shared_linear_residual, in place) and the two
+    # norms per block as s2_dit_ada_in passes: bit for bit the stack above.
+    def forward_fused():
+        res_v.copy_(x_v0)
+        capi.shared_linear(text_in, None, w_text, b_text, capi.ACT_NONE, y_video=x_t)
+        res_t.copy_(x_t)
+        for i, blk in enumerate(blocks):
+            md = mods[i]
+            capi.ada_in(res_v, res_t, vr, tr, md["a_shift"], md["a_scale"], out_video=hin_v,
+                        out_text=hin_t)
+            capi.awa_qkv_forward(plans[i % 2], hin_v, hin_t, blk["qkv"], blk["bqkv"],
+                                 blk["norms"], freqs, workspace=ws, out_video=a_v, out_text=a_t)
+            capi.shared_linear_residual(a_v, a_t, blk["o"], blk["bo"], vr, tr, res_v, res_t,
+                                        md["a_gate"])
+            capi.ada_in(res_v, res_t, vr, tr, md["m_shift"], md["m_scale"], out_video=hin_v,
+                        out_text=hin_t)
+            capi.shared_linear(hin_v, hin_t, blk["up"], blk["bup"], capi.ACT_GELU, y_video=h_v,
+                               y_text=h_t)
+            capi.shared_linear_residual(h_v, h_t, blk["dn"], blk["bdn"], vr, tr, res_v, res_t,
+                                        md["m_gate"])
+
     def timed(fn):
         for _ in range(warmup):
             fn()
@@ -643,7 +665,11 @@ def stack_7b(steps, warmup):
     ms = timed(forward)
     finite = bool(torch.isfinite(x_v.float()).all().item())
     ms_full = timed(forward_full)
+    full_out = res_v.clone()
+    ms_fused = timed(forward_fused)
     finite = finite and bool(torch.isfinite(res_v).all().item())
+    same = bool(torch.equal(full_out, res_v))
+    del full_out
 
     m = lv + lt
     gemm = 2 * m * D * (3 * D + D + 2 * F)
@@ -662,10 +688,15 @@ def stack_7b(steps, warmup):
             "steps": steps, "warmup": warmup, "ms_per_stack": round(ms, 3),
             "ms_per_block": round(ms / STACK_BLOCKS, 4), "stack_tflop": round(flops / 1e12, 3),
             "tflops": round(tf, 1), "pct_bf16_peak": round(100 * tf / PEAK_BF16_TFLOPS, 2),
-            "ms_per_stack_with_modulation": round(ms_full, 3),
+            "ms_per_stack_with_modulation": round(min(ms_fused, ms_full), 3),
+            "ms_per_stack_with_modulation_residual_in_gemm_epilogue": round(ms_fused, 3),
+            "ms_per_stack_with_modulation_separate_residual": round(ms_full, 3),
+            "fused_equals_separate_bit_for_bit": same,
             "modulation_note": "fp32 residual stream; each block's norm + AdaSingle modulation "
-                               "and gated residual sums (s2_dit_ada_in once, s2_dit_ada_out_in "
-                               "twice per block, s2_dit_ada_out after the last)",
+                               "and gated residual sums: the residual sums in the out and "
+                               "MLP-down GEMM epilogues (s2_shared_linear_residual) and two "
+                               "s2_dit_ada_in passes per block; separately: s2_dit_ada_in once, "
+                               "s2_dit_ada_out_in twice per block, s2_dit_ada_out after the last",
             "output_finite": finite}
 
 
@@ -905,24 +936,32 @@ def main():
         return total_ms / steps, per_op, wall
 
     def full_block(steps, warmup):
-        """The whole block around the hot path (regular windows): an fp32
-        residual stream, the norm and AdaSingle modulation before the
-        attention (s2_dit_ada_in, bf16 out), the attention's gate and
-        residual sum fused with the MLP's norm and modulation
-        (s2_dit_ada_out_in) and the MLP's gate and residual sum
-        (s2_dit_ada_out, in place).  Algorithmic bytes per value: 6 (fp32
-        in, bf16 out), 12 (fp32 residual and bf16 branch in, fp32 residual
-        and bf16 out) and 10 (fp32 residual and bf16 branch in, fp32 out)."""
-        res_v = torch.randn(lv, HIDDEN, generator=gen, device=dev)
-        res_t = torch.randn(lt, HIDDEN, generator=gen, device=dev)
+        """The whole block around the hot path (regular windows) on an fp32
+        residual stream: the norm and AdaSingle modulation before the
+        attention (s2_dit_ada_in, bf16 out), the fused QKV + attention, the
+        out projection with the attention's gate and residual sum in its
+        epilogue (s2_shared_linear_residual, in place), the MLP's norm and
+        modulation (s2_dit_ada_in), the MLP up projection with GELU and the
+        down projection with the MLP's gate and residual sum in its epilogue.
+        The same block with the projections writing bf16 blobs and separate
+        gate / residual passes (s2_dit_ada_out_in, s2_dit_ada_out), the chain
+        the fused form replaces bit for bit, is timed beside it.  Algorithmic
+        bytes per value of the modulation passes: 6 (fp32 in, bf16 out), 12
+        (fp32 residual and bf16 branch in, fp32 residual and bf16 out) and 10
+        (fp32 residual and bf16 branch in, fp32 out)."""
+        res0_v = torch.randn(lv, HIDDEN, generator=gen, device=dev)
+        res0_t = torch.randn(lt, HIDDEN, generator=gen, device=dev)
+        res_v, res_t = res0_v.clone(), res0_t.clone()
         mods = {k: torch.randn(1, HIDDEN, generator=gen, device=dev) * 0.1 + (1.0 if k.endswith("scale") else 0.0)
                 for k in ("attn_shift", "attn_scale", "attn_gate", "mlp_shift", "mlp_scale", "mlp_gate")}
         hin_v = torch.empty(lv, HIDDEN, dtype=bf, device=dev)
         hin_t = torch.empty(lt, HIDDEN, dtype=bf, device=dev)
         vr, tr = [lv], [lt]
-        fops = ["attn_norm_modulate", "qkv_attention", "out",
-                "attn_gate_residual_mlp_norm_modulate", "mlp_up", "mlp_down",
-                "mlp_gate_residual"]
+        fused_names = ["attn_norm_modulate", "qkv_attention", "out_gate_residual",
+                       "mlp_norm_modulate", "mlp_up", "mlp_down_gate_residual"]
+        split_names = ["attn_norm_modulate", "qkv_attention", "out",
+                       "attn_gate_residual_mlp_norm_modulate", "mlp_up", "mlp_down",
+                       "mlp_gate_residual"]
 
         def fstep(ev=None):
             def mark(i):
@@ -935,10 +974,31 @@ def main():
             capi.awa_qkv_forward(plans[0], hin_v, hin_t, w_qkv, b[3 * HIDDEN], norms, freqs,
                                  workspace=ws, out_video=a_v, out_text=a_t)
             mark(2)
+            capi.shared_linear_residual(a_v, a_t, w_o, b[HIDDEN], vr, tr, res_v, res_t,
+                                        mods["attn_gate"])
+            mark(3)
+            capi.ada_in(res_v, res_t, vr, tr, mods["mlp_shift"], mods["mlp_scale"],
+                        out_video=hin_v, out_text=hin_t)
+            mark(4)
+            capi.shared_linear(hin_v, hin_t, w_up, b[MLP], capi.ACT_GELU, y_video=h_v, y_text=h_t)
+            mark(5)
+            capi.shared_linear_residual(h_v, h_t, w_dn, b[HIDDEN], vr, tr, res_v, res_t,
+                                        mods["mlp_gate"])
+            mark(6)
+
+        def sstep(ev=None):
+            def mark(i):
+                if ev is not None:
+                    ev[i].record()
+            mark(0)
+            capi.ada_in(res_v, res_t, vr, tr, mods["attn_shift"], mods["attn_scale"],
+                        out_video=hin_v, out_text=hin_t)
+            mark(1)
+            capi.awa_qkv_forward(plans[0], hin_v, hin_t, w_qkv, b[3 * HIDDEN], norms, freqs,
+                                 workspace=ws, out_video=a_v, out_text=a_t)
+            mark(2)
             capi.shared_linear(a_v, a_t, w_o, b[HIDDEN], capi.ACT_NONE, y_video=o_v, y_text=o_t)
             mark(3)
-            # the attention's gate and residual sum with the MLP's norm and
-            # modulation, one pass over the residual stream
             capi.ada_out_in(res_v, res_t, o_v, o_t, vr, tr, mods["attn_gate"], mods["mlp_shift"],
                             mods["mlp_scale"], h_video=hin_v, h_text=hin_t)
             mark(4)
@@ -949,31 +1009,62 @@ def main():
             capi.ada_out(res_v, res_t, y_v, y_t, vr, tr, mods["mlp_gate"])
             mark(7)
 
-        for _ in range(warmup):
-            fstep()
+        def timed(fn, names):
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+                   for _ in range(steps)]
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            start.record()
+            for i in range(steps):
+                fn(evs[i])
+            end.record()
+            torch.cuda.synchronize()
+            assert bool(torch.isfinite(res_v).all())
+            per = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps
+                   for j, op in enumerate(names)}
+            return start.elapsed_time(end) / steps, per
+
+        # one block from the same residual both ways: bit for bit
+        fstep()
+        fused_out = res_v.clone()
+        res_v.copy_(res0_v)
+        res_t.copy_(res0_t)
+        sstep()
         torch.cuda.synchronize()
-        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(fops) + 1)] for _ in range(steps)]
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record()
-        for i in range(steps):
-            fstep(evs[i])
-        end.record()
-        torch.cuda.synchronize()
-        assert bool(torch.isfinite(res_v).all())
-        per = {op: sum(e[j].elapsed_time(e[j + 1]) for e in evs) / steps for j, op in enumerate(fops)}
+        same = bool(torch.equal(fused_out, res_v))
+        ms_f, per_f = timed(fstep, fused_names)
+        ms_s, per_s = timed(sstep, split_names)
         m_rows = lv + lt
 
-        def hbm(op, bytes_per_value):
+        def hbm(per, op, bytes_per_value):
             nbytes = bytes_per_value * m_rows * HIDDEN
             return {"ms": round(per[op], 4), "algorithmic_bytes": int(nbytes),
                     "gbs": round(nbytes / (per[op] * 1e-3) / 1e9, 1),
                     "frac_hbm_peak": round(nbytes / (per[op] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+        m = lv + lt
+        fused = {
+            "ms": round(ms_f, 4),
+            "ops_ms": {op: round(v, 4) for op, v in per_f.items()},
+            "out_gate_residual": op_record(per_f["out_gate_residual"], 2 * m * HIDDEN * HIDDEN),
+            "mlp_down_gate_residual": op_record(per_f["mlp_down_gate_residual"], 2 * m * MLP * HIDDEN),
+            "norm_modulate": hbm(per_f, "attn_norm_modulate", 6.0),
+        }
+        separate = {
+            "ms": round(ms_s, 4),
+            "ops_ms": {op: round(v, 4) for op, v in per_s.items()},
+            "norm_modulate": hbm(per_s, "attn_norm_modulate", 6.0),
+            "gate_residual_norm_modulate": hbm(per_s, "attn_gate_residual_mlp_norm_modulate", 12.0),
+            "gate_residual": hbm(per_s, "mlp_gate_residual", 10.0),
+        }
+        best = "residual_in_gemm_epilogue" if ms_f <= ms_s else "separate_residual_passes"
         return {
-            "ms": round(start.elapsed_time(end) / steps, 4),
-            "ops_ms": {op: round(v, 4) for op, v in per.items()},
-            "norm_modulate": hbm("attn_norm_modulate", 6.0),
-            "gate_residual_norm_modulate": hbm("attn_gate_residual_mlp_norm_modulate", 12.0),
-            "gate_residual": hbm("mlp_gate_residual", 10.0),
+            "ms": round(min(ms_f, ms_s), 4),
+            "chain": best,
+            "residual_in_gemm_epilogue": fused,
+            "separate_residual_passes": separate,
+            "fused_equals_separate_bit_for_bit": same,
             "note": "fp32 residual stream; per-sample modulation vectors; regular windows",
         }
 

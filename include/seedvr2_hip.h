@@ -461,6 +461,27 @@ S2_API int s2_dit_ada_out_in(int hidden, int batch, const int* video_rows, const
                              const float* text_scale, void* h_video, void* h_text,
                              s2_dtype h_dtype, long h_stride, s2_stream_t stream);
 
+/* The attention's out projection or the MLP's down projection with the gated
+ * residual sum in its epilogue: y = x W^T + bias over the video and text
+ * streams as s2_shared_linear_forward computes it with bf16 y (no
+ * activation), then out = res + y * (gate[b] + *_gate) as s2_dit_ada_out
+ * computes it from that y, bit for bit, without writing y to memory.  x is
+ * bf16 [m][k] per stream, k % 64 == 0; n (the hidden size) % 8 == 0, at most
+ * 4096; video_rows / text_rows as above, summing to m_video / m_text.  res
+ * and out rows have pitch n and res_dtype, 16-byte aligned; out is either
+ * res (in place) or does not overlap it.  No counterpart in the reference
+ * (there the branch output is a blob the next layers read,
+ * seedvr2_dit.cpp:722-833); it is the block's two GEMM + residual pairs in
+ * one pass over the residual rows. */
+S2_API int s2_shared_linear_residual(const void* x_video, int m_video, const void* x_text,
+                                     int m_text, const uint16_t* weight, const float* bias,
+                                     int n, int k, int batch, const int* video_rows,
+                                     const int* text_rows, const void* res_video,
+                                     const void* res_text, s2_dtype res_dtype,
+                                     const float* gate, const float* video_gate,
+                                     const float* text_gate, void* out_video, void* out_text,
+                                     s2_stream_t stream);
+
 /* ---- DecomposedConv3D (VAE) ---------------------------------------------- */
 /* The causal 3-D convolution of the VAE (src/seedvr2/decomposed_conv3d.h:33-88,
  * decomposed_conv3d.cpp:605-755) as one implicit GEMM on the matrix cores:

@@ -43,6 +43,7 @@ EXPORTS = (
     "s2_awa_qkv_forward", "s2_gelu", "s2_swiglu_pack_weight", "s2_awa_plan_cache_rope",
     "s2_stream_wait", "s2_stream_scratch_acquire", "s2_stream_scratch_release",
     "s2_binary_op", "s2_unary_op", "s2_reduce", "s2_rms_norm", "s2_copy_2d",
+    "s2_shared_linear_residual",
 )
 
 
@@ -172,6 +173,8 @@ def lib() -> ctypes.CDLL:
         L.s2_dit_ada_out_in.argtypes = [ci, ci, P(ci), P(ci), vp, vp, ci, cl, vp, vp, ci, cl, vp,
                                         vp, vp, vp, vp, cl, cf, vp, vp, vp, vp, vp, vp, vp, vp,
                                         ci, cl, vp]
+        L.s2_shared_linear_residual.argtypes = [vp, ci, vp, ci, vp, vp, ci, ci, ci, P(ci), P(ci),
+                                                vp, vp, ci, vp, vp, vp, vp, vp, vp]
         _LIB = L
     return _LIB
 
@@ -550,6 +553,32 @@ def ada_out_in(x_video, x_text, y_video, y_text, video_rows, text_rows, gate, sh
                                   _dtype_code(h_video), hs or hidden, _stream(stream)),
           "s2_dit_ada_out_in")
     return out_video, out_text, h_video, h_text
+
+
+def shared_linear_residual(x_video, x_text, weight_bf16, bias, video_rows, text_rows, res_video,
+                           res_text, gate, video_gate=None, text_gate=None, out_video=None,
+                           out_text=None, stream=None):
+    """s2_shared_linear_residual: out = res + (x W^T + b, rounded to bf16) *
+    (gate[b] + *_gate); in place (out = res) by default.  Returns
+    (out_video, out_text)."""
+    import torch
+    n, k = weight_bf16.shape
+    assert weight_bf16.dtype == torch.bfloat16 and weight_bf16.is_contiguous()
+    m0 = x_video.shape[0]
+    m1 = 0 if x_text is None else x_text.shape[0]
+    if out_video is None:
+        out_video = res_video
+    if out_text is None and m1:
+        out_text = res_text
+    for t in (x_video, x_text, res_video, res_text, out_video, out_text):
+        assert t is None or t.shape[0] == 0 or t.is_contiguous()
+    check(lib().s2_shared_linear_residual(
+        _ptr(x_video), m0, _ptr(x_text) if m1 else None, m1, _ptr(weight_bf16), _ptr(bias), n, k,
+        len(video_rows), _ints(video_rows), _ints(text_rows) if text_rows is not None else None,
+        _ptr(res_video), _ptr(res_text) if m1 else None, _dtype_code(res_video), _ptr(gate),
+        _ptr(video_gate), _ptr(text_gate), _ptr(out_video), _ptr(out_text) if m1 else None,
+        _stream(stream)), "s2_shared_linear_residual")
+    return out_video, out_text
 
 
 # ---- DiT frontend and tail, sampler step -------------------------------------

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include "awa_plan.h"
+#include "block_kernels.h"
 
 // Activation element types (in_kind, out_kind, x_kind, y_kind) are the
 // s2_dtype values: 0 fp32, 1 bf16, 2 fp16.
@@ -47,5 +48,25 @@ hipError_t launch_shared_linear_noalloc(const void* x0, int m0, const void* x1, 
                                         int x_kind, const uint16_t* w, const float* bias, int n,
                                         int k, int act, void* y0, void* y1, int y_kind,
                                         hipStream_t stream);
+
+// The DiT block's gated residual sum in the epilogue of the projection that
+// feeds it (the attention's out projection, the MLP's down projection):
+// out = x + y * (gate[sample] + gate_s), y the projection rounded to bf16 (the
+// value a bf16 output blob holds), out in the element type of x, as
+// launch_ada_out computes it from that blob.  Rows have pitch n; a row's
+// sample comes from the cumulative row ends of its stream.
+struct LinearResidual {
+    const void* x[2];          // residual rows of the video / text stream
+    void* out[2];              // output rows (may be x)
+    int x_kind;                // residual and out element type
+    const float* gate;         // [batch][n]
+    const float* gate_s[2];    // the stream's own [n] vector, or null
+    AdaRows rows;
+};
+// y = x W^T + b over the two streams (bf16 activations, k % 64 == 0,
+// n % 8 == 0) with the residual epilogue in place of the y stores.
+hipError_t launch_shared_linear_residual(const uint16_t* x0, int m0, const uint16_t* x1, int m1,
+                                         const uint16_t* w, const float* bias, int n, int k,
+                                         const LinearResidual& res, hipStream_t stream);
 
 }  // namespace s2

@@ -1088,6 +1088,43 @@ int s2_dit_ada_out(int hidden, int batch, const int* video_rows, const int* text
     return S2_OK;
 }
 
+int s2_shared_linear_residual(const void* x_video, int m_video, const void* x_text, int m_text,
+                              const uint16_t* weight, const float* bias, int n, int k, int batch,
+                              const int* video_rows, const int* text_rows, const void* res_video,
+                              const void* res_text, s2_dtype res_dtype, const float* gate,
+                              const float* video_gate, const float* text_gate, void* out_video,
+                              void* out_text, s2_stream_t stream) {
+    s2::LinearResidual r = {};
+    const int rc = ada_rows(n, batch, video_rows, text_rows, &r.rows);
+    if (rc != S2_OK) return rc;
+    if (r.rows.video_rows != m_video || r.rows.text_rows != m_text)
+        return fail(S2_ERR_INVALID, "row counts do not sum to m_video / m_text");
+    if (!weight || k <= 0 || k % 64 != 0 || n % 8 != 0 || (long)256 * k * 2 > 0x7fffffffL)
+        return fail(S2_ERR_INVALID, "weight, k (multiple of 64) or n (multiple of 8)");
+    if (!dtype_ok(res_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
+    const bool vid = m_video > 0, txt = m_text > 0;
+    if ((vid && (!x_video || !res_video || !out_video)) || (txt && (!x_text || !res_text || !out_text)))
+        return fail(S2_ERR_INVALID, "null stream pointer");
+    if ((vid && (!aligned(x_video, 16) || !aligned(res_video, 16) || !aligned(out_video, 16))) ||
+        (txt && (!aligned(x_text, 16) || !aligned(res_text, 16) || !aligned(out_text, 16))) ||
+        !aligned(weight, 16))
+        return fail(S2_ERR_INVALID, "operands must be 16-byte aligned");
+    if (!gate || !aligned(gate, 16) || !ada_vec_ok(video_gate) || !ada_vec_ok(text_gate))
+        return fail(S2_ERR_INVALID, "gate vectors must be non-null (gate) and 16-byte aligned");
+    r.x[0] = res_video;
+    r.x[1] = res_text;
+    r.out[0] = out_video;
+    r.out[1] = out_text;
+    r.x_kind = (int)res_dtype;
+    r.gate = gate;
+    r.gate_s[0] = video_gate;
+    r.gate_s[1] = text_gate;
+    S2_HIP(s2::launch_shared_linear_residual((const uint16_t*)x_video, m_video,
+                                             (const uint16_t*)x_text, m_text, weight, bias, n, k,
+                                             r, (hipStream_t)stream));
+    return S2_OK;
+}
+
 int s2_dit_ada_out_in(int hidden, int batch, const int* video_rows, const int* text_rows,
                       const void* x_video, const void* x_text, s2_dtype x_dtype, long x_stride,
                       const void* y_video, const void* y_text, s2_dtype y_dtype, long y_stride,

@@ -305,12 +305,12 @@ struct AwaQkvArgs {
     uint16_t* vt;
 };
 
-template <int YK, int ACT, int AWA = 0>
+template <int YK, int ACT, int AWA = 0, int RES = 0>
 __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     const uint16_t* __restrict__ x0, int m0, const uint16_t* __restrict__ x1, int m1,
     const uint16_t* __restrict__ wgt, const float* __restrict__ bias, int n, int k,
     void* __restrict__ y0, void* __restrict__ y1, int mv, int mtiles, int ntiles, SkTail sk,
-    AwaQkvArgs awa) {
+    AwaQkvArgs awa, LinearResidual res) {
     constexpr int BM = 256, BN = 256, BK = 64;
     constexpr int TB = BM * BK * 2;   // 32 KB per operand per stage
     constexpr int SB = 2 * TB;        // 64 KB per stage
@@ -794,6 +794,100 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         }
     };
 
+    // Residual epilogue: thread (sub, ch) holds the bf16 projection of
+    // columns col0 + 8 ch .. + 7 of tile rows sub + 16 c; all residual loads
+    // go out before the first store.  out may be x: each element is read and
+    // written by one thread.
+    auto residual_store = [&](const u32x4 (&sv)[16], int sub, int ch) {
+        if constexpr (RES != 0) {
+#pragma clang fp contract(off)
+            const int col = col0 + ch * 8;
+            if (col >= n) return;
+            int cur = -1;
+            float g[8];
+            // two halves of eight rows: the half's residual loads (raw, two
+            // 16-byte chunks for fp32, one for 16-bit types) go out first
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                int loc[8];   // stream << 30 | row within the stream; -1: no row
+                u32x4 raw[8][2];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const int r = row0 + 16 * (8 * h + c) + sub;
+                    const int st = r < m0 ? 0 : (r >= mv && r < mv + m1 ? 1 : -1);
+                    const int local = st == 0 ? r : r - mv;
+                    loc[c] = st < 0 ? -1 : (st << 30) | local;
+                    if (st < 0) continue;
+                    const long e = (long)local * n + col;
+                    const void* xs = st ? res.x[1] : res.x[0];
+                    if (res.x_kind == 0) {
+                        raw[c][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>((const float*)xs + e));
+                        raw[c][1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>((const float*)xs + e + 4));
+                    } else {
+                        raw[c][0] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>((const uint16_t*)xs + e));
+                    }
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    if (loc[c] < 0) continue;
+                    const int st = loc[c] >> 30;
+                    const int local = loc[c] & 0x3fffffff;
+                    // the row's sample: the number of its stream's row ends
+                    // at or below it (the ends are read with uniform indices)
+                    int b = 0;
+                    for (int j = 0; j + 1 < res.rows.batch; ++j) {
+                        const int e = st ? res.rows.end[kAdaMaxBatch + j] : res.rows.end[j];
+                        if (local >= e) b = j + 1;
+                    }
+                    const int key = st * kAdaMaxBatch + b;
+                    if (key != cur) {
+                        cur = key;
+                        const float* ga = res.gate + (long)b * n + col;
+                        const float* gs = st ? res.gate_s[1] : res.gate_s[0];
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) g[i] = gs ? ga[i] + gs[col + i] : ga[i];
+                    }
+                    float xv[8];
+                    if (res.x_kind == 0) {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) xv[i] = __uint_as_float(raw[c][i >> 2][i & 3]);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < 8; ++i) {
+                            const uint16_t hv = (uint16_t)(raw[c][0][i >> 1] >> (16 * (i & 1)));
+                            xv[i] = res.x_kind == 1 ? bf16_to_f32(hv)
+                                                    : (float)__builtin_bit_cast(_Float16, hv);
+                        }
+                    }
+                    const u32x4 yw = sv[8 * h + c];
+                    float o[8];
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const uint32_t w = yw[i >> 1];
+                        const float y = __uint_as_float(i & 1 ? (w & 0xffff0000u) : (w << 16));
+                        const float p = y * g[i];
+                        o[i] = xv[i] + p;
+                    }
+                    const long e = (long)local * n + col;
+                    void* os = st ? res.out[1] : res.out[0];
+                    if (res.x_kind == 0) {
+                        u32x4 a, b2;
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            a[i] = __float_as_uint(o[i]);
+                            b2[i] = __float_as_uint(o[4 + i]);
+                        }
+                        __builtin_nontemporal_store(a, reinterpret_cast<u32x4*>((float*)os + e));
+                        __builtin_nontemporal_store(b2, reinterpret_cast<u32x4*>((float*)os + e + 4));
+                    } else {
+                        store4(os, e, o[0], o[1], o[2], o[3], res.x_kind);
+                        store4(os, e + 4, o[4], o[5], o[6], o[7], res.x_kind);
+                    }
+                }
+            }
+        }
+    };
+
     // y tile = act(acc + bias)
     auto epilogue = [&]() {
         if constexpr (AWA != 0) {
@@ -850,6 +944,10 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             u32x4 sv[16];
 #pragma unroll
             for (int c = 0; c < 16; ++c) sv[c] = *(const u32x4*)(lds + (16 * c + sub) * EP + ch * 16);
+            if constexpr (RES != 0) {
+                residual_store(sv, sub, ch);
+                return;
+            }
 #pragma unroll
             for (int c = 0; c < 16; ++c) {
                 const uint32_t off = (uint32_t)((16 * c + sub) * pitch + col0 * 2 + ch * 16) | drop;
@@ -1246,7 +1344,7 @@ static hipError_t linear_impl(const void* x0, int m0, const void* x1, int m1, co
         const long blocks = (long)sk.dp_tiles + sk.sk_groups;
         shared_linear_256_kernel<YK, ACT><<<(unsigned)blocks, 512, 0, stream>>>(
             (const uint16_t*)x0, m0, (const uint16_t*)x1, m1, w, bias, n, k, y0, y1, mv, mtiles,
-            ntiles, sk, AwaQkvArgs{});
+            ntiles, sk, AwaQkvArgs{}, LinearResidual{});
         return hipGetLastError();
     }
     const int mt0 = (m0 + 127) / 128;
@@ -1317,6 +1415,27 @@ hipError_t launch_shared_linear_noalloc(const void* x0, int m0, const void* x1, 
                            SkSource::kStatic);
 }
 
+hipError_t launch_shared_linear_residual(const uint16_t* x0, int m0, const uint16_t* x1, int m1,
+                                         const uint16_t* w, const float* bias, int n, int k,
+                                         const LinearResidual& res, hipStream_t stream) {
+    if (k % 64 != 0 || n % 8 != 0 || (long)256 * k * 2 > 0x7fffffffL ||
+        (long)256 * n * 4 > 0x7fffffffL)
+        return hipErrorInvalidValue;
+    const int mv = (m0 + 7) / 8 * 8;
+    const int ntiles = (n + 255) / 256;
+    const int mtiles = (mv + m1 + 255) / 256;
+    const long tiles = (long)mtiles * ntiles;
+    if (tiles == 0) return hipSuccess;
+    SkTail sk;
+    hipError_t e = plan_sk_tail(tiles, k / 64, SkSource::kStream, stream, &sk);
+    if (e != hipSuccess) return e;
+    const long blocks = (long)sk.dp_tiles + sk.sk_groups;
+    shared_linear_256_kernel<1, S2_ACT_NONE, 0, 1><<<(unsigned)blocks, 512, 0, stream>>>(
+        x0, m0, x1, m1, w, bias, n, k, nullptr, nullptr, mv, mtiles, ntiles, sk, AwaQkvArgs{},
+        res);
+    return hipGetLastError();
+}
+
 hipError_t launch_awa_qkv(const s2_awa_plan& plan, const uint16_t* x_video, const uint16_t* x_text,
                           int k, const uint16_t* w, const float* bias, const float* norm,
                           const float2* rope, uint16_t* q, uint16_t* kk, uint16_t* vt,
@@ -1352,11 +1471,11 @@ hipError_t launch_awa_qkv(const s2_awa_plan& plan, const uint16_t* x_video, cons
     if (d == 128)
         shared_linear_256_kernel<1, S2_ACT_NONE, 128><<<(unsigned)blocks, 512, 0, stream>>>(
             x_video, plan.video_tokens, x_text, plan.text_tokens, w, bias, n, k, nullptr, nullptr,
-            plan.qkv_text_row, mtiles, ntiles, sk, a);
+            plan.qkv_text_row, mtiles, ntiles, sk, a, LinearResidual{});
     else
         shared_linear_256_kernel<1, S2_ACT_NONE, 64><<<(unsigned)blocks, 512, 0, stream>>>(
             x_video, plan.video_tokens, x_text, plan.text_tokens, w, bias, n, k, nullptr, nullptr,
-            plan.qkv_text_row, mtiles, ntiles, sk, a);
+            plan.qkv_text_row, mtiles, ntiles, sk, a, LinearResidual{});
     return hipGetLastError();
 }
 
