@@ -451,6 +451,22 @@ def vae_conv3d(reps=5, cpu_threads=16, cpu=True):
                         "ms": round(ms, 3), "tflop": round(flops / 1e12, 3),
                         "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
                         "frac_bf16_peak": round(flops / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+            if cout <= 3:
+                # bound by its input: the narrow kernel reads each input row
+                # once (and the rows above and below a band of rows once
+                # more), writes the output and passes two frames of partial
+                # sums from forward to forward
+                esz = 2 if dt == torch.bfloat16 else 4
+                nbytes = (cin * frames * h * w * esz + cout * frames * h * w * esz +
+                          2 * 2 * cout * h * w * 4)
+                out[key].update({
+                    "bound": "hbm", "algorithmic_bytes": int(nbytes),
+                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                    "bytes_note": "input frames once, output, memory partial sums read and "
+                                  "written; a layer that cached its last two 128-channel input "
+                                  "frames instead would also read those (1.42 GB per 4-frame "
+                                  "bf16 slice in all)"})
             del x, y
         del conv, wts
         torch.cuda.empty_cache()

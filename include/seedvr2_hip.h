@@ -518,14 +518,22 @@ S2_API int s2_conv3d_pack_weights(const s2_conv3d_config* config, const float* w
 /* The temporal memory (:727-755): the last kernel_t - stride_t frames of the
  * padded input, kept in this library's staged layout (bf16 channel-last);
  * only s2_conv3d_forward reads or writes it.  *frames = kernel_t - stride_t
- * (0: the layer keeps no memory). */
+ * (0: the layer keeps no memory).  Layers of at most 3 output channels with
+ * a 3x3x3 window, unit strides and dilations, one pixel of spatial padding
+ * and 16..128 input channels (a multiple of 16; the VAE's RGB output conv)
+ * keep instead what those two frames contribute to the next forward's first
+ * two output frames: fp32 [2][num_output][height][width]. */
 S2_API int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, int width,
                                   size_t* bytes, int* frames);
 /* Workspace of a forward: the staged input frames (and copied memory
  * frames), plus, for layers whose output tiles would leave most of the chip
  * idle, fp32 partial tiles of a k loop split over the temporal taps.  A
  * smaller workspace that still holds the staged frames is accepted; the
- * forward then runs the k loop unsplit. */
+ * forward then runs the k loop unsplit.  The layers of at most 3 output
+ * channels above read their input in place: their workspace is a copy of
+ * the memory, used only when next_memory overlaps memory and the forward
+ * has more than 4 output frames (it may be NULL otherwise), and they take no
+ * pad_right / pad_bottom. */
 S2_API int s2_conv3d_workspace_bytes(const s2_conv3d_config* config, int frames, int height,
                                      int width, int memory_frames, size_t* bytes);
 /* The workspace of s2_conv3d_forward_padded: the staged frames are those of

@@ -37,7 +37,7 @@ CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-I" + INCLUDE,
              "-I" + os.path.join(CSRC, "ncnn"), "-I" + os.path.join(CSRC, "layers")]
 
 HIP_SOURCES = ["awa_kernels.hip", "linear_kernels.hip", "pipeline_kernels.hip", "block_kernels.hip",
-               "conv3d_kernels.hip", "mha_kernels.hip", "graph_ops_kernels.hip", "capi.hip",
+               "conv3d_kernels.hip", "conv3d_narrow_kernels.hip", "mha_kernels.hip", "graph_ops_kernels.hip", "capi.hip",
                "awa_plan.cpp", "stream_scratch.cpp"]
 LAYER_SOURCES = ["ncnn/mat.cpp", "ncnn/layer.cpp", "ncnn/net.cpp", "ncnn/builtin_layers.cpp",
                  "layers/hip_allocator.cpp",

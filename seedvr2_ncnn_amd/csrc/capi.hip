@@ -1223,7 +1223,10 @@ int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, int width
         return fail(S2_ERR_INVALID, "invalid configuration");
     const int cache = std::max(config->kernel_t - config->stride_t, 0);
     *frames = cache;
-    *bytes = (size_t)cache * height * width * s2::conv3d_cpad(config->num_input) * 2;
+    if (s2::conv3d_narrow(conv3d_shape(config)))   // partial sums of two output frames
+        *bytes = (size_t)2 * config->num_output * height * width * 4;
+    else
+        *bytes = (size_t)cache * height * width * s2::conv3d_cpad(config->num_input) * 2;
     return S2_OK;
 }
 
@@ -1243,6 +1246,13 @@ int s2_conv3d_workspace_bytes_padded(const s2_conv3d_config* config, int frames,
     if (!bytes || !conv3d_out(config, frames, height + pad_bottom, width + pad_right,
                               memory_frames, &to, &ho, &wo))
         return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
+    if (s2::conv3d_narrow(conv3d_shape(config))) {
+        // a copy of the memory, for a forward that rewrites it in place
+        if (pad_right || pad_bottom)
+            return fail(S2_ERR_INVALID, "layers of at most 3 output channels take no extra padding");
+        *bytes = align256((size_t)2 * config->num_output * height * width * 4);
+        return S2_OK;
+    }
     *bytes = align256((size_t)(frames + memory_frames) * height * width *
                       s2::conv3d_cpad(config->num_input) * 2);
     // fp32 partial tiles when the k loop is split over the temporal taps
@@ -1278,14 +1288,42 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
     if (!conv3d_out(config, frames, height + pad_bottom, width + pad_right, mem, &to, &ho, &wo))
         return fail(S2_ERR_INVALID, "invalid DecomposedConv3D configuration or input shape");
     if (memory && memory_frames <= 0) return fail(S2_ERR_INVALID, "memory without frames");
-    if (!packed_weights || !input || !output || !workspace) return fail(S2_ERR_INVALID, "null pointer");
+    if (!packed_weights || !input || !output) return fail(S2_ERR_INVALID, "null pointer");
     if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return fail(S2_ERR_INVALID, "unsupported dtype");
     const long plane_in = (long)height * width;
     if (in_cstep < (long)frames * plane_in || in_cstep % 4 != 0 || !aligned(input, 16))
         return fail(S2_ERR_INVALID, "input channel stride or alignment");
     if (out_cstep < (long)to * ho * wo) return fail(S2_ERR_INVALID, "output channel stride");
-    if (!aligned(workspace, 256)) return fail(S2_ERR_INVALID, "workspace alignment");
     const s2::Conv3dShape s = conv3d_shape(config);
+    if (s2::conv3d_narrow(s)) {
+        if (pad_right || pad_bottom)
+            return fail(S2_ERR_INVALID, "layers of at most 3 output channels take no extra padding");
+        if (mem && mem != 2) return fail(S2_ERR_INVALID, "the memory holds 2 frames");
+        if ((memory && !aligned(memory, 4)) || (next_memory && !aligned(next_memory, 4)))
+            return fail(S2_ERR_INVALID, "memory alignment");
+        const int prefix = mem > 0 ? mem : config->head_frames;
+        const size_t mem_bytes = (size_t)2 * s.cout * plane_in * 4;
+        // workgroups of different output frames run at once when there are
+        // more than kNarrowSlots of them (with the memory's two): a memory
+        // rewritten in place is read from a copy then
+        const float* mem_in = (const float*)memory;
+        if (mem && next_memory && to + 2 > s2::kNarrowSlots &&
+            (const uint8_t*)next_memory < (const uint8_t*)memory + mem_bytes &&
+            (const uint8_t*)memory < (const uint8_t*)next_memory + mem_bytes) {
+            if (!workspace || !aligned(workspace, 256) || workspace_bytes < mem_bytes)
+                return fail(S2_ERR_INVALID, "workspace too small");
+            S2_HIP(hipMemcpyAsync(workspace, memory, mem_bytes, hipMemcpyDeviceToDevice,
+                                  (hipStream_t)stream));
+            mem_in = (const float*)workspace;
+        }
+        S2_HIP(s2::launch_conv3d_narrow(s, input, (int)in_dtype, in_cstep, frames, height, width,
+                                        prefix, mem, to, (const uint16_t*)packed_weights, bias,
+                                        output, (int)out_dtype, out_cstep, mem_in,
+                                        (float*)next_memory, (hipStream_t)stream));
+        return S2_OK;
+    }
+    if (!workspace) return fail(S2_ERR_INVALID, "null pointer");
+    if (!aligned(workspace, 256)) return fail(S2_ERR_INVALID, "workspace alignment");
     const size_t frame_elems = (size_t)plane_in * s.cpad;
     const size_t frame_bytes = frame_elems * 2;
     if ((size_t)(mem + frames) * frame_bytes > workspace_bytes)

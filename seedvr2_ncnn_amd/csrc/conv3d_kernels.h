@@ -84,6 +84,33 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
                          void* out, int out_kind, long out_cstep, float* part,
                          hipStream_t stream);
 
+// Layers of at most 3 output channels with a 3x3x3 window, unit strides and
+// dilations, one pixel of spatial padding and 16..128 input channels (a
+// multiple of 16) run conv3d_narrow_kernels.hip: the window positions are the
+// MFMA columns and the temporal memory holds partial sums of the next
+// forward's first two output frames, [2][cout][H][W] fp32, instead of input
+// frames.
+inline bool conv3d_narrow(const Conv3dShape& s) {
+    return s.cout <= 3 && s.cin >= 16 && s.cin <= 128 && s.cin % 16 == 0 && s.kt == 3 &&
+           s.kh == 3 && s.kw == 3 && s.st == 1 && s.sh == 1 && s.sw == 1 && s.dt == 1 &&
+           s.dh == 1 && s.dw == 1 && s.ph == 1 && s.pw == 1;
+}
+// output frames one narrow-conv workgroup accumulates (more: several groups)
+constexpr int kNarrowSlots = 6;
+// Narrow conv over `frames` planar input frames (channel stride in_cstep,
+// type in_kind) of height x width: padded frame p is input frame
+// max(p - prefix, 0); mem = 2 with mem_in the previous forward's partial sums
+// (prefix 2, the memory frames not read), mem = 0 without (prefix =
+// head_frames).  out_frames = frames + prefix - 2.  mem_out (or null)
+// receives the partial sums for the next forward; it must not be mem_in when
+// out_frames + 2 > kNarrowSlots (workgroups of different output frames read
+// and write the memory concurrently).
+hipError_t launch_conv3d_narrow(const Conv3dShape& s, const void* input, int in_kind,
+                                long in_cstep, int frames, int height, int width, int prefix,
+                                int mem, int out_frames, const uint16_t* packed, const float* bias,
+                                void* out, int out_kind, long out_cstep, const float* mem_in,
+                                float* mem_out, hipStream_t stream);
+
 // VAEUpsample3D's shuffle: packed [channels*tr*sr*sr][frames][h][w] (channel
 // stride packed_cstep) -> out [channels][frames*tr - remove_head][h*sr][w*sr]
 // (channel stride out_cstep), elements of type kind (0 fp32; 1, 2 16-bit)

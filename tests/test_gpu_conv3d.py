@@ -8,6 +8,8 @@ oracle on the unrounded fp32 operands with the path's bar (max-abs <= 2e-2,
 cosine >= 0.9999), and against the oracle on the bf16-rounded operands with
 a tight bound (1e-4 of the output scale) that isolates the kernel's own
 arithmetic (summation order only)."""
+import ctypes
+
 import numpy as np
 import pytest
 
@@ -268,3 +270,86 @@ def test_layer_rejects_mismatched_blobs():
     assert layer.conv_memory(reset=True) == 0
     assert layer.forward_planar(x[:, :, :6], (8, 6, 2, 32), (8, 6, 2, 64))[0] == 0
     set_vae_memory_state(0)
+
+
+# ---- layers of at most 3 output channels (conv3d_narrow_kernels.hip) ----------
+# The VAE's RGB output conv and its kin (3x3x3, unit strides, one pixel of
+# padding, 16..128 input channels) run the narrow kernel, whose temporal
+# memory holds partial sums of the next forward's first two output frames.
+# The chains below compare slices against the oracle run on the whole clip:
+# head frames, frames that need several workgroups per pixel (more than 6
+# output frames with the memory's two), memory buffers rewritten in place,
+# single-frame slices, ragged strips and rows read element by element.
+
+@pytest.mark.parametrize("cin,cout", [(128, 3), (64, 1), (16, 2)])
+@pytest.mark.parametrize("hw", [(6, 10), (9, 136), (5, 250)])
+@pytest.mark.parametrize("reuse", [False, True])
+def test_conv3d_narrow_memory_chains_slices(cin, cout, hw, reuse):
+    cfgs = _cfg(cin, cout)
+    x, wts, bias = _case(cin, cout, 14, hw[0], hw[1], cfgs, 5 + cin + cout)
+    conv = _device(cfgs[0], wts, bias)
+    outs = []
+    # 6 frames with head frames: 6 output frames + 2 memory frames = 2 groups;
+    # then 5 (2 groups, the in-place memory read from a copy), 1, 2
+    for i, (a, b) in enumerate([(0, 6), (6, 11), (11, 12), (12, 14)]):
+        outs.append(_run(conv, x[:, a:b], use_memory=i > 0, keep_memory=True,
+                         reuse_memory_buffer=reuse))
+    got = np.concatenate(outs, axis=1)
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)
+    assert got.shape == ref.shape
+    assert_close(got, ref)
+    _, tight, _ = oracle.decomposed_conv3d(cfgs[1], bf16_round(x), bf16_round(wts), bias)
+    assert float(np.max(np.abs(got - tight))) <= 1e-4 * max(1.0, float(np.max(np.abs(tight))))
+
+
+@pytest.mark.parametrize("head", [0, 1, 2, 4])
+def test_conv3d_narrow_head_frames(head):
+    cfgs = _cfg(32, 3, head=head)
+    x, wts, bias = _case(32, 3, 4, 7, 129, cfgs, 40 + head)
+    _check(_run(_device(cfgs[0], wts, bias), x), x, wts, bias, cfgs[1])
+
+
+@pytest.mark.parametrize("in_dtype,out_dtype", [("bf16", "bf16"), ("f16", "f32"), ("f32", "f16"),
+                                                ("f32", "f32")])
+@pytest.mark.parametrize("cstep_pad", [0, 4])
+def test_conv3d_narrow_blob_types(in_dtype, out_dtype, cstep_pad):
+    import torch
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+    cfgs = _cfg(128, 3)
+    x, wts, bias = _case(128, 3, 3, 10, 256, cfgs, 17)
+    if in_dtype != "f32":
+        x = torch.from_numpy(x).to(dt[in_dtype]).float().numpy()    # the stored values
+    conv = _device(cfgs[0], wts, bias)
+    a = _run(conv, x[:, :1], cstep_pad=cstep_pad, dtype=dt[in_dtype], out_dtype=dt[out_dtype],
+             keep_memory=True)
+    b = _run(conv, x[:, 1:], cstep_pad=cstep_pad, dtype=dt[in_dtype], out_dtype=dt[out_dtype],
+             use_memory=True, keep_memory=True)
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)
+    assert_close(np.concatenate([a, b], axis=1), ref)
+
+
+def test_conv3d_narrow_720p_rows_against_torch():
+    """The RGB output conv (128 -> 3) on 2 frames of 90 x 1280 pixels (ten
+    128-column strips, bands of rows over the CUs) continuing a memory,
+    against torch's fp32 conv3d on the CPU over the same bf16-rounded
+    operands."""
+    import torch
+    cfgs = _cfg(128, 3)
+    x, wts, bias = _case(128, 3, 4, 90, 1280, cfgs, 23)
+    conv = _device(cfgs[0], wts, bias)
+    a = _run(conv, x[:, :2], keep_memory=True)
+    b = _run(conv, x[:, 2:], use_memory=True, keep_memory=True)
+    got = np.concatenate([a, b], axis=1)
+    xp = np.concatenate([np.repeat(bf16_round(x)[:, :1], 2, axis=1), bf16_round(x)], axis=1)
+    ref = torch.nn.functional.conv3d(
+        torch.from_numpy(xp)[None], torch.from_numpy(bf16_round(wts)).permute(1, 2, 0, 3, 4),
+        torch.from_numpy(bias), padding=(0, 1, 1))[0].numpy()
+    assert got.shape == ref.shape
+    assert float(np.max(np.abs(got - ref))) <= 1e-4 * max(1.0, float(np.max(np.abs(ref))))
+
+
+def test_conv3d_narrow_rejects_extra_padding():
+    cfgs = _cfg(128, 3)
+    n = ctypes.c_size_t()
+    assert capi.lib().s2_conv3d_workspace_bytes_padded(ctypes.byref(cfgs[0]), 2, 8, 8, 1, 0, 0,
+                                                       ctypes.byref(n)) != 0
