@@ -527,7 +527,7 @@ S2_API int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, in
                                   size_t* bytes, int* frames);
 /* Workspace of a forward: the staged input frames (and copied memory
  * frames), plus, for layers whose output tiles would leave most of the chip
- * idle, fp32 partial tiles of a k loop split over the temporal taps.  A
+ * idle, fp32 partial tiles of a k loop split into ranges of k-steps.  A
  * smaller workspace that still holds the staged frames is accepted; the
  * forward then runs the k loop unsplit.  The layers of at most 3 output
  * channels above read their input in place: their workspace is a copy of

@@ -1255,10 +1255,10 @@ int s2_conv3d_workspace_bytes_padded(const s2_conv3d_config* config, int frames,
     }
     *bytes = align256((size_t)(frames + memory_frames) * height * width *
                       s2::conv3d_cpad(config->num_input) * 2);
-    // fp32 partial tiles when the k loop is split over the temporal taps
+    // fp32 partial tiles when the k loop is split into ranges
     const s2::Conv3dShape s = conv3d_shape(config);
     const long mo = (long)to * ho * wo;
-    const int splits = s2::conv3d_tap_split(s, mo, wo);
+    const int splits = s2::conv3d_k_split(s, mo, wo);
     if (splits > 1) *bytes += align256((size_t)splits * s.cout * mo * 4);
     return S2_OK;
 }
@@ -1362,14 +1362,14 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
                                    s.cpad, staged + (size_t)lead * frame_elems,
                                    tail_in_stage ? (uint16_t*)next_memory : nullptr,
                                    (long)(frames - cache) * plane_in, st));
-    // fp32 partial tiles of a k loop split over the taps, after the staged
+    // fp32 partial tiles of a k loop split into ranges, after the staged
     // frames, when the workspace holds them (s2_conv3d_workspace_bytes counts
     // them; a smaller workspace runs the whole k loop per tile instead)
     float* part = nullptr;
     {
         const size_t need = align256((size_t)(mem + frames) * frame_bytes);
         const long mo = (long)to * ho * wo;
-        const int splits = s2::conv3d_tap_split(s, mo, wo);
+        const int splits = s2::conv3d_k_split(s, mo, wo);
         if (splits > 1 && workspace_bytes >= need + (size_t)splits * s.cout * mo * 4)
             part = (float*)((uint8_t*)workspace + need);
     }

@@ -45,13 +45,28 @@ inline long conv3d_gemm_tiles(const Conv3dShape& s, long m) {
     if (s.cout <= 128) return (m + 511) / 512 * ((s.cout + 127) / 128);
     return (m + 255) / 256 * ((s.cout + 255) / 256);
 }
-// Temporal taps the implicit-GEMM kernel splits its k loop over (one
-// workgroup per tap and tile, partial tiles summed by a second pass) when its
-// tiles would leave most of the chip idle: layers of at least 64 input
-// channels with fewer tiles than 256 (the CU count).  1: no split.
-inline int conv3d_tap_split(const Conv3dShape& s, long m, int wo) {
-    if (s.cpad < 64 || s.kt < 2 || conv3d_halo_width(s, wo) > 0) return 1;
-    return conv3d_gemm_tiles(s, m) < 256 ? s.kt : 1;
+// Ranges the implicit-GEMM kernel splits its k loop into (one workgroup per
+// range and tile, partial tiles summed by a second pass) when its tiles
+// would leave most of the chip idle: layers of at least 64 input channels
+// with fewer tiles than the CUs (256 on MI355X).  The count of the fewest
+// rounds of workgroups per k-step: s ranges of a tiles-tile layer take
+// ceil(tiles * s / 256) rounds of 1/s of the loop; the smallest such s up to
+// 8 (more partial tiles cost more than they fill).  1: no split.
+inline int conv3d_k_split(const Conv3dShape& s, long m, int wo) {
+    if (s.cpad < 64 || conv3d_halo_width(s, wo) > 0) return 1;
+    const long tiles = conv3d_gemm_tiles(s, m);
+    if (tiles >= 256) return 1;
+    const long steps = (long)s.kt * s.kh * s.kw * (s.cpad / 64);
+    int best = 1;
+    double best_t = 1.0;
+    for (int sp = 2; sp <= 8 && sp <= steps; ++sp) {
+        const double t = (double)((tiles * sp + 255) / 256) / sp;
+        if (t < best_t - 1e-9) {
+            best = sp;
+            best_t = t;
+        }
+    }
+    return best;
 }
 // Packed weight row length: window positions x cpad, rounded up to 64.
 inline long conv3d_kp(const Conv3dShape& s) {
@@ -75,7 +90,7 @@ hipError_t launch_conv3d_pack_weights(const float* weights, const Conv3dShape& s
 // hold every input frame these outputs read).  Both buffers < 2 GiB; mem > 0
 // needs ho*wo % 8 == 0.  out: planar [cout][...], element (co, t, y, x) at
 // co*out_cstep + (t*Ho + y)*Wo + x, type out_kind; bias fp32 [cout] or null.
-// part: fp32 scratch of conv3d_tap_split(s, frames_out*ho*wo, wo) x cout x
+// part: fp32 scratch of conv3d_k_split(s, frames_out*ho*wo, wo) x cout x
 // frames_out*ho*wo floats for the split k loop, or null (no split).
 hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
                          size_t memory_bytes, const uint16_t* staged, size_t staged_bytes,

@@ -155,11 +155,13 @@ struct ConvArgs {
     int shift, fbase, t0;
     int mtiles, ntiles;
     int ytiles, xtiles;   // halo kernel: output tiles per frame
-    // k loop split over the temporal taps: workgroup row blockIdx.y takes
-    // tap blockIdx.y and stores its raw fp32 tile to part + blockIdx.y *
-    // part_split (planar [cout][M]); null: the whole loop, normal epilogue
+    // k loop split into `splits` ranges of whole k-steps: workgroup row
+    // blockIdx.y takes range blockIdx.y and stores its raw fp32 tile to part +
+    // blockIdx.y * part_split (planar [cout][M]); null: the whole loop,
+    // normal epilogue
     float* part;
     long part_split;
+    int splits;
 };
 
 // Eight waves in a grid of 128x64 wave tiles (4x2 MFMA 32x32x16
@@ -290,10 +292,13 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
         for (int j = 0; j < AJ; ++j) voffa[j] = (rmask[j] & bit) ? rbase[j] + koff : 0x80000000u;
     };
     const int cpc = SMALL ? 1 : a.cpad / 64;   // k-steps per window position
-    // taps [tap0, tap0 + ntaps) of the k loop (all of them unless split)
-    const int tap0 = (!SMALL && a.part) ? (int)blockIdx.y : 0;
-    const int kbase = tap0 * a.kh * a.kw * cpc;
-    const int nk = (!SMALL && a.part) ? a.kh * a.kw * cpc : a.kp / 64;
+    // k-steps [kbase, kbase + nk) of the loop (all of them unless split)
+    int kbase = 0, nk = a.kp / 64;
+    if (!SMALL && a.part) {
+        const int all = a.kt * a.kh * a.kw * cpc;
+        kbase = (int)((long)blockIdx.y * all / a.splits);
+        nk = (int)((long)(blockIdx.y + 1) * all / a.splits) - kbase;
+    }
     // SMALL: this wave's 16-byte part of a pixel and window position within
     // a k-step; the position of k-step ks is ks * (64 / cpad) + its index
     const int parts = a.cpad / 8;
@@ -361,14 +366,15 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
             for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
     // window position and channel chunk of the next k-step to issue
-    int tap = tap0, ky = 0, kx = 0, cc = 0;
+    int cc = kbase % cpc, kx = (kbase / cpc) % a.kw, ky = (kbase / cpc / a.kw) % a.kh;
+    int tap = kbase / cpc / a.kw / a.kh;
     if (SMALL) {
         set_step_small(0);
     } else {
-        set_tap(tap0);
-        set_pos(0, 0);
+        set_tap(tap);
+        set_pos(ky, kx);
     }
-    issue(0, 0, 0);
+    issue(0, 0, cc);
 #pragma unroll 1
     for (int ks = 0; ks < nk; ++ks) {
         const int stage = ks & 1;
@@ -731,7 +737,7 @@ __global__ __launch_bounds__(256) void conv3d_reduce_kernel(const float* __restr
 
 template <int BN, bool SMALL>
 void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
-    const dim3 grid((unsigned)(a.mtiles * a.ntiles), a.part ? (unsigned)a.kt : 1u);
+    const dim3 grid((unsigned)(a.mtiles * a.ntiles), a.part ? (unsigned)a.splits : 1u);
     if (a.out_kind == 1)
         conv3d_kernel<BN, 1, SMALL><<<grid, 512, 0, stream>>>(a);
     else if (a.out_kind == 2)
@@ -898,7 +904,8 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.ytiles = a.xtiles = 0;
     a.part = nullptr;
     a.part_split = 0;
-    const int splits = part ? conv3d_tap_split(s, m, wo) : 1;
+    const int splits = part ? conv3d_k_split(s, m, wo) : 1;
+    a.splits = splits;
     if (splits > 1) {
         a.part = part;
         a.part_split = (long)s.cout * m;

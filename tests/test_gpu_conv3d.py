@@ -97,10 +97,13 @@ SHAPES = [
     (64, 160, 2, 10, 192, {}),                         # 64-column tiles (192 = 3 x 64)
     (128, 3, 2, 9, 320, {}),                           # RGB output in 64-column tiles
     # layers of at least 64 input channels with fewer than 256 implicit-GEMM
-    # tiles split the k loop over the temporal taps (most small cases above
-    # do too); these two are a latent-width frame and two temporal taps
+    # tiles split the k loop into ranges of k-steps (most small cases above
+    # do too; the ranges cross window positions and temporal taps); these
+    # are a latent-width frame, two temporal taps, and the 720p latent
+    # layer's 114 tiles (two ranges)
     (512, 512, 1, 9, 16, {}),                          # 512 channels, 3 taps
     (64, 96, 3, 6, 10, dict(k=(2, 3, 3))),             # 2 taps
+    (512, 512, 1, 90, 160, {}),                        # 114 tiles, 2 ranges
 ]
 
 
@@ -114,8 +117,8 @@ def test_conv3d_matches_oracle(cin, cout, frames, h, w, kw):
 
 # The unsplit implicit-GEMM k loop of layers with several temporal taps: one
 # workgroup advances from tap to tap and runs the bias epilogue on the whole
-# sum.  Small layers of at least 64 input channels split their k loop over
-# the taps when the workspace holds the partial tiles; a workspace with only
+# sum.  Small layers of at least 64 input channels split their k loop into
+# ranges when the workspace holds the partial tiles; a workspace with only
 # the staged frames (which the forward accepts) runs them unsplit.
 @pytest.mark.parametrize("cin,cout,frames,h,w,kw", [
     (64, 128, 3, 10, 12, {}),                    # 512 x 128 tiles, 3 taps

@@ -71,7 +71,7 @@ def test_downsample_input_valid_only_after_padding(device, h, w):
     without padding until the bottom (right) zero padding lengthens it to 3;
     the workspace and the output follow the padded extent
     (vae_downsample3d.cpp:145-172).  64 -> 128 channels over 3 taps: the few
-    output tiles split the k loop over the taps."""
+    output tiles split the k loop into ranges."""
     import torch
     g = np.random.default_rng(40 + h)
     c, f = 64, 3
