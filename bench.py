@@ -862,6 +862,12 @@ def main():
     assert torch.cuda.is_available() and capi.device_count() >= 1, "needs a gfx950 GPU"
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.vae_only:
         threads = args.cpu_threads or job_cpu_threads()
         print(json.dumps({"vae_conv3d": vae_conv3d(cpu_threads=threads,
@@ -1083,13 +1089,6 @@ def main():
             "fused_equals_separate_bit_for_bit": same,
             "note": "fp32 residual stream; per-sample modulation vectors; regular windows",
         }
-
-    if args.copy_calibration:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-        dst = torch.empty_like(src)
-        dst.copy_(src)
-        torch.cuda.synchronize()
-        del src, dst
 
     m = lv + lt
     gemm = {"qkv": 2 * m * HIDDEN * 3 * HIDDEN, "out": 2 * m * HIDDEN * HIDDEN,

@@ -114,7 +114,10 @@ __global__ __launch_bounds__(256, 3 - buffers<KIND>()) void conv3d_narrow_kernel
     const int lane = tid & 63;
     const int wave = tid >> 6;
 
-    int bid = blockIdx.x;
+    // consecutive logical workgroups (the strips of a band, then the next
+    // band) run on one XCD, so the halo pixels and rows a workgroup reads of
+    // its neighbours' strips and bands come from that XCD's L2
+    int bid = xcd_remap(blockIdx.x, gridDim.x);
     const int strip = bid % a.strips;
     bid /= a.strips;
     const int band = bid % a.bands;
