@@ -817,7 +817,165 @@ def v3_block(steps, warmup):
                               for n in names}
         out["fused_qkv" if fused else "separate_qkv"] = rec
     plan.close()
+    del ws, q, a_v, a_t, o_v, o_t, h_v, h_t, y_v, y_t
+    torch.cuda.empty_cache()
+    out["graph"] = v3_graph(steps, warmup, flops)
     return out
+
+
+def _v3_graph_text():
+    """The v3 block at 720p as an ncnn .param (one block, regular windows):
+    DiTAdaIn -> q / k / v SharedLinear -> AdaptiveWindowAttention (8-input
+    form) -> out SharedLinear -> DiTAdaOutIn -> gate / up SharedLinear ->
+    Swish, BinaryOp mul per stream -> down SharedLinear -> DiTAdaOut, Splits
+    where a blob has several readers, as an ncnn export writes them."""
+    D, F = HIDDEN, V3_MLP
+    layers = [("Input", f"in{i}", [], [f"in{i}"], "") for i in range(10)]
+    layers += [
+        ("DiTAdaIn", "ada_in", ["in0", "in1", "in4", "in5"], ["h_v", "h_t"], f"0={D} 1=1.000000e-05 2=0"),
+        ("SharedLinear", "q", ["h_v", "h_t"], ["q_v", "q_t"], f"0={D} 1={D} 2=1"),
+        ("SharedLinear", "k", ["h_v", "h_t"], ["k_v", "k_t"], f"0={D} 1={D} 2=1"),
+        ("SharedLinear", "v", ["h_v", "h_t"], ["v_v", "v_t"], f"0={D} 1={D} 2=1"),
+        ("AdaptiveWindowAttention", "attn", ["q_v", "k_v", "v_v", "q_t", "k_t", "v_t", "in2", "in3"],
+         ["a_v", "a_t"], f"0={HEADS} 1={HEAD_DIM} 2={TARGET[0]} 3={TARGET[1]} 4={TARGET[2]} 5=0 "
+                         f"6=1.000000e-05 7={PAIRS} 8=0 9=0 10=0"),
+        ("SharedLinear", "out", ["a_v", "a_t"], ["o_v", "o_t"], f"0={D} 1={D} 2=1"),
+        ("DiTAdaOutIn", "ada_out_in", ["in0", "in1", "o_v", "o_t", "in6", "in7", "in8"],
+         ["r_v", "r_t", "m_v", "m_t"], f"0={D} 1=1.000000e-05 2=0"),
+        ("SharedLinear", "gate", ["m_v", "m_t"], ["g_v", "g_t"], f"0={F} 1={D} 2=1"),
+        ("SharedLinear", "up", ["m_v", "m_t"], ["u_v", "u_t"], f"0={F} 1={D} 2=1"),
+        ("Swish", "silu_v", ["g_v"], ["sg_v"], ""), ("Swish", "silu_t", ["g_t"], ["sg_t"], ""),
+        ("BinaryOp", "glu_v", ["sg_v", "u_v"], ["gu_v"], "0=2"),
+        ("BinaryOp", "glu_t", ["sg_t", "u_t"], ["gu_t"], "0=2"),
+        ("SharedLinear", "down", ["gu_v", "gu_t"], ["y_v", "y_t"], f"0={D} 1={F} 2=1"),
+        ("DiTAdaOut", "ada_out", ["r_v", "r_t", "y_v", "y_t", "in9"], ["out0", "out1"], f"0={D} 2=0"),
+    ]
+    uses = {}
+    for _, _, bottoms, _, _ in layers:
+        for b_ in bottoms:
+            uses[b_] = uses.get(b_, 0) + 1
+    taken, lines, blobs = {}, [], set()
+    for type_, name, bottoms, tops, params in layers:
+        nb = []
+        for b_ in bottoms:
+            if uses[b_] > 1:
+                nb.append(f"{b_}_s{taken.get(b_, 0)}")
+                taken[b_] = taken.get(b_, 0) + 1
+            else:
+                nb.append(b_)
+        lines.append(f"{type_} {name} {len(nb)} {len(tops)} " + " ".join(nb + tops) + (" " + params if params else ""))
+        blobs.update(tops)
+        for t in tops:
+            if uses.get(t, 0) > 1:
+                st = [f"{t}_s{i}" for i in range(uses[t])]
+                lines.append(f"Split split_{t} 1 {len(st)} {t} " + " ".join(st))
+                blobs.update(st)
+    return "7767517\n" + f"{len(lines)} {len(blobs)}\n" + "\n".join(lines) + "\n"
+
+
+def v3_graph(steps, warmup, flops):
+    """The v3 block of v3_block as a graph: the .param above and a raw-fp32
+    .bin of seeded weights, loaded by seedvr2::DiTBlockGraph (the ncnn Net /
+    Extractor with its graph folds: q / k / v stacked into the attention's
+    fused QKV projection, gate / up / Swish / mul into the SwiGLU epilogue)
+    and run on device blobs (bf16 video and text rows, fp32 modulation
+    vectors, the shape blobs on the host), through the C wrapper the graph
+    tests use (tests/harness/liblayer_harness.so).  Each run ends with its
+    outputs copied out and the stream synchronised, so the time includes the
+    executor's host work; the norm / modulation passes (DiTAdaIn,
+    DiTAdaOutIn, DiTAdaOut) run too, and are not in the FLOPs."""
+    import ctypes
+    import numpy as np
+    import torch
+    path = os.path.join(ROOT, "tests", "harness", "liblayer_harness.so")
+    if not os.path.exists(path):
+        return {"skipped": "tests/harness/liblayer_harness.so is not built"}
+    L = ctypes.CDLL(path)
+    P, vp, ci = ctypes.POINTER, ctypes.c_void_p, ctypes.c_int
+
+    class HBlob(ctypes.Structure):
+        _fields_ = [("dims", ci), ("w", ci), ("h", ci), ("elemsize", ci), ("device", ci), ("data", vp)]
+    L.h_graph_create.argtypes = [ctypes.c_char_p, vp, ctypes.c_long, ci, ci, P(vp)]
+    L.h_graph_fused_swiglu.argtypes = [vp]
+    L.h_graph_fused_qkv.argtypes = [vp]
+    L.h_graph_destroy.argtypes = [vp]
+    L.h_graph_run.argtypes = [vp, P(ci), P(ci), ci, P(HBlob), P(HBlob), ci, P(ctypes.c_char_p)]
+    D, F = HIDDEN, V3_MLP
+    g = np.random.default_rng(31)
+    parts = []
+
+    def lin(n, k):
+        parts.append((0.02 * g.standard_normal((n, k), dtype=np.float32)))
+        parts.append((0.02 * g.standard_normal(n, dtype=np.float32)))
+    for _ in range(3):
+        lin(D, D)
+    parts.append((1.0 + 0.02 * g.standard_normal(4 * HEAD_DIM, dtype=np.float32)))
+    parts.append((10000.0 ** (-np.arange(PAIRS, dtype=np.float64) / PAIRS)).astype(np.float32))
+    lin(D, D)
+    lin(F, D)
+    lin(F, D)
+    lin(D, F)
+    model = b"".join(np.ascontiguousarray(p_, dtype="<f4").tobytes() for p_ in parts)
+    del parts
+    nbytes = len(model)
+    buf = ctypes.create_string_buffer(model, nbytes)
+    del model
+    h = ctypes.c_void_p()
+    text = _v3_graph_text()
+    ret = L.h_graph_create(text.encode(), buf, nbytes, 0, 3, ctypes.byref(h))
+    del buf
+    if ret != 0:
+        return {"skipped": f"graph load returned {ret}"}
+    try:
+        dev = torch.device("cuda:0")
+        gen = torch.Generator(device=dev).manual_seed(12)
+        lv = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2]
+        lt = TEXT_TOKENS
+        x_v = torch.randn(lv, D, generator=gen, device=dev).to(torch.bfloat16)
+        x_t = torch.randn(lt, D, generator=gen, device=dev).to(torch.bfloat16)
+        mods = [torch.randn(1, D, generator=gen, device=dev) * 0.1 + (1.0 if k in (1, 4) else 0.0)
+                for k in range(6)]
+        shape = np.asarray([VIDEO_SHAPE], np.float32)
+        tlen = np.asarray([[lt]], np.float32)
+        ins = (HBlob * 10)()
+        ins[0] = HBlob(2, D, lv, 2, 1, x_v.data_ptr())
+        ins[1] = HBlob(2, D, lt, 2, 1, x_t.data_ptr())
+        ins[2] = HBlob(2, 3, 1, 4, 0, shape.ctypes.data)
+        ins[3] = HBlob(2, 1, 1, 4, 0, tlen.ctypes.data)
+        for i, m_ in enumerate(mods):
+            ins[4 + i] = HBlob(2, D, 1, 4, 1, m_.data_ptr())
+        o_v = torch.empty(lv, D, dtype=torch.bfloat16, device=dev)
+        o_t = torch.empty(lt, D, dtype=torch.bfloat16, device=dev)
+        outs = (HBlob * 2)()
+        outs[0] = HBlob(2, D, lv, 2, 1, o_v.data_ptr())
+        outs[1] = HBlob(2, D, lt, 2, 1, o_t.data_ptr())
+        sh = np.asarray(VIDEO_SHAPE, np.int32)
+        tl = np.asarray([lt], np.int32)
+        names = (ctypes.c_char_p * 1)()
+        ip = ctypes.POINTER(ctypes.c_int)
+
+        def run():
+            r = L.h_graph_run(h, sh.ctypes.data_as(ip), tl.ctypes.data_as(ip), 1, ins, outs, 0, names)
+            if r != 0:
+                raise RuntimeError(f"graph run returned {r}")
+        torch.cuda.synchronize()
+        for _ in range(max(2, warmup)):
+            run()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            run()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        total = sum(flops.values())
+        rec = {"ms_per_block": round(ms, 4), "tflops_hot_path": round(total / (ms * 1e-3) / 1e12, 1),
+               "fused_swiglu": L.h_graph_fused_swiglu(h), "fused_qkv": L.h_graph_fused_qkv(h),
+               "output_finite": bool(torch.isfinite(o_v.float()).all().item()),
+               "note": "wall time per graph run (host executor + device work + output copy "
+                       "and stream sync); includes the block's norm / modulation passes"}
+        return rec
+    finally:
+        L.h_graph_destroy(h)
 
 
 def main():
