@@ -112,6 +112,89 @@ __global__ __launch_bounds__(kStageThreads) void conv3d_stage_kernel(
     }
 }
 
+// Staging for at least 64 channel slots (cpad a multiple of 64) and 16-byte
+// aligned channel rows, without LDS: a thread loads 8 pixels of 8 channels
+// (one 16-byte run per channel, two for fp32), transposes them in registers
+// and stores 8 pixels' 16-byte channel runs.  Eight consecutive lanes hold the
+// eight channel groups of a 64-channel block for one pixel run, the next
+// eight lanes the next run: a load instruction reads 128 contiguous bytes of
+// each of 8 channel rows, a store instruction writes 128 contiguous bytes
+// (the block's 64 channels) of each of 8 pixels.  A block covers 256 pixels
+// of 64 channels; pixels past the end are not written, channels at and above
+// cin are written as zeros.
+template <int KIND>
+__global__ __launch_bounds__(256) void conv3d_stage_t_kernel(
+    const void* __restrict__ in, long cstep, int cin, long pixels, int cpad,
+    uint16_t* __restrict__ staged, uint16_t* __restrict__ tail, long tail_q0) {
+    const int t = threadIdx.x;
+    const int h = (t & 7);                // channel group within the block
+    const int g = (t >> 3) & 31;          // pixel run within the block
+    const long q = (long)blockIdx.x * 256 + 8 * g;
+    const int c0 = blockIdx.y * 64 + 8 * h;
+    if (q >= pixels) return;
+    const bool full = q + 8 <= pixels;
+    uint32_t w[8][4];   // channel i, pixel pair d (bf16 pairs)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int c = c0 + i;
+        uint32_t v[4] = {0u, 0u, 0u, 0u};
+        if (c < cin) {
+            const long base = (long)c * cstep + q;
+            if (KIND == 0) {
+                float f[8];
+                if (full) {
+                    const float4 a = *reinterpret_cast<const float4*>((const float*)in + base);
+                    const float4 b = *reinterpret_cast<const float4*>((const float*)in + base + 4);
+                    f[0] = a.x, f[1] = a.y, f[2] = a.z, f[3] = a.w;
+                    f[4] = b.x, f[5] = b.y, f[6] = b.z, f[7] = b.w;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) f[e] = q + e < pixels ? ((const float*)in)[base + e] : 0.f;
+                }
+#pragma unroll
+                for (int d = 0; d < 4; ++d) v[d] = pack2_bf16_rne(f[2 * d], f[2 * d + 1]);
+            } else {
+                uint4 u = make_uint4(0, 0, 0, 0);
+                if (full) {
+                    u = *reinterpret_cast<const uint4*>((const uint16_t*)in + base);
+                } else {
+                    uint16_t e16[8];
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) e16[e] = q + e < pixels ? ((const uint16_t*)in)[base + e] : 0;
+                    u = make_uint4(e16[0] | (e16[1] << 16), e16[2] | (e16[3] << 16),
+                                   e16[4] | (e16[5] << 16), e16[6] | (e16[7] << 16));
+                }
+                const uint32_t r[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    if (KIND == 2)
+                        v[d] = pack2_bf16_rne((float)__builtin_bit_cast(_Float16, (uint16_t)(r[d] & 0xffffu)),
+                                              (float)__builtin_bit_cast(_Float16, (uint16_t)(r[d] >> 16)));
+                    else
+                        v[d] = r[d];
+                }
+            }
+        }
+#pragma unroll
+        for (int d = 0; d < 4; ++d) w[i][d] = v[d];
+    }
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        if (!full && q + p >= pixels) break;
+        uint32_t o[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t lo = w[2 * d][p >> 1], hi = w[2 * d + 1][p >> 1];
+            o[d] = (p & 1) ? ((lo >> 16) | (hi & 0xffff0000u)) : ((lo & 0xffffu) | (hi << 16));
+        }
+        const uint4 val = make_uint4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<uint4*>(staged + (q + p) * cpad + c0) = val;
+        // pixels from tail_q0 on are the next temporal memory as well
+        if (tail && q + p >= tail_q0)
+            *reinterpret_cast<uint4*>(tail + (q + p - tail_q0) * cpad + c0) = val;
+    }
+}
+
 // ---- weights: [kt][cout][cin][kh][kw] fp32 -> [cout][kp] bf16 ----------------
 
 // row co of the packed weights: k = p * cpad + ci for window position p =
@@ -827,6 +910,19 @@ hipError_t launch_conv3d_stage(const void* input, int in_kind, long in_cstep, in
     // 16-byte runs need 16-byte aligned channel rows
     const int esz = in_kind == 0 ? 4 : 2;
     const int vec = ((uintptr_t)input % 16) == 0 && (in_cstep * esz) % 16 == 0;
+    if (cpad >= 64 && cpad % 64 == 0 && vec) {
+        const dim3 grid((unsigned)((pixels + 255) / 256), (unsigned)(cpad / 64));
+        if (in_kind == 1)
+            conv3d_stage_t_kernel<1><<<grid, 256, 0, stream>>>(input, in_cstep, cin, pixels, cpad,
+                                                               staged, tail, tail_q0);
+        else if (in_kind == 2)
+            conv3d_stage_t_kernel<2><<<grid, 256, 0, stream>>>(input, in_cstep, cin, pixels, cpad,
+                                                               staged, tail, tail_q0);
+        else
+            conv3d_stage_t_kernel<0><<<grid, 256, 0, stream>>>(input, in_cstep, cin, pixels, cpad,
+                                                               staged, tail, tail_q0);
+        return hipGetLastError();
+    }
     if (cpad < 64)
         stage_launch<64>(input, in_kind, in_cstep, cin, pixels, cpad, vec, staged, tail, tail_q0,
                          stream);
