@@ -356,3 +356,43 @@ def test_conv3d_narrow_rejects_extra_padding():
     n = ctypes.c_size_t()
     assert capi.lib().s2_conv3d_workspace_bytes_padded(ctypes.byref(cfgs[0]), 2, 8, 8, 1, 0, 0,
                                                        ctypes.byref(n)) != 0
+
+
+# ---- at most 8 input channels, 3x3x3, unit strides (conv3d_rgbin_kernel) ------
+# The encoder's RGB-input conv and its kin run with the output channels as the
+# MFMA rows; 32..128 outputs in multiples of 32, ragged strips and rows, slice
+# chains through the memory (copied in front of the staged input), every
+# output type, rows that leave in 16-byte runs (widths a multiple of 8) and
+# rows that do not.
+
+@pytest.mark.parametrize("cin,cout,frames,h,w", [
+    (3, 128, 4, 9, 200),     # two strips, the second ragged
+    (8, 64, 3, 7, 130),      # two waves idle, a strip of 2 pixels
+    (3, 32, 2, 5, 10),       # one wave of output channels
+    (5, 96, 3, 33, 128),     # one full strip, rows over several bands
+    (8, 64, 2, 6, 136),      # 16-byte output runs with two waves idle
+])
+def test_conv3d_rgb_input(cin, cout, frames, h, w):
+    cfgs = _cfg(cin, cout)
+    x, wts, bias = _case(cin, cout, frames, h, w, cfgs, 70 + cin + cout)
+    _check(_run(_device(cfgs[0], wts, bias), x), x, wts, bias, cfgs[1])
+
+
+@pytest.mark.parametrize("out_dtype,w", [("bf16", 150), ("bf16", 152), ("f16", 150),
+                                         ("f16", 152), ("f32", 152)])
+def test_conv3d_rgb_input_chain_and_types(out_dtype, w):
+    # widths a multiple of 8 take the 16-byte store path for 16-bit outputs
+    import torch
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+    cfgs = _cfg(3, 128, head=1)
+    x, wts, bias = _case(3, 128, 6, 12, w, cfgs, 90)
+    # outputs of magnitude below 4, where one bf16 rounding stays under the
+    # 2e-2 bar (1.4 M outputs of unit variance reach 5 and beyond)
+    x = (0.5 * x).astype(np.float32)
+    conv = _device(cfgs[0], wts, bias)
+    parts = []
+    for i, (a, b) in enumerate([(0, 2), (2, 5), (5, 6)]):
+        parts.append(_run(conv, x[:, a:b], out_dtype=dt[out_dtype], use_memory=i > 0,
+                          keep_memory=True))
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)
+    assert_close(np.concatenate(parts, axis=1), ref)
