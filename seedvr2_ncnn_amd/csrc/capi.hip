@@ -1350,18 +1350,21 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
     uint16_t* staged = (uint16_t*)workspace;
     if (lead > 0)
         S2_HIP(hipMemcpyAsync(staged, memory, (size_t)lead * frame_bytes, hipMemcpyDeviceToDevice, st));
-    // The next memory is the last `cache` padded frames.  When they are all
-    // input frames the staging pass writes them as well, unless the kernel
+    // The next memory is the last `cache` padded frames.  The staging pass
+    // writes the input frames among them (all of them, or the last `frames`
+    // after cache - frames earlier ones, copied below), unless the kernel
     // still has to read `memory` and next_memory overlaps it.
     const uint8_t* mlo = (const uint8_t*)memory;
     const uint8_t* nlo = (const uint8_t*)next_memory;
     const bool overlap = memory && next_memory && nlo < mlo + (size_t)mem * frame_bytes &&
                          mlo < nlo + (size_t)std::max(cache, 0) * frame_bytes;
-    const bool tail_in_stage = want_memory && frames >= cache && (kmem == 0 || !overlap);
+    const bool tail_in_stage = want_memory && (kmem == 0 || !overlap);
+    const int early = std::max(cache - frames, 0);   // next-memory frames from before the input
     S2_HIP(s2::launch_conv3d_stage(input, (int)in_dtype, in_cstep, s.cin, (long)frames * plane_in,
                                    s.cpad, staged + (size_t)lead * frame_elems,
-                                   tail_in_stage ? (uint16_t*)next_memory : nullptr,
-                                   (long)(frames - cache) * plane_in, st));
+                                   tail_in_stage ? (uint16_t*)next_memory + (size_t)early * frame_elems
+                                                 : nullptr,
+                                   (long)std::max(frames - cache, 0) * plane_in, st));
     // fp32 partial tiles of a k loop split into ranges, after the staged
     // frames, when the workspace holds them (s2_conv3d_workspace_bytes counts
     // them; a smaller workspace runs the whole k loop per tile instead)
@@ -1390,10 +1393,10 @@ int s2_conv3d_forward_padded(const s2_conv3d_config* config, const void* packed_
                                  (int)out_dtype, out_cstep, part, st));
         t0 += n;
     }
-    if (want_memory && !tail_in_stage) {
+    if (want_memory) {
         // frames in ascending order: frame f comes from v >= f, so a memory
         // buffer reused as next_memory is read before it is overwritten
-        for (int f = 0; f < cache; ++f) {
+        for (int f = 0; f < (tail_in_stage ? early : cache); ++f) {
             const int v = vframe((long)padded - cache + f);
             const uint8_t* src = v < kmem ? mlo + (size_t)v * frame_bytes
                                           : (const uint8_t*)(staged + (size_t)(v - kmem) * frame_elems);

@@ -19,6 +19,7 @@
 
 #include "conv3d_kernels.h"
 #include "s2_device.h"
+#include "stream_scratch.h"
 
 namespace s2 {
 namespace {
@@ -26,6 +27,8 @@ namespace {
 constexpr int kStageThreads = 256;
 
 __device__ __forceinline__ int lds_swizzle(int r) { return ((r >> 1) ^ ((r & 1) << 2)) & 7; }
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 // ---- staging: planar -> channel-last bf16 ------------------------------------
 
@@ -245,7 +248,81 @@ struct ConvArgs {
     float* part;
     long part_split;
     int splits;
+    // conv3d_pp_kernel with a split k loop: one 256x256 fp32 slot per
+    // (tile, range) workgroup and one arrival counter per tile (zero between
+    // launches); the last range of a tile to arrive sums the slots and runs
+    // the normal epilogue, so no second pass reads part.  null: part.
+    float* slots;
+    int* counters;
 };
+
+// Epilogue of a TM x TN grid of 32x32 accumulators whose first row is GEMM
+// row r0 and first column output channel c0: register r of an accumulator
+// is row 8(r/4) + 4g + r%4, column l32, so each lane holds 4 consecutive
+// output pixels of one output channel: one 16-byte (fp32) or 8-byte store
+// into that plane.  part: the raw fp32 partial tile of k range blockIdx.y
+// goes to part + blockIdx.y * part_split (planar [cout][M]) instead.
+template <int TM, int TN, int OK>
+__device__ __forceinline__ void conv3d_epilogue(const ConvArgs& a, const f32x16 (&acc)[TM][TN],
+                                                int r0, int c0, int l32, int g, float* part) {
+    if (part) {
+        float* pp = part + (long)blockIdx.y * a.part_split;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const int col = c0 + 32 * j + l32;
+            if (col >= a.cout) continue;
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int rg = 0; rg < 4; ++rg) {
+                    const int m = r0 + 32 * i + 8 * rg + 4 * g;
+                    const long idx = (long)col * a.M + m;
+                    if ((a.M & 3) == 0 && m + 3 < a.M) {
+                        // m and M multiples of 4: a 16-byte aligned run
+                        *reinterpret_cast<float4*>(pp + idx) =
+                            make_float4(acc[i][j][4 * rg], acc[i][j][4 * rg + 1],
+                                        acc[i][j][4 * rg + 2], acc[i][j][4 * rg + 3]);
+                    } else {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            if (m + e < a.M) pp[idx + e] = acc[i][j][4 * rg + e];
+                    }
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+        const int col = c0 + 32 * j + l32;
+        if (col >= a.cout) continue;
+        const float bv = a.bias ? a.bias[col] : 0.f;
+        const long cbase = (long)col * a.out_cstep + a.out_off;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int rg = 0; rg < 4; ++rg) {
+                const int m = r0 + 32 * i + 8 * rg + 4 * g;
+                const float v0 = acc[i][j][4 * rg] + bv, v1 = acc[i][j][4 * rg + 1] + bv;
+                const float v2 = acc[i][j][4 * rg + 2] + bv, v3 = acc[i][j][4 * rg + 3] + bv;
+                if (a.vec_ok && m + 3 < a.M) {
+                    store4(a.out, cbase + m, v0, v1, v2, v3, OK);
+                } else {
+                    const float v[4] = {v0, v1, v2, v3};
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (m + e >= a.M) continue;
+                        const long idx = cbase + m + e;
+                        if (OK == 1)
+                            ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
+                        else if (OK == 2)
+                            ((_Float16*)a.out)[idx] = (_Float16)v[e];
+                        else
+                            ((float*)a.out)[idx] = v[e];
+                    }
+                }
+            }
+    }
+}
 
 // Eight waves in a grid of 128x64 wave tiles (4x2 MFMA 32x32x16
 // accumulators, 128 fp32 per lane), as in the SharedLinear GEMM: BN = 256
@@ -496,67 +573,304 @@ __global__ __launch_bounds__(512, 1) void conv3d_kernel(ConvArgs a) {
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Epilogue: register r of a 32x32 accumulator is row 8(r/4) + 4g + r%4,
-    // column l32, so each lane holds 4 consecutive output pixels of one
-    // output channel: one 16-byte (fp32) or 8-byte store into that plane.
-    if (!SMALL && a.part) {
-        // raw partial tile of this tap, fp32 [cout][M]
-        float* pp = a.part + (long)blockIdx.y * a.part_split;
+    conv3d_epilogue<TM, TN, OK>(a, acc, row0 + wm * 32 * TM, col0 + wn * 32 * TN, l32, g,
+                                SMALL ? nullptr : a.part);
+}
+
+// ---- the implicit GEMM on the ping-pong schedule (more than 128 outputs) -----
+//
+// conv3d_kernel's tiles (256x256, wave tiles 128x64, 64-k steps of one
+// window position and channel chunk, two LDS stages) with the SharedLinear
+// GEMM's main loop: the two waves of each SIMD (group 0 = waves 0-3, tile
+// rows 0-127; group 1 = waves 4-7, rows 128-255) take turns, one issuing the
+// 32 MFMAs of a whole 64-k step from fragment registers while the other
+// reads its next step's fragments from LDS, so the matrix core does not wait
+// on LDS reads.  Every phase ends at a workgroup barrier; group 1 runs one
+// phase behind group 0.  Each wave loads A rows and B rows 128 grp + 32 wq
+// + 8 j + lane / 8 (j < 4) of a step, its group's half of the stage:
+//
+//   phase     2s                             2s + 1
+//   group 0   DMA of step s + 1 into stage   MFMAs of step s,
+//             (s + 1) % 2, read step s       wait for its DMA
+//   group 1   MFMAs of step s - 1            read step s, wait for its DMA
+//                                            of step s + 1, DMA of step s + 2
+//                                            into stage s % 2
+//
+// Group 0 writes the stage both groups finished reading in phases 2s - 2
+// and 2s - 1; group 1 the stage it has just read (group 0 read it in phase
+// 2s).  A step's data is complete before the barrier that ends phase 2s + 1
+// (group 0's half) or 2s - 1 (group 1's, issued two phases earlier), and
+// group 0 reads step s + 1 in phase 2s + 2.
+template <int OK>
+__global__ __launch_bounds__(512, 1) void conv3d_pp_kernel(ConvArgs a) {
+    constexpr int BN = 256, BM = 256, BK = 64, RB = BK * 2;
+    constexpr int TA = BM * RB, SB = TA + BN * RB;
+    constexpr int GROUP = 4;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * SB];
+    // per loaded row: padded frame of tap 0 and window origin offset, read
+    // when the tap changes (kept out of registers: the fragments of a whole
+    // step and the accumulators take 224 of them)
+    __shared__ uint2 rinfo[4 * 512];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2, wq = wave & 3;
+    const int l32 = lane & 31;
+    const int g = lane >> 5;
+    const int sw = lds_swizzle(l32);
+    const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+
+    const int lid = xcd_remap(blockIdx.x, gridDim.x);
+    const int group_size = GROUP * a.ntiles;
+    const int first_m = (lid / group_size) * GROUP;
+    const int gm = min(a.mtiles - first_m, GROUP);
+    const int mt = first_m + (lid % group_size) % gm;
+    const int nt = (lid % group_size) / gm;
+    const int row0 = mt * BM;
+    const int col0 = nt * BN;
+
+    const uint32_t pix = (uint32_t)(a.cpad * 2);
+    const uint32_t frame_bytes = (uint32_t)(a.H * a.W) * pix;
+    const int hw = a.Ho * a.Wo;
+    // the tile rows this lane loads (A and B alike): lrow + 8 j; rows 8
+    // apart have swizzles that differ in bit 2
+    const int lrow = 128 * grp + 32 * wq + (lane >> 3);
+    const uint32_t chk_even = (uint32_t)(((lane & 7) ^ lds_swizzle(lrow)) * 16);
+    const uint32_t chk_odd = chk_even ^ 64u;
+    uint32_t rmask[4];
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-            const int col = col0 + wn * 32 * TN + 32 * j + l32;
-            if (col >= a.cout) continue;
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int rg = 0; rg < 4; ++rg) {
-                    const int m = row0 + wm * 32 * TM + 32 * i + 8 * rg + 4 * g;
-                    const long idx = (long)col * a.M + m;
-                    if ((a.M & 3) == 0 && m + 3 < a.M) {
-                        // m and M multiples of 4: a 16-byte aligned run
-                        *reinterpret_cast<float4*>(pp + idx) =
-                            make_float4(acc[i][j][4 * rg], acc[i][j][4 * rg + 1],
-                                        acc[i][j][4 * rg + 2], acc[i][j][4 * rg + 3]);
-                    } else {
-#pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            if (m + e < a.M) pp[idx + e] = acc[i][j][4 * rg + e];
-                    }
-                }
+    for (int j = 0; j < 4; ++j) {
+        const int m = row0 + lrow + 8 * j;
+        int rpf = INT_MIN / 2;
+        uint32_t rpix = (j & 1) ? chk_odd : chk_even;
+        rmask[j] = 0;
+        if (m < a.M) {
+            const int to = m / hw;
+            const int rem = m - to * hw;
+            const int yo = rem / a.Wo;
+            const int xo = rem - yo * a.Wo;
+            const int yb = yo * a.sh - a.ph, xb = xo * a.sw - a.pw;
+            rpf = (a.t0 + to) * a.st;
+            rpix += (uint32_t)(yb * a.W + xb) * pix;
+            uint32_t mk = 0;
+            for (int ky = 0; ky < a.kh; ++ky) {
+                if ((unsigned)(yb + ky * a.dh) >= (unsigned)a.H) continue;
+                for (int kx = 0; kx < a.kw; ++kx)
+                    if ((unsigned)(xb + kx * a.dw) < (unsigned)a.W) mk |= 1u << (ky * a.kw + kx);
+            }
+            rmask[j] = mk;
         }
-        return;
+        rinfo[j * 512 + tid] = make_uint2((uint32_t)rpf, rpix);
     }
+    const uint32_t voffb0 = (uint32_t)(lrow * a.kp * 2);
+    const i32x4 ra = wave_uniform(buffer_rsrc(a.staged, a.staged_bytes));
+    const i32x4 rm = wave_uniform(buffer_rsrc(a.memory, a.memory_bytes));
+    const i32x4 rb = wave_uniform(buffer_rsrc(
+        a.packed + (long)col0 * a.kp, (uint32_t)(min(a.cout - col0, BN) * a.kp * 2)));
+
+    // temporal tap and window position of the step a wave issues next, as in
+    // conv3d_kernel (each lane reads only its own rinfo entries)
+    uint32_t rbase[4];
+    int memsel[4];
+    auto set_tap = [&](int tap) {
+        const int dtap = tap * a.dt - a.shift;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-        const int col = col0 + wn * 32 * TN + 32 * j + l32;
-        if (col >= a.cout) continue;
-        const float bv = a.bias ? a.bias[col] : 0.f;
-        const long cbase = (long)col * a.out_cstep + a.out_off;
+        for (int j = 0; j < 4; ++j) {
+            const uint2 ri = rinfo[j * 512 + tid];
+            const int v = max((int)ri.x + dtap, 0);
+            const bool fm = v < a.mem;
+            const int sf = fm ? v : v - a.mem - a.fbase;
+            rbase[j] = (uint32_t)sf * frame_bytes + ri.y;
+            memsel[j] = __builtin_amdgcn_readfirstlane((int)fm);
+        }
+    };
+    const int cpc = a.cpad / 64;
+    int kbase = 0, nk = a.kp / 64;
+    if (a.part) {
+        const int all = a.kt * a.kh * a.kw * cpc;
+        kbase = (int)((long)blockIdx.y * all / a.splits);
+        nk = (int)((long)(blockIdx.y + 1) * all / a.splits) - kbase;
+    }
+    // Steps walk (tap, channel chunk, ky, kx) with kx fastest: the nine
+    // window positions of one 64-channel chunk follow each other, so the
+    // shifted A tiles they read overlap in L2 (with the chunk fastest, as the
+    // packed k order runs, a chunk is read again only nine positions later,
+    // past what L2 holds for all the workgroups of an XCD).  The packed
+    // weights are read at the matching k offset.
+    const int khw = a.kh * a.kw;
+    int tap = kbase / (cpc * khw);
+    int cc = (kbase / khw) % cpc, ky = (kbase % khw) / a.kw, kx = kbase % a.kw;
+    set_tap(tap);
+    int next = 0;   // the step this wave issues next
+    auto issue = [&](int stage) {
+        const uint32_t st = lds_base + stage * SB + (uint32_t)((128 * grp + 32 * wq) * RB);
+        const uint32_t soffa = (uint32_t)(cc * RB);
+        const uint32_t soffb = (uint32_t)(((tap * khw + ky * a.kw + kx) * cpc + cc) * RB);
+        const uint32_t koff = (uint32_t)(ky * a.dh * a.W + kx * a.dw) * pix;
+        const uint32_t bit = 1u << (ky * a.kw + kx);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
+        for (int j = 0; j < 4; ++j)
+            lds_dma16(memsel[j] ? rm : ra, st + j * 8 * RB,
+                      (rmask[j] & bit) ? rbase[j] + koff : 0x80000000u, soffa);
 #pragma unroll
-            for (int rg = 0; rg < 4; ++rg) {
-                const int m = row0 + wm * 32 * TM + 32 * i + 8 * rg + 4 * g;
-                const float v0 = acc[i][j][4 * rg] + bv, v1 = acc[i][j][4 * rg + 1] + bv;
-                const float v2 = acc[i][j][4 * rg + 2] + bv, v3 = acc[i][j][4 * rg + 3] + bv;
-                if (a.vec_ok && m + 3 < a.M) {
-                    store4(a.out, cbase + m, v0, v1, v2, v3, OK);
-                } else {
-                    const float v[4] = {v0, v1, v2, v3};
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        if (m + e >= a.M) continue;
-                        const long idx = cbase + m + e;
-                        if (OK == 1)
-                            ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
-                        else if (OK == 2)
-                            ((_Float16*)a.out)[idx] = (_Float16)v[e];
-                        else
-                            ((float*)a.out)[idx] = v[e];
-                    }
+        for (int j = 0; j < 4; ++j)
+            lds_dma16(rb, st + TA + j * 8 * RB,
+                      voffb0 + (uint32_t)(j * 8 * a.kp * 2) + ((j & 1) ? chk_odd : chk_even), soffb);
+        if (++next < nk && ++kx == a.kw) {
+            kx = 0;
+            if (++ky == a.kh) {
+                ky = 0;
+                if (++cc == cpc) {
+                    cc = 0;
+                    set_tap(++tap);
                 }
             }
+        }
+    };
+
+    f32x16 acc[4][2];
+    bf16x8 fa[4][4], fb[4][2];
+    auto read_step = [&](int stage) {
+        const uint8_t* st = lds + stage * SB;
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk) {
+            const int pc = ((2 * kk + g) ^ sw) * 16;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                fa[kk][i] = as_bf16x8(*(const uint4*)(st + (grp * 128 + 32 * i + l32) * RB + pc));
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+                fb[kk][j] = as_bf16x8(*(const uint4*)(st + TA + (wq * 64 + 32 * j + l32) * RB + pc));
+        }
+    };
+    auto barrier = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        asm volatile("s_barrier" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    };
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+    // steps 0 and 1 by both groups
+    issue(0);
+    if (nk > 1) issue(1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    barrier();
+    if (grp == 1) barrier();
+#pragma unroll 1
+    for (int s = 0; s < nk; ++s) {
+        // memory phase
+        if (grp == 0 && s >= 1 && s + 1 < nk) issue((s + 1) & 1);
+        read_step(s & 1);
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (grp == 1) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // its half of step s + 1
+            if (s + 2 < nk) issue(s & 1);
+        }
+        barrier();
+        // MFMA phase
+        __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+        for (int kk = 0; kk < BK / 16; ++kk)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[kk][i], fb[kk][j],
+                                                                        acc[i][j], 0, 0, 0);
+        __builtin_amdgcn_s_setprio(0);
+        if (grp == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // its half of step s + 1
+        barrier();
     }
+    if (grp == 0) barrier();
+
+    if (a.part && a.slots) {
+        // slot layout: float4 c (4 accumulator registers) of thread tid at
+        // byte (c * 512 + tid) * 16.  The stores write through; every wave
+        // waits for its own before the barrier, and the arrival is an
+        // agent-scope acquire-release read-modify-write that releases this
+        // range's slot and, for the last range, acquires the others'.
+        constexpr int kFlags = 1 | 16;   // coherent across the XCDs' L2s
+        const int tile = lid;
+        auto slot = [&](int r) {
+            return __builtin_amdgcn_make_buffer_rsrc(
+                a.slots + ((long)tile * a.splits + r) * (BM * BN), (short)0, BM * BN * 4, 0x00020000);
+        };
+        const __amdgpu_buffer_rsrc_t mine = slot((int)blockIdx.y);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const f32x4 v = {acc[i][j][4 * c], acc[i][j][4 * c + 1], acc[i][j][4 * c + 2],
+                                     acc[i][j][4 * c + 3]};
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), mine,
+                                                           tid * 16, ((i * 2 + j) * 4 + c) * 512 * 16,
+                                                           kFlags);
+                }
+        __shared__ int arrival;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0)
+            arrival = __hip_atomic_fetch_add(&a.counters[tile], 1, __ATOMIC_ACQ_REL,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (arrival != a.splits - 1) return;
+        // the sum of every range in range order, as conv3d_reduce_kernel adds
+        // them, so the result does not depend on the order of arrival; with
+        // two ranges the other range's slot is added to this one's registers
+        // (p0 + p1 either way round)
+        const bool two = a.splits == 2;
+#pragma unroll 1
+        for (int r = two ? 1 : 0; r < a.splits; ++r) {
+            const __amdgpu_buffer_rsrc_t other = slot(two ? 1 - (int)blockIdx.y : r);
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                __builtin_amdgcn_sched_barrier(0);
+                f32x4 v[2][2][4];
+#pragma unroll
+                for (int iq = 0; iq < 2; ++iq)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            v[iq][j][c] = __builtin_bit_cast(
+                                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                           other, tid * 16, (((2 * h + iq) * 2 + j) * 4 + c) * 512 * 16,
+                                           kFlags));
+#pragma unroll
+                for (int iq = 0; iq < 2; ++iq)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j)
+#pragma unroll
+                        for (int c = 0; c < 4; ++c) {
+                            f32x16& d = acc[2 * h + iq][j];
+                            if (r == 0 && !two) {
+                                d[4 * c] = v[iq][j][c].x;
+                                d[4 * c + 1] = v[iq][j][c].y;
+                                d[4 * c + 2] = v[iq][j][c].z;
+                                d[4 * c + 3] = v[iq][j][c].w;
+                            } else {
+                                d[4 * c] += v[iq][j][c].x;
+                                d[4 * c + 1] += v[iq][j][c].y;
+                                d[4 * c + 2] += v[iq][j][c].z;
+                                d[4 * c + 3] += v[iq][j][c].w;
+                            }
+                        }
+            }
+        }
+        if (tid == 0)
+            __hip_atomic_store(&a.counters[tile], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        conv3d_epilogue<4, 2, OK>(a, acc, row0 + 128 * grp, col0 + 64 * wq, l32, g, nullptr);
+        return;
+    }
+    conv3d_epilogue<4, 2, OK>(a, acc, row0 + 128 * grp, col0 + 64 * wq, l32, g, a.part);
 }
 
 // ---- 3x3 spatial windows, stride 1: the halo kernel --------------------------
@@ -863,7 +1177,6 @@ __global__ __launch_bounds__(256) void conv3d_reduce_kernel(const float* __restr
 // row it stages the nine input rows (3 taps x 3 rows) of the strip and one
 // pixel each side, prefetched into registers during the previous row's
 // MFMAs.  Wave w computes output channels 32w .. 32w + 31.
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kRgbInHaloW = 130;
 constexpr int kRgbInRowBytes = kRgbInHaloW * 16;
 constexpr int kRgbInBuf = 9 * kRgbInRowBytes;
@@ -1080,10 +1393,19 @@ void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
 
 template <int BN>
 void launch_conv3d_kernel(const ConvArgs& a, hipStream_t stream) {
-    if (a.cpad < 64)
+    if (a.cpad < 64) {
         launch_conv3d_kernel<BN, true>(a, stream);
-    else
+    } else if (BN == 256) {
+        const dim3 grid((unsigned)(a.mtiles * a.ntiles), a.part ? (unsigned)a.splits : 1u);
+        if (a.out_kind == 1)
+            conv3d_pp_kernel<1><<<grid, 512, 0, stream>>>(a);
+        else if (a.out_kind == 2)
+            conv3d_pp_kernel<2><<<grid, 512, 0, stream>>>(a);
+        else
+            conv3d_pp_kernel<0><<<grid, 512, 0, stream>>>(a);
+    } else {
         launch_conv3d_kernel<BN, false>(a, stream);
+    }
 }
 
 // ---- VAEUpsample3D's depth-to-space shuffle (vae_upsample3d.cpp:270-318) ----
@@ -1249,6 +1571,8 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     a.ytiles = a.xtiles = 0;
     a.part = nullptr;
     a.part_split = 0;
+    a.slots = nullptr;
+    a.counters = nullptr;
     const int splits = part ? conv3d_k_split(s, m, wo) : 1;
     a.splits = splits;
     if (splits > 1) {
@@ -1305,9 +1629,25 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
     } else {
         a.mtiles = (int)((m + 255) / 256);
         a.ntiles = (s.cout + 255) / 256;
+        if (a.part && !small) {
+            // the split-k scratch of the stream (256x256 fp32 slots and
+            // counters, one each per CU) when it holds a slot per workgroup;
+            // otherwise the partial tiles go to part and a second pass
+            size_t bytes = 0;
+            void* base = nullptr;
+            if (splitk_scratch_bytes(&bytes) == hipSuccess) {
+                const size_t slot = (size_t)256 * 256 * sizeof(float);
+                const long groups = (long)(bytes / (slot + sizeof(int)));
+                if ((long)a.mtiles * a.ntiles * splits <= groups &&
+                    stream_scratch(kScratchSplitK, stream, bytes, &base) == hipSuccess) {
+                    a.slots = (float*)base;
+                    a.counters = (int*)((char*)base + (size_t)groups * slot);
+                }
+            }
+        }
         launch_conv3d_kernel<256>(a, stream);
     }
-    if (a.part) {
+    if (a.part && !a.slots) {
         const long n = (long)s.cout * m;
         conv3d_reduce_kernel<<<(unsigned)((n + 255) / 256), 256, 0, stream>>>(
             a.part, splits, a.part_split, s.cout, (int)m, bias, out, out_kind, out_cstep,

@@ -146,6 +146,20 @@ def test_conv3d_unsplit_taps_at_256_tiles():
     _check(got, x, wts, bias, cfgs[1])
 
 
+# More than 128 outputs (256 x 256 tiles on the ping-pong schedule) with the
+# memory read in place: 80 pixels a frame keep each 8-row DMA group in one
+# frame; 2 + 3 frames, the second slice's memory buffer reused or not.
+@pytest.mark.parametrize("reuse", [False, True])
+def test_conv3d_memory_chains_256_outputs(reuse):
+    cfgs = _cfg(64, 256)
+    x, wts, bias = _case(64, 256, 5, 8, 10, cfgs, 13)
+    conv = _device(cfgs[0], wts, bias)
+    a = _run(conv, x[:, :2], keep_memory=True)
+    b = _run(conv, x[:, 2:], use_memory=True, keep_memory=True, reuse_memory_buffer=reuse)
+    _, ref, _ = oracle.decomposed_conv3d(cfgs[1], x, wts, bias)
+    assert_close(np.concatenate([a, b], axis=1), ref)
+
+
 # (10, 12): the implicit-GEMM kernel; (6, 120): the halo kernel.  A channel
 # stride padded by 4 elements leaves 16-bit channel rows without 16-byte
 # alignment, which the staging pass reads element by element.
