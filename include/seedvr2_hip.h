@@ -529,7 +529,10 @@ S2_API int s2_conv3d_memory_bytes(const s2_conv3d_config* config, int height, in
  * frames), plus, for layers whose output tiles would leave most of the chip
  * idle, fp32 partial tiles of a k loop split into ranges of k-steps.  A
  * smaller workspace that still holds the staged frames is accepted; the
- * forward then runs the k loop unsplit.  The layers of at most 3 output
+ * forward then runs the k loop unsplit.  Layers of more than 128 output
+ * channels whose split fits one workgroup per compute unit sum the ranges
+ * in the stream's split-k scratch instead (as s2_shared_linear does) and
+ * leave that part of the workspace unused.  The layers of at most 3 output
  * channels above read their input in place: their workspace is a copy of
  * the memory, used only when next_memory overlaps memory and the forward
  * has more than 4 output frames (it may be NULL otherwise), and they take no
