@@ -1164,46 +1164,64 @@ __global__ __launch_bounds__(256) void conv3d_reduce_kernel(const float* __restr
 // ---- at most 8 input channels, 3x3x3, unit strides: the RGB-input conv ----------
 //
 // The encoder's first conv (3 -> 128 channels) reads little and writes a
-// 128-channel bf16 frame per input frame: it is bound by its output bytes.
-// As an implicit GEMM with the pixels as rows, every lane stores 4 pixels of
-// one channel, so a store instruction touches 32 channel planes.  Here the
-// output channels are the MFMA rows and the pixels the columns:
-//   D[co][x] = sum over the 28 window positions (27 and a zero one) and 8
-//              staged channels of W[co][pos*8 + c] X[pos][x][c],
-// one 32x32x16 MFMA per two positions, each lane's B operand one 16-byte
-// staged pixel (the 8 channels of one position) read from LDS, so a store
-// instruction writes 32 consecutive pixels of two channels.  A workgroup
-// owns a 128-pixel strip of one output frame and a band of rows; per output
-// row it stages the nine input rows (3 taps x 3 rows) of the strip and one
-// pixel each side, prefetched into registers during the previous row's
-// MFMAs.  Wave w computes output channels 32w .. 32w + 31.
+// 128-channel bf16 frame per input frame: it is bound by its output bytes,
+// which must leave in long runs of one channel plane (stores of 4 pixels of
+// 32 channels at a time, as the implicit GEMM's lanes hold them, take more
+// than twice as long).  The product is
+//   D[x][co] = sum over the 28 window positions (27 and a zero one) and 8
+//              staged channels of X[pos][x][c] W[co][pos*8 + c],
+// one 32x32x16 MFMA per two positions and 32 pixels, each lane's A operand
+// one 16-byte staged pixel (the 8 channels of one position) read from LDS,
+// its B operand 8 weights held in registers; a lane then holds 4
+// consecutive pixels of one channel per accumulator group, converted and
+// written to a [channel][pixel] LDS tile 8 bytes at a time, from which the
+// strip rows leave 256 bytes per channel.  A workgroup owns a 128-pixel
+// strip of one output frame and a band of rows; per output row a group of
+// four waves stages the nine input rows (3 taps x 3 rows) of the strip and
+// one pixel each side; wave w of a group computes output channels 32w ..
+// 32w + 31.
+//
+// Waves 0-3 (group 0) take the band's even rows, waves 4-7 (group 1) its odd
+// rows, each group with its own LDS halo buffers and output tile.  A row
+// takes two phases, each ended by a workgroup barrier:
+//   X: the MFMAs on the row's halo, the group's next row's halo (loaded
+//      during the previous Y) into the other buffer, the outputs into LDS;
+//   Y: the loads of the row after next, the output stores.
+// Group 1 runs one phase behind group 0, so that one group's stores drain
+// while the other group's MFMAs run.
 constexpr int kRgbInHaloW = 130;
 constexpr int kRgbInRowBytes = kRgbInHaloW * 16;
 constexpr int kRgbInBuf = 9 * kRgbInRowBytes;
 constexpr int kRgbInLoads = (9 * kRgbInHaloW + 255) / 256;
 constexpr int kRgbInOutPitch = 136;   // bf16 per staged output row (128 pixels + 8)
 constexpr int kRgbInOutBytes = 128 * kRgbInOutPitch * 2;
+constexpr int kRgbInGroupBytes = 2 * kRgbInBuf + kRgbInOutBytes;
 
-// 16-bit outputs whose rows allow 16-byte stores (VEC8) leave through a
-// [channel][pixel] LDS tile: each thread then stores 16-byte runs of 8 pixels
-// of one channel, a wave instruction the 256-byte strip rows of 4 channels.
+// 16-bit outputs whose rows allow 16-byte stores (VEC8) leave through the
+// group's LDS tile: each thread then stores 16-byte runs of 8 pixels of one
+// channel, a wave instruction the 256-byte strip rows of 4 channels.
+// Otherwise (fp32 outputs, rows not a multiple of 8 pixels) each lane stores
+// its accumulators element by element.
 template <int OK, bool VEC8>
-__global__ __launch_bounds__(256, 2) void conv3d_rgbin_kernel(ConvArgs a, int strips, int bands,
+__global__ __launch_bounds__(512, 1) void conv3d_rgbin_kernel(ConvArgs a, int strips, int bands,
                                                               int band_rows) {
-    constexpr int kLds = 2 * kRgbInBuf + 16 + (VEC8 ? kRgbInOutBytes : 0);
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLds];
-    uint16_t* const otile = (uint16_t*)(lds + 2 * kRgbInBuf + 16);
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kRgbInGroupBytes + 16];
+    const int tid = threadIdx.x;
+    const int gt = tid & 255;   // thread of the group
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = wave >> 2;
+    const int l32 = lane & 31;
+    const int khalf = lane >> 5;
+    uint8_t* const glds = lds + grp * kRgbInGroupBytes;
+    uint16_t* const otile = (uint16_t*)(glds + 2 * kRgbInBuf);
+    const uint8_t* const zchunk = lds + 2 * kRgbInGroupBytes;
     // the output as raw bytes (VEC8: below 2 GiB, checked by the launcher)
     const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
         a.out, (short)0, VEC8 ? (int)((long)a.cout * a.out_cstep * 2 < 0x7fffffffL
                                           ? (long)a.cout * a.out_cstep * 2 : 0x7fffffffL)
                               : 0,
         0x00020000);
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l32 = lane & 31;
-    const int khalf = lane >> 5;
     int bid = xcd_remap(blockIdx.x, gridDim.x);
     const int strip = bid % strips;
     bid /= strips;
@@ -1212,7 +1230,7 @@ __global__ __launch_bounds__(256, 2) void conv3d_rgbin_kernel(ConvArgs a, int st
     const int x0 = strip * 128;
     const int y0 = band * band_rows;
     const int y1 = min(a.Ho, y0 + band_rows);
-    const int co0 = 32 * wave;
+    const int co0 = 32 * (wave & 3);
     const bool active = co0 < a.cout;
 
     // weights: A operand rows co0 + l32, k = 16 ks + 8 khalf .. + 7 (window
@@ -1227,11 +1245,9 @@ __global__ __launch_bounds__(256, 2) void conv3d_rgbin_kernel(ConvArgs a, int st
             u = *reinterpret_cast<const uint4*>(a.packed + (long)(co0 + l32) * a.kp + k);
         wa[ks] = as_bf16x8(u);
     }
-    // accumulator register r of a lane is output channel 8(r/4) + 4 khalf + r%4
-    float bv[16];
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-        bv[r] = (active && a.bias) ? a.bias[co0 + 8 * (r >> 2) + 4 * khalf + (r & 3)] : 0.f;
+    // the output channel of a lane's accumulators
+    const int co = co0 + l32;
+    const float bv = (active && a.bias) ? a.bias[co] : 0.f;
     // B operand addresses (byte offsets in a halo buffer) of position
     // 2 ks + khalf for pixel column l32 of tile 0; tiles j add 512 bytes
     uint32_t boff[14];
@@ -1240,7 +1256,7 @@ __global__ __launch_bounds__(256, 2) void conv3d_rgbin_kernel(ConvArgs a, int st
         const int pos = min(2 * ks + khalf, 26);   // 27 reads the zero chunk instead
         boff[ks] = (uint32_t)((pos / 3) * kRgbInRowBytes + (l32 + pos % 3) * 16);
     }
-    if (tid == 0) *reinterpret_cast<uint4*>(lds + 2 * kRgbInBuf) = make_uint4(0, 0, 0, 0);
+    if (tid == 0) *reinterpret_cast<uint4*>(lds + 2 * kRgbInGroupBytes) = make_uint4(0, 0, 0, 0);
 
     const uint32_t pix = 16;
     const uint32_t frame_bytes = (uint32_t)(a.H * a.W) * pix;
@@ -1248,20 +1264,19 @@ __global__ __launch_bounds__(256, 2) void conv3d_rgbin_kernel(ConvArgs a, int st
     // Staged halo of output row y: item i = (tap * 3 + ky) * 130 + column.
     // Every load is issued, from a clamped address where the pixel lies in
     // the padding (store_rows zeroes those), so that no load sits under a
-    // branch: the wait before the halo is stored then leaves the loads issued
-    // after them, and the output stores, alone.  ok: one bit per load.
+    // branch.  ok: one bit per load.
     auto load_rows = [&](int y, uint4 (&v)[kRgbInLoads], uint32_t& ok) {
         ok = 0;
 #pragma unroll
         for (int k = 0; k < kRgbInLoads; ++k) {
-            const int i = min(tid + 256 * k, 9 * kRgbInHaloW - 1);
+            const int i = min(gt + 256 * k, 9 * kRgbInHaloW - 1);
             const int row = i / kRgbInHaloW, c = i - row * kRgbInHaloW;
             const int tap = row / 3, ky = row - 3 * tap;
             const int yy = y + ky - a.ph, xx = x0 - a.pw + c;
             const int fv = max(tbase + tap * a.dt, 0) - a.fbase;
             uint32_t off = (uint32_t)max(fv, 0) * frame_bytes +
                            (uint32_t)(min(max(yy, 0), a.H - 1) * a.W + min(max(xx, 0), a.W - 1)) * pix;
-            const bool in = tid + 256 * k < 9 * kRgbInHaloW && (unsigned)yy < (unsigned)a.H &&
+            const bool in = gt + 256 * k < 9 * kRgbInHaloW && (unsigned)yy < (unsigned)a.H &&
                             (unsigned)xx < (unsigned)a.W && fv >= 0 && off + 16 <= a.staged_bytes;
             off = min(off, a.staged_bytes - 16);
             v[k] = *reinterpret_cast<const uint4*>((const uint8_t*)a.staged + off);
@@ -1269,81 +1284,120 @@ __global__ __launch_bounds__(256, 2) void conv3d_rgbin_kernel(ConvArgs a, int st
         }
     };
     auto store_rows = [&](int buf, const uint4 (&v)[kRgbInLoads], uint32_t ok) {
-        // the loads are the last vector memory instructions issued: one wait
-        // for all of them on every path (the compiler's own waits would sit
-        // under the per-item branches and leave a wait-for-all at the loop
-        // head, behind the output stores)
-        __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+        // 16-byte output runs: every load and store is unconditional, so the
+        // compiler's waits for the loads leave the eight output stores that
+        // followed them in flight; otherwise one wait for all
+        if constexpr (!VEC8) __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
 #pragma unroll
         for (int k = 0; k < kRgbInLoads; ++k) {
-            const int i = tid + 256 * k;
+            const int i = gt + 256 * k;
             const uint32_t m = 0u - ((ok >> k) & 1);
             if (i < 9 * kRgbInHaloW)
-                *reinterpret_cast<uint4*>(lds + buf * kRgbInBuf + i * 16) =
+                *reinterpret_cast<uint4*>(glds + buf * kRgbInBuf + i * 16) =
                     make_uint4(v[k].x & m, v[k].y & m, v[k].z & m, v[k].w & m);
         }
     };
+    auto barrier = [] {
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
+    // the group's rows y0 + grp + 2i, i < rounds (past y1: no MFMAs or
+    // stores, the phases and barriers only)
+    const int rounds = (y1 - y0 + 1) / 2;
+    auto row_of = [&](int i) { return min(y0 + grp + 2 * i, y1 - 1); };
     uint4 pre[kRgbInLoads];
     uint32_t pre_ok = 0;
-    if (y0 < y1) {
-        load_rows(y0, pre, pre_ok);
+    if (rounds > 0) {
+        load_rows(row_of(0), pre, pre_ok);
         store_rows(0, pre, pre_ok);
+        load_rows(row_of(1), pre, pre_ok);
     }
     __builtin_amdgcn_s_waitcnt(0x0F70);   // weights and bias on every path
-    __syncthreads();
-    for (int y = y0; y < y1; ++y) {
-        const int buf = (y - y0) & 1;
-        // the next row's loads (the last row reloads its own)
-        load_rows(min(y + 1, y1 - 1), pre, pre_ok);
+    barrier();
+    if (grp == 1) barrier();
+    for (int i = 0; i < rounds; ++i) {
+        const int y = y0 + grp + 2 * i;
+        const bool valid = y < y1;
+        const int buf = i & 1;
+        // phase X
         f32x16 acc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j] = f32x16{};
-        if (active) {
-            const uint8_t* hb = lds + buf * kRgbInBuf;
-#pragma unroll
-            for (int ks = 0; ks < 14; ++ks) {
+        if (active && valid) {
+            // B fragments read one k-step ahead of their MFMAs: in phase X
+            // only one wave of each SIMD issues MFMAs, so nothing else hides
+            // the LDS latency
+            const uint8_t* hb = glds + buf * kRgbInBuf;
+            uint4 bf[2][4];
+            auto read_b = [&](int ks, uint4 (&b)[4]) {
                 // position 27 (lanes 32-63 of the last k-step) reads the zero chunk
                 const bool z = ks == 13 && khalf == 1;
-                const uint8_t* bp = z ? lds + 2 * kRgbInBuf : hb + boff[ks];
+                const uint8_t* bp = z ? zchunk : hb + boff[ks];
                 const int js = z ? 0 : 512;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const uint4 b = *reinterpret_cast<const uint4*>(bp + js * j);
-                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(wa[ks], as_bf16x8(b), acc[j],
-                                                                     0, 0, 0);
-                }
+                for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const uint4*>(bp + js * j);
+            };
+            read_b(0, bf[0]);
+#pragma unroll
+            for (int ks = 0; ks < 14; ++ks) {
+                __builtin_amdgcn_sched_barrier(0);
+                if (ks + 1 < 14) read_b(ks + 1, bf[(ks + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(bf[ks & 1][j]), wa[ks],
+                                                                     acc[j], 0, 0, 0);
             }
+            __builtin_amdgcn_sched_barrier(0);
         }
-        // the next row's halo goes to the other buffer before any output
-        // store is issued (its loads were issued first); after the last row
-        // the buffer, read by no one any more, takes that row again, so the
-        // wait for the loads is on every path
+        // the next row's halo into the other buffer (after the last row the
+        // buffer, read by no one any more, takes a row again)
         store_rows(buf ^ 1, pre, pre_ok);
-        if (active) {
-            // D[co][x]: register r of lane l is channel co0 + 8(r/4) + 4(l/32)
-            // + r%4 at pixel column l%32 of tile j
-            const long rowo = a.out_off + ((long)to * a.Ho + y) * a.Wo;
-            if constexpr (VEC8) {
+        // D[x][co]: register 4q + e of lane l is pixel 32j + 8q + 4(l/32) + e
+        // of tile j, channel co: four consecutive pixels, one 8-byte LDS write
+        if constexpr (VEC8) {
+            if (active && valid) {
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const int co = co0 + 8 * (r >> 2) + 4 * khalf + (r & 3);
-                        const float v = acc[j][r] + bv[r];
-                        otile[co * kRgbInOutPitch + 32 * j + l32] =
-                            OK == 2 ? __builtin_bit_cast(uint16_t, (_Float16)v) : f32_to_bf16(v);
+                    for (int q = 0; q < 4; ++q) {
+                        const float v0 = acc[j][4 * q] + bv, v1 = acc[j][4 * q + 1] + bv;
+                        const float v2 = acc[j][4 * q + 2] + bv, v3 = acc[j][4 * q + 3] + bv;
+                        const uint2 w = OK == 2 ? make_uint2(pack2_f16_rne(v0, v1), pack2_f16_rne(v2, v3))
+                                                : make_uint2(pack2_bf16_rne(v0, v1), pack2_bf16_rne(v2, v3));
+                        *reinterpret_cast<uint2*>(otile + co * kRgbInOutPitch + 32 * j + 8 * q + 4 * khalf) = w;
                     }
-            } else
+            }
+        }
+        barrier();
+        // phase Y: the loads of the row after next, then the stores
+        load_rows(row_of(i + 2), pre, pre_ok);
+        const long rowo = a.out_off + ((long)to * a.Ho + y) * a.Wo;
+        if constexpr (VEC8) {
+            // 16-byte runs through a buffer descriptor of the output: a run
+            // past the channel count or the row (x >= Wo; Wo % 8 == 0), or of
+            // a row past the band, takes an offset past the range and is
+            // dropped, so every thread issues all eight stores
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int x = x0 + 32 * j + l32;
-                if (x >= a.Wo) continue;
+            for (int k = 0; k < 8; ++k) {
+                const int c = gt + 256 * k;
+                const int co = c >> 4, x = x0 + 8 * (c & 15);
+                const uint4 v = *reinterpret_cast<const uint4*>(otile + co * kRgbInOutPitch + 8 * (c & 15));
+                const bool keep = valid && co < a.cout && x < a.Wo;
+                const uint32_t off = keep ? (uint32_t)(((long)co * a.out_cstep + rowo + x) * 2) : 0x80000000u;
+                __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, ro, off, 0, 2);
+            }
+        } else if (active && valid) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const int co = co0 + 8 * (r >> 2) + 4 * khalf + (r & 3);
+                    const int x = x0 + 32 * j + 8 * (r >> 2) + 4 * khalf + (r & 3);
+                    if (x >= a.Wo) continue;
                     const long idx = (long)co * a.out_cstep + rowo + x;
-                    const float v = acc[j][r] + bv[r];
+                    const float v = acc[j][r] + bv;
                     if (OK == 1)
                         ((uint16_t*)a.out)[idx] = f32_to_bf16(v);
                     else if (OK == 2)
@@ -1351,27 +1405,10 @@ __global__ __launch_bounds__(256, 2) void conv3d_rgbin_kernel(ConvArgs a, int st
                     else
                         ((float*)a.out)[idx] = v;
                 }
-            }
         }
-        if constexpr (VEC8) {
-            __syncthreads();   // the output tile is complete
-            // 16-byte runs through a buffer descriptor of the output: a run
-            // past the channel count or the row (x >= Wo; Wo % 8 == 0) takes
-            // an offset past the range and is dropped, so every thread
-            // issues all eight stores
-            const long rowo = a.out_off + ((long)to * a.Ho + y) * a.Wo;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int c = tid + 256 * i;
-                const int co = c >> 4, x = x0 + 8 * (c & 15);
-                const uint4 v = *reinterpret_cast<const uint4*>(otile + min(co, 127) * kRgbInOutPitch + 8 * (c & 15));
-                const bool keep = co < a.cout && x < a.Wo;
-                const uint32_t off = keep ? (uint32_t)(((long)co * a.out_cstep + rowo + x) * 2) : 0x80000000u;
-                __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, ro, off, 0, 0);
-            }
-        }
-        __syncthreads();
+        barrier();
     }
+    if (grp == 0) barrier();
 }
 
 bool conv3d_rgbin_ok(const Conv3dShape& s, int mem, int ho, int wo, int h, int w) {
@@ -1580,10 +1617,10 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
         a.part_split = (long)s.cout * m;
     }
     if (!a.part && conv3d_rgbin_ok(s, mem, ho, wo, height, width)) {
-        // one band of rows per workgroup, about two workgroups per CU
+        // one band of rows per workgroup, one workgroup per CU
         const int strips = (wo + 127) / 128;
         const int cus = 256;
-        const int bands = std::max(1, std::min(ho, 2 * cus / std::max(1, strips * frames_out)));
+        const int bands = std::max(1, std::min(ho, cus / std::max(1, strips * frames_out)));
         const int band_rows = (ho + bands - 1) / bands;
         const int nb = (ho + band_rows - 1) / band_rows;
         const long blocks = (long)strips * nb * frames_out;
@@ -1592,15 +1629,15 @@ hipError_t launch_conv3d(const Conv3dShape& s, const uint16_t* memory, int mem,
         const bool vec8 = ((uintptr_t)out % 16) == 0 && out_cstep % 8 == 0 && wo % 8 == 0 &&
                           a.out_off % 8 == 0 && (long)s.cout * out_cstep * 2 < 0x7fffffffL;
         if (out_kind == 1 && vec8)
-            conv3d_rgbin_kernel<1, true><<<(unsigned)blocks, 256, 0, stream>>>(a, strips, nb, band_rows);
+            conv3d_rgbin_kernel<1, true><<<(unsigned)blocks, 512, 0, stream>>>(a, strips, nb, band_rows);
         else if (out_kind == 2 && vec8)
-            conv3d_rgbin_kernel<2, true><<<(unsigned)blocks, 256, 0, stream>>>(a, strips, nb, band_rows);
+            conv3d_rgbin_kernel<2, true><<<(unsigned)blocks, 512, 0, stream>>>(a, strips, nb, band_rows);
         else if (out_kind == 1)
-            conv3d_rgbin_kernel<1, false><<<(unsigned)blocks, 256, 0, stream>>>(a, strips, nb, band_rows);
+            conv3d_rgbin_kernel<1, false><<<(unsigned)blocks, 512, 0, stream>>>(a, strips, nb, band_rows);
         else if (out_kind == 2)
-            conv3d_rgbin_kernel<2, false><<<(unsigned)blocks, 256, 0, stream>>>(a, strips, nb, band_rows);
+            conv3d_rgbin_kernel<2, false><<<(unsigned)blocks, 512, 0, stream>>>(a, strips, nb, band_rows);
         else
-            conv3d_rgbin_kernel<0, false><<<(unsigned)blocks, 256, 0, stream>>>(a, strips, nb, band_rows);
+            conv3d_rgbin_kernel<0, false><<<(unsigned)blocks, 512, 0, stream>>>(a, strips, nb, band_rows);
         return hipGetLastError();
     }
     if (halo) {
