@@ -467,6 +467,20 @@ def vae_conv3d(reps=5, cpu_threads=16, cpu=True):
                                   "written; a layer that cached its last two 128-channel input "
                                   "frames instead would also read those (1.42 GB per 4-frame "
                                   "bf16 slice in all)"})
+            elif cin <= 8:
+                # bound by its output: the RGB-input kernel writes cout
+                # channel planes per frame from a few input channels (the
+                # staged 8-channel pixels and the memory frames are read
+                # once more than the input planes, and counted here)
+                esz = 2 if dt == torch.bfloat16 else 4
+                nbytes = (cin * frames * h * w * esz + cout * frames * h * w * esz +
+                          (frames + 2) * h * w * 16)
+                out[key].update({
+                    "bound": "hbm", "algorithmic_bytes": int(nbytes),
+                    "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    "frac_hbm_peak": round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                    "bytes_note": "input planes and output planes once, the 8-channel staged "
+                                  "pixels (input and 2 memory frames) once"})
             del x, y
         del conv, wts
         torch.cuda.empty_cache()
