@@ -123,6 +123,10 @@ int DecomposedConv3D::create_pipeline(const ncnn::Option& /*opt*/)
 int DecomposedConv3D::create_pipeline_impl()
 {
     std::lock_guard<std::mutex> lock(mutex);
+    // the host-blob path runs on the default stream: own its scratch
+    const int sret = host_scratch.take(0);
+    if (sret != S2_OK)
+        return sret;
     int devices = 0;
     if (s2_device_count(&devices) != S2_OK || devices == 0 || weight_data.empty() ||
         config.groups != 1)
@@ -133,6 +137,7 @@ int DecomposedConv3D::create_pipeline_impl()
 int DecomposedConv3D::destroy_pipeline(const ncnn::Option& /*opt*/)
 {
     std::lock_guard<std::mutex> lock(mutex);
+    host_scratch.drop();
     packed_gpu.release();
     bias_gpu.release();
     workspace.release();

@@ -96,6 +96,7 @@ private:
     mutable int memory_frames;
     mutable int memory_w, memory_h;
     mutable size_t memory_elemsize;
+    StreamScratchRef host_scratch;   // the default stream's kernel scratch (split k ranges)
 };
 
 ncnn::Layer* decomposed_conv3d_layer_creator(void* userdata);
