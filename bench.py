@@ -1309,7 +1309,7 @@ def main():
         qf = gemm["qkv"]
         stages[mode + "_fused"] = {
             "rope_table_ms": round(accf["rope_table"], 4),
-            "qkv_prologue_broadcast_ms": round(accf["prologue"], 4),
+            "qkv_projection_ms": round(accf["prologue"], 4),
             "qkv_prologue_tflops": round(qf / (accf["prologue"] * 1e-3) / 1e12, 1),
             "attention_kernel_ms": round(accf["attention"], 4),
             "text_pool_ms": round(accf["text_pool"], 4),

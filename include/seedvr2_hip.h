@@ -218,8 +218,8 @@ S2_API int s2_awa_qkv_forward(const s2_awa_plan* plan, const void* x_video, cons
  * reference.  While enabled on the calling thread, every s2_awa_forward
  * records HIP events on its stream around its four kernels: RoPE table,
  * prologue (window gather, RMSNorm, RoPE), attention, text pool
- * (s2_awa_qkv_forward: RoPE table, QKV projection with the fused prologue
- * and the text broadcast, attention, text pool).
+ * (s2_awa_qkv_forward: RoPE table, QKV projection with the fused prologue,
+ * attention, text pool).
  * s2_awa_stage_times waits for the last such forward and returns the four
  * durations in milliseconds. */
 S2_API int s2_awa_stage_timing(int enable);

@@ -31,10 +31,6 @@ hipError_t launch_awa_qkv(const s2_awa_plan& plan, const uint16_t* x_video, cons
                           int k, const uint16_t* w, const float* bias, const float* norm,
                           const float2* rope, uint16_t* q, uint16_t* kk, uint16_t* vt,
                           hipStream_t stream);
-// Copies the staged text Q/K/V^T into every window segment of its sample and
-// zeroes the V^T padding keys of every segment.
-hipError_t launch_awa_text_broadcast(const s2_awa_plan& plan, uint16_t* q, uint16_t* k,
-                                     uint16_t* vt, hipStream_t stream);
 
 hipError_t launch_cast_f32_bf16(const float* src, uint16_t* dst, size_t n, hipStream_t stream);
 hipError_t launch_gelu(const void* x, void* y, size_t n, int kind, hipStream_t stream);

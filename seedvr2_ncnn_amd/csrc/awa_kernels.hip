@@ -115,7 +115,12 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
     const int tid = threadIdx.x;
     const int d0 = (tid % TPR) * 8;
     const int rot_width = pairs * 6;
-    const long head_rows = (long)head * seg_total + w.seg_off;
+    // a video chunk writes the window's segment, a text chunk (row0 >=
+    // n_video) its sample's staging rows; rows past lim are padding
+    const bool text_chunk = ch.row0 >= w.n_video;
+    const int lim = text_chunk ? w.seq : w.n_video;
+    const long base_row = text_chunk ? (long)w.ts_row - w.n_video : (long)w.seg_off;
+    const long head_rows = (long)head * seg_total + base_row;
 
     constexpr int NP = CHUNK / RPP;      // rows per thread
     // Every row's q, k and v loads are issued before any of them is used, so
@@ -145,11 +150,11 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
             const int d = d0 + 2 * pp;
             const int axis = d / (2 * pairs > 0 ? 2 * pairs : 1);
             const int pair = (d - axis * 2 * pairs) >> 1;
-            const bool rot = d < rot_width && r < w.seq;
+            const bool rot = d < rot_width && r < lim;
             cs[pass][pp] = rot ? rope[pos[axis < 3 ? axis : 0] * pairs + pair] : make_float2(1.f, 0.f);
         }
         const long src = video ? tc.src : (long)w.text_off + tt;
-        const bool ok = r < w.seq;
+        const bool ok = r < lim;
         const TIn* bq = video || !ok ? vq : tq;
         const TIn* bk = video || !ok ? vk : tk;
         const TIn* bv = video || !ok ? vv : tv;
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
         const int rl = pass * RPP + tid / TPR;   // row within the chunk
         const int r = ch.row0 + rl;               // row within the window sequence
         uint16_t qb[8], kb[8], vb[8];
-        if (r < w.seq) {
+        if (r < lim) {
             const bool video = r < w.n_video;
             float q[8], k[8], v[8];
             rq[pass].to_float(q);
@@ -219,8 +224,7 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
                 }
             }
         } else {
-            // padding rows: zero keys are masked in attention, zero values keep
-            // p * v finite
+            // padding rows (the attention masks them as keys in any case)
 #pragma unroll
             for (int i = 0; i < 8; ++i) qb[i] = kb[i] = vb[i] = 0;
         }
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(256) void awa_prologue_kernel(
         const int c8 = idx - d * (CHUNK / 8);
         const uint4 val =
             *reinterpret_cast<const uint4*>(&vt_lds[d * VTP + (((c8 ^ (d >> 3)) & 7) << 3)]);
-        *reinterpret_cast<uint4*>(vt_out + ((long)head * D + d) * seg_total + w.seg_off + ch.row0 +
+        *reinterpret_cast<uint4*>(vt_out + ((long)head * D + d) * seg_total + base_row + ch.row0 +
                                   c8 * 8) = val;
     }
 }
@@ -343,9 +347,12 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     const int wave = tid >> 6;
     const int l32 = lane & 31;
     const int g = lane >> 5;
-    const long head_rows = (long)it.head * seg_total + w.seg_off;
-    const int padded = (w.seq + kSegAlign - 1) / kSegAlign * kSegAlign;
-    const int nkt = (w.seq + KT - 1) / KT;
+    // The window's sequence is its video rows (segment rows seg_off ..) then
+    // its sample's text rows (staging rows ts_row ..), each padded to whole
+    // key tiles: nvt video tiles, then the text tiles.
+    const long head_k = (long)it.head * seg_total;   // the head's row 0 of Q and K
+    const int nvt = (w.n_video + KT - 1) / KT;
+    const int nkt = nvt + (w.text_len + KT - 1) / KT;
 
     // this thread's norm weights for the score bound below (their latency
     // overlaps that of the Q loads and the first DMAs)
@@ -359,7 +366,8 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
     bf16x8 qf[NKK];
     {
         const bool valid = qrow < w.seq;
-        const uint16_t* qp = q_in + (head_rows + qrow) * D + 8 * g;
+        const long row = qrow < w.n_video ? (long)w.seg_off + qrow : (long)w.ts_row + qrow - w.n_video;
+        const uint16_t* qp = q_in + (head_k + row) * D + 8 * g;
 #pragma unroll
         for (int kk = 0; kk < NKK; ++kk) {
             uint4 raw = make_uint4(0, 0, 0, 0);
@@ -368,11 +376,10 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
         }
     }
 
-    // DMA sources: this (window, head)'s K rows [padded][D] and V^T rows
-    // [D][seg_total] starting at the window's segment.
-    const i32x4 rk = buffer_rsrc(k_in + head_rows * D, (uint32_t)(padded * D * 2));
-    const i32x4 rv = buffer_rsrc(vt_in + (long)it.head * D * seg_total + w.seg_off,
-                                 (uint32_t)(((long)(D - 1) * seg_total + padded) * 2));
+    // DMA sources: the head's K rows [seg_total][D] and V^T rows
+    // [D][seg_total]; a tile's first key row goes in the scalar offset.
+    const i32x4 rk = buffer_rsrc(k_in + head_k * D, (uint32_t)(seg_total * D * 2));
+    const i32x4 rv = buffer_rsrc(vt_in + head_k * D, (uint32_t)(seg_total * D * 2));
     uint32_t koff[KI_W], voff[VI_W];
 #pragma unroll
     for (int j = 0; j < KI_W; ++j) {
@@ -387,16 +394,25 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
         voff[j] = (uint32_t)(((long)d * seg_total + c * 8) * 2);
     }
     const uint32_t lds_base = (uint32_t)(uintptr_t)lds;
+    // first key row of tile kt, and the number of its keys that are real
+    // (KT or more but in the last tile of either part)
+    auto tile_row = [&](int kt) {
+        return kt < nvt ? w.seg_off + kt * KT : w.ts_row + (kt - nvt) * KT;
+    };
+    auto tile_keys = [&](int kt) {
+        return kt < nvt ? w.n_video - kt * KT : w.text_len - (kt - nvt) * KT;
+    };
     auto issue = [&](int stage, int kt) {
         const uint32_t st = lds_base + stage * SB;
+        const uint32_t key0 = (uint32_t)__builtin_amdgcn_readfirstlane(tile_row(kt));
 #pragma unroll
         for (int j = 0; j < KI_W; ++j)
             lds_dma16(rk, __builtin_amdgcn_readfirstlane(st + (wave * KI_W + j) * 1024), koff[j],
-                      (uint32_t)(kt * KT * D * 2));
+                      key0 * (D * 2));
 #pragma unroll
         for (int j = 0; j < VI_W; ++j)
             lds_dma16(rv, __builtin_amdgcn_readfirstlane(st + KB + (wave * VI_W + j) * 1024),
-                      voff[j], (uint32_t)(kt * KT * 2));
+                      voff[j], key0 * 2);
     };
 
     f32x16 o[NDT];
@@ -481,6 +497,32 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
             __syncthreads();   // tile kt visible to all waves; tile kt-1 no longer read
             if (kt + 2 < nkt) issue((u + 2) % STAGES, kt + 2);
             const uint8_t* st = lds + u * SB;
+            // The last tile of either part holds nkeys < KT real keys; the
+            // rest of its rows are padding with whatever the workspace holds
+            // there.  Their scores are masked below, and their V^T entries
+            // are zeroed here (probability 0 times a NaN would reach the
+            // sum): the tile's D x 4 key chunks of 8, one or two a thread, by
+            // all waves, active or not, before one more barrier.
+            const int nkeys = tile_keys(kt);
+            const bool partial = nkeys < KT;
+            if (partial) {
+                // an opaque copy of the thread index: the chunk addresses stay
+                // in this branch instead of being hoisted, per stage, into
+                // registers the tile loop needs
+                int t0 = tid;
+                asm volatile("" : "+v"(t0));
+#pragma unroll
+                for (int idx = t0; idx < D * 4; idx += 256) {
+                    const int r = idx >> 2, c = idx & 3;
+                    uint8_t* chunk = lds + u * SB + KB + r * (KT * 2) + ((c ^ vt_swizzle(r)) * 16);
+                    if (8 * c >= nkeys) {
+                        *(uint4*)chunk = make_uint4(0, 0, 0, 0);
+                    } else if (8 * c + 8 > nkeys) {
+                        for (int e = nkeys - 8 * c; e < 8; ++e) ((uint16_t*)chunk)[e] = 0;
+                    }
+                }
+                __syncthreads();
+            }
 
             // S^T = K Q^T
             // a wave whose 32 query rows all lie past the sequence (the last
@@ -509,14 +551,13 @@ __global__ __launch_bounds__(256, 3) void awa_attention_kernel(
                 else
                     s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kk], qf[kk], s, 0, 0, 0);
             }
-            // keys past the window's sequence (only in the last tile) are masked
-            const int key_base = kt * KT;
-            if (key_base + KT > w.seq) {
+            // scores of the padding keys are masked
+            if (partial) {
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     // register i of lane group g holds key 16*(i/8) + 8g + (i%8)
-                    const int key = key_base + 16 * (i >> 3) + 8 * g + (i & 7);
-                    if (key >= w.seq) s[i] = -INFINITY;
+                    const int key = 16 * (i >> 3) + 8 * g + (i & 7);
+                    if (key >= nkeys) s[i] = -INFINITY;
                 }
             }
             float alpha = 1.f;
@@ -644,77 +685,6 @@ __global__ void awa_text_pool_kernel(const SampleMeta* __restrict__ samples,
 }
 
 // ---------------------------------------------------------------------------
-// Text broadcast of the fused QKV path: one workgroup per (window, head)
-// copies the sample's text Q and K rows and V^T keys from the staging rows
-// (where the fused projection wrote each text token once) to the rows after
-// the window's video tokens, which is where the window sequence
-// [video tokens] ++ [text tokens] (:886-927) expects them, and zeroes the
-// V^T keys of the segment's padding (zero values keep p * v finite for the
-// masked keys).
-constexpr int kBroadcastSplit = 4;   // workgroups per (window, head)
-
-template <int D>
-__global__ __launch_bounds__(256) void awa_text_broadcast_kernel(const WinMeta* __restrict__ wins,
-                                                                 long seg_total, long seg_text,
-                                                                 uint16_t* __restrict__ q,
-                                                                 uint16_t* __restrict__ k,
-                                                                 uint16_t* __restrict__ vt) {
-    constexpr int CPR = D / 8;                    // 16-byte chunks per row
-    constexpr int DC = D / kBroadcastSplit;       // V^T channels of this workgroup
-    constexpr int U = DC / 4;                     // channels per thread and pass
-    const WinMeta w = wins[blockIdx.x];
-    const int head = blockIdx.y;
-    const int part = blockIdx.z;
-    const int tid = threadIdx.x;
-    const long hq = (long)head * seg_total;
-    // Q and K: this workgroup's share of the text rows' 16-byte chunks,
-    // every load issued before any store
-    const int nq = w.text_len * CPR;
-    const int q0 = nq * part / kBroadcastSplit, q1 = nq * (part + 1) / kBroadcastSplit;
-    for (int base = q0; base < q1; base += 256 * 2) {
-        uint4 vq[2], vk[2];
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int idx = base + u * 256 + tid;
-            if (idx < q1) {
-                const int t = idx / CPR;
-                const long src = (hq + seg_text + w.text_off + t) * D + (idx - t * CPR) * 8;
-                vq[u] = *reinterpret_cast<const uint4*>(q + src);
-                vk[u] = *reinterpret_cast<const uint4*>(k + src);
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const int idx = base + u * 256 + tid;
-            if (idx < q1) {
-                const int t = idx / CPR;
-                const long dst = (hq + w.seg_off + w.n_video + t) * D + (idx - t * CPR) * 8;
-                *reinterpret_cast<uint4*>(q + dst) = vq[u];
-                *reinterpret_cast<uint4*>(k + dst) = vk[u];
-            }
-        }
-    }
-    // V^T keys [n_video, padded) of this workgroup's channels: the text
-    // keys, then zeros; lanes along the keys, U channels per thread in flight
-    const int nk = (w.seq + kSegAlign - 1) / kSegAlign * kSegAlign - w.n_video;
-    const int dbase = part * DC + (tid >> 6);
-    for (int j0 = 0; j0 < nk; j0 += 64) {
-        const int j = j0 + (tid & 63);
-        uint16_t v[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint16_t* row = vt + ((long)head * D + dbase + 4 * u) * seg_total;
-            v[u] = (j < w.text_len) ? row[seg_text + w.text_off + j] : (uint16_t)0;
-        }
-        if (j < nk) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-                vt[((long)head * D + dbase + 4 * u) * seg_total + w.seg_off + w.n_video + j] = v[u];
-        }
-    }
-}
-
-// ---------------------------------------------------------------------------
 // Plan tables (AdaptiveWindowPlan's per-token arrays) from the same index math.
 __global__ void awa_plan_tables_kernel(const WinMeta* __restrict__ wins, int* __restrict__ indices,
                                        int* __restrict__ inverse, int* __restrict__ positions) {
@@ -814,20 +784,6 @@ hipError_t launch_awa_text_pool(const s2_awa_plan& plan, const float* partial, v
     return hipGetLastError();
 }
 
-hipError_t launch_awa_text_broadcast(const s2_awa_plan& plan, uint16_t* q, uint16_t* k,
-                                     uint16_t* vt, hipStream_t stream) {
-    if (plan.num_windows == 0) return hipSuccess;
-    dim3 grid(plan.num_windows, plan.config.heads, kBroadcastSplit);
-    if (plan.config.head_dim == 128)
-        awa_text_broadcast_kernel<128><<<grid, 256, 0, stream>>>(plan.d_wins, plan.seg_total,
-                                                                 plan.seg_text, q, k, vt);
-    else if (plan.config.head_dim == 64)
-        awa_text_broadcast_kernel<64><<<grid, 256, 0, stream>>>(plan.d_wins, plan.seg_total,
-                                                                plan.seg_text, q, k, vt);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
-}
 
 hipError_t launch_awa_plan_tables(const s2_awa_plan& plan, int* indices, int* inverse,
                                   int* positions, hipStream_t stream) {

@@ -32,8 +32,10 @@ struct WinMeta {
     int tpart_off;        // first row of this window's text partials
     int grow_off;         // first row of this window's video tokens in the row space of
                           // the fused QKV projection (even; see s2_awa_plan::qkv_text_row)
+    int ts_row;           // first workspace row of the sample's text tokens (staged once
+                          // per sample, a multiple of kSegAlign)
 };
-static_assert(sizeof(WinMeta) == 72, "WinMeta layout");
+static_assert(sizeof(WinMeta) == 76, "WinMeta layout");
 
 // Per-sample record for the text mean-pool.
 struct SampleMeta {
@@ -52,7 +54,8 @@ struct AttnItem {
     int pad_;
 };
 
-// Segment rows are padded to this multiple so every key tile is whole.
+// A window's segment (its video rows) and a sample's text staging rows are
+// padded to this multiple: whole 32-key tiles and 64-row prologue chunks.
 constexpr int kSegAlign = 64;
 
 // Entries of slack after a cos/sin table: a reader may fetch the three
@@ -74,7 +77,9 @@ struct QkvRow {
     int pos2;    // position axis 2 | kind << 16
 };
 
-// One prologue work item: 64 rows of one window's sequence.
+// One prologue work item: 64 rows of one window's sequence -- video rows of
+// the window (row0 < n_video), or text rows of its sample (row0 >= n_video,
+// written once per sample to the staging rows).
 struct ChunkRef {
     int window;
     int row0;
@@ -112,13 +117,14 @@ struct s2_awa_plan {
     int max_window_tokens = 0;
     int rope_positions = 0;                 // rows of the cos/sin table
     long seg_total = 0;                     // row pitch of the Q/K/V^T workspace: the padded
-                                            // window segments, then text staging rows
-    long seg_text = 0;                      // first text staging row (the fused QKV path
-                                            // writes each text token's Q/K/V^T there once)
+                                            // window segments (video rows), then the
+                                            // samples' padded text staging rows
+    long seg_text = 0;                      // first text staging row (each text token's
+                                            // Q/K/V^T is written there once)
     // Row space of the fused QKV projection (s2_awa_qkv_forward): the video
     // tokens in window order, each window's run starting at an even row
-    // (WinMeta::grow_off), then the text tokens from qkv_text_row (a multiple
-    // of 8) to qkv_rows.
+    // (WinMeta::grow_off), then from qkv_text_row (a multiple of 8) to
+    // qkv_rows the text tokens, each sample's run starting at an even row.
     int qkv_text_row = 0;
     int qkv_rows = 0;
     s2::QkvRow* d_qkv_rows = nullptr;       // [qkv_rows rounded up to 256]

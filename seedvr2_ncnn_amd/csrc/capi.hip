@@ -436,7 +436,9 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
         m.tpart_off = tpart;
         m.grow_off = grow;
         grow += (s.token_count + 1) / 2 * 2;
-        const int padded = (m.seq + s2::kSegAlign - 1) / s2::kSegAlign * s2::kSegAlign;
+        // the segment holds the window's video rows only: each sample's text
+        // rows are staged once, after all segments
+        const int padded = (m.n_video + s2::kSegAlign - 1) / s2::kSegAlign * s2::kSegAlign;
         for (int r = 0; r < padded; r += s2::kSegAlign) chunks.push_back(s2::ChunkRef{i, r});
         seg += padded;
         tpart += m.text_len;
@@ -445,11 +447,33 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
         rope_pos = std::max(rope_pos, m.text_len);
         plan->max_window_tokens = std::max(plan->max_window_tokens, m.n_video);
     }
-    // text staging rows of the fused QKV path after the window segments
+    // Text staging rows after the window segments: sample b's text at ts_row
+    // (padded to kSegAlign), written once by the prologue's text chunks (on
+    // the sample's first window) or by the fused QKV projection; the
+    // attention reads every window's text keys and queries there.
     plan->seg_text = seg;
-    plan->seg_total = seg + (plan->text_tokens + s2::kSegAlign - 1) / s2::kSegAlign * s2::kSegAlign;
+    std::vector<int> ts_row(batch), tr_off(batch);
+    int tr = 0;   // text rows of the fused QKV row space, each sample's run even
+    for (int b = 0; b < batch; ++b) {
+        ts_row[b] = (int)seg;
+        tr_off[b] = tr;
+        const int padded = (text_lengths[b] + s2::kSegAlign - 1) / s2::kSegAlign * s2::kSegAlign;
+        const s2::WinMeta& fw = plan->win_meta[first_win[b]];
+        for (int r = 0; r < padded; r += s2::kSegAlign)
+            chunks.push_back(s2::ChunkRef{first_win[b], fw.n_video + r});
+        seg += padded;
+        tr += (text_lengths[b] + 1) / 2 * 2;
+    }
+    for (s2::WinMeta& m : plan->win_meta) m.ts_row = ts_row[m.sample];
+    plan->seg_total = std::max<long>(seg, 1);
+    // the attention addresses a head's Q/K rows and V^T keys through one
+    // buffer descriptor with 32-bit offsets
+    if (plan->seg_total * config->head_dim * 2 > 0xffffffffL) {
+        delete plan;
+        return fail(S2_ERR_INVALID, "attention workspace rows beyond 32-bit buffer offsets");
+    }
     plan->qkv_text_row = (grow + 7) / 8 * 8;
-    plan->qkv_rows = plan->qkv_text_row + plan->text_tokens;
+    plan->qkv_rows = plan->qkv_text_row + tr;
     plan->text_partial_rows = tpart;
     plan->rope_positions = rope_pos;
     plan->num_chunks = (int)chunks.size();
@@ -514,15 +538,18 @@ int s2_awa_plan_create(const s2_awa_config* config, const int* video_shapes,
             }
         }
     }
-    for (int R = plan->qkv_text_row; R < qkv_tiles * 256; ++R) {
-        const int t = R - plan->qkv_text_row;
-        s2::QkvRow& q = qrows[R];
-        q.dest = (int)plan->seg_text + t;
-        if (t < plan->text_tokens) {
-            const int tt = t - text_off[text_sample[t]];
-            q.src = t;
-            q.pos01 = tt | (tt << 16);
-            q.pos2 = tt | (2 << 16);
+    // text runs: sample b's tokens from qkv_text_row + tr_off[b] (even), to
+    // its staging rows; a run's gap row keeps the staging row that follows
+    for (int b = 0; b < batch; ++b) {
+        const int run = (text_lengths[b] + 1) / 2 * 2;
+        for (int tt = 0; tt < run; ++tt) {
+            s2::QkvRow& q = qrows[plan->qkv_text_row + tr_off[b] + tt];
+            q.dest = ts_row[b] + tt;
+            if (tt < text_lengths[b]) {
+                q.src = text_off[b] + tt;
+                q.pos01 = tt | (tt << 16);
+                q.pos2 = tt | (2 << 16);
+            }
         }
     }
 
@@ -738,7 +765,6 @@ int s2_awa_qkv_forward(const s2_awa_plan* plan, const void* x_video, const void*
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[1], s));
     S2_HIP(s2::launch_awa_qkv(*plan, (const uint16_t*)x_video, (const uint16_t*)x_text, hidden,
                               qkv_weight, qkv_bias, norm_weights, rope, q, k, vt, s));
-    S2_HIP(s2::launch_awa_text_broadcast(*plan, q, k, vt, s));
     if (tm.on) S2_HIP(hipEventRecord(tm.ev[2], s));
     S2_HIP(s2::launch_awa_attention(*plan, q, k, vt, out_video, (int)out_dtype, tpart,
                                     norm_weights, s));
