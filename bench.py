@@ -57,13 +57,12 @@ def attention_flops(shifted):
 
 def prologue_bytes(shifted, hidden=HIDDEN):
     """Algorithmic HBM bytes of the attention prologue: read the bf16 q, k, v
-    of every video and text token once, write the windowed bf16 Q, K and V^T
-    of every video token once and of the text tokens once per window.  The
-    window index math reads no tables."""
-    from seedvr2_ncnn_amd import capi
-    wins, _, _ = capi.plan_windows([VIDEO_SHAPE], TARGET, shifted)
+    of every video and text token once and write the windowed bf16 Q, K and
+    V^T of every token once (a window's video rows to its segment, a sample's
+    text rows to its one staging copy).  The window index math reads no
+    tables; the same for both window modes."""
     lv = VIDEO_SHAPE[0] * VIDEO_SHAPE[1] * VIDEO_SHAPE[2]
-    return (lv + TEXT_TOKENS) * 3 * hidden * 2 + (lv + len(wins) * TEXT_TOKENS) * 3 * hidden * 2
+    return 2 * (lv + TEXT_TOKENS) * 3 * hidden * 2
 
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "shared_linear_mlp_up_720p_video_traffic.md")
