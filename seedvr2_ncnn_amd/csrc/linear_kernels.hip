@@ -393,6 +393,32 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         return e;
     };
 
+    // acc + bias (and the activation) of this wave's rows of the tile, as
+    // 16-bit values in the LDS staging rows (pitch EP); the 16-bit outputs
+    // of the plain epilogue
+    auto stage_own_rows = [&]() {
+        if constexpr (YK != 0 && AWA == 0 && ACT != S2_ACT_SWIGLU) {
+            const EpiIds ei = epi_ids();
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int cl = ei.wn * 64 + 32 * j + ei.l32;
+                const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        float v = acc[i][j][r] + bv;
+                        if (ACT == S2_ACT_GELU) v = gelu(v);
+                        const int rl = ei.wm * 128 + 32 * i + 8 * (r >> 2) + 4 * ei.g + (r & 3);
+                        if (YK == 2)
+                            *(_Float16*)(lds + rl * EP + cl * 2) = (_Float16)v;
+                        else
+                            *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
+                    }
+            }
+        }
+    };
+
     // acc = sum over 64-k iterations [kb, ke) of the current tile.
     //
     // Ping-pong main loop.  The two waves of each SIMD (wave w and w + 4:
@@ -411,7 +437,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     //             read step s               wait for its DMA
     //   group 1   MFMAs of step s - 1       read step s, wait for its DMA of
     //                                       step s + 1, DMA B of step s + 2
-    auto mainloop = [&](int kb, int ke) {
+    auto mainloop = [&](int kb, int ke, bool early) {
         const int grp = wave >> 2;
         const int wq = wave & 3;
         // plain: the tile's rows of each stream; fused QKV: whole streams,
@@ -531,7 +557,9 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             if (grp == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // A of step s + 1
             barrier();
         }
-        if (grp == 0) barrier();
+        // group 0's barrier matching group 1's last MFMA phase; with an early
+        // epilogue group 0 stages its rows first (epilogue)
+        if (grp == 0 && !early) barrier();
     };
 
     // Fused QKV epilogue.  The tile's 256 columns lie in one of q, k, v
@@ -889,7 +917,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
     };
 
     // y tile = act(acc + bias)
-    auto epilogue = [&]() {
+    auto epilogue = [&](bool early) {
         if constexpr (AWA != 0) {
             awa_epilogue();
             return;
@@ -900,24 +928,67 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         }
         const EpiIds ei = epi_ids();
         if (YK && (n & 7) == 0) {
-            __syncthreads();   // every wave is done reading the last stage
+            const int pitch = ny * 2;
+            const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+                (char*)y0 + (long)row0 * pitch, (short)0, max(min(m0 - row0, BM), 0) * pitch,
+                kRawBufferFormat);
+            const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+                (char*)y1 + (long)(row0 - mv) * pitch, (short)0,
+                row0 + BM > mv ? min(mv + m1 - row0, BM) * pitch : 0, kRawBufferFormat);
+            if constexpr (RES == 0) {
+                // Thread t of group g (waves 4g .. 4g + 3) stores 16-byte
+                // chunk t%32 of rows 128g + t/32 + 8c, all sixteen LDS reads
+                // before the first store; a wave's two rows lie in one 8-row
+                // group, hence in one stream.
+                //
+                // Early schedule (a whole tile): group 1's last MFMA phase
+                // reads no stage (its fragments are in registers, no DMA is
+                // in flight), so group 0 stages its rows 0-127 meanwhile and
+                // meets group 1 at the end of that phase (mainloop left that
+                // barrier to here); then group 0 stores while group 1 stages
+                // rows 128-255, and group 1 stores last.  Otherwise both
+                // groups stage, then store.  The barriers are plain s_barrier:
+                // group 0's stores need no wait before group 1 goes on.
+                const int g0 = ei.wm;
+                const int t = ei.tid - 256 * g0;
+                const int ch = t & 31;
+                const int sub = t >> 5;
+                const int lw = ei.wn;   // wave within the group
+                const uint32_t drop = col0 + ch * 8 < n ? 0u : 0x80000000u;
+                auto store_rows = [&]() {
+                    u32x4 sv[16];
 #pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int cl = ei.wn * 64 + 32 * j + ei.l32;
-                const float bv = (bias && col0 + cl < n) ? bias[col0 + cl] : 0.f;
+                    for (int c = 0; c < 16; ++c)
+                        sv[c] = *(const u32x4*)(lds + (128 * g0 + 8 * c + sub) * EP + ch * 16);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        float v = acc[i][j][r] + bv;
-                        if (ACT == S2_ACT_GELU) v = gelu(v);
-                        const int rl = ei.wm * 128 + 32 * i + 8 * (r >> 2) + 4 * ei.g + (r & 3);
-                        if (YK == 2)
-                            *(_Float16*)(lds + rl * EP + cl * 2) = (_Float16)v;
+                    for (int c = 0; c < 16; ++c) {
+                        const int rl = 128 * g0 + 8 * c + sub;
+                        const uint32_t off = (uint32_t)(rl * pitch + col0 * 2 + ch * 16) | drop;
+                        if (row0 + 128 * g0 + 8 * c + 2 * lw < mv)
+                            __builtin_amdgcn_raw_buffer_store_b128(sv[c], rs0, off, 0, kNonTemporal);
                         else
-                            *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
+                            __builtin_amdgcn_raw_buffer_store_b128(sv[c], rs1, off, 0, kNonTemporal);
                     }
+                };
+                auto plain_barrier = [] {
+                    __builtin_amdgcn_sched_barrier(0);
+                    asm volatile("s_barrier" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                };
+                const bool first_half = early && g0 == 0;
+                if (!early) plain_barrier();   // every wave is done reading the last stage
+                stage_own_rows();
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                if (first_half) {
+                    plain_barrier();
+                    store_rows();
+                }
+                plain_barrier();
+                if (!first_half) store_rows();
+                return;
             }
+            __syncthreads();   // every wave is done reading the last stage
+            stage_own_rows();
             __syncthreads();
             // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows
             // t/32 + 16c, all sixteen LDS reads issued before the first store.
@@ -931,13 +1002,6 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             const int ch = ei.tid & 31;
             const int sub = ei.tid >> 5;
             const int wv = ei.wm * 4 + ei.wn;
-            const int pitch = ny * 2;
-            const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
-                (char*)y0 + (long)row0 * pitch, (short)0, max(min(m0 - row0, BM), 0) * pitch,
-                kRawBufferFormat);
-            const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
-                (char*)y1 + (long)(row0 - mv) * pitch, (short)0,
-                row0 + BM > mv ? min(mv + m1 - row0, BM) * pitch : 0, kRawBufferFormat);
             // offsets are below 2^31 (the launcher checks 256 rows of output):
             // bit 31 takes a chunk past n out of every range
             const uint32_t drop = col0 + ch * 8 < n ? 0u : 0x80000000u;
@@ -1053,8 +1117,13 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
             build_rows();
             __syncthreads();
         }
-        mainloop(kb, ke);
         bool finish = kb == 0 && ke == nk;
+        // the plain 16-bit epilogue of a whole tile without an activation runs
+        // early (see epilogue); with GELU the early schedule would serialise
+        // the two groups' VALU work, which otherwise shares the SIMDs
+        const bool early = AWA == 0 && RES == 0 && ACT == S2_ACT_NONE && YK != 0 &&
+                           (n & 7) == 0 && finish;
+        mainloop(kb, ke, early);
         if (!finish) {
             // slot layout: float4 c (4 accumulator registers) of thread tid
             // at byte (c * 512 + tid) * 16; the chunk index goes in soffset
@@ -1135,7 +1204,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 finish = true;
             }
         }
-        if (finish) epilogue();
+        if (finish) epilogue(early);
         // every memory operation of this segment is complete: a real
         // s_waitcnt (not asm) lets the compiler's wait insertion know, so
         // it adds no vmcnt wait of its own inside the next main loop
