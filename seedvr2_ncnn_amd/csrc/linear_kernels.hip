@@ -928,18 +928,18 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
         }
         const EpiIds ei = epi_ids();
         if (YK && (n & 7) == 0) {
-            const int pitch = ny * 2;
-            const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
-                (char*)y0 + (long)row0 * pitch, (short)0, max(min(m0 - row0, BM), 0) * pitch,
-                kRawBufferFormat);
-            const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
-                (char*)y1 + (long)(row0 - mv) * pitch, (short)0,
-                row0 + BM > mv ? min(mv + m1 - row0, BM) * pitch : 0, kRawBufferFormat);
             if constexpr (RES == 0) {
                 // Thread t of group g (waves 4g .. 4g + 3) stores 16-byte
                 // chunk t%32 of rows 128g + t/32 + 8c, all sixteen LDS reads
-                // before the first store; a wave's two rows lie in one 8-row
-                // group, hence in one stream.
+                // before the first store.  Each stream's rows of the tile go
+                // through a buffer descriptor bounded by those rows, so the
+                // range check drops a row past its stream, and a chunk past
+                // n (an offset with bit 31 set: offsets are below 2^31, the
+                // launcher checks 256 rows of output), without a branch per
+                // store; a wave's two rows lie in one 8-row group, hence in
+                // one stream.  The output is not read again by this launch:
+                // the stores are non-temporal, leaving the L2 to the operand
+                // tiles.
                 //
                 // Early schedule (a whole tile): group 1's last MFMA phase
                 // reads no stage (its fragments are in registers, no DMA is
@@ -949,6 +949,13 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 // rows 128-255, and group 1 stores last.  Otherwise both
                 // groups stage, then store.  The barriers are plain s_barrier:
                 // group 0's stores need no wait before group 1 goes on.
+                const int pitch = ny * 2;
+                const __amdgpu_buffer_rsrc_t rs0 = __builtin_amdgcn_make_buffer_rsrc(
+                    (char*)y0 + (long)row0 * pitch, (short)0, max(min(m0 - row0, BM), 0) * pitch,
+                    kRawBufferFormat);
+                const __amdgpu_buffer_rsrc_t rs1 = __builtin_amdgcn_make_buffer_rsrc(
+                    (char*)y1 + (long)(row0 - mv) * pitch, (short)0,
+                    row0 + BM > mv ? min(mv + m1 - row0, BM) * pitch : 0, kRawBufferFormat);
                 const int g0 = ei.wm;
                 const int t = ei.tid - 256 * g0;
                 const int ch = t & 31;
@@ -985,40 +992,19 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                 }
                 plain_barrier();
                 if (!first_half) store_rows();
-                return;
-            }
-            __syncthreads();   // every wave is done reading the last stage
-            stage_own_rows();
-            __syncthreads();
-            // 256 rows x 512 bytes: thread t stores 16-byte chunk t%32 of rows
-            // t/32 + 16c, all sixteen LDS reads issued before the first store.
-            // Each stream's rows of the tile go through a buffer descriptor
-            // bounded by those rows, so the range check drops a row past its
-            // stream, and a chunk past n (given an offset past every bound),
-            // without a branch per store.  A wave's two rows lie in one 8-row
-            // group, hence in one stream.  The output is not read again by
-            // this launch: the stores are non-temporal, leaving the L2 to the
-            // operand tiles.
-            const int ch = ei.tid & 31;
-            const int sub = ei.tid >> 5;
-            const int wv = ei.wm * 4 + ei.wn;
-            // offsets are below 2^31 (the launcher checks 256 rows of output):
-            // bit 31 takes a chunk past n out of every range
-            const uint32_t drop = col0 + ch * 8 < n ? 0u : 0x80000000u;
-            u32x4 sv[16];
+            } else {
+                // the residual epilogue: thread t holds 16-byte chunk t%32 of
+                // tile rows t/32 + 16c
+                __syncthreads();   // every wave is done reading the last stage
+                stage_own_rows();
+                __syncthreads();
+                const int ch = ei.tid & 31;
+                const int sub = ei.tid >> 5;
+                u32x4 sv[16];
 #pragma unroll
-            for (int c = 0; c < 16; ++c) sv[c] = *(const u32x4*)(lds + (16 * c + sub) * EP + ch * 16);
-            if constexpr (RES != 0) {
+                for (int c = 0; c < 16; ++c)
+                    sv[c] = *(const u32x4*)(lds + (16 * c + sub) * EP + ch * 16);
                 residual_store(sv, sub, ch);
-                return;
-            }
-#pragma unroll
-            for (int c = 0; c < 16; ++c) {
-                const uint32_t off = (uint32_t)((16 * c + sub) * pitch + col0 * 2 + ch * 16) | drop;
-                if (row0 + 16 * c + 2 * wv < mv)
-                    __builtin_amdgcn_raw_buffer_store_b128(sv[c], rs0, off, 0, kNonTemporal);
-                else
-                    __builtin_amdgcn_raw_buffer_store_b128(sv[c], rs1, off, 0, kNonTemporal);
             }
             return;
         }
