@@ -114,7 +114,7 @@ __device__ __forceinline__ void norm_modulate(const float (&v)[NG][4], int lane,
 template <int K>
 __device__ __forceinline__ float stored(float x) {
     if (K == 1) return bf16_to_f32(f32_to_bf16(x));
-    if (K == 2) return (float)(_Float16)x;
+    if (K == 2) return (float)f32_to_f16(x);
     return x;
 }
 

@@ -315,7 +315,7 @@ __device__ __forceinline__ void conv3d_epilogue(const ConvArgs& a, const f32x16 
                         if (OK == 1)
                             ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
                         else if (OK == 2)
-                            ((_Float16*)a.out)[idx] = (_Float16)v[e];
+                            ((_Float16*)a.out)[idx] = f32_to_f16(v[e]);
                         else
                             ((float*)a.out)[idx] = v[e];
                     }
@@ -1118,7 +1118,7 @@ __global__ __launch_bounds__(512, 1) void conv3d_halo_kernel(ConvArgs a) {
                         if (OK == 1)
                             ((uint16_t*)a.out)[idx] = f32_to_bf16(v[e]);
                         else if (OK == 2)
-                            ((_Float16*)a.out)[idx] = (_Float16)v[e];
+                            ((_Float16*)a.out)[idx] = f32_to_f16(v[e]);
                         else
                             ((float*)a.out)[idx] = v[e];
                     }
@@ -1156,7 +1156,7 @@ __global__ __launch_bounds__(256) void conv3d_reduce_kernel(const float* __restr
     if (out_kind == 1)
         ((uint16_t*)out)[idx] = f32_to_bf16(v);
     else if (out_kind == 2)
-        ((_Float16*)out)[idx] = (_Float16)v;
+        ((_Float16*)out)[idx] = f32_to_f16(v);
     else
         ((float*)out)[idx] = v;
 }
@@ -1401,7 +1401,7 @@ __global__ __launch_bounds__(512, 1) void conv3d_rgbin_kernel(ConvArgs a, int st
                     if (OK == 1)
                         ((uint16_t*)a.out)[idx] = f32_to_bf16(v);
                     else if (OK == 2)
-                        ((_Float16*)a.out)[idx] = (_Float16)v;
+                        ((_Float16*)a.out)[idx] = f32_to_f16(v);
                     else
                         ((float*)a.out)[idx] = v;
                 }

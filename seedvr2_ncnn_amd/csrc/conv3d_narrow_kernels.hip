@@ -325,7 +325,7 @@ __global__ __launch_bounds__(256, 3 - buffers<KIND>()) void conv3d_narrow_kernel
                 if (a.out_kind == 1)
                     ((uint16_t*)a.out)[o] = f32_to_bf16(r);
                 else if (a.out_kind == 2)
-                    ((_Float16*)a.out)[o] = (_Float16)r;
+                    ((_Float16*)a.out)[o] = f32_to_f16(r);
                 else
                     ((float*)a.out)[o] = r;
             } else if (a.mem_out) {

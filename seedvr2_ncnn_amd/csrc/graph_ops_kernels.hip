@@ -31,7 +31,7 @@ __device__ __forceinline__ void st(void* p, long i, int kind, float v) {
     if (kind == 1)
         ((uint16_t*)p)[i] = f32_to_bf16(v);
     else if (kind == 2)
-        ((_Float16*)p)[i] = (_Float16)v;
+        ((_Float16*)p)[i] = f32_to_f16(v);
     else
         ((float*)p)[i] = v;
 }

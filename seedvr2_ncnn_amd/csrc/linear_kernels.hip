@@ -43,7 +43,7 @@ __device__ __forceinline__ void store1(void* y, long idx, float v) {
     if (YK == 1)
         ((uint16_t*)y)[idx] = f32_to_bf16(v);
     else if (YK == 2)
-        ((_Float16*)y)[idx] = (_Float16)v;
+        ((_Float16*)y)[idx] = f32_to_f16(v);
     else
         ((float*)y)[idx] = v;
 }
@@ -411,7 +411,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                         if (ACT == S2_ACT_GELU) v = gelu(v);
                         const int rl = ei.wm * 128 + 32 * i + 8 * (r >> 2) + 4 * ei.g + (r & 3);
                         if (YK == 2)
-                            *(_Float16*)(lds + rl * EP + cl * 2) = (_Float16)v;
+                            *(_Float16*)(lds + rl * EP + cl * 2) = f32_to_f16(v);
                         else
                             *(__bf16*)(lds + rl * EP + cl * 2) = (__bf16)v;
                     }
@@ -810,7 +810,7 @@ __global__ __launch_bounds__(512, 1) void shared_linear_256_kernel(
                         uint16_t hb[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
-                            hb[e] = YK == 2 ? __builtin_bit_cast(uint16_t, (_Float16)o[e])
+                            hb[e] = YK == 2 ? __builtin_bit_cast(uint16_t, f32_to_f16(o[e]))
                                             : __builtin_bit_cast(uint16_t, (__bf16)o[e]);
                         typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
                         const u32x2 hv = {hb[0] | ((uint32_t)hb[1] << 16),
@@ -1226,7 +1226,7 @@ __global__ void gelu_kernel(const T* x, T* y, size_t n) {
         else if constexpr (std::is_same<T, uint16_t>::value)
             y[i] = __builtin_bit_cast(uint16_t, (__bf16)gelu(bf16_to_f32(x[i])));
         else
-            y[i] = (_Float16)gelu((float)x[i]);
+            y[i] = f32_to_f16(gelu((float)x[i]));
     }
 }
 

@@ -43,10 +43,20 @@ __device__ __forceinline__ uint32_t pack2_bf16_rne(float lo, float hi) {
            ((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)hi) << 16);
 }
 
+// Storage conversion fp32 -> fp16, round to nearest even, of x as rounded to
+// fp32.  The empty asm keeps the compiler from folding the conversion into
+// the fma, add or multiply that produced x (a v_fma_mix*_f16 rounds the exact
+// result once, which differs from rounding to fp32 and then to fp16 when the
+// fp32 value lies on an fp16 midpoint).
+__device__ __forceinline__ _Float16 f32_to_f16(float x) {
+    asm("" : "+v"(x));
+    return (_Float16)x;
+}
+
 // two floats -> packed fp16 pair (low, high), round to nearest even
 __device__ __forceinline__ uint32_t pack2_f16_rne(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+    return (uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16(lo)) |
+           ((uint32_t)__builtin_bit_cast(uint16_t, f32_to_f16(hi)) << 16);
 }
 
 // Four consecutive floats stored at element `idx` of an activation buffer of

@@ -206,6 +206,42 @@ def test_fp16_activations(mv, mt, k, n, act):
         assert _tight(yv.float().cpu().numpy(), bf16_round(xv), bf16_round(w), b, act) < tol
 
 
+# one full wave of 256 tiles (no split tail), a split tail (860 tiles), and an
+# n that is not a multiple of 8 (the direct-store epilogue)
+@pytest.mark.parametrize("mv,mt,k,n", [(4000, 64, 256, 4096), (21600, 64, 2560, 2560),
+                                       (300, 40, 128, 260)])
+@pytest.mark.parametrize("act", [0, 1])
+def test_bf16_activations_16bit_outputs(mv, mt, k, n, act):
+    """bf16 activations with fp16 and bf16 outputs: each 16-bit output is the
+    round-to-nearest-even of the fp32 output of the same call (one rounding
+    of the fp32 accumulators), on every epilogue the 256x256-tile kernel
+    has."""
+    import torch
+    g = np.random.default_rng(mv + n + act)
+    xv = bf16_round(g.standard_normal((mv, k), dtype=np.float32))
+    xt = bf16_round(g.standard_normal((mt, k), dtype=np.float32))
+    w = (0.02 * g.standard_normal((n, k), dtype=np.float32))
+    b = (0.02 * g.standard_normal(n)).astype(np.float32)
+    tv = torch.from_numpy(xv).cuda().to(torch.bfloat16)
+    tt = torch.from_numpy(xt).cuda().to(torch.bfloat16)
+    wb = capi.cast_f32_to_bf16(torch.from_numpy(w).cuda())
+    tb = torch.from_numpy(b).cuda()
+    outs = {}
+    for odt in (torch.float32, torch.float16, torch.bfloat16):
+        yv, yt = capi.shared_linear(tv, tt, wb, tb, act, out_dtype=odt)
+        torch.cuda.synchronize()
+        assert yv.dtype == odt and yt.dtype == odt
+        outs[odt] = (yv.float().cpu().numpy(), yt.float().cpu().numpy())
+    yv, yt = outs[torch.float32]
+    for got, ref in zip(outs[torch.float16], (yv, yt)):
+        np.testing.assert_array_equal(got, ref.astype(np.float16).astype(np.float32))
+    for got, ref in zip(outs[torch.bfloat16], (yv, yt)):
+        np.testing.assert_array_equal(got, bf16_round(ref))
+    rows = np.concatenate([np.arange(0, 3), g.integers(0, mv, 24), np.arange(mv - 3, mv)]).astype(np.int32)
+    assert_close(yv[rows], oracle.linear(xv, w, b, act, rows=rows, threads=THREADS), "video rows")
+    assert_close(yt, oracle.linear(xt, w, b, act, threads=THREADS), "text")
+
+
 def test_fp32_activations_medium_shape():
     """fp32 activations take the 128x128-tile path (rounded to bf16 while
     staged): a 4,100-row, K = 2560 -> N = 2560 projection with GELU."""
