@@ -13,7 +13,7 @@ import pytest
 
 import oracle
 from common import (COSINE_TOL, MAX_ABS_TOL, Layer, assert_close, awa_param_string,
-                    make_awa_inputs, oracle_awa)
+                    bf16_round, make_awa_inputs, oracle_awa)
 from seedvr2_ncnn_amd import capi
 
 pytestmark = pytest.mark.gpu
@@ -189,10 +189,15 @@ def test_image_grid_64x64_dim2560(shifted):
     shapes, tl = [(1, 64, 64)], [64]
     case = make_awa_inputs(404 + shifted, shapes, tl, 20, 128, 21, bf16=True)
     rv, rt = oracle_awa(case, 20, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl)
+    outs = {}
     for out_dtype in (torch.float32, torch.bfloat16):
         ov, ot = _run_capi(case, 20, 128, (4, 3, 3), shifted, 21, shapes, tl, True, out_dtype)
         assert_close(ov, rv, f"video {out_dtype}")
         assert_close(ot, rt, f"text {out_dtype}")
+        outs[out_dtype] = (ov, ot)
+    # the bf16 output is the round-to-nearest-even of the fp32 one (one rounding)
+    for got, ref in zip(outs[torch.bfloat16], outs[torch.float32]):
+        np.testing.assert_array_equal(got, bf16_round(ref))
 
 
 @pytest.mark.parametrize("shifted", [0, 1])
@@ -203,11 +208,16 @@ def test_image_grid_64x64_dim2560_fp16(shifted):
     shapes, tl = [(1, 64, 64)], [64]
     case = make_awa_inputs(414 + shifted, shapes, tl, 20, 128, 21, fp16=True)
     rv, rt = oracle_awa(case, 20, 128, (4, 3, 3), shifted, 1e-5, 21, shapes, tl)
+    outs = {}
     for out_dtype in (torch.float16, torch.float32):
         ov, ot = _run_capi(case, 20, 128, (4, 3, 3), shifted, 21, shapes, tl, False, out_dtype,
                            in_dtype=torch.float16)
         assert_close(ov, rv, f"video {out_dtype}")
         assert_close(ot, rt, f"text {out_dtype}")
+        outs[out_dtype] = (ov, ot)
+    # the fp16 output is the round-to-nearest-even of the fp32 one (one rounding)
+    for got, ref in zip(outs[torch.float16], outs[torch.float32]):
+        np.testing.assert_array_equal(got, ref.astype(np.float16).astype(np.float32))
 
 
 @pytest.mark.parametrize("shifted", [0, 1])

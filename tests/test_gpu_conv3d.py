@@ -179,6 +179,26 @@ def test_conv3d_16bit_blobs_and_padded_cstep(in_dtype, out_dtype, hw, cstep_pad)
     assert_close(got, ref)
 
 
+# (64, 128, 10x12): the implicit-GEMM kernel; (64, 128, 6x120): the halo
+# kernel; (128, 3): the narrow output kernel; (3, 128): the RGB input kernel
+@pytest.mark.parametrize("cin,cout,hw", [(64, 128, (10, 12)), (64, 128, (6, 120)),
+                                         (128, 3, (10, 256)), (3, 128, (16, 16))])
+def test_conv3d_16bit_outputs_round_the_fp32_output(cin, cout, hw):
+    """bf16 and fp16 outputs are the round-to-nearest-even of the fp32
+    output of the same call (one rounding of the fp32 result)."""
+    import torch
+    cfgs = _cfg(cin, cout)
+    x, wts, bias = _case(cin, cout, 2, hw[0], hw[1], cfgs, 29 + cin)
+    x = bf16_round(x)
+    conv = _device(cfgs[0], wts, bias)
+    outs = {odt: _run(conv, x, dtype=torch.bfloat16, out_dtype=odt)
+            for odt in (torch.float32, torch.bfloat16, torch.float16)}
+    ref = outs[torch.float32]
+    np.testing.assert_array_equal(outs[torch.bfloat16], bf16_round(ref))
+    np.testing.assert_array_equal(outs[torch.float16], ref.astype(np.float16).astype(np.float32))
+    _check(ref, x, wts, bias, cfgs[1])
+
+
 # 6x10 frames copy the memory in front of the staged input (a DMA group of
 # 8 rows can straddle two frames); 8x10 frames read it in place, except with
 # 16 input channels (16-channel pixels always copy it); the halo kernel's

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from common import assert_close
+from common import assert_close, bf16_round
 from seedvr2_ncnn_amd import capi
 
 pytestmark = pytest.mark.gpu
@@ -59,6 +59,22 @@ def test_mha_explicit_scale_and_16bit_blobs():
         xs = torch.from_numpy(x).to(dt).float().numpy()    # the stored values
         got = _run(mha, xs, dtype=dt, out_dtype=odt)
         assert_close(got, oracle.mha(xs, 2, *ws, scale=0.3, threads=16))
+
+
+def test_mha_16bit_outputs_round_the_fp32_output():
+    """bf16 and fp16 outputs are the round-to-nearest-even of the fp32
+    output of the same call (one rounding of the fp32 result)."""
+    import torch
+    g = np.random.default_rng(12)
+    x = bf16_round(g.standard_normal((333, 256)).astype(np.float32))
+    ws = _weights(g, 256, 256)
+    mha = _device(2, ws)
+    outs = {odt: _run(mha, x, dtype=torch.bfloat16, out_dtype=odt)
+            for odt in (torch.float32, torch.bfloat16, torch.float16)}
+    ref = outs[torch.float32]
+    np.testing.assert_array_equal(outs[torch.bfloat16], bf16_round(ref))
+    np.testing.assert_array_equal(outs[torch.float16], ref.astype(np.float16).astype(np.float32))
+    assert_close(ref, oracle.mha(x, 2, *ws, threads=16))
 
 
 def test_mha_vae_frame_rows():
